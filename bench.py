@@ -1,0 +1,181 @@
+#!/usr/bin/env python3
+"""Attention-forward benchmark on one MI355X (the BASELINE.json metric).
+
+A step is one fused attention forward over one batch of synthetic input of the
+headline workload (SDXL self-attention fp16
+[2,10,4096,64], scale 1/8), called through the drop-in native op
+cmpext3.ops.attention with Q/K/V already resident in HBM.  W untimed warmup
+steps, then exactly K timed steps between synchronisations; prints ONE JSON
+line.
+
+  value        TFLOP/s over the K timed steps, FLOPs = 4*B*H*Sq*Sk*D
+  roofline     dominant kernel: FLOPs per launch / average launch duration,
+               measured with HIP events on the launch stream, vs the 2516.6
+               TFLOP/s dense fp16 MFMA peak; traffic = HBM bytes per launch
+               from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
+               (null if absent)
+  cpu_baseline stock torch SDPA on the host CPU (what the reference runs for CPU
+               tensors), same workload and dtype, bounded to ~10 s
+  configs      the same kernel timing for every BASELINE config (informational)
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+                       [--no-cpu-baseline] [--no-configs]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "torch-cmp-patch_amd"))
+sys.path.insert(0, REPO)
+os.environ.setdefault("CMPEXT3_AUTOPATCH", "0")
+
+
+def _ensure_built() -> None:
+    import sysconfig
+    pkg = os.path.join(REPO, "torch-cmp-patch_amd", "cmpext3")
+    native = os.path.join(pkg, "_native" + sysconfig.get_config_var("EXT_SUFFIX"))
+    if not (os.path.exists(os.path.join(pkg, "libcmpext3_attn.so")) and os.path.exists(native)):
+        import subprocess
+        subprocess.run([sys.executable, os.path.join(REPO, "torch-cmp-patch_amd", "build.py")],
+                       check=True)
+
+
+def _traffic_from_profile(workload: str):
+    """HBM bytes per launch from profiles/<kernel>_<workload>_hbm.txt, if committed."""
+    path = os.path.join(REPO, "profiles", f"attn_fwd_{workload}_hbm.txt")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"^hbm_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def time_kernel(fn, steps: int, warmup: int):
+    """(wall seconds for `steps` calls, mean per-call device seconds from events)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    end = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        start[i].record()
+        fn()
+        end[i].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    dev = sum(s.elapsed_time(e) for s, e in zip(start, end)) / steps / 1e3
+    return wall, dev
+
+
+def cpu_baseline(wl, budget_s: float = 10.0):
+    import torch
+    import torch.nn.functional as F
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    q, k, v = wl.make_inputs("cpu")
+    t0 = time.perf_counter()
+    F.scaled_dot_product_attention(q, k, v, is_causal=wl.causal, scale=wl.eff_scale)  # warmup
+    one = time.perf_counter() - t0
+    n = max(1, min(20, int(budget_s / max(one, 1e-3))))
+    t0 = time.perf_counter()
+    for _ in range(n):
+        F.scaled_dot_product_attention(q, k, v, is_causal=wl.causal, scale=wl.eff_scale)
+    dt = (time.perf_counter() - t0) / n
+    return {
+        "value": round(wl.flops() / dt / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "reference",
+        "sample": (f"stock torch.nn.functional.scaled_dot_product_attention on host CPU tensors "
+                   f"(the reference's path for CPU inputs), full {wl.name} workload "
+                   f"{list(wl.shapes()[0])} {wl.dtype}, 1 warmup + {n} timed calls, "
+                   f"{dt * 1e3:.1f} ms/call, os.cpu_count()={os.cpu_count()}"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default=None)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (attention forward shards per "
+              "(batch, head) with no exchange; see DESIGN.md). Run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    _ensure_built()
+    import torch
+    import cmpext3
+    from cmpext3 import workloads as W
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    wl = W.BY_NAME[args.workload] if args.workload else W.HEADLINE
+    torch.manual_seed(0)
+    q, k, v = wl.make_inputs("cuda")
+    fn = lambda: cmpext3.ops.attention(q, k, v, wl.eff_scale, wl.causal)  # noqa: E731
+
+    wall, dev = time_kernel(fn, args.steps, args.warmup)
+    ms = wall / args.steps * 1e3
+    value = wl.flops() * args.steps / wall / 1e12
+    achieved = wl.flops() / dev / 1e12
+    peak = W.PEAK_TFLOPS[wl.dtype]
+    traffic = _traffic_from_profile(wl.name)
+
+    configs = {}
+    if not args.no_configs:
+        for other in W.WORKLOADS:
+            qo, ko, vo = other.make_inputs("cuda")
+            f2 = lambda: cmpext3.ops.attention(qo, ko, vo, other.eff_scale, other.causal)  # noqa
+            _, d2 = time_kernel(f2, 20, 5)
+            configs[other.name] = {
+                "us_per_launch": round(d2 * 1e6, 2),
+                "tflops": round(other.flops() / d2 / 1e12, 2),
+                "pct_fp16_mfma_peak": round(100 * other.flops() / d2 / 1e12 / 2516.6, 2),
+                "pct_dtype_peak": round(100 * other.flops() / d2 / 1e12 / W.PEAK_TFLOPS[other.dtype], 2),
+                "hbm_gbs_algorithmic": round(other.bytes() / d2 / 1e9, 1),
+            }
+            del qo, ko, vo
+
+    line = {
+        "metric": "attention fwd TFLOP/s and % of MI355X fp16/bf16 MFMA peak; x vs host-CPU SDPA",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"fp16": "f16", "bf16": "bf16", "fp32": "f32"}[wl.dtype],
+        "data": "synthetic (seeded N(0,1) Q/K/V, CPU generator -> device)",
+        "config": {"workload": wl.name, "B": wl.B, "H": wl.H, "Sq": wl.Sq, "Sk": wl.Sk,
+                   "D": wl.D, "causal": wl.causal, "scale": wl.eff_scale,
+                   "entry": "cmpext3.ops.attention -> cmpext3_attn_fwd"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": peak,
+                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
+                     "kernel_us": round(dev * 1e6, 3), "flops_per_launch": wl.flops()},
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(wl),
+        "configs": configs,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

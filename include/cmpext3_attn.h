@@ -1,0 +1,92 @@
+/*
+ * cmpext3_attn.h -- C ABI of the MI355X (gfx950) fused attention forward.
+ *
+ * One entry point computes O = softmax(scale * Q K^T [+ causal mask]) V for
+ * [B, H, S, D] tensors that already live in device memory.  It allocates
+ * nothing: the caller owns every buffer, including the output.  All launches
+ * go on the stream the caller passes.
+ *
+ * Reference interfaces this replaces (WifiLast/torch-cmp-patch):
+ *   - launch_flash_attention_hfma2(q, k, v, o, B, H, Sq, Sk, D, qs, ks, vs, os,
+ *     scale, stream) -> bool              src/cuda/fp16_flash_attention_hfma2.cu:269-272
+ *   - launch_attention_fp16(q, k, v, o, B, H, S, D, scale, causal)
+ *                                          src/main.cpp:93 (fp16_attention.cu:328-386)
+ *   - launch_attention_fp32(q, k, v, o, B, H, S, D, scale)
+ *                                          src/main.cpp:92 (fp32_attention.cu:200-221)
+ * The three reference launchers are merged into one call that takes the
+ * dtype as an argument, accepts Sq != Sk and causal masking for every dtype,
+ * and reports failure through a return code instead of silently returning
+ * (the reference's fp16/fp32 launchers return void and may leave the output
+ * unwritten, src/main.cpp:1741-1765).
+ *
+ * Strides are in ELEMENTS, ordered {batch, head, seq}; the last (head-dim)
+ * dimension must be contiguous, as in the reference's HFMA2 launcher.
+ */
+#ifndef CMPEXT3_ATTN_H
+#define CMPEXT3_ATTN_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CMPEXT3_ATTN_ABI_VERSION 1
+
+/* dtype codes */
+#define CMPEXT3_DTYPE_F16  0
+#define CMPEXT3_DTYPE_BF16 1
+#define CMPEXT3_DTYPE_F32  2
+
+/* return codes */
+#define CMPEXT3_OK                 0
+#define CMPEXT3_E_INVALID          1  /* null pointer, negative size, bad stride */
+#define CMPEXT3_E_DTYPE            2  /* dtype code not one of the above */
+#define CMPEXT3_E_HEAD_DIM         3  /* D outside 1..256 or not a multiple of 8 (f16/bf16) / 4 (f32) */
+#define CMPEXT3_E_ALIGN            4  /* a base pointer or a row stride is not 16-byte aligned */
+#define CMPEXT3_E_EMPTY_KEYS       5  /* Sk == 0 with Sq > 0: softmax over nothing */
+#define CMPEXT3_E_LAUNCH           6  /* the HIP launch itself failed */
+#define CMPEXT3_E_TOO_LARGE        7  /* a size does not fit the kernel's index arithmetic */
+
+/*
+ * Fused attention forward.
+ *
+ *   q : [B, H, Sq, D]   k, v : [B, H, Sk, D]   o : [B, H, Sq, D]  (all `dtype`)
+ *   *_str[3] : element strides of dims {0, 1, 2}; dim 3 has stride 1.
+ *   scale    : multiplier of Q K^T (any finite value, 0 and negative allowed).
+ *   causal   : non-zero -> key j is visible to query i iff j <= i
+ *              (top-left aligned, the torch `is_causal` convention also for
+ *              Sq != Sk).
+ *   stream   : HIP stream to launch on (0 = the null stream).
+ *
+ * Returns CMPEXT3_OK, or one of the CMPEXT3_E_* codes above, in which case
+ * nothing was launched except for CMPEXT3_E_LAUNCH.  B*H*Sq == 0 is a no-op.
+ * Thread-safe; no host synchronisation.
+ */
+int cmpext3_attn_fwd(const void* q, const void* k, const void* v, void* o,
+                     int dtype, int B, int H, int Sq, int Sk, int D,
+                     const int64_t q_str[3], const int64_t k_str[3],
+                     const int64_t v_str[3], const int64_t o_str[3],
+                     float scale, int causal, hipStream_t stream);
+
+/* Human-readable text for a return code (static storage). */
+const char* cmpext3_attn_strerror(int code);
+
+/* CMPEXT3_ATTN_ABI_VERSION of the loaded library. */
+int cmpext3_attn_abi_version(void);
+
+/*
+ * Which kernel family and tile shape cmpext3_attn_fwd would pick for these
+ * arguments, written as text into buf (at most len bytes, NUL-terminated).
+ * Returns the same code cmpext3_attn_fwd would return before launching.
+ * Host-only: touches no device.
+ */
+int cmpext3_attn_describe(int dtype, int B, int H, int Sq, int Sk, int D,
+                          int causal, char* buf, int len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CMPEXT3_ATTN_H */

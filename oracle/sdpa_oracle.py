@@ -1,0 +1,171 @@
+"""CPU oracle for the fused attention forward.  TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+this module, and only to CHECK the HIP path (or to time a CPU baseline); the
+product path (the cmpext3 package) never imports it.
+
+Three restatements of O = softmax(scale * Q K^T [causal]) V:
+
+  sdpa_np    numpy float64, blocked over query rows (fast enough for the full
+             BASELINE shapes through BLAS);
+  sdpa_c     the C restatement in sdpa_oracle.c, float64, one row at a time
+             (small shapes; built by `make -C oracle`);
+  sdpa_loops pure-Python loops, for tiny brute-force cases only.
+
+Reference behaviour restated (WifiLast/torch-cmp-patch):
+  - math: tests_hardware/test_attention_bf16_routing.py:47-53 (fp32 matmul ->
+    softmax -> matmul) and tests_hardware/test_attention_causal.py:44-53
+    (causal = triu(diagonal=1) masked to -inf);
+  - default scale 1/sqrt(D): src/main.cpp:1700-1703;
+  - causal for Sq != Sk is top-left aligned (key j visible to query i iff
+    j <= i), which is torch's is_causal convention;
+  - max-abs error bar and the fp32-upcast oracle: tools/dev_flash_attn.py:24-27.
+Rows with no visible key give NaN, as torch's math SDPA does.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from typing import Optional
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libsdpa_oracle.so")
+_lib = None
+
+
+def default_scale(d: int) -> float:
+    """1/sqrt(D), the scale SDPA uses when none is given (src/main.cpp:1700-1703)."""
+    return 1.0 / math.sqrt(d)
+
+
+def _as_f64(x) -> np.ndarray:
+    try:
+        import torch
+        if isinstance(x, torch.Tensor):
+            return x.detach().to("cpu", torch.float64).numpy()
+    except ImportError:  # pragma: no cover
+        pass
+    return np.asarray(x, dtype=np.float64)
+
+
+def causal_visible(sq: int, sk: int) -> np.ndarray:
+    """[sq, sk] bool: key j visible to query i iff j <= i (top-left aligned)."""
+    return np.tril(np.ones((sq, sk), dtype=bool))
+
+
+def sdpa_np(q, k, v, scale: Optional[float] = None, causal: bool = False,
+            block: int = 512) -> np.ndarray:
+    """float64 SDPA over [B, H, S, D] arrays or tensors, blocked over query rows."""
+    q, k, v = _as_f64(q), _as_f64(k), _as_f64(v)
+    B, H, Sq, D = q.shape
+    Sk = k.shape[2]
+    Dv = v.shape[3]
+    if scale is None:
+        scale = default_scale(D)
+    out = np.empty((B, H, Sq, Dv), dtype=np.float64)
+    if Sk == 0:
+        out[...] = np.nan
+        return out
+    for b in range(B):
+        for h in range(H):
+            kt = k[b, h].T
+            for i0 in range(0, Sq, block):
+                i1 = min(Sq, i0 + block)
+                s = (q[b, h, i0:i1] @ kt) * scale
+                if causal:
+                    vis = causal_visible(Sq, Sk)[i0:i1]
+                    s = np.where(vis, s, -np.inf)
+                m = s.max(axis=1, keepdims=True)
+                with np.errstate(invalid="ignore"):
+                    e = np.exp(s - m)
+                    out[b, h, i0:i1] = (e @ v[b, h]) / e.sum(axis=1, keepdims=True)
+    return out
+
+
+def _load_c():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise FileNotFoundError(f"{_LIB_PATH} not built; run `make -C oracle`")
+        lib = ctypes.CDLL(_LIB_PATH)
+        p = ctypes.POINTER(ctypes.c_double)
+        i64 = ctypes.c_int64
+        lib.sdpa_oracle_f64.argtypes = [p, p, p, p, i64, i64, i64, i64, i64, i64,
+                                        ctypes.c_double, ctypes.c_int]
+        lib.sdpa_oracle_f64.restype = ctypes.c_int
+        _lib = lib
+    return _lib
+
+
+def c_available() -> bool:
+    try:
+        _load_c()
+        return True
+    except (OSError, FileNotFoundError):
+        return False
+
+
+def sdpa_c(q, k, v, scale: Optional[float] = None, causal: bool = False) -> np.ndarray:
+    """float64 SDPA through the C restatement (sdpa_oracle.c)."""
+    lib = _load_c()
+    q = np.ascontiguousarray(_as_f64(q))
+    k = np.ascontiguousarray(_as_f64(k))
+    v = np.ascontiguousarray(_as_f64(v))
+    B, H, Sq, D = q.shape
+    Sk, Dv = k.shape[2], v.shape[3]
+    if scale is None:
+        scale = default_scale(D)
+    out = np.empty((B, H, Sq, Dv), dtype=np.float64)
+    p = ctypes.POINTER(ctypes.c_double)
+    rc = lib.sdpa_oracle_f64(q.ctypes.data_as(p), k.ctypes.data_as(p), v.ctypes.data_as(p),
+                             out.ctypes.data_as(p), B, H, Sq, Sk, D, Dv, float(scale),
+                             1 if causal else 0)
+    if rc != 0:
+        raise RuntimeError(f"sdpa_oracle_f64 failed with code {rc}")
+    return out
+
+
+def sdpa_loops(q, k, v, scale: Optional[float] = None, causal: bool = False) -> np.ndarray:
+    """Pure-Python brute force (tiny inputs only)."""
+    q, k, v = _as_f64(q), _as_f64(k), _as_f64(v)
+    B, H, Sq, D = q.shape
+    Sk, Dv = k.shape[2], v.shape[3]
+    if scale is None:
+        scale = default_scale(D)
+    out = np.empty((B, H, Sq, Dv), dtype=np.float64)
+    for b in range(B):
+        for h in range(H):
+            for i in range(Sq):
+                keys = [j for j in range(Sk) if not causal or j <= i]
+                if not keys:
+                    out[b, h, i, :] = math.nan
+                    continue
+                s = [scale * sum(float(q[b, h, i, d]) * float(k[b, h, j, d]) for d in range(D))
+                     for j in keys]
+                m = max(s)
+                w = [math.exp(x - m) for x in s]
+                z = sum(w)
+                for e in range(Dv):
+                    out[b, h, i, e] = sum(w[t] * float(v[b, h, j, e])
+                                          for t, j in enumerate(keys)) / z
+    return out
+
+
+def max_abs_err(got, want) -> float:
+    """max |got - want| over all elements (NaN anywhere -> inf)."""
+    g, w = _as_f64(got), _as_f64(want)
+    if g.shape != w.shape:
+        raise ValueError(f"shape {g.shape} vs {w.shape}")
+    if g.size == 0:
+        return 0.0
+    d = np.abs(g - w)
+    if not np.all(np.isfinite(d)):
+        return math.inf
+    return float(d.max())
+
+
+# North-star tolerances (max abs error vs the fp32/f64 CPU oracle).
+TOLERANCE = {"fp16": 1e-2, "bf16": 2e-2, "fp32": 1e-4}

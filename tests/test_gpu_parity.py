@@ -1,0 +1,163 @@
+"""GPU parity of the fused attention forward, called through the C ABI.
+
+Bar (north star): max |kernel - oracle| <= 1e-2 (fp16), 2e-2 (bf16), 1e-4 (fp32),
+where the oracle is float64 SDPA on the CPU over the same dtype-rounded inputs
+(oracle/sdpa_oracle.py: sdpa_np for large shapes, the C restatement sdpa_c
+for the small sweep).
+
+Covers the five BASELINE configs at full size, then edge cases the reference
+exercises or that the tiling makes risky: ragged Sq/Sk (tile tails), Sk=1,
+cross-attention, causal with Sq <, =, > Sk (top-left), every head-dim bucket
+including non-power-of-two D, negative / zero / large scale, [B,S,H,D]-memory
+views and other strided inputs, and bitwise determinism across reruns.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from cmpext3 import abi
+from cmpext3 import workloads as W
+from oracle import sdpa_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL = orc.TOLERANCE
+
+
+def _run(q, k, v, scale, causal):
+    out = abi.attn_fwd(q, k, v, scale, causal)
+    torch.cuda.synchronize()
+    return out
+
+
+def _inputs(dtype, B, H, Sq, Sk, D, seed=0, kv_std=1.0, device="cuda"):
+    wl = W.Workload("case", dtype, B, H, Sq, Sk, D, kv_std=kv_std, seed=seed)
+    return wl.make_inputs(device)
+
+
+@pytest.mark.parametrize("wl", W.WORKLOADS, ids=[w.name for w in W.WORKLOADS])
+def test_baseline_config_full_size(wl):
+    q, k, v = wl.make_inputs("cuda")
+    out = _run(q, k, v, wl.eff_scale, wl.causal)
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), wl.eff_scale, wl.causal)
+    err = orc.max_abs_err(out.cpu(), ref)
+    print(f"{wl.name}: max abs err {err:.3e} (tol {TOL[wl.dtype]:.0e})", flush=True)
+    assert err <= TOL[wl.dtype]
+
+
+SMALL = [
+    # dtype, B, H, Sq, Sk, D, causal
+    ("fp16", 1, 1, 1, 1, 64, False),
+    ("fp16", 1, 2, 7, 1, 64, False),
+    ("fp16", 2, 3, 100, 77, 64, False),
+    ("fp16", 1, 2, 129, 300, 40, False),
+    ("fp16", 1, 1, 257, 65, 80, False),
+    ("fp16", 2, 2, 128, 128, 128, True),
+    ("fp16", 1, 2, 200, 333, 64, True),     # causal Sq < Sk
+    ("fp16", 1, 2, 333, 200, 64, True),     # causal Sq > Sk
+    ("bf16", 1, 2, 77, 77, 128, True),
+    ("bf16", 2, 2, 300, 129, 64, False),
+    ("bf16", 1, 1, 1, 513, 128, False),
+    ("bf16", 1, 3, 190, 190, 96, True),
+    ("fp32", 1, 2, 67, 67, 40, False),
+    ("fp32", 2, 2, 130, 70, 64, False),
+    ("fp32", 1, 2, 129, 129, 64, True),
+    ("fp32", 1, 1, 50, 300, 128, True),
+    ("fp32", 1, 1, 300, 50, 32, True),
+]
+
+
+@pytest.mark.parametrize("case", SMALL, ids=[
+    f"{c[0]}-B{c[1]}H{c[2]}-q{c[3]}k{c[4]}d{c[5]}{'-causal' if c[6] else ''}" for c in SMALL])
+def test_small_shapes(case):
+    dtype, B, H, Sq, Sk, D, causal = case
+    q, k, v = _inputs(dtype, B, H, Sq, Sk, D, seed=Sq * 7 + Sk)
+    scale = 1.0 / math.sqrt(D)
+    out = _run(q, k, v, scale, causal)
+    ref = orc.sdpa_c(q.cpu(), k.cpu(), v.cpu(), scale, causal)
+    err = orc.max_abs_err(out.cpu(), ref)
+    assert err <= TOL[dtype], f"max abs err {err:.3e}"
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+@pytest.mark.parametrize("D", [8, 16, 24, 40, 48, 56, 64, 72, 80, 96, 112, 128, 136, 160, 192,
+                               200, 256])
+def test_head_dim_buckets(dtype, D):
+    if dtype == "fp32" and D % 4:
+        pytest.skip("fp32 needs D % 4 == 0")
+    q, k, v = _inputs(dtype, 1, 2, 70, 90, D, seed=D)
+    scale = 1.0 / math.sqrt(D)
+    out = _run(q, k, v, scale, False)
+    ref = orc.sdpa_c(q.cpu(), k.cpu(), v.cpu(), scale, False)
+    assert orc.max_abs_err(out.cpu(), ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+@pytest.mark.parametrize("scale", [-0.125, 0.0, 0.5, 1e-3])
+@pytest.mark.parametrize("causal", [False, True])
+def test_scale_values(dtype, scale, causal):
+    q, k, v = _inputs(dtype, 1, 2, 96, 80, 64, seed=11)
+    out = _run(q, k, v, scale, causal)
+    ref = orc.sdpa_c(q.cpu(), k.cpu(), v.cpu(), scale, causal)
+    assert orc.max_abs_err(out.cpu(), ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+def test_bshd_views_and_strided_kv(dtype):
+    wl = W.Workload("v", dtype, 2, 5, 150, 150, 64, seed=21)
+    q, k, v = wl.make_inputs("cuda", layout="bshd")   # [B,H,S,D] views of [B,S,H,D]
+    assert not q.is_contiguous()
+    # K/V sliced out of a longer sequence: seq stride larger than D
+    big_k = torch.randn(2, 5, 400, 64, dtype=q.dtype, device="cuda")
+    big_v = torch.randn(2, 5, 400, 64, dtype=q.dtype, device="cuda")
+    k2, v2 = big_k[:, :, 100:250], big_v[:, :, 100:250]
+    for kk, vv in ((k, v), (k2, v2)):
+        for causal in (False, True):
+            out = _run(q, kk, vv, 0.125, causal)
+            ref = orc.sdpa_np(q.cpu(), kk.cpu(), vv.cpu(), 0.125, causal)
+            assert orc.max_abs_err(out.cpu(), ref) <= TOL[dtype]
+
+
+def test_output_stride_is_honoured():
+    q, k, v = _inputs("fp16", 2, 4, 64, 64, 64, seed=3)
+    o = torch.full((2, 64, 4, 64), float("nan"), dtype=q.dtype, device="cuda").transpose(1, 2)
+    rc = abi.attn_fwd_raw(q, k, v, o, 0.125, False)
+    torch.cuda.synchronize()
+    assert rc == abi.OK
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), 0.125, False)
+    assert orc.max_abs_err(o.cpu(), ref) <= TOL["fp16"]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+def test_deterministic_rerun(dtype):
+    """Same input twice -> bitwise identical output (an LDS race would show here)."""
+    q, k, v = _inputs(dtype, 2, 4, 500, 500, 64, seed=9)
+    a = _run(q, k, v, 0.125, True)
+    b = _run(q, k, v, 0.125, True)
+    assert torch.equal(a, b)
+
+
+def test_causal_differs_from_noncausal():
+    """Reference check tests_hardware/test_attention_causal.py:113-130: the causal
+    flag must actually reach the kernel."""
+    q, k, v = _inputs("fp16", 1, 4, 256, 256, 128, seed=0)
+    a = _run(q, k, v, 128 ** -0.5, True)
+    b = _run(q, k, v, 128 ** -0.5, False)
+    assert (a.float() - b.float()).abs().max().item() > 1e-3
+
+
+def test_empty_and_rejected_inputs_launch_nothing():
+    q, k, v = _inputs("fp16", 1, 2, 64, 64, 64)
+    o = torch.empty_like(q)
+    empty_q = q[:, :, :0]
+    assert abi.attn_fwd_raw(empty_q, k, v, o[:, :, :0], 0.125) == abi.OK
+    assert abi.attn_fwd_raw(q, k[:, :, :0], v[:, :, :0], o, 0.125) == abi.E_EMPTY_KEYS
+    odd = torch.randn(1, 2, 64, 36, dtype=torch.float16, device="cuda")
+    assert abi.attn_fwd_raw(odd, odd, odd, torch.empty_like(odd), 0.125) == abi.E_HEAD_DIM
+    mis = torch.randn(1, 2, 64 * 64 + 1, dtype=torch.float16, device="cuda")[..., 1:]
+    mis = mis.view(1, 2, 64, 64)
+    assert abi.attn_fwd_raw(mis, k, v, o, 0.125) == abi.E_ALIGN

@@ -1,0 +1,194 @@
+"""cmpext3 (MI355X build) -- routes torch.nn.functional.scaled_dot_product_attention
+through a hand-written gfx950 fused attention forward.
+
+Drop-in for the SDPA path of WifiLast/torch-cmp-patch's ``cmpext3`` package
+(cmpext3/__init__.py there): the same import-time patch, the same
+``enable()/disable()/is_enabled()/autoselect_report()`` controls, the same
+``ops`` handle on the native module, the same environment knobs
+(``CMPEXT3_AUTOPATCH``, ``CMPEXT3_DISABLE_OPS`` with the ``attention`` alias,
+``CMPEXT3_AUTOSELECT*``, ``CMPEXT3_VERBOSE``) and the same fallback rules.
+
+    import cmpext3          # patches F.scaled_dot_product_attention on import
+    cmpext3.disable()       # stock SDPA again
+    cmpext3.enable()
+
+What runs where:
+  * fp16 / bf16 [B,H,S,D] on the GPU: MFMA kernel (bf16 natively, no cast);
+  * fp32 on the GPU: fp32-MFMA kernel (causal included);
+  * causal (top-left, torch convention) and cross-attention (Sq != Sk) for
+    every dtype; head dims up to 256;
+  * stock torch for ``attn_mask``, ``dropout_p != 0``, non-4D inputs, live
+    autograd, CPU tensors and any other dtype -- the cases where the reference
+    itself falls back (cmpext3/__init__.py:624-628 there) -- and for any
+    argument the native op rejects (RuntimeError/TypeError), e.g. GQA head
+    counts or an empty key sequence.
+
+Only the attention op of the reference is in this package: its other patched
+ops (linear, conv, norms, activations, ...) and its NVML clock/power side
+effect are deliberately absent.
+"""
+from __future__ import annotations
+
+import os
+from typing import Any, Callable
+
+import torch
+import torch.nn.functional as F
+
+try:
+    from . import _native as _C
+except ImportError as exc:  # the product path never runs without its kernels
+    raise ImportError(
+        "cmpext3 native extension not built (cmpext3/_native*.so and "
+        "libcmpext3_attn.so). Build it with: python torch-cmp-patch_amd/build.py"
+    ) from exc
+
+# Raw, unpatched access to the native op(s): ops.attention(q, k, v, scale=None,
+# causal=False).  Same role as the reference's `ops = _C` (cmpext3/__init__.py:216).
+ops = _C
+
+from . import autoselect  # noqa: E402
+
+__all__ = ["enable", "disable", "is_enabled", "autoselect_report", "ops", "autoselect"]
+
+_SUPPORTED_DTYPES = (torch.float16, torch.float32, torch.bfloat16)
+_ORIGINALS: dict[tuple[Any, str], Callable] = {}
+_ENABLED = False
+
+# CMPEXT3_DISABLE_OPS=attention (or =scaled_dot_product_attention) keeps SDPA
+# stock; parsed once at import, like the reference (cmpext3/__init__.py:258-261).
+_OP_ALIASES = {"scaled_dot_product_attention": "attention"}
+_DISABLED_OPS = frozenset(
+    part.strip() for part in os.environ.get("CMPEXT3_DISABLE_OPS", "").split(",") if part.strip()
+)
+
+
+def _grad_safe(*tensors: Any) -> bool:
+    """True when a forward-only kernel cannot break autograd for these tensors:
+    inference mode, grad mode off, or no tensor argument requires grad."""
+    if torch.is_inference_mode_enabled() or not torch.is_grad_enabled():
+        return True
+    return not any(isinstance(t, torch.Tensor) and t.requires_grad for t in tensors)
+
+
+def _usable(*tensors: Any) -> bool:
+    """True when every tensor argument is a GPU fp16/fp32/bf16 tensor.
+    Non-tensor arguments are ignored."""
+    for t in tensors:
+        if isinstance(t, torch.Tensor) and (not t.is_cuda or t.dtype not in _SUPPORTED_DTYPES):
+            return False
+    return True
+
+
+def _install(target: Any, name: str, wrapper: Callable) -> None:
+    if name in _DISABLED_OPS or _OP_ALIASES.get(name, name) in _DISABLED_OPS:
+        return
+    slot = (target, name)
+    if slot not in _ORIGINALS:
+        _ORIGINALS[slot] = getattr(target, name)
+    _keep_scriptable(wrapper, _ORIGINALS[slot])
+    setattr(target, name, wrapper)
+
+
+def _keep_scriptable(wrapper: Callable, original: Callable) -> None:
+    """Let torch.jit.script keep resolving the patched name to the stock op.
+
+    TorchScript maps builtins by object identity; a Python wrapper in place of
+    F.scaled_dot_product_attention would otherwise make any scripted caller
+    try (and fail) to compile the wrapper.  Registering the wrapper as an
+    alias of the original's aten builtin keeps scripted code on stock while
+    eager calls go through the wrapper (same contract as the reference,
+    cmpext3/__init__.py:332-346).
+    """
+    from torch.jit import _builtins
+    op = _builtins._find_builtin(original)
+    if op is not None:
+        _builtins._register_builtin(wrapper, op)
+
+
+def _restore(target: Any, name: str) -> None:
+    original = _ORIGINALS.pop((target, name), None)
+    if original is not None:
+        setattr(target, name, original)
+
+
+_DTYPE_TAG = {torch.float16: "fp16", torch.float32: "fp32", torch.bfloat16: "bf16"}
+
+
+def _dispatch(op: str, ref: torch.Tensor, key: tuple,
+              native_call: Callable, stock_call: Callable) -> Any:
+    """Serve one call from the native kernel or stock torch.
+
+    With autoselect on, the choice is measured once per signature (correctness
+    first, then speed; see cmpext3/autoselect.py).  With it off: native, and
+    stock only when native raises RuntimeError/TypeError.
+    """
+    if autoselect.enabled():
+        try:
+            return autoselect.choose(f"{op} {_DTYPE_TAG.get(ref.dtype, ref.dtype)}",
+                                     key, native_call, stock_call)
+        except TypeError as exc:
+            if "unhashable" not in str(exc):
+                raise
+            # unhashable signature: skip measuring, behave as autoselect-off
+    try:
+        return native_call()
+    except (RuntimeError, TypeError):
+        return stock_call()
+
+
+def _patched_sdpa(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False,
+                  scale=None, **kwargs):
+    """F.scaled_dot_product_attention replacement (reference: cmpext3/__init__.py:609-633).
+
+    Bails to stock for attn_mask, dropout, non-4D query, live autograd and
+    non-GPU / unsupported dtypes.  Extra keyword arguments (e.g. enable_gqa)
+    reach only the stock call; the native op sees (q, k, v, scale, is_causal)
+    positionally and rejects shapes it does not support.
+    """
+    orig = _ORIGINALS[(F, "scaled_dot_product_attention")]
+
+    def stock():
+        return orig(query, key, value, attn_mask=attn_mask, dropout_p=dropout_p,
+                    is_causal=is_causal, scale=scale, **kwargs)
+
+    if (attn_mask is not None or dropout_p != 0.0
+            or not isinstance(query, torch.Tensor) or query.dim() != 4
+            or not _grad_safe(query, key, value)
+            or not _usable(query, key, value)):
+        return stock()
+    return _dispatch("attention", query,
+                     (query.shape, query.dtype, key.shape, value.shape, scale, is_causal),
+                     lambda: _C.attention(query, key, value, scale, is_causal),
+                     stock)
+
+
+def enable() -> None:
+    """Patch F.scaled_dot_product_attention (idempotent)."""
+    global _ENABLED
+    if _ENABLED:
+        return
+    if hasattr(F, "scaled_dot_product_attention"):
+        _install(F, "scaled_dot_product_attention", _patched_sdpa)
+    _ENABLED = True
+
+
+def disable() -> None:
+    """Restore every patched function to stock (no-op when not enabled)."""
+    global _ENABLED
+    for target, name in list(_ORIGINALS.keys()):
+        _restore(target, name)
+    _ENABLED = False
+
+
+def is_enabled() -> bool:
+    return _ENABLED
+
+
+def autoselect_report() -> str:
+    """Every native-vs-stock decision made so far, as printable text."""
+    return autoselect.format_report()
+
+
+if os.environ.get("CMPEXT3_AUTOPATCH", "1") != "0":
+    enable()

@@ -1,0 +1,98 @@
+"""ctypes binding of the C ABI in include/cmpext3_attn.h, for torch tensors.
+
+This is the FFI stub a host program written in Python would use to call the
+library directly (the torch extension `cmpext3._native` is the other caller).
+The library is loaded from this package directory; loading it needs no GPU.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcmpext3_attn.so")
+
+# Every function include/cmpext3_attn.h declares.
+SYMBOLS = ("cmpext3_attn_fwd", "cmpext3_attn_strerror", "cmpext3_attn_abi_version",
+           "cmpext3_attn_describe")
+
+DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
+OK, E_INVALID, E_DTYPE, E_HEAD_DIM, E_ALIGN, E_EMPTY_KEYS, E_LAUNCH, E_TOO_LARGE = range(8)
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is not built (python torch-cmp-patch_amd/build.py)")
+        L = ctypes.CDLL(LIB_PATH)
+        i64p = ctypes.POINTER(ctypes.c_int64)
+        vp = ctypes.c_void_p
+        ci = ctypes.c_int
+        L.cmpext3_attn_fwd.argtypes = [vp, vp, vp, vp, ci, ci, ci, ci, ci, ci,
+                                       i64p, i64p, i64p, i64p, ctypes.c_float, ci, vp]
+        L.cmpext3_attn_fwd.restype = ci
+        L.cmpext3_attn_strerror.argtypes = [ci]
+        L.cmpext3_attn_strerror.restype = ctypes.c_char_p
+        L.cmpext3_attn_abi_version.argtypes = []
+        L.cmpext3_attn_abi_version.restype = ci
+        L.cmpext3_attn_describe.argtypes = [ci, ci, ci, ci, ci, ci, ci, ctypes.c_char_p, ci]
+        L.cmpext3_attn_describe.restype = ci
+        _lib = L
+    return _lib
+
+
+def strerror(code: int) -> str:
+    return lib().cmpext3_attn_strerror(code).decode()
+
+
+def describe(dtype: int, B: int, H: int, Sq: int, Sk: int, D: int, causal: bool = False):
+    buf = ctypes.create_string_buffer(256)
+    rc = lib().cmpext3_attn_describe(dtype, B, H, Sq, Sk, D, int(causal), buf, 256)
+    return rc, buf.value.decode()
+
+
+def dtype_code(dtype) -> int:
+    import torch
+    return {torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16, torch.float32: DTYPE_F32}[dtype]
+
+
+def _strides(t):
+    arr = (ctypes.c_int64 * 3)(t.stride(0), t.stride(1), t.stride(2))
+    return arr
+
+
+def attn_fwd_raw(q, k, v, o, scale: float, causal: bool = False, stream=None,
+                 D: Optional[int] = None) -> int:
+    """Call cmpext3_attn_fwd on [B,H,S,D] tensors (any strides with unit last stride).
+    Returns the C return code; launches on `stream` (a torch.cuda.Stream, a raw
+    handle, or None for the current stream)."""
+    import torch
+    if stream is None:
+        handle = torch.cuda.current_stream(q.device).cuda_stream if q.is_cuda else 0
+    elif isinstance(stream, int):
+        handle = stream
+    else:
+        handle = stream.cuda_stream
+    B, H, Sq, Dq = q.shape
+    return lib().cmpext3_attn_fwd(
+        ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()),
+        ctypes.c_void_p(v.data_ptr()), ctypes.c_void_p(o.data_ptr()),
+        dtype_code(q.dtype), B, H, Sq, k.shape[2], Dq if D is None else D,
+        _strides(q), _strides(k), _strides(v), _strides(o),
+        ctypes.c_float(scale), int(causal), ctypes.c_void_p(handle))
+
+
+def attn_fwd(q, k, v, scale: Optional[float] = None, causal: bool = False, stream=None):
+    """Allocate O like q (contiguous [B,H,Sq,D]) and run the kernel through the C ABI.
+    Raises RuntimeError with the library's message on a non-zero return code."""
+    import torch
+    o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    if scale is None:
+        scale = q.shape[-1] ** -0.5
+    rc = attn_fwd_raw(q, k, v, o, scale, causal, stream)
+    if rc != OK:
+        raise RuntimeError(f"cmpext3_attn_fwd: {strerror(rc)} (code {rc})")
+    return o

@@ -1,0 +1,141 @@
+// C ABI of the fused attention forward: argument validation and kernel dispatch.
+//
+// Replaces the reference's three launchers (launch_flash_attention_hfma2,
+// launch_attention_fp16, launch_attention_fp32; src/main.cpp:92-108) and the
+// shape/alignment checks its torch binding does before calling them
+// (src/main.cpp:1637-1650, 1669-1681, 1741-1768).  Unsupported input is
+// reported by return code and nothing is launched, so the caller can fall
+// back; the reference's void launchers instead skipped the launch and left the
+// output unwritten (src/main.cpp:1741-1765).
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/cmpext3_attn.h"
+#include "attn_common.h"
+
+namespace cmpext3 {
+hipError_t launch_mfma16(const FwdParams& p, bool bf16, bool causal, hipStream_t s);
+hipError_t launch_mfma32(const FwdParams& p, bool causal, hipStream_t s);
+int mfma16_bucket(int D);
+int mfma32_bucket(int D);
+void describe_mfma16(int D, int Sq, char* buf, int len);
+void describe_mfma32(int D, int Sq, char* buf, int len);
+}  // namespace cmpext3
+
+namespace {
+
+int elem_size(int dtype) {
+  switch (dtype) {
+    case CMPEXT3_DTYPE_F16:
+    case CMPEXT3_DTYPE_BF16: return 2;
+    case CMPEXT3_DTYPE_F32: return 4;
+  }
+  return 0;
+}
+
+// Checks that need no pointers: sizes, dtype, head dim.
+int check_shape(int dtype, int B, int H, int Sq, int Sk, int D) {
+  const int es = elem_size(dtype);
+  if (es == 0) return CMPEXT3_E_DTYPE;
+  if (B < 0 || H < 0 || Sq < 0 || Sk < 0 || D < 0) return CMPEXT3_E_INVALID;
+  if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;  // nothing to compute
+  if (Sk == 0) return CMPEXT3_E_EMPTY_KEYS;
+  if (D == 0 || D > 256) return CMPEXT3_E_HEAD_DIM;
+  if (D % (16 / es) != 0) return CMPEXT3_E_HEAD_DIM;  // whole 16-byte chunks per row
+  // workgroup count and in-kernel int arithmetic on (b*H + h) and row indices
+  if ((int64_t)B * H * ((Sq + 63) / 64) > (int64_t)INT32_MAX / 2) return CMPEXT3_E_TOO_LARGE;
+  if (Sq > INT32_MAX - 512 || Sk > INT32_MAX - 512) return CMPEXT3_E_TOO_LARGE;
+  return CMPEXT3_OK;
+}
+
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+// A stride only matters if its dimension has more than one index.
+bool stride_ok(const int64_t s[3], int n0, int n1, int n2, int es) {
+  const int64_t n[3] = {n0, n1, n2};
+  for (int i = 0; i < 3; ++i) {
+    if (n[i] <= 1) continue;
+    if (s[i] < 0) return false;
+    if ((s[i] * es) % 16 != 0) return false;
+  }
+  return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cmpext3_attn_abi_version(void) { return CMPEXT3_ATTN_ABI_VERSION; }
+
+const char* cmpext3_attn_strerror(int code) {
+  switch (code) {
+    case CMPEXT3_OK: return "success";
+    case CMPEXT3_E_INVALID: return "invalid argument (null pointer, negative size or stride)";
+    case CMPEXT3_E_DTYPE: return "unsupported dtype (expected f16, bf16 or f32)";
+    case CMPEXT3_E_HEAD_DIM:
+      return "unsupported head dim (need 1..256 and a multiple of 8 for f16/bf16, 4 for f32)";
+    case CMPEXT3_E_ALIGN: return "misaligned tensor (base pointers and row strides must be 16-byte aligned)";
+    case CMPEXT3_E_EMPTY_KEYS: return "key/value sequence is empty";
+    case CMPEXT3_E_LAUNCH: return "HIP kernel launch failed";
+    case CMPEXT3_E_TOO_LARGE: return "problem too large for 32-bit tile indexing";
+  }
+  return "unknown error code";
+}
+
+int cmpext3_attn_describe(int dtype, int B, int H, int Sq, int Sk, int D, int causal, char* buf,
+                          int len) {
+  const int rc = check_shape(dtype, B, H, Sq, Sk, D);
+  if (buf && len > 0) {
+    if (rc != CMPEXT3_OK) {
+      snprintf(buf, len, "unsupported: %s", cmpext3_attn_strerror(rc));
+    } else if ((int64_t)B * H * Sq == 0) {
+      snprintf(buf, len, "empty problem: no launch");
+    } else {
+      char kb[160];
+      if (dtype == CMPEXT3_DTYPE_F32)
+        cmpext3::describe_mfma32(D, Sq, kb, sizeof kb);
+      else
+        cmpext3::describe_mfma16(D, Sq, kb, sizeof kb);
+      snprintf(buf, len, "%s%s", kb, causal ? " causal" : "");
+    }
+  }
+  return rc;
+}
+
+int cmpext3_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype, int B, int H,
+                     int Sq, int Sk, int D, const int64_t q_str[3], const int64_t k_str[3],
+                     const int64_t v_str[3], const int64_t o_str[3], float scale, int causal,
+                     hipStream_t stream) {
+  int rc = check_shape(dtype, B, H, Sq, Sk, D);
+  if (rc != CMPEXT3_OK) return rc;
+  if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;
+  if (!q || !k || !v || !o || !q_str || !k_str || !v_str || !o_str) return CMPEXT3_E_INVALID;
+  if (!isfinite(scale)) return CMPEXT3_E_INVALID;
+  const int es = elem_size(dtype);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return CMPEXT3_E_ALIGN;
+  if (!stride_ok(q_str, B, H, Sq, es) || !stride_ok(k_str, B, H, Sk, es) ||
+      !stride_ok(v_str, B, H, Sk, es) || !stride_ok(o_str, B, H, Sq, es))
+    return CMPEXT3_E_ALIGN;
+
+  cmpext3::FwdParams p;
+  memset(&p, 0, sizeof p);
+  p.q = q; p.k = k; p.v = v; p.o = o;
+  p.q_b = q_str[0]; p.q_h = q_str[1]; p.q_s = q_str[2];
+  p.k_b = k_str[0]; p.k_h = k_str[1]; p.k_s = k_str[2];
+  p.v_b = v_str[0]; p.v_h = v_str[1]; p.v_s = v_str[2];
+  p.o_b = o_str[0]; p.o_h = o_str[1]; p.o_s = o_str[2];
+  p.B = B; p.H = H; p.Sq = Sq; p.Sk = Sk; p.D = D;
+  // exp2-domain multiplier; a negative scale is folded into Q's sign bits
+  p.c = fabsf(scale) * cmpext3::kLog2e;
+  p.q_sign = (scale < 0.f) ? (dtype == CMPEXT3_DTYPE_F32 ? 0x80000000u : 0x80008000u) : 0u;
+
+  hipError_t err;
+  if (dtype == CMPEXT3_DTYPE_F32)
+    err = cmpext3::launch_mfma32(p, causal != 0, stream);
+  else
+    err = cmpext3::launch_mfma16(p, dtype == CMPEXT3_DTYPE_BF16, causal != 0, stream);
+  return err == hipSuccess ? CMPEXT3_OK : CMPEXT3_E_LAUNCH;
+}
+
+}  // extern "C"

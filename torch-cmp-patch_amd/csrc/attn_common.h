@@ -1,0 +1,68 @@
+// Shared definitions of the gfx950 attention-forward kernels.
+//
+// Both kernel families compute O = softmax(scale * Q K^T [+ causal]) V for one
+// (batch, head, query-block) per workgroup, streaming K/V tiles through LDS with
+// an online (running max / running sum) softmax in the exp2 domain.  The math
+// is the one of the reference's flash kernel (Q pre-scaled by scale*log2(e),
+// exp2 online softmax, fp32 running max/sum/output, one final 1/l:
+// src/cuda/fp16_flash_attention_hfma2.cu:98-109,162-192,216-238), laid out for
+// CDNA4 MFMA instead of HFMA2 dot pairs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cmpext3 {
+
+struct FwdParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  // element strides of dims {batch, head, seq}; head-dim stride is 1
+  int64_t q_b, q_h, q_s;
+  int64_t k_b, k_h, k_s;
+  int64_t v_b, v_h, v_s;
+  int64_t o_b, o_h, o_s;
+  int B, H, Sq, Sk, D;
+  int n_qblk;       // query blocks per (batch, head)
+  int n_wg;         // workgroups launched = B * H * n_qblk
+  float c;          // |scale| * log2(e): scores enter exp2 as s * c - m
+  uint32_t q_sign;  // sign mask XORed into Q words when scale < 0
+};
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kNumXcd = 8;  // MI355X: 8 XCDs, each with its own L2
+
+// The command processor hands workgroup i to XCD i % 8.  Give every XCD one
+// contiguous range of logical tiles so that the query blocks of one head, which
+// all stream the same K/V, share that XCD's L2.
+__device__ __forceinline__ int xcd_remap(int wg, int n) {
+  const int x = wg % kNumXcd;
+  const int j = wg / kNumXcd;
+  const int base = n / kNumXcd;
+  const int rem = n % kNumXcd;
+  return x * base + (x < rem ? x : rem) + j;
+}
+
+// max / sum of a value with its partner 32 lanes away (v_permlane32_swap):
+// lane L receives {x[L mod 32], x[32 + L mod 32]} in the two results.
+__device__ __forceinline__ float xhalf_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xhalf_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace cmpext3

@@ -1,0 +1,308 @@
+// Fused attention forward for fp32 on gfx950 fp32 MFMA (v_mfma_f32_16x16x4f32).
+//
+// Same structure as the fp16/bf16 kernel (one workgroup = one (batch, head)
+// pair x BQ query rows; K/V tiles double-buffered through LDS; S^T = K Q^T so
+// that each lane owns one query column), but on 16x16 fp32 MFMA blocks: the
+// products are exact fp32 products accumulated in fp32, so no precision is
+// given up anywhere (the north-star bound for fp32 is 1e-4 max abs error).
+// In the 16x16 accumulator a lane holds 4 consecutive keys of one query, so a
+// row reduction spans the 4 lane groups (two cross-lane steps), and P^T feeds
+// the PV MFMA's B operand one accumulator element per k-step, lane-local.
+// V stays row-major in LDS: a PV A-operand element is V[key][d] with d along
+// the 16 lanes of a group, which is a conflict-free LDS read.
+//
+// Reference: src/cuda/fp32_attention.cu:35-198 (one thread per query row,
+// serial D loops, non-causal only, Sq == Sk only, D <= 128, and 1/l taken
+// through an fp16 reciprocal at :179-180).  This kernel drops every one of
+// those limits; 1/l is an fp32 reciprocal.
+#include "attn_common.h"
+
+namespace cmpext3 {
+
+__device__ __forceinline__ f32x4 mma32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// DK: head dim bucket (multiple of 4, zero-padded above D); NQB: 16-row query
+// blocks per wave.
+template <int DK, int NW, int NQB, int BK, bool CAUSAL>
+__global__ void __launch_bounds__(NW * 64)
+attn_fwd_mfma32(const FwdParams p) {
+  constexpr int NT = NW * 64;
+  constexpr int QPW = 16 * NQB;
+  constexpr int BQ = NW * QPW;
+  constexpr int DPV = (DK + 15) / 16 * 16;                  // PV output rows
+  constexpr int RSK = ((DK / 4) % 2 == 0) ? DK + 4 : DK;    // 4*odd floats: conflict-free
+  constexpr int RSV = DPV + 4;                              // 4 mod 16 floats
+  constexpr int KTILE = BK * RSK;
+  constexpr int VTILE = BK * RSV;
+  constexpr int KCH = DK / 4;       // 16-byte chunks per K row
+  constexpr int VCH = DPV / 4;
+  constexpr int KLD = (BK * KCH + NT - 1) / NT;
+  constexpr int VLD = (BK * VCH + NT - 1) / NT;
+  constexpr int NKB = BK / 16;
+  constexpr int NDB = DPV / 16;
+  constexpr int NKS = DK / 4;
+  static_assert(BK % 16 == 0 && DK % 4 == 0, "tile shape");
+
+  __shared__ __attribute__((aligned(16))) float lds[2 * (KTILE + VTILE)];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int l16 = lane & 15;
+  const int g = lane >> 4;
+
+  const int tile = xcd_remap(blockIdx.x, p.n_wg);
+  const int bh = tile / p.n_qblk;
+  int qblk = tile - bh * p.n_qblk;
+  if (CAUSAL) qblk = p.n_qblk - 1 - qblk;
+  const int b = bh / p.H;
+  const int h = bh - b * p.H;
+  const int q0 = qblk * BQ;
+
+  const float* __restrict__ qg = (const float*)p.q + b * p.q_b + h * p.q_h;
+  const float* __restrict__ kg = (const float*)p.k + b * p.k_b + h * p.k_h;
+  const float* __restrict__ vg = (const float*)p.v + b * p.v_b + h * p.v_h;
+  float* __restrict__ og = (float*)p.o + b * p.o_b + h * p.o_h;
+
+  const int Sq = p.Sq, Sk = p.Sk, D = p.D;
+  const int qw0 = q0 + wave * QPW;
+
+  int kend = Sk;
+  if (CAUSAL) kend = min(Sk, q0 + BQ);
+  const int ntiles = (kend + BK - 1) / BK;
+
+  // Q^T as the B operand: lane (l16, g) holds Q[row][4s + g]
+  float qf[NQB][NKS];
+  const float qsign = p.q_sign ? -1.f : 1.f;
+#pragma unroll
+  for (int qb = 0; qb < NQB; ++qb) {
+    const int row = qw0 + 16 * qb + l16;
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) {
+      const int d = 4 * s + g;
+      qf[qb][s] = (row < Sq && d < D) ? qsign * qg[(int64_t)row * p.q_s + d] : 0.f;
+    }
+  }
+
+  f32x4 oacc[NQB][NDB];
+#pragma unroll
+  for (int qb = 0; qb < NQB; ++qb)
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) oacc[qb][db] = (f32x4){};
+  float m_run[NQB], l_run[NQB];
+#pragma unroll
+  for (int qb = 0; qb < NQB; ++qb) {
+    m_run[qb] = -INFINITY;
+    l_run[qb] = 0.f;
+  }
+  const float c = p.c;
+
+  u32x4 kreg[KLD], vreg[VLD];
+  auto load_tile = [&](int t) {
+    const int k0 = t * BK;
+#pragma unroll
+    for (int it = 0; it < KLD; ++it) {
+      const int ci = it * NT + tid;
+      const int r = ci / KCH, c4 = ci - (ci / KCH) * KCH;
+      u32x4 x = {0u, 0u, 0u, 0u};
+      if ((BK * KCH % NT == 0 || ci < BK * KCH) && k0 + r < Sk && 4 * c4 < D)
+        x = *(const u32x4*)(kg + (int64_t)(k0 + r) * p.k_s + 4 * c4);
+      kreg[it] = x;
+    }
+#pragma unroll
+    for (int it = 0; it < VLD; ++it) {
+      const int ci = it * NT + tid;
+      const int r = ci / VCH, c4 = ci - (ci / VCH) * VCH;
+      u32x4 x = {0u, 0u, 0u, 0u};
+      if ((BK * VCH % NT == 0 || ci < BK * VCH) && k0 + r < Sk && 4 * c4 < D)
+        x = *(const u32x4*)(vg + (int64_t)(k0 + r) * p.v_s + 4 * c4);
+      vreg[it] = x;
+    }
+  };
+  auto store_tile = [&](int buf) {
+    float* ks = lds + buf * (KTILE + VTILE);
+    float* vs = ks + KTILE;
+#pragma unroll
+    for (int it = 0; it < KLD; ++it) {
+      const int ci = it * NT + tid;
+      if (BK * KCH % NT == 0 || ci < BK * KCH) {
+        const int r = ci / KCH, c4 = ci - (ci / KCH) * KCH;
+        *(u32x4*)(ks + r * RSK + 4 * c4) = kreg[it];
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < VLD; ++it) {
+      const int ci = it * NT + tid;
+      if (BK * VCH % NT == 0 || ci < BK * VCH) {
+        const int r = ci / VCH, c4 = ci - (ci / VCH) * VCH;
+        *(u32x4*)(vs + r * RSV + 4 * c4) = vreg[it];
+      }
+    }
+  };
+
+  if (ntiles > 0) load_tile(0);
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    store_tile(buf);
+    __syncthreads();
+    if (t + 1 < ntiles) load_tile(t + 1);
+
+    const int k0 = t * BK;
+    const bool active = !CAUSAL || k0 <= qw0 + QPW - 1;
+    if (active) {
+      const float* ks = lds + buf * (KTILE + VTILE);
+      const float* vs = ks + KTILE;
+
+      f32x4 sacc[NQB][NKB];
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) sacc[qb][kb] = (f32x4){};
+        const float* krow = ks + (16 * kb + l16) * RSK + g;
+#pragma unroll
+        for (int s = 0; s < NKS; ++s) {
+          const float a = krow[4 * s];
+#pragma unroll
+          for (int qb = 0; qb < NQB; ++qb) sacc[qb][kb] = mma32(a, qf[qb][s], sacc[qb][kb]);
+        }
+      }
+
+      const bool need_mask = (k0 + BK > Sk) || (CAUSAL && k0 + BK - 1 > qw0);
+      float cm = c;
+      if (need_mask) {
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+          const int qrow = qw0 + 16 * qb + l16;
+#pragma unroll
+          for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int key = k0 + 16 * kb + 4 * g + r;
+              const bool dead = key >= Sk || (CAUSAL && key > qrow);
+              sacc[qb][kb][r] = dead ? -INFINITY : sacc[qb][kb][r] * c;
+            }
+        }
+        cm = 1.f;
+      }
+
+      float pr[NQB][NKB][4];
+#pragma unroll
+      for (int qb = 0; qb < NQB; ++qb) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sacc[qb][kb][r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_tile = (mx == -INFINITY) ? -INFINITY : mx * cm;
+        const float m_new = fmaxf(m_run[qb], m_tile);
+        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+        const float alpha = fast_exp2(m_run[qb] - m_use);
+        m_run[qb] = m_new;
+        float lsum = l_run[qb] * alpha;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) oacc[qb][db] *= alpha;
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float pv = fast_exp2(sacc[qb][kb][r] * cm - m_use);
+            pr[qb][kb][r] = pv;
+            lsum += pv;
+          }
+        l_run[qb] = lsum;
+      }
+
+      // O^T += V^T P^T, one 4-key k-slice per (kb, r)
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float a = vs[(16 * kb + 4 * g + r) * RSV + 16 * db + l16];
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb) oacc[qb][db] = mma32(a, pr[qb][kb][r], oacc[qb][db]);
+          }
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int qb = 0; qb < NQB; ++qb) {
+    float l = l_run[qb];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    const float inv = 1.f / l;
+    const int qrow = qw0 + 16 * qb + l16;
+    if (qrow < Sq) {
+      float* orow = og + (int64_t)qrow * p.o_s;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const int d = 16 * db + 4 * g;
+        if (d < D) *(f32x4*)(orow + d) = oacc[qb][db] * inv;
+      }
+    }
+  }
+}
+
+template <int DK, bool CAUSAL>
+hipError_t launch_mfma32_inst(const FwdParams& p0, hipStream_t stream) {
+  constexpr int NW = 4;
+  constexpr int NQB = (DK <= 128) ? 2 : 1;
+  constexpr int BK = (DK <= 128) ? 32 : 16;
+  constexpr int BQ = NW * 16 * NQB;
+  FwdParams p = p0;
+  p.n_qblk = (p.Sq + BQ - 1) / BQ;
+  p.n_wg = p.B * p.H * p.n_qblk;
+  if (p.n_wg == 0) return hipSuccess;
+  hipLaunchKernelGGL((attn_fwd_mfma32<DK, NW, NQB, BK, CAUSAL>), dim3(p.n_wg), dim3(NW * 64), 0,
+                     stream, p);
+  return hipGetLastError();
+}
+
+static const int kMfma32Dk[] = {16, 32, 40, 48, 64, 80, 96, 128, 160, 192, 256};
+
+int mfma32_bucket(int D) {
+  for (int dk : kMfma32Dk)
+    if (D <= dk) return dk;
+  return -1;
+}
+
+template <bool CAUSAL>
+static hipError_t launch_mfma32_dk(const FwdParams& p, int dk, hipStream_t s) {
+  switch (dk) {
+    case 16: return launch_mfma32_inst<16, CAUSAL>(p, s);
+    case 32: return launch_mfma32_inst<32, CAUSAL>(p, s);
+    case 40: return launch_mfma32_inst<40, CAUSAL>(p, s);
+    case 48: return launch_mfma32_inst<48, CAUSAL>(p, s);
+    case 64: return launch_mfma32_inst<64, CAUSAL>(p, s);
+    case 80: return launch_mfma32_inst<80, CAUSAL>(p, s);
+    case 96: return launch_mfma32_inst<96, CAUSAL>(p, s);
+    case 128: return launch_mfma32_inst<128, CAUSAL>(p, s);
+    case 160: return launch_mfma32_inst<160, CAUSAL>(p, s);
+    case 192: return launch_mfma32_inst<192, CAUSAL>(p, s);
+    case 256: return launch_mfma32_inst<256, CAUSAL>(p, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_mfma32(const FwdParams& p, bool causal, hipStream_t s) {
+  const int dk = mfma32_bucket(p.D);
+  if (dk < 0) return hipErrorInvalidValue;
+  return causal ? launch_mfma32_dk<true>(p, dk, s) : launch_mfma32_dk<false>(p, dk, s);
+}
+
+void describe_mfma32(int D, int Sq, char* buf, int len) {
+  const int dk = mfma32_bucket(D);
+  const int bq = dk <= 128 ? 128 : 64;
+  snprintf(buf, len, "mfma32 16x16x4f32 S^T-form: DK=%d DPV=%d waves=4 BQ=%d BK=%d qblocks=%d", dk,
+           (dk + 15) / 16 * 16, bq, dk <= 128 ? 32 : 16, (Sq + bq - 1) / bq);
+}
+
+}  // namespace cmpext3

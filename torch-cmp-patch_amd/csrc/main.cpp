@@ -1,0 +1,133 @@
+// cmpext3._native -- torch binding of the fused attention forward.
+//
+// attention(query, key, value, scale=None, causal=False) -> Tensor
+//   Same signature and error convention as the reference's binding
+//   (src/main.cpp:2353-2358 -> custom_attention_forward, :1603-1774): every
+//   unsupported input raises RuntimeError (TORCH_CHECK) so that the Python
+//   patch falls back to stock SDPA.  The compute goes through the C ABI in
+//   include/cmpext3_attn.h on the caller's current stream.
+//
+// Differences from the reference binding, by design:
+//   * bf16 runs natively (the reference casts bf16 -> fp16 -> bf16, :1623-1627);
+//   * causal, Sq != Sk and strided inputs are accepted for every dtype;
+//   * a [B,S,H,D]-memory query (diffusers/webui layout viewed as [B,H,S,D])
+//     gets its output in [B,S,H,D] memory too, returned as the same kind of
+//     view (the reference's HFMA2 path does this for fp16, :1652);
+//   * head dims that are not a whole number of 16-byte chunks, and tensors
+//     whose base pointer or row strides are not 16-byte aligned, are repacked
+//     into zero-padded contiguous copies instead of being rejected.
+#include <cmath>
+
+#include <torch/extension.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+
+#include "../../include/cmpext3_attn.h"
+
+namespace {
+
+int dtype_code(at::ScalarType t) {
+  switch (t) {
+    case at::kHalf: return CMPEXT3_DTYPE_F16;
+    case at::kBFloat16: return CMPEXT3_DTYPE_BF16;
+    case at::kFloat: return CMPEXT3_DTYPE_F32;
+    default: return -1;
+  }
+}
+
+int launch(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v,
+           torch::Tensor& o, int dtype, int D, float scale, bool causal, hipStream_t stream) {
+  const int64_t qs[3] = {q.stride(0), q.stride(1), q.stride(2)};
+  const int64_t ks[3] = {k.stride(0), k.stride(1), k.stride(2)};
+  const int64_t vs[3] = {v.stride(0), v.stride(1), v.stride(2)};
+  const int64_t os[3] = {o.stride(0), o.stride(1), o.stride(2)};
+  if (q.stride(3) != 1 || k.stride(3) != 1 || v.stride(3) != 1 || o.stride(3) != 1)
+    return CMPEXT3_E_ALIGN;
+  return cmpext3_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dtype,
+                          (int)q.size(0), (int)q.size(1), (int)q.size(2), (int)k.size(2), D, qs,
+                          ks, vs, os, scale, causal ? 1 : 0, stream);
+}
+
+bool is_bshd_view(const torch::Tensor& t) {
+  // [B,H,S,D] view of [B,S,H,D] memory
+  const int64_t H = t.size(1), S = t.size(2), D = t.size(3);
+  return H > 1 && S > 1 && t.stride(3) == 1 && t.stride(1) == D && t.stride(2) == H * D &&
+         t.stride(0) == S * H * D;
+}
+
+}  // namespace
+
+torch::Tensor attention(torch::Tensor query, torch::Tensor key, torch::Tensor value,
+                        c10::optional<double> scale_arg, bool causal) {
+  TORCH_CHECK(query.dim() == 4, "cmpext3 attention: query must be 4D [B, H, S, D]");
+  TORCH_CHECK(key.dim() == 4, "cmpext3 attention: key must be 4D");
+  TORCH_CHECK(value.dim() == 4, "cmpext3 attention: value must be 4D");
+  TORCH_CHECK(query.is_cuda() && key.is_cuda() && value.is_cuda(),
+              "cmpext3 attention: tensors must be on the GPU");
+  TORCH_CHECK(query.device() == key.device() && query.device() == value.device(),
+              "cmpext3 attention: device mismatch");
+  TORCH_CHECK(query.scalar_type() == key.scalar_type() && query.scalar_type() == value.scalar_type(),
+              "cmpext3 attention: q, k, v must share one dtype");
+  const int dtype = dtype_code(query.scalar_type());
+  TORCH_CHECK(dtype >= 0, "cmpext3 attention: unsupported dtype ", query.scalar_type());
+
+  const int64_t B = query.size(0), H = query.size(1), Sq = query.size(2), D = query.size(3);
+  const int64_t Sk = key.size(2);
+  TORCH_CHECK(key.size(0) == B && key.size(1) == H && key.size(3) == D,
+              "cmpext3 attention: key shape mismatch");
+  TORCH_CHECK(value.size(0) == B && value.size(1) == H && value.size(2) == Sk && value.size(3) == D,
+              "cmpext3 attention: value shape mismatch");
+  TORCH_CHECK(D >= 1 && D <= 256, "cmpext3 attention: head dim ", D, " outside 1..256");
+  TORCH_CHECK(Sk > 0 || B * H * Sq == 0, "cmpext3 attention: empty key sequence");
+
+  const float scale = scale_arg.has_value() ? (float)scale_arg.value()
+                                            : 1.0f / std::sqrt((float)D);
+  TORCH_CHECK(std::isfinite(scale), "cmpext3 attention: non-finite scale");
+
+  const at::hip::HIPGuardMasqueradingAsCUDA guard(query.device());
+  hipStream_t stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA(query.device().index()).stream();
+
+  torch::Tensor out = is_bshd_view(query)
+                          ? torch::empty({B, Sq, H, D}, query.options()).transpose(1, 2)
+                          : torch::empty({B, H, Sq, D}, query.options());
+  if (out.numel() == 0) return out;
+
+  int rc = launch(query, key, value, out, dtype, (int)D, scale, causal, stream);
+  if (rc == CMPEXT3_E_ALIGN || rc == CMPEXT3_E_HEAD_DIM) {
+    // Repack into contiguous copies zero-padded to whole 16-byte chunks.
+    // Zero columns add nothing to Q K^T, and the padded V columns only produce
+    // output columns that are cut away again; `scale` already used the true D.
+    const int64_t chunk = (dtype == CMPEXT3_DTYPE_F32) ? 4 : 8;
+    const int64_t Dp = (D + chunk - 1) / chunk * chunk;
+    TORCH_CHECK(Dp <= 256, "cmpext3 attention: padded head dim ", Dp, " exceeds 256");
+    auto pad = [&](const torch::Tensor& t) {
+      return Dp == D ? t.clone(at::MemoryFormat::Contiguous)
+                     : at::constant_pad_nd(t, {0, Dp - D}, 0).contiguous();
+    };
+    torch::Tensor qp = pad(query), kp = pad(key), vp = pad(value);
+    torch::Tensor op = torch::empty({B, H, Sq, Dp}, query.options());
+    rc = launch(qp, kp, vp, op, dtype, (int)Dp, scale, causal, stream);
+    if (rc == CMPEXT3_OK) out = (Dp == D) ? op : op.narrow(3, 0, D).contiguous();
+  }
+  TORCH_CHECK(rc == CMPEXT3_OK, "cmpext3 attention: ", cmpext3_attn_strerror(rc));
+  return out;
+}
+
+std::string describe(int64_t dtype, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
+                     bool causal) {
+  char buf[256];
+  cmpext3_attn_describe((int)dtype, (int)B, (int)H, (int)Sq, (int)Sk, (int)D, causal ? 1 : 0, buf,
+                        sizeof buf);
+  return std::string(buf);
+}
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.doc() = "cmpext3 native ops for MI355X (gfx950): fused attention forward";
+  m.def("attention", &attention, "Fused SDPA forward (fp16/bf16/fp32, causal or not)",
+        py::arg("query"), py::arg("key"), py::arg("value"), py::arg("scale") = py::none(),
+        py::arg("causal") = false);
+  m.def("describe", &describe, "Kernel/tile choice for a problem (host only)", py::arg("dtype"),
+        py::arg("B"), py::arg("H"), py::arg("Sq"), py::arg("Sk"), py::arg("D"),
+        py::arg("causal") = false);
+  m.def("abi_version", &cmpext3_attn_abi_version, "C ABI version of libcmpext3_attn.so");
+}
