@@ -14,7 +14,8 @@
  *     tests_hardware/test_attention_causal.py:44-53 (triu(diagonal=1) masked
  *     to -inf, i.e. key j visible to query i iff j <= i, top-left aligned,
  *     which is torch's is_causal convention also for Sq != Sk).
- * A row with no visible key yields NaN, as torch's math SDPA does.
+ * A row with no visible key (only possible when Sk == 0) yields zeros, as
+ * torch's math SDPA does for an empty key sequence.
  *
  * Layout: contiguous [B, H, S, D] (q, o) and [B, H, Sk, D] / [B, H, Sk, Dv].
  * Pinning (tests/test_oracle.py): agreement with torch's math SDPA on CPU,
@@ -40,7 +41,7 @@ int sdpa_oracle_f64(const double* q, const double* k, const double* v, double* o
       const int64_t nvis = causal ? (i + 1 < Sk ? i + 1 : Sk) : Sk;
       double* orow = oh + i * Dv;
       if (nvis == 0) {
-        for (int64_t e = 0; e < Dv; ++e) orow[e] = NAN;
+        for (int64_t e = 0; e < Dv; ++e) orow[e] = 0.0;
         continue;
       }
       double m = -INFINITY;

@@ -20,7 +20,7 @@ Reference behaviour restated (WifiLast/torch-cmp-patch):
   - causal for Sq != Sk is top-left aligned (key j visible to query i iff
     j <= i), which is torch's is_causal convention;
   - max-abs error bar and the fp32-upcast oracle: tools/dev_flash_attn.py:24-27.
-Rows with no visible key give NaN, as torch's math SDPA does.
+Rows with no visible key (Sk == 0) give zeros, as torch's math SDPA does.
 """
 from __future__ import annotations
 
@@ -67,7 +67,7 @@ def sdpa_np(q, k, v, scale: Optional[float] = None, causal: bool = False,
         scale = default_scale(D)
     out = np.empty((B, H, Sq, Dv), dtype=np.float64)
     if Sk == 0:
-        out[...] = np.nan
+        out[...] = 0.0
         return out
     for b in range(B):
         for h in range(H):
@@ -141,7 +141,7 @@ def sdpa_loops(q, k, v, scale: Optional[float] = None, causal: bool = False) -> 
             for i in range(Sq):
                 keys = [j for j in range(Sk) if not causal or j <= i]
                 if not keys:
-                    out[b, h, i, :] = math.nan
+                    out[b, h, i, :] = 0.0
                     continue
                 s = [scale * sum(float(q[b, h, i, d]) * float(k[b, h, j, d]) for d in range(D))
                      for j in keys]

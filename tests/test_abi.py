@@ -1,0 +1,91 @@
+"""C ABI checks that need no GPU: the library loads, exports every function
+include/*.h declares, and rejects bad arguments before touching the device."""
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from cmpext3 import abi
+
+REPO = Path(__file__).resolve().parents[1]
+
+
+def _declared_functions():
+    names = set()
+    for h in (REPO / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"^\s*(?:int|const char\*|void)\s+(cmpext3_\w+)\s*\(", text, re.M))
+    return names
+
+
+def test_header_declares_what_the_binding_lists():
+    assert _declared_functions() == set(abi.SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    out = subprocess.run(["nm", "-D", "--defined-only", abi.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = _declared_functions() - exported
+    assert not missing, missing
+    lib = abi.lib()
+    for name in _declared_functions():
+        assert hasattr(lib, name)
+
+
+def test_version_and_messages():
+    assert abi.lib().cmpext3_attn_abi_version() == 1
+    for code in range(8):
+        assert abi.strerror(code) and abi.strerror(code) != "unknown error code"
+    assert abi.strerror(99) == "unknown error code"
+
+
+@pytest.mark.parametrize("dtype,D,expect", [
+    (abi.DTYPE_F16, 64, abi.OK), (abi.DTYPE_BF16, 128, abi.OK), (abi.DTYPE_F32, 40, abi.OK),
+    (abi.DTYPE_F16, 36, abi.E_HEAD_DIM), (abi.DTYPE_F32, 6, abi.E_HEAD_DIM),
+    (abi.DTYPE_F16, 264, abi.E_HEAD_DIM), (7, 64, abi.E_DTYPE),
+])
+def test_describe_classifies(dtype, D, expect):
+    rc, text = abi.describe(dtype, 2, 10, 4096, 4096, D)
+    assert rc == expect
+    if rc == abi.OK:
+        assert "mfma" in text
+
+
+def test_describe_baseline_configs():
+    from cmpext3 import workloads as W
+    for w in W.WORKLOADS:
+        rc, text = abi.describe(abi.dtype_code(w.torch_dtype), w.B, w.H, w.Sq, w.Sk, w.D, w.causal)
+        assert rc == abi.OK, text
+        assert ("causal" in text) == w.causal
+
+
+def _call(q=16, k=16, v=16, o=16, dtype=abi.DTYPE_F16, B=1, H=1, Sq=8, Sk=8, D=64,
+          strides=(512, 512, 64), scale=0.125):
+    st = (ctypes.c_int64 * 3)(*strides)
+    return abi.lib().cmpext3_attn_fwd(ctypes.c_void_p(q), ctypes.c_void_p(k), ctypes.c_void_p(v),
+                                      ctypes.c_void_p(o), dtype, B, H, Sq, Sk, D, st, st, st, st,
+                                      ctypes.c_float(scale), 0, None)
+
+
+# Fake device addresses: every case below must be rejected before any launch.
+def test_rejections_before_launch():
+    assert _call(dtype=5) == abi.E_DTYPE
+    assert _call(B=-1) == abi.E_INVALID
+    assert _call(D=0) == abi.E_HEAD_DIM
+    assert _call(D=12) == abi.E_HEAD_DIM
+    assert _call(Sk=0) == abi.E_EMPTY_KEYS
+    assert _call(q=0) == abi.E_INVALID
+    assert _call(q=24) == abi.E_ALIGN
+    assert _call(strides=(512, 512, 60)) == abi.E_ALIGN
+    assert _call(scale=float("inf")) == abi.E_INVALID
+    assert _call(scale=float("nan")) == abi.E_INVALID
+
+
+def test_empty_problem_is_a_noop_even_without_pointers():
+    assert _call(q=0, k=0, v=0, o=0, Sq=0) == abi.OK
+    assert _call(q=0, k=0, v=0, o=0, B=0) == abi.OK

@@ -1,0 +1,395 @@
+"""Dispatch-layer tests of the cmpext3 SDPA patch (CPU only, no GPU).
+
+Mirrors the reference's mock-based suite for this path
+(tests/test_cmpext3_monkeypatch.py there: TestGradSafe/TestUsable,
+TestEnableDisable :91-180, TestAutoselect :476-643,
+TestScaledDotProductAttention :857-926), written against this package: the
+native module is a fake whose `attention` is a MagicMock (`native` fixture),
+and force_eligible() lets CPU tensors through the GPU/dtype gate.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import cmpext3
+from conftest import PKG_ROOT, STOCK_SDPA, force_eligible
+
+
+def _called_once_with_tensors(mock_fn, *expected):
+    assert mock_fn.call_count == 1, f"expected 1 call, got {mock_fn.call_count}"
+    args, kwargs = mock_fn.call_args
+    assert kwargs == {}
+    assert len(args) == len(expected)
+    for got, want in zip(args, expected):
+        if isinstance(want, torch.Tensor):
+            assert isinstance(got, torch.Tensor) and torch.equal(got, want)
+        else:
+            assert got == want
+
+
+def _qkv(*shape):
+    return torch.randn(*shape), torch.randn(*shape), torch.randn(*shape)
+
+
+class TestGradSafe:
+    def test_true_when_grad_disabled(self):
+        x = torch.randn(2, requires_grad=True)
+        with torch.no_grad():
+            assert cmpext3._grad_safe(x) is True
+
+    def test_true_in_inference_mode(self):
+        x = torch.randn(2, requires_grad=True)
+        with torch.inference_mode():
+            assert cmpext3._grad_safe(x) is True
+
+    def test_false_when_any_tensor_requires_grad(self):
+        assert cmpext3._grad_safe(torch.randn(2), torch.randn(2, requires_grad=True)) is False
+
+    def test_true_when_no_tensor_requires_grad(self):
+        assert cmpext3._grad_safe(torch.randn(2), torch.randn(2)) is True
+
+    def test_non_tensor_args_are_ignored(self):
+        assert cmpext3._grad_safe(1, "x", None) is True
+
+
+class TestUsable:
+    def test_true_for_non_tensor_args(self):
+        assert cmpext3._usable(1, "x", None) is True
+
+    def test_false_for_cpu_tensor(self):
+        assert cmpext3._usable(torch.randn(2)) is False
+
+    @pytest.mark.parametrize("dtype,ok", [(torch.int64, False), (torch.float64, False),
+                                          (torch.float16, True), (torch.float32, True),
+                                          (torch.bfloat16, True)])
+    def test_dtype_gate_on_fake_gpu_tensor(self, monkeypatch, dtype, ok):
+        x = torch.zeros(2, dtype=dtype)
+        monkeypatch.setattr(torch.Tensor, "is_cuda", property(lambda self: True))
+        assert cmpext3._usable(x) is ok
+
+
+class TestEnableDisable:
+    def test_enable_installs_sdpa(self, patched):
+        assert cmpext3.is_enabled() is True
+        assert F.scaled_dot_product_attention is cmpext3._patched_sdpa
+
+    def test_disable_restores_original(self, patched):
+        orig = cmpext3._ORIGINALS[(F, "scaled_dot_product_attention")]
+        cmpext3.disable()
+        assert F.scaled_dot_product_attention is orig is STOCK_SDPA
+        assert cmpext3.is_enabled() is False
+        cmpext3.enable()  # keep the fixture's teardown meaningful
+
+    def test_enable_is_idempotent(self, patched):
+        first = cmpext3._ORIGINALS[(F, "scaled_dot_product_attention")]
+        cmpext3.enable()
+        assert cmpext3._ORIGINALS[(F, "scaled_dot_product_attention")] is first
+        assert F.scaled_dot_product_attention is cmpext3._patched_sdpa
+
+    def test_disable_without_enable_is_noop(self):
+        assert cmpext3.is_enabled() is False
+        cmpext3.disable()
+        assert cmpext3.is_enabled() is False
+        assert F.scaled_dot_product_attention is STOCK_SDPA
+
+    @pytest.mark.parametrize("names", [{"attention"}, {"scaled_dot_product_attention"}])
+    def test_disable_ops_pins_attention_to_stock(self, monkeypatch, names):
+        monkeypatch.setattr(cmpext3, "_DISABLED_OPS", frozenset(names))
+        cmpext3.enable()
+        try:
+            assert F.scaled_dot_product_attention is STOCK_SDPA
+        finally:
+            cmpext3.disable()
+
+    def test_ops_alias_is_native_module(self, native):
+        assert cmpext3.ops is native
+
+    def test_torchscript_still_sees_stock_sdpa(self, patched):
+        @torch.jit.script
+        def f(q, k, v):
+            return F.scaled_dot_product_attention(q, k, v)
+        q = torch.randn(1, 1, 4, 8)
+        assert torch.allclose(f(q, q, q), STOCK_SDPA(q, q, q))
+
+    def test_import_patches_unless_autopatch_is_zero(self):
+        code = ("import torch.nn.functional as F, cmpext3; "
+                "print(F.scaled_dot_product_attention is cmpext3._patched_sdpa)")
+        for env_val, want in (("1", "True"), ("0", "False")):
+            env = dict(os.environ, CMPEXT3_AUTOPATCH=env_val, PYTHONPATH=str(PKG_ROOT))
+            out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True,
+                                 text=True, timeout=300)
+            assert out.returncode == 0, out.stderr
+            assert out.stdout.strip().splitlines()[-1] == want
+
+    def test_disable_ops_env_var_is_read_at_import(self):
+        code = ("import torch.nn.functional as F, cmpext3; "
+                "print(F.scaled_dot_product_attention is cmpext3._patched_sdpa)")
+        env = dict(os.environ, CMPEXT3_AUTOPATCH="1", CMPEXT3_DISABLE_OPS="conv2d, attention",
+                   PYTHONPATH=str(PKG_ROOT))
+        out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True,
+                             text=True, timeout=300)
+        assert out.returncode == 0, out.stderr
+        assert out.stdout.strip().splitlines()[-1] == "False"
+
+
+class TestScaledDotProductAttention:
+    def test_calls_native_when_eligible(self, patched, native, monkeypatch):
+        force_eligible(monkeypatch)
+        q, k, v = _qkv(1, 2, 3, 4)
+        native.attention.return_value = "native-result"
+        assert F.scaled_dot_product_attention(q, k, v) == "native-result"
+        _called_once_with_tensors(native.attention, q, k, v, None, False)
+
+    def test_passes_scale_and_is_causal_positionally(self, patched, native, monkeypatch):
+        force_eligible(monkeypatch)
+        q, k, v = _qkv(1, 2, 3, 4)
+        native.attention.return_value = "native-result"
+        assert F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=0.3) == "native-result"
+        _called_once_with_tensors(native.attention, q, k, v, 0.3, True)
+
+    def test_falls_back_when_attn_mask_given(self, patched, native, monkeypatch):
+        force_eligible(monkeypatch)
+        q, k, v = _qkv(1, 2, 3, 4)
+        out = F.scaled_dot_product_attention(q, k, v, attn_mask=torch.zeros(3, 3, dtype=torch.bool))
+        native.attention.assert_not_called()
+        assert out.shape == q.shape
+
+    def test_falls_back_when_dropout_nonzero(self, patched, native, monkeypatch):
+        force_eligible(monkeypatch)
+        q, k, v = _qkv(1, 2, 3, 4)
+        F.scaled_dot_product_attention(q, k, v, dropout_p=0.1)
+        native.attention.assert_not_called()
+
+    def test_falls_back_on_non_4d_query(self, patched, native, monkeypatch):
+        force_eligible(monkeypatch)
+        q, k, v = _qkv(2, 3, 4)
+        F.scaled_dot_product_attention(q, k, v)
+        native.attention.assert_not_called()
+
+    def test_falls_back_when_not_gpu(self, patched, native):
+        q, k, v = _qkv(1, 2, 3, 4)
+        out = F.scaled_dot_product_attention(q, k, v)
+        native.attention.assert_not_called()
+        assert torch.allclose(out, STOCK_SDPA(q, k, v))
+
+    def test_falls_back_when_autograd_is_live(self, patched, native, monkeypatch):
+        monkeypatch.setattr(torch.Tensor, "is_cuda", property(lambda self: True))
+        q = torch.randn(1, 2, 3, 4, requires_grad=True)
+        k, v = torch.randn(1, 2, 3, 4), torch.randn(1, 2, 3, 4)
+        monkeypatch.setattr(cmpext3, "_ORIGINALS",
+                            {**cmpext3._ORIGINALS, (F, "scaled_dot_product_attention"):
+                             lambda *a, **kw: "stock"})
+        assert F.scaled_dot_product_attention(q, k, v) == "stock"
+        native.attention.assert_not_called()
+
+    def test_falls_back_on_native_runtime_error(self, patched, native, monkeypatch):
+        force_eligible(monkeypatch)
+        native.attention.side_effect = RuntimeError("boom")
+        q, k, v = _qkv(1, 2, 3, 4)
+        out = F.scaled_dot_product_attention(q, k, v)
+        native.attention.assert_called_once()
+        assert torch.allclose(out, STOCK_SDPA(q, k, v))
+
+    def test_falls_back_on_native_type_error(self, patched, native, monkeypatch):
+        force_eligible(monkeypatch)
+        native.attention.side_effect = TypeError("bad args")
+        q, k, v = _qkv(1, 2, 3, 4)
+        assert F.scaled_dot_product_attention(q, k, v).shape == q.shape
+
+    def test_extra_kwargs_reach_only_stock(self, patched, native, monkeypatch):
+        force_eligible(monkeypatch)
+        native.attention.side_effect = RuntimeError("gqa head count")
+        q = torch.randn(1, 4, 3, 8)
+        k, v = torch.randn(1, 2, 3, 8), torch.randn(1, 2, 3, 8)
+        out = F.scaled_dot_product_attention(q, k, v, enable_gqa=True)
+        _called_once_with_tensors(native.attention, q, k, v, None, False)
+        assert torch.allclose(out, STOCK_SDPA(q, k, v, enable_gqa=True))
+
+
+class TestAutoselect:
+    @staticmethod
+    def _timed(monkeypatch, autoselect, timings):
+        monkeypatch.setattr(autoselect, "_time", lambda fn: (timings[fn], fn()))
+
+    def test_picks_the_faster_implementation(self, autoselecting, monkeypatch):
+        calls = {"native": 0, "stock": 0}
+
+        def native():
+            calls["native"] += 1
+            return torch.zeros(4)
+
+        def stock():
+            calls["stock"] += 1
+            return torch.zeros(4)
+
+        self._timed(monkeypatch, autoselecting, {native: 0.001, stock: 0.010})
+        autoselecting.choose("op", ("k",), native, stock)
+        d = autoselecting._decisions[("k",)]
+        assert d.use_native and d.speedup == pytest.approx(10.0)
+        before = calls["stock"]
+        for _ in range(3):
+            autoselecting.choose("op", ("k",), native, stock)
+        assert calls["stock"] == before
+
+    def test_picks_stock_when_the_kernel_is_slower(self, autoselecting, monkeypatch):
+        calls = {"native": 0}
+
+        def native():
+            calls["native"] += 1
+            return torch.zeros(4)
+
+        def stock():
+            return torch.zeros(4)
+
+        self._timed(monkeypatch, autoselecting, {native: 0.010, stock: 0.001})
+        autoselecting.choose("op", ("k",), native, stock)
+        assert not autoselecting._decisions[("k",)].use_native
+        before = calls["native"]
+        for _ in range(3):
+            autoselecting.choose("op", ("k",), native, stock)
+        assert calls["native"] == before
+
+    def test_rejects_a_kernel_whose_output_disagrees(self, autoselecting, monkeypatch):
+        native = lambda: torch.full((4,), 10.0)  # noqa: E731
+        stock = lambda: torch.zeros(4)  # noqa: E731
+        self._timed(monkeypatch, autoselecting, {native: 0.001, stock: 0.010})
+        got = autoselecting.choose("op", ("k",), native, stock)
+        d = autoselecting._decisions[("k",)]
+        assert not d.use_native and "mismatch" in d.note
+        assert torch.equal(got, torch.zeros(4))
+
+    def test_tolerates_rounding_differences(self, autoselecting, monkeypatch):
+        native = lambda: torch.ones(4) * (1.0 + 1e-6)  # noqa: E731
+        stock = lambda: torch.ones(4)  # noqa: E731
+        self._timed(monkeypatch, autoselecting, {native: 0.001, stock: 0.010})
+        autoselecting.choose("op", ("k",), native, stock)
+        assert autoselecting._decisions[("k",)].use_native
+
+    @pytest.mark.parametrize("dtype,rel,ok", [(torch.float16, 2e-2, True), (torch.float16, 4e-2, False),
+                                              (torch.bfloat16, 4e-2, True), (torch.float32, 2e-3, False)])
+    def test_per_dtype_tolerance(self, autoselecting, monkeypatch, dtype, rel, ok):
+        native = lambda: (torch.ones(8) * (1 + rel)).to(dtype)  # noqa: E731
+        stock = lambda: torch.ones(8).to(dtype)  # noqa: E731
+        self._timed(monkeypatch, autoselecting, {native: 0.001, stock: 0.010})
+        autoselecting.choose("op", ("k",), native, stock)
+        assert autoselecting._decisions[("k",)].use_native is ok
+
+    def test_rejects_non_finite_output(self, autoselecting, monkeypatch):
+        native = lambda: torch.full((4,), float("nan"))  # noqa: E731
+        stock = lambda: torch.zeros(4)  # noqa: E731
+        self._timed(monkeypatch, autoselecting, {native: 0.001, stock: 0.010})
+        autoselecting.choose("op", ("k",), native, stock)
+        assert not autoselecting._decisions[("k",)].use_native
+
+    def test_shape_mismatch_is_rejected(self, autoselecting, monkeypatch):
+        native = lambda: torch.zeros(5)  # noqa: E731
+        stock = lambda: torch.zeros(4)  # noqa: E731
+        self._timed(monkeypatch, autoselecting, {native: 0.001, stock: 0.010})
+        autoselecting.choose("op", ("k",), native, stock)
+        assert "shape" in autoselecting._decisions[("k",)].note
+
+    def test_kernel_that_raises_is_never_probed_again(self, autoselecting):
+        calls = {"native": 0}
+
+        def native():
+            calls["native"] += 1
+            raise RuntimeError("unsupported shape")
+
+        stock = lambda: torch.zeros(4)  # noqa: E731
+        for _ in range(3):
+            assert torch.equal(autoselecting.choose("op", ("k",), native, stock), torch.zeros(4))
+        assert calls["native"] == 1
+        assert "RuntimeError" in autoselecting._decisions[("k",)].note
+
+    def test_one_off_failure_does_not_overturn_a_good_decision(self, autoselecting, monkeypatch):
+        state = {"fail": False}
+        calls = {"stock": 0}
+
+        def native():
+            if state["fail"]:
+                raise RuntimeError("transient")
+            return torch.zeros(4)
+
+        def stock():
+            calls["stock"] += 1
+            return torch.zeros(4)
+
+        self._timed(monkeypatch, autoselecting, {native: 0.001, stock: 0.010})
+        autoselecting.choose("op", ("k",), native, stock)
+        settled = calls["stock"]
+        state["fail"] = True
+        autoselecting.choose("op", ("k",), native, stock)
+        assert calls["stock"] == settled + 1
+        assert autoselecting._decisions[("k",)].use_native
+        state["fail"] = False
+        autoselecting.choose("op", ("k",), native, stock)
+        assert calls["stock"] == settled + 1
+
+    def test_out_of_memory_during_probe_records_nothing(self, autoselecting):
+        def native():
+            raise torch.OutOfMemoryError("probe OOM")
+
+        stock = lambda: torch.zeros(4)  # noqa: E731
+        assert torch.equal(autoselecting.choose("op", ("k",), native, stock), torch.zeros(4))
+        assert ("k",) not in autoselecting._decisions
+        assert autoselecting._probe_counts.get("op", 0) == 0
+
+    def test_stops_probing_after_too_many_signatures(self, autoselecting, monkeypatch):
+        native = lambda: torch.zeros(4)  # noqa: E731
+        stock = lambda: torch.zeros(4)  # noqa: E731
+        self._timed(monkeypatch, autoselecting, {native: 0.001, stock: 0.010})
+        cap = autoselecting._MAX_SIGNATURES_PER_OP
+        for i in range(cap + 5):
+            autoselecting.choose("op", ("k", i), native, stock)
+        assert autoselecting._probe_counts["op"] == cap
+        beyond = autoselecting._decisions[("k", cap + 3)]
+        assert beyond.use_native and "not probed" in beyond.note
+
+    def test_disabled_autoselect_always_uses_the_kernel(self, monkeypatch):
+        from cmpext3 import autoselect
+        calls = {"stock": 0}
+
+        def stock():
+            calls["stock"] += 1
+            return torch.ones(4)
+
+        monkeypatch.setattr(autoselect, "_ENABLED", False)
+        got = cmpext3._dispatch("op", torch.zeros(4), ("k",), lambda: torch.zeros(4), stock)
+        assert torch.equal(got, torch.zeros(4)) and calls["stock"] == 0
+
+    def test_sdpa_signature_key_and_report(self, autoselecting, patched, native, monkeypatch):
+        force_eligible(monkeypatch)
+        q, k, v = _qkv(1, 2, 3, 4)
+        native.attention.side_effect = lambda *a: STOCK_SDPA(q, k, v)
+        F.scaled_dot_product_attention(q, k, v, scale=0.5)
+        keys = list(autoselecting._decisions)
+        assert keys == [(q.shape, q.dtype, k.shape, v.shape, 0.5, False)]
+        assert "attention fp32" in cmpext3.autoselect_report()
+
+    def test_report_when_empty(self, autoselecting):
+        assert "no kernel decisions" in cmpext3.autoselect_report()
+
+
+def test_missing_native_extension_fails_loudly(tmp_path):
+    """The product path must not import without its HIP library."""
+    import shutil
+    dst = tmp_path / "cmpext3"
+    shutil.copytree(PKG_ROOT / "cmpext3", dst, ignore=shutil.ignore_patterns("*.so", "__pycache__"))
+    env = dict(os.environ, PYTHONPATH=str(tmp_path), CMPEXT3_AUTOPATCH="0")
+    out = subprocess.run([sys.executable, "-c", "import cmpext3"], env=env, capture_output=True,
+                         text=True, timeout=300)
+    assert out.returncode != 0 and "native extension not built" in out.stderr
+
+
+def test_product_package_never_imports_the_oracle():
+    src = PKG_ROOT / "cmpext3"
+    for path in src.glob("*.py"):
+        text = path.read_text()
+        assert "import oracle" not in text and "from oracle" not in text, path
+        assert "sdpa_oracle" not in text, path
