@@ -108,6 +108,10 @@ def main() -> int:
     ap.add_argument("--workload", default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
+    ap.add_argument("--calibrate-copy-mb", type=int, default=0,
+                    help="after the timed loop, run 3 plain elementwise copies (fp32, out = in*1) "
+                         "of this many MiB: the known-traffic kernel that scales rocprofv3 "
+                         "FETCH_SIZE/WRITE_SIZE readings")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -135,6 +139,15 @@ def main() -> int:
     achieved = wl.flops() / dev / 1e12
     peak = W.PEAK_TFLOPS[wl.dtype]
     traffic = _traffic_from_profile(wl.name)
+
+    if args.calibrate_copy_mb > 0:
+        n = args.calibrate_copy_mb * (1 << 20) // 4
+        src = torch.rand(n, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
 
     configs = {}
     if not args.no_configs:

@@ -33,6 +33,10 @@ HIP_SOURCES = ["attn_fwd_mfma16.hip", "attn_fwd_mfma32.hip", "attn_abi.cpp"]
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in arch VGPRs (no AGPR<->VGPR copies around the
+    # softmax), and no sNaN quieting in front of every v_max: the kernels
+    # never rely on signalling-NaN semantics.
+    "-mllvm", "-amdgpu-mfma-vgpr-form", "-mno-amdgpu-ieee", "-fno-honor-nans",
     f"-I{INCLUDE}",
 ]
 

@@ -117,6 +117,10 @@ int cmpext3_attn_fwd(const void* q, const void* k, const void* v, void* o, int d
   if (!stride_ok(q_str, B, H, Sq, es) || !stride_ok(k_str, B, H, Sk, es) ||
       !stride_ok(v_str, B, H, Sk, es) || !stride_ok(o_str, B, H, Sq, es))
     return CMPEXT3_E_ALIGN;
+  // the fp16/bf16 kernel addresses one K/V tile with 32-bit element offsets
+  if (dtype != CMPEXT3_DTYPE_F32 &&
+      (k_str[2] * 64 + 256 > INT32_MAX || v_str[2] * 64 + 256 > INT32_MAX))
+    return CMPEXT3_E_TOO_LARGE;
 
   cmpext3::FwdParams p;
   memset(&p, 0, sizeof p);

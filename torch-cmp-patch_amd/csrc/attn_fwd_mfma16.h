@@ -1,0 +1,408 @@
+// Fused attention forward for fp16 / bf16 on gfx950 MFMA (v_mfma_f32_32x32x16_{f16,bf16}).
+// Kernel template; attn_fwd_mfma16.hip instantiates the shipped tile table.
+//
+// Work split: a workgroup owns one (batch, head) pair and BQ = NW * QB * 32
+// query rows; each of its NW waves owns QB blocks of 32 query rows for the
+// whole key sweep.  K/V are streamed in tiles of BK keys through
+// double-buffered LDS, and the next tile's global loads are in flight while
+// the current one is computed.
+//
+// S^T form.  The kernel computes S^T = K Q^T (rows = keys, columns = queries).
+// In the 32x32 MFMA accumulator a lane holds one column, so each lane owns one
+// query row: its running max, running sum and output rescale are lane-local,
+// and a row reduction is one v_permlane32_swap between the two 16-key halves.
+// The output is accumulated transposed too, O^T = V^T P^T, so P^T goes from
+// the score accumulator straight into the B operand of the PV MFMA.  K rows
+// are fed to the score MFMA in a bit-permuted order (bits 2 and 3 of the row
+// index swapped) so that each lane ends up holding 8 consecutive keys per
+// 16-key PV slice.  V stays row-major in LDS; its A operand (8 keys at one d
+// per lane) is read with ds_read_b64_tr_b16, whose 16-lane transpose turns
+// four rows of 16 d's into 4 consecutive keys per lane.
+//
+// VALU diet (at D = 64 the softmax costs as much issue time as the MFMAs):
+//  * PRESCALE: Q is multiplied by scale*log2(e) once at load, and the score
+//    MFMA chain starts from a "bias" accumulator holding -m (the row's
+//    current exp2 offset), so the accumulator already holds s*c - m and
+//    p = exp2(acc) needs no per-score FMA.  Used for fp16 when |c| <= 1, so
+//    the scaled Q cannot overflow.  Otherwise scores are scaled per element.
+//  * Lazy rescale: the offset m is only raised when a tile's row maximum
+//    exceeds it by more than 8 (log2 units); then P <= 2^8, which fp16/bf16
+//    and the fp32 sums hold exactly enough.  The rescale of O and l is a
+//    wave-uniform branch that is almost never taken after the first tile.
+//  * P is packed with v_cvt_pk_{f16,bf16}_f32 and summed with v_dot2 into an
+//    fp32 row sum, so the normaliser uses exactly the rounded P that the PV
+//    MFMA consumes.
+//
+// Reference algorithm: src/cuda/fp16_flash_attention_hfma2.cu:72-243 (Q
+// pre-scaled by scale*log2e, exp2 online softmax with fp32 running max/sum and
+// fp32 output accumulator, one final 1/l).  The reference's bf16 path casts to
+// fp16 at the boundary (src/main.cpp:1623-1627); here bf16 runs natively.
+#pragma once
+
+#include "attn_common.h"
+
+namespace cmpext3 {
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+template <typename T> struct Elt;
+
+template <> struct Elt<_Float16> {
+  static __device__ __forceinline__ f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
+  }
+  static __device__ __forceinline__ f32x2 unpack(uint32_t w) {
+    return __builtin_convertvector(__builtin_bit_cast(f16x2, w), f32x2);
+  }
+  // acc + lo(w) + hi(w) in fp32
+  static __device__ __forceinline__ float sum2(uint32_t w, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), (f16x2){1.0f16, 1.0f16}, acc, false);
+  }
+};
+
+template <> struct Elt<__bf16> {
+  static __device__ __forceinline__ f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+  }
+  static __device__ __forceinline__ f32x2 unpack(uint32_t w) {
+    return (f32x2){__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u)};
+  }
+  static __device__ __forceinline__ float sum2(uint32_t w, float acc) {
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), one, acc, false);
+  }
+};
+
+// MFMA row m of a 32-key block reads K row perm_row(m): bits 2 and 3 swapped.
+__device__ __forceinline__ int perm_row(int m) {
+  return (m & 0x13) | ((m & 4) << 1) | ((m & 8) >> 1);
+}
+
+// Key (inside its 32-key block) of accumulator element r of half hh, given the
+// permuted K feed: MFMA row 8*(r/4) + 4*hh + r%4 -> key 16*(r/8) + 8*hh + r%8.
+__device__ __forceinline__ int acc_key(int r, int hh) {
+  return 16 * (r >> 3) + 8 * hh + (r & 7);
+}
+
+__device__ __forceinline__ uint2 lds_tr16_b64(const uint16_t* p) {
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  return __builtin_bit_cast(uint2, v);
+}
+
+constexpr float kRescaleThreshold = 8.0f;  // log2 units: P stays <= 256
+
+// DK: head dim padded to a multiple of 16 (score k-steps); DP: padded to a
+// multiple of 32 (output rows of the PV MFMA).  Columns D..DP-1 are zero.
+// OCC: waves per SIMD the register allocation must allow (occupancy target).
+template <typename T, int DK, int DP, int NW, int QB, int BK, int OCC, bool CAUSAL, bool PRESCALE>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
+attn_fwd_mfma16(const FwdParams p) {
+  constexpr int NT = NW * 64;
+  constexpr int QPW = 32 * QB;          // query rows per wave
+  constexpr int BQ = NW * QPW;
+  constexpr int RSK = DK + 8;           // K tile row stride (halves): 16-byte pad
+  constexpr int RSV = DP + 8;           // V tile row stride (halves)
+  constexpr int KTILE = BK * RSK;
+  constexpr int VTILE = BK * RSV;
+  constexpr int KCH = DK / 8;           // 16-byte chunks per K row
+  constexpr int VCH = DP / 8;
+  constexpr int KLD = (BK * KCH + NT - 1) / NT;
+  constexpr int VLD = (BK * VCH + NT - 1) / NT;
+  constexpr int NKB = BK / 32;          // 32-key blocks per tile
+  constexpr int NCH = BK / 16;          // 16-key PV slices per tile
+  constexpr int NDB = DP / 32;          // 32-row output blocks
+  constexpr int NKS = DK / 16;          // score k-steps
+  static_assert(BK % 32 == 0 && DK % 16 == 0 && DP % 32 == 0 && DK <= DP, "tile shape");
+
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * (KTILE + VTILE)];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int l32 = lane & 31;
+  const int hh = lane >> 5;
+
+  // ---- which (batch, head, query block) this workgroup owns
+  const int tile = xcd_remap(blockIdx.x, p.n_wg);
+  const int bh = tile / p.n_qblk;
+  int qblk = tile - bh * p.n_qblk;
+  if (CAUSAL) qblk = p.n_qblk - 1 - qblk;  // longest key sweeps first
+  const int b = bh / p.H;
+  const int h = bh - b * p.H;
+  const int q0 = qblk * BQ;
+
+  const uint16_t* __restrict__ qg = (const uint16_t*)p.q + b * p.q_b + h * p.q_h;
+  const uint16_t* kg = (const uint16_t*)p.k + b * p.k_b + h * p.k_h;
+  const uint16_t* vg = (const uint16_t*)p.v + b * p.v_b + h * p.v_h;
+  uint16_t* __restrict__ og = (uint16_t*)p.o + b * p.o_b + h * p.o_h;
+
+  const int Sq = p.Sq, Sk = p.Sk, D = p.D;
+  const int qw0 = q0 + wave * QPW;      // first query row of this wave
+
+  int kend = Sk;
+  if (CAUSAL) kend = min(Sk, q0 + BQ);
+  const int ntiles = (kend + BK - 1) / BK;
+
+  // ---- Q as the B operand of S^T = K Q^T: lane holds Q[row][16s + 8hh .. +8]
+  const float cq = p.q_sign ? -p.c : p.c;  // signed scale*log2(e) for PRESCALE
+  u32x4 qf[QB][NKS];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int row = qw0 + 32 * qb + l32;
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) {
+      const int d = 16 * s + 8 * hh;
+      u32x4 x = {0u, 0u, 0u, 0u};
+      if (row < Sq && d < D) x = *(const u32x4*)(qg + (int64_t)row * p.q_s + d);
+      if (PRESCALE) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const f32x2 f = Elt<T>::unpack(x[w]) * cq;
+          x[w] = Elt<T>::pack(f[0], f[1]);
+        }
+      } else {
+        x ^= p.q_sign;
+      }
+      qf[qb][s] = x;
+    }
+  }
+
+  // ---- running state per query block (lane = one query row)
+  f32x16 oacc[QB][NDB];
+  f32x16 bias[QB];
+  float mb[QB], lsum[QB];
+  bool first[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) oacc[qb][db] = (f32x16){};
+    bias[qb] = (f32x16){};
+    mb[qb] = 0.f;
+    lsum[qb] = 0.f;
+    first[qb] = true;
+  }
+  const float c = p.c;
+
+  // ---- per-thread global/LDS offsets of its tile chunks (fixed across tiles)
+  int kgo[KLD], klo[KLD], krow[KLD];
+  bool kok[KLD];
+#pragma unroll
+  for (int it = 0; it < KLD; ++it) {
+    const int ci = it * NT + tid;
+    const int r = ci / KCH, c8 = ci - r * KCH;
+    krow[it] = r;
+    kok[it] = (BK * KCH % NT == 0 || ci < BK * KCH) && 8 * c8 < D;
+    kgo[it] = r * (int)p.k_s + 8 * c8;
+    klo[it] = r * RSK + 8 * c8;
+  }
+  int vgo[VLD], vlo[VLD], vrow[VLD];
+  bool vok[VLD];
+#pragma unroll
+  for (int it = 0; it < VLD; ++it) {
+    const int ci = it * NT + tid;
+    const int r = ci / VCH, c8 = ci - r * VCH;
+    vrow[it] = r;
+    vok[it] = (BK * VCH % NT == 0 || ci < BK * VCH) && 8 * c8 < D;
+    vgo[it] = r * (int)p.v_s + 8 * c8;
+    vlo[it] = r * RSV + 8 * c8;
+  }
+  const int64_t kstep = (int64_t)BK * p.k_s, vstep = (int64_t)BK * p.v_s;
+
+  u32x4 kreg[KLD], vreg[VLD];
+  const bool cols_full = (D == DK) && (D == DP);  // no zero-filled head-dim columns
+  auto load_tile = [&](int t) {
+    const int k0 = t * BK;
+    const uint16_t* kt = kg + t * kstep;
+    const uint16_t* vt = vg + t * vstep;
+    if (cols_full && k0 + BK <= Sk) {
+      // interior tile: every chunk this thread owns is in bounds
+#pragma unroll
+      for (int it = 0; it < KLD; ++it)
+        if (BK * KCH % NT == 0 || it * NT + tid < BK * KCH) kreg[it] = *(const u32x4*)(kt + kgo[it]);
+#pragma unroll
+      for (int it = 0; it < VLD; ++it)
+        if (BK * VCH % NT == 0 || it * NT + tid < BK * VCH) vreg[it] = *(const u32x4*)(vt + vgo[it]);
+      return;
+    }
+#pragma unroll
+    for (int it = 0; it < KLD; ++it) {
+      u32x4 x = {0u, 0u, 0u, 0u};
+      if (kok[it] && k0 + krow[it] < Sk) x = *(const u32x4*)(kt + kgo[it]);
+      kreg[it] = x;
+    }
+#pragma unroll
+    for (int it = 0; it < VLD; ++it) {
+      u32x4 x = {0u, 0u, 0u, 0u};
+      if (vok[it] && k0 + vrow[it] < Sk) x = *(const u32x4*)(vt + vgo[it]);
+      vreg[it] = x;
+    }
+  };
+  auto store_tile = [&](int buf) {
+    uint16_t* ks = lds + buf * (KTILE + VTILE);
+    uint16_t* vs = ks + KTILE;
+#pragma unroll
+    for (int it = 0; it < KLD; ++it)
+      if (BK * KCH % NT == 0 || it * NT + tid < BK * KCH) *(u32x4*)(ks + klo[it]) = kreg[it];
+#pragma unroll
+    for (int it = 0; it < VLD; ++it)
+      if (BK * VCH % NT == 0 || it * NT + tid < BK * VCH) *(u32x4*)(vs + vlo[it]) = vreg[it];
+  };
+
+  // lane-constant parts of the LDS read addresses
+  const int k_rd = perm_row(l32) * RSK + 8 * hh;
+  const int jj = lane & 15, gg = lane >> 4;
+  const int v_rd = (8 * (gg >> 1) + (jj >> 2)) * RSV + 16 * (gg & 1) + 4 * (jj & 3);
+
+  if (ntiles > 0) load_tile(0);
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    store_tile(buf);
+    __syncthreads();
+    if (t + 1 < ntiles) load_tile(t + 1);
+
+    const int k0 = t * BK;
+    const uint16_t* ks = lds + buf * (KTILE + VTILE);
+    const uint16_t* vs = ks + KTILE;
+
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const int qlo = qw0 + 32 * qb;      // first row of this query block
+      if (CAUSAL && k0 > qlo + 31) continue;  // every key of the tile is in the future
+
+      // ---- S^T blocks: acc = bias + K Q^T  (PRESCALE: already s*c - m)
+      f32x16 sacc[NKB];
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        f32x16 acc = PRESCALE ? bias[qb] : (f32x16){};
+        const uint16_t* kr = ks + 32 * kb * RSK + k_rd;
+#pragma unroll
+        for (int s = 0; s < NKS; ++s) acc = Elt<T>::mma(*(const u32x4*)(kr + 16 * s), qf[qb][s], acc);
+        sacc[kb] = acc;
+      }
+
+      const int qrow = qlo + l32;
+      const bool need_mask = (k0 + BK > Sk) || (CAUSAL && k0 + BK - 1 > qlo);
+      if (!PRESCALE) {
+        // exp2-domain scores: x = s * c - m
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sacc[kb][r] = __builtin_fmaf(sacc[kb][r], c, -mb[qb]);
+      }
+      if (need_mask) {
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = k0 + 32 * kb + acc_key(r, hh);
+            if (key >= Sk || (CAUSAL && key > qrow)) sacc[kb][r] = -INFINITY;
+          }
+      }
+
+      // ---- tile row max (relative to the current offset), lazy rescale
+      float mq[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // 4 independent chains
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; r += 2)
+          mq[(r >> 1) & 3] = fmaxf(mq[(r >> 1) & 3], fmaxf(sacc[kb][r], sacc[kb][r + 1]));
+      float mx = xhalf_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])));
+      const bool need = first[qb] ? (mx > -INFINITY) : (mx > kRescaleThreshold);
+      if (__builtin_amdgcn_ballot_w64(need)) {
+        const float delta = need ? mx : 0.f;
+        const float alpha = fast_exp2(-delta);
+        mb[qb] += delta;
+        lsum[qb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) oacc[qb][db] *= alpha;
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) sacc[kb] -= delta;
+        if (PRESCALE) bias[qb] = (f32x16){} - mb[qb];
+        first[qb] = first[qb] && !need;
+      }
+
+      // ---- P = exp2(x) packed to T; row sum from the packed values
+      u32x4 pf[NCH];
+      float ls[2] = {lsum[qb], 0.f};  // two independent dot2 chains
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+          u32x4 w;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            w[e] = Elt<T>::pack(fast_exp2(sacc[kb][8 * cc + 2 * e]),
+                                fast_exp2(sacc[kb][8 * cc + 2 * e + 1]));
+            ls[e & 1] = Elt<T>::sum2(w[e], ls[e & 1]);
+          }
+          pf[2 * kb + cc] = w;
+        }
+      lsum[qb] = ls[0] + ls[1];
+
+      // ---- O^T += V^T P^T  (V^T fragments via the LDS transpose read)
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+        for (int ch = 0; ch < NCH; ++ch) {
+          const uint16_t* vp = vs + 16 * ch * RSV + 32 * db + v_rd;
+          const uint2 lo = lds_tr16_b64(vp);
+          const uint2 hi = lds_tr16_b64(vp + 4 * RSV);
+          const u32x4 a = {lo.x, lo.y, hi.x, hi.y};
+          oacc[qb][db] = Elt<T>::mma(a, pf[ch], oacc[qb][db]);
+        }
+      }
+    }
+  }
+
+  // ---- epilogue: combine the two halves' partial sums, normalise, store
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const float inv = 1.f / xhalf_sum(lsum[qb]);
+    const int qrow = qw0 + 32 * qb + l32;
+    if (qrow < Sq) {
+      uint16_t* orow = og + (int64_t)qrow * p.o_s;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d = 32 * db + 8 * g + 4 * hh;
+          if (d < D) {
+            u32x2 w;
+            w[0] = Elt<T>::pack(oacc[qb][db][4 * g + 0] * inv, oacc[qb][db][4 * g + 1] * inv);
+            w[1] = Elt<T>::pack(oacc[qb][db][4 * g + 2] * inv, oacc[qb][db][4 * g + 3] * inv);
+            *(u32x2*)(orow + d) = w;
+          }
+        }
+      }
+    }
+  }
+}
+
+// Launch one instance: grid = B*H*ceil(Sq/BQ) workgroups of NW waves.
+template <typename T, int DK, int NW, int QB, int BK, int OCC, bool CAUSAL, bool PRESCALE>
+hipError_t launch_mfma16_cfg(const FwdParams& p0, hipStream_t stream) {
+  constexpr int DP = (DK + 31) / 32 * 32;
+  constexpr int BQ = NW * QB * 32;
+  FwdParams p = p0;
+  p.n_qblk = (p.Sq + BQ - 1) / BQ;
+  p.n_wg = p.B * p.H * p.n_qblk;
+  if (p.n_wg == 0) return hipSuccess;
+  hipLaunchKernelGGL((attn_fwd_mfma16<T, DK, DP, NW, QB, BK, OCC, CAUSAL, PRESCALE>), dim3(p.n_wg),
+                     dim3(NW * 64), 0, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace cmpext3
