@@ -97,7 +97,7 @@ def test_head_dim_buckets(dtype, D):
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
-@pytest.mark.parametrize("scale", [-0.125, 0.0, 0.5, 1e-3])
+@pytest.mark.parametrize("scale", [-0.125, 0.0, 0.5, 1e-3, 1.0, -2.0])
 @pytest.mark.parametrize("causal", [False, True])
 def test_scale_values(dtype, scale, causal):
     q, k, v = _inputs(dtype, 1, 2, 96, 80, 64, seed=11)
