@@ -122,5 +122,6 @@ def test_autoselect_probe_on_gpu(patched, autoselecting):
 
 def test_describe_names_the_kernel():
     text = cmpext3.ops.describe(0, 2, 10, 4096, 4096, 64, False)
-    assert "mfma16" in text and "DK=64" in text
+    assert "pipe16" in text and "DK=64" in text
+    assert "mfma16" in cmpext3.ops.describe(0, 2, 10, 4096, 4096, 256, False)
     assert "mfma32" in cmpext3.ops.describe(2, 2, 8, 4096, 4096, 40, False)

@@ -96,25 +96,43 @@ def test_head_dim_buckets(dtype, D):
     assert orc.max_abs_err(out.cpu(), ref) <= TOL[dtype]
 
 
-@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
-@pytest.mark.parametrize("scale", [-0.125, 0.0, 0.5, 1e-3, 1.0, -2.0])
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("D", [8, 24, 32, 40, 56, 64, 72, 80, 96, 112, 128])
 @pytest.mark.parametrize("causal", [False, True])
-def test_scale_values(dtype, scale, causal):
-    q, k, v = _inputs(dtype, 1, 2, 96, 80, 64, seed=11)
+def test_head_dim_buckets_long_keys(dtype, D, causal):
+    """Key sweeps of 256+ keys take the software-pipelined kernel for head-dim
+    buckets up to 128; Sk = 275 gives an odd number of 32-key tiles (the loop
+    runs a masked padding tile) and a ragged last tile."""
+    q, k, v = _inputs(dtype, 1, 2, 70, 275, D, seed=D + 1000 * causal)
+    text = abi.describe(abi.dtype_code(q.dtype), 1, 2, 70, 275, D, causal)[1]
+    assert "pipe16" in text
+    scale = 1.0 / math.sqrt(D)
     out = _run(q, k, v, scale, causal)
     ref = orc.sdpa_c(q.cpu(), k.cpu(), v.cpu(), scale, causal)
     assert orc.max_abs_err(out.cpu(), ref) <= TOL[dtype]
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
-def test_bshd_views_and_strided_kv(dtype):
-    wl = W.Workload("v", dtype, 2, 5, 150, 150, 64, seed=21)
+@pytest.mark.parametrize("scale", [-0.125, 0.0, 0.5, 1e-3, 1.0, -2.0])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("Sk", [80, 300])
+def test_scale_values(dtype, scale, causal, Sk):
+    q, k, v = _inputs(dtype, 1, 2, 96, Sk, 64, seed=11)
+    out = _run(q, k, v, scale, causal)
+    ref = orc.sdpa_c(q.cpu(), k.cpu(), v.cpu(), scale, causal)
+    assert orc.max_abs_err(out.cpu(), ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+@pytest.mark.parametrize("S", [150, 300])
+def test_bshd_views_and_strided_kv(dtype, S):
+    wl = W.Workload("v", dtype, 2, 5, S, S, 64, seed=21)
     q, k, v = wl.make_inputs("cuda", layout="bshd")   # [B,H,S,D] views of [B,S,H,D]
     assert not q.is_contiguous()
     # K/V sliced out of a longer sequence: seq stride larger than D
-    big_k = torch.randn(2, 5, 400, 64, dtype=q.dtype, device="cuda")
-    big_v = torch.randn(2, 5, 400, 64, dtype=q.dtype, device="cuda")
-    k2, v2 = big_k[:, :, 100:250], big_v[:, :, 100:250]
+    big_k = torch.randn(2, 5, S + 250, 64, dtype=q.dtype, device="cuda")
+    big_v = torch.randn(2, 5, S + 250, 64, dtype=q.dtype, device="cuda")
+    k2, v2 = big_k[:, :, 100:100 + S], big_v[:, :, 100:100 + S]
     for kk, vv in ((k, v), (k2, v2)):
         for causal in (False, True):
             out = _run(q, kk, vv, 0.125, causal)
@@ -139,6 +157,58 @@ def test_deterministic_rerun(dtype):
     a = _run(q, k, v, 0.125, True)
     b = _run(q, k, v, 0.125, True)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_wide_score_range(dtype, causal):
+    """Scores spanning tens of log2 units: the running exp2 offset must move
+    (and O, l be rescaled) many times, in both directions of the key sweep."""
+    Sk = 300 if causal else 333
+    q, k, v = _inputs(dtype, 1, 2, 200, Sk, 64, seed=5)
+    q = (q.float() * 12).to(q.dtype)
+    out = _run(q, k, v, 0.125, causal)
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), 0.125, causal)
+    assert orc.max_abs_err(out.cpu(), ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("order", ["rising", "falling"])
+def test_monotone_scores(dtype, order):
+    """Scores rising by ~9 log2 units per 32 keys force a rescale on every key
+    tile; falling scores never rescale after the first and underflow later
+    tiles' probabilities."""
+    Sk, D = 1000, 64
+    j = torch.arange(Sk, dtype=torch.float32)
+    if order == "falling":
+        j = j.flip(0)
+    kf = (0.05 * j)[:, None].expand(Sk, D)
+    k = kf.to(getattr(torch, {"fp16": "float16", "bf16": "bfloat16"}[dtype]))[None, None].repeat(1, 2, 1, 1)
+    q = torch.full((1, 2, 64, D), 0.5, dtype=k.dtype)
+    v = torch.randn(1, 2, Sk, D, generator=torch.Generator().manual_seed(3)).to(k.dtype)
+    q, k, v = q.cuda(), k.cuda(), v.cuda()
+    out = _run(q, k, v, 0.125, False)
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), 0.125, False)
+    assert orc.max_abs_err(out.cpu(), ref) <= TOL[dtype]
+
+
+def test_huge_kv_row_stride_falls_back():
+    """K/V rows further apart than the pipelined kernel's 32-bit buffer offsets
+    reach ((Sk + 32) * stride * 2 bytes >= 2^31): the other fp16 kernel runs."""
+    Sk, D, stride = 40, 64, 15_000_000
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    base_k = torch.empty(Sk, stride, dtype=torch.float16, device="cuda")
+    base_v = torch.empty(Sk, stride, dtype=torch.float16, device="cuda")
+    base_k[:, :D] = torch.randn(Sk, D, generator=gen, device="cuda").half()
+    base_v[:, :D] = torch.randn(Sk, D, generator=gen, device="cuda").half()
+    k = base_k[:, :D][None, None]
+    v = base_v[:, :D][None, None]
+    assert k.stride(2) == stride
+    q = torch.randn(1, 1, 50, D, generator=gen, device="cuda").half()
+    out = _run(q, k, v, 0.125, False)
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), 0.125, False)
+    assert orc.max_abs_err(out.cpu(), ref) <= TOL["fp16"]
+    del base_k, base_v
 
 
 def test_causal_differs_from_noncausal():

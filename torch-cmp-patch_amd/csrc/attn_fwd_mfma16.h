@@ -101,19 +101,41 @@ __device__ __forceinline__ uint2 lds_tr16_b64(const uint16_t* p) {
   return __builtin_bit_cast(uint2, v);
 }
 
-constexpr float kRescaleThreshold = 8.0f;  // log2 units: P stays <= 256
+constexpr float kSumHi = 256.0f;         // tile row sum above this: offset must rise
+constexpr float kSumLo = 1.0f / 256.0f;  // first tile row sum below this: offset too high
+
+// Chunk swizzle of LDS row r (DK / 8 sixteen-byte chunks per row).  For the
+// K fragment reads (16 lanes: rows 0..15 of a 32-row block, one chunk), the
+// transposed V reads (32 lanes: 4 consecutive rows x 4 consecutive chunks)
+// and the 16-byte tile writes, every 64-bank LDS cycle hits distinct banks.
+template <int DK>
+__device__ __forceinline__ int lds_swz(int r) {
+  if constexpr (DK == 32) return (r >> 2) & 3;
+  else if constexpr (DK == 64) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+  else return ((r & 3) << 2) | ((r >> 2) & 3);  // DK == 128
+}
 
 // DK: head dim padded to a multiple of 16 (score k-steps); DP: padded to a
 // multiple of 32 (output rows of the PV MFMA).  Columns D..DP-1 are zero.
 // OCC: waves per SIMD the register allocation must allow (occupancy target).
-template <typename T, int DK, int DP, int NW, int QB, int BK, int OCC, bool CAUSAL, bool PRESCALE>
+// OPT bit 0: raise the wave's issue priority (s_setprio) while it issues MFMAs.
+// OPT bit 1: unpadded XOR-swizzled LDS rows instead of 16-byte padding (only
+// for DK == DP in {32, 64, 128}).  OPT bit 2: decide the rescale from the
+// tile's row sum after the exponentials instead of from the row max before
+// them (measured slower on MI355X: the PV MFMAs then wait for the whole sum).
+// The padded, max-first form is the default.
+template <typename T, int DK, int DP, int NW, int QB, int BK, int OCC, bool CAUSAL, bool PRESCALE,
+          int OPT = 0>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
 attn_fwd_mfma16(const FwdParams p) {
   constexpr int NT = NW * 64;
   constexpr int QPW = 32 * QB;          // query rows per wave
   constexpr int BQ = NW * QPW;
-  constexpr int RSK = DK + 8;           // K tile row stride (halves): 16-byte pad
-  constexpr int RSV = DP + 8;           // V tile row stride (halves)
+  // LDS rows padded by 16 bytes (a 64-row K/V tile then reads without
+  // measurable bank conflicts), or unpadded with XOR-swizzled 16-byte chunks.
+  constexpr bool SWZ = (OPT & 2) && (DK == DP) && (DK == 32 || DK == 64 || DK == 128);
+  constexpr int RSK = SWZ ? DK : DK + 8;  // K tile row stride (halves)
+  constexpr int RSV = SWZ ? DP : DP + 8;  // V tile row stride (halves)
   constexpr int KTILE = BK * RSK;
   constexpr int VTILE = BK * RSV;
   constexpr int KCH = DK / 8;           // 16-byte chunks per K row
@@ -205,7 +227,7 @@ attn_fwd_mfma16(const FwdParams p) {
     krow[it] = r;
     kok[it] = (BK * KCH % NT == 0 || ci < BK * KCH) && 8 * c8 < D;
     kgo[it] = r * (int)p.k_s + 8 * c8;
-    klo[it] = r * RSK + 8 * c8;
+    klo[it] = r * RSK + 8 * (SWZ ? (c8 ^ lds_swz<DK>(r)) : c8);
   }
   int vgo[VLD], vlo[VLD], vrow[VLD];
   bool vok[VLD];
@@ -216,7 +238,7 @@ attn_fwd_mfma16(const FwdParams p) {
     vrow[it] = r;
     vok[it] = (BK * VCH % NT == 0 || ci < BK * VCH) && 8 * c8 < D;
     vgo[it] = r * (int)p.v_s + 8 * c8;
-    vlo[it] = r * RSV + 8 * c8;
+    vlo[it] = r * RSV + 8 * (SWZ ? (c8 ^ lds_swz<DP>(r)) : c8);
   }
   const int64_t kstep = (int64_t)BK * p.k_s, vstep = (int64_t)BK * p.v_s;
 
@@ -260,10 +282,24 @@ attn_fwd_mfma16(const FwdParams p) {
       if (BK * VCH % NT == 0 || it * NT + tid < BK * VCH) *(u32x4*)(vs + vlo[it]) = vreg[it];
   };
 
-  // lane-constant parts of the LDS read addresses
-  const int k_rd = perm_row(l32) * RSK + 8 * hh;
+  // lane-constant parts of the LDS read addresses (halves within a tile)
+  int k_rd[NKS];  // + 32*kb*RSK
+  {
+    const int r = perm_row(l32);
+#pragma unroll
+    for (int s = 0; s < NKS; ++s)
+      k_rd[s] = r * RSK + (SWZ ? 8 * ((2 * s + hh) ^ lds_swz<DK>(r)) : 16 * s + 8 * hh);
+  }
   const int jj = lane & 15, gg = lane >> 4;
-  const int v_rd = (8 * (gg >> 1) + (jj >> 2)) * RSV + 16 * (gg & 1) + 4 * (jj & 3);
+  int v_rd[NDB][2];  // + 16*ch*RSV
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int r = 8 * (gg >> 1) + (jj >> 2) + 4 * half;
+      const int col = 32 * db + 16 * (gg & 1) + 4 * (jj & 3);
+      v_rd[db][half] = r * RSV + (SWZ ? 8 * ((col >> 3) ^ lds_swz<DP>(r)) + (col & 7) : col);
+    }
 
   if (ntiles > 0) load_tile(0);
 
@@ -282,88 +318,137 @@ attn_fwd_mfma16(const FwdParams p) {
       const int qlo = qw0 + 32 * qb;      // first row of this query block
       if (CAUSAL && k0 > qlo + 31) continue;  // every key of the tile is in the future
 
-      // ---- S^T blocks: acc = bias + K Q^T  (PRESCALE: already s*c - m)
+      // ---- S^T blocks in the exp2 domain: x = s*c - m (PRESCALE: the MFMA
+      // chain starts from bias = -m and Q already carries c)
       f32x16 sacc[NKB];
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
-        f32x16 acc = PRESCALE ? bias[qb] : (f32x16){};
-        const uint16_t* kr = ks + 32 * kb * RSK + k_rd;
-#pragma unroll
-        for (int s = 0; s < NKS; ++s) acc = Elt<T>::mma(*(const u32x4*)(kr + 16 * s), qf[qb][s], acc);
-        sacc[kb] = acc;
-      }
-
       const int qrow = qlo + l32;
       const bool need_mask = (k0 + BK > Sk) || (CAUSAL && k0 + BK - 1 > qlo);
-      if (!PRESCALE) {
-        // exp2-domain scores: x = s * c - m
+      auto scores = [&]() {
 #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
+        for (int kb = 0; kb < NKB; ++kb) {
+          f32x16 acc = PRESCALE ? bias[qb] : (f32x16){};
+          const uint16_t* kr = ks + 32 * kb * RSK;
+          if (OPT & 1) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-          for (int r = 0; r < 16; ++r) sacc[kb][r] = __builtin_fmaf(sacc[kb][r], c, -mb[qb]);
-      }
-      if (need_mask) {
+          for (int s = 0; s < NKS; ++s) acc = Elt<T>::mma(*(const u32x4*)(kr + k_rd[s]), qf[qb][s], acc);
+          if (OPT & 1) __builtin_amdgcn_s_setprio(0);
+          sacc[kb] = acc;
+        }
+        if (!PRESCALE) {
 #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
+          for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = k0 + 32 * kb + acc_key(r, hh);
-            if (key >= Sk || (CAUSAL && key > qrow)) sacc[kb][r] = -INFINITY;
-          }
-      }
+            for (int r = 0; r < 16; ++r) sacc[kb][r] = __builtin_fmaf(sacc[kb][r], c, -mb[qb]);
+        }
+        if (need_mask) {
+#pragma unroll
+          for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int key = k0 + 32 * kb + acc_key(r, hh);
+              if (key >= Sk || (CAUSAL && key > qrow)) sacc[kb][r] = -INFINITY;
+            }
+        }
+      };
+      scores();
 
-      // ---- tile row max (relative to the current offset), lazy rescale
-      float mq[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // 4 independent chains
+      // ---- P = exp2(x) packed to T against the current offset; the tile's
+      // row sum (this lane's half) from the packed values
+      u32x4 pf[NCH];
+      float ls[2];
+      auto exp_pack = [&]() {
+        ls[0] = 0.f;
+        ls[1] = 0.f;  // two independent dot2 chains
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; r += 2)
-          mq[(r >> 1) & 3] = fmaxf(mq[(r >> 1) & 3], fmaxf(sacc[kb][r], sacc[kb][r + 1]));
-      float mx = xhalf_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])));
-      const bool need = first[qb] ? (mx > -INFINITY) : (mx > kRescaleThreshold);
-      if (__builtin_amdgcn_ballot_w64(need)) {
-        const float delta = need ? mx : 0.f;
+          for (int cc = 0; cc < 2; ++cc) {
+            u32x4 w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              w[e] = Elt<T>::pack(fast_exp2(sacc[kb][8 * cc + 2 * e]),
+                                  fast_exp2(sacc[kb][8 * cc + 2 * e + 1]));
+              ls[e & 1] = Elt<T>::sum2(w[e], ls[e & 1]);
+            }
+            pf[2 * kb + cc] = w;
+          }
+      };
+      // Raise the offset to the tile's row max (never lower it after the first
+      // live tile); rescale O and l by 2^-delta.  Returns delta.
+      auto rescale_to_max = [&]() {
+        float mq = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mq = fmaxf(mq, sacc[kb][r]);
+        const float mx = xhalf_max(mq);
+        float delta = first[qb] ? mx : fmaxf(mx, 0.f);
+        if (mx == -INFINITY) delta = 0.f;
         const float alpha = fast_exp2(-delta);
         mb[qb] += delta;
         lsum[qb] *= alpha;
 #pragma unroll
         for (int db = 0; db < NDB; ++db) oacc[qb][db] *= alpha;
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) sacc[kb] -= delta;
         if (PRESCALE) bias[qb] = (f32x16){} - mb[qb];
-        first[qb] = first[qb] && !need;
-      }
+        first[qb] = first[qb] && (mx == -INFINITY);
+        return delta;
+      };
 
-      // ---- P = exp2(x) packed to T; row sum from the packed values
-      u32x4 pf[NCH];
-      float ls[2] = {lsum[qb], 0.f};  // two independent dot2 chains
+      float lt;
+      if (!(OPT & 4)) {
+        // max-first: rescale when the tile max exceeds the offset by 8
+        float mq = -INFINITY;
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-          u32x4 w;
+          for (int r = 0; r < 16; ++r) mq = fmaxf(mq, sacc[kb][r]);
+        const bool need = xhalf_max(mq) > (first[qb] ? -INFINITY : 8.f);
+        if (__builtin_amdgcn_ballot_w64(need)) {
+          const float delta = rescale_to_max();
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            w[e] = Elt<T>::pack(fast_exp2(sacc[kb][8 * cc + 2 * e]),
-                                fast_exp2(sacc[kb][8 * cc + 2 * e + 1]));
-            ls[e & 1] = Elt<T>::sum2(w[e], ls[e & 1]);
-          }
-          pf[2 * kb + cc] = w;
+          for (int kb = 0; kb < NKB; ++kb) sacc[kb] -= delta;
         }
-      lsum[qb] = ls[0] + ls[1];
+        exp_pack();
+        lt = ls[0] + ls[1];
+      } else {
+        // ---- lazy rescale, decided from the tile sum: above 2^8 a P may
+        // have left the headroom; on the first tile, below 2^-8 the offset
+        // sits far above the scores.  Only then recompute the scores (the K
+        // tile is still in LDS), take the row max and redo the exponentials;
+        // the common path keeps no scores alive past the exponentials.
+        exp_pack();
+        lt = ls[0] + ls[1];
+        const bool need = !(lt <= kSumHi) || (first[qb] && lt < kSumLo);
+        if (__builtin_amdgcn_ballot_w64(need)) {
+          // the clobber makes the K fragments be read again instead of the
+          // first pass's scores being kept live for this branch
+          asm volatile("" ::: "memory");
+          scores();
+          const float delta = rescale_to_max();
+#pragma unroll
+          for (int kb = 0; kb < NKB; ++kb) sacc[kb] -= delta;
+          exp_pack();
+          lt = ls[0] + ls[1];
+        } else {
+          first[qb] = false;
+        }
+      }
+      lsum[qb] += lt;
 
       // ---- O^T += V^T P^T  (V^T fragments via the LDS transpose read)
+      if (OPT & 1) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
 #pragma unroll
         for (int ch = 0; ch < NCH; ++ch) {
-          const uint16_t* vp = vs + 16 * ch * RSV + 32 * db + v_rd;
-          const uint2 lo = lds_tr16_b64(vp);
-          const uint2 hi = lds_tr16_b64(vp + 4 * RSV);
+          const uint16_t* vp = vs + 16 * ch * RSV;
+          const uint2 lo = lds_tr16_b64(vp + v_rd[db][0]);
+          const uint2 hi = lds_tr16_b64(vp + v_rd[db][1]);
           const u32x4 a = {lo.x, lo.y, hi.x, hi.y};
           oacc[qb][db] = Elt<T>::mma(a, pf[ch], oacc[qb][db]);
         }
       }
+      if (OPT & 1) __builtin_amdgcn_s_setprio(0);
     }
   }
 
@@ -392,7 +477,8 @@ attn_fwd_mfma16(const FwdParams p) {
 }
 
 // Launch one instance: grid = B*H*ceil(Sq/BQ) workgroups of NW waves.
-template <typename T, int DK, int NW, int QB, int BK, int OCC, bool CAUSAL, bool PRESCALE>
+template <typename T, int DK, int NW, int QB, int BK, int OCC, bool CAUSAL, bool PRESCALE,
+          int OPT = 0>
 hipError_t launch_mfma16_cfg(const FwdParams& p0, hipStream_t stream) {
   constexpr int DP = (DK + 31) / 32 * 32;
   constexpr int BQ = NW * QB * 32;
@@ -400,7 +486,7 @@ hipError_t launch_mfma16_cfg(const FwdParams& p0, hipStream_t stream) {
   p.n_qblk = (p.Sq + BQ - 1) / BQ;
   p.n_wg = p.B * p.H * p.n_qblk;
   if (p.n_wg == 0) return hipSuccess;
-  hipLaunchKernelGGL((attn_fwd_mfma16<T, DK, DP, NW, QB, BK, OCC, CAUSAL, PRESCALE>), dim3(p.n_wg),
+  hipLaunchKernelGGL((attn_fwd_mfma16<T, DK, DP, NW, QB, BK, OCC, CAUSAL, PRESCALE, OPT>), dim3(p.n_wg),
                      dim3(NW * 64), 0, stream, p);
   return hipGetLastError();
 }

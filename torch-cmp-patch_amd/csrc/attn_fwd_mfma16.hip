@@ -1,5 +1,8 @@
 // Instantiations and tile table of the fp16/bf16 MFMA attention kernel
-// (kernel template in attn_fwd_mfma16.h).
+// (kernel template in attn_fwd_mfma16.h), and the fp16/bf16 entry point:
+// head dims up to 128 go to the software-pipelined kernel
+// (attn_fwd_pipe16.hip); larger head dims, and K/V row strides too large for
+// its 32-bit buffer offsets, run this one.
 //
 // The tile table replaces the reference's hard-coded per-head-dim template
 // table (src/cuda/fp16_flash_attention_hfma2.cu:278-285) and its build-time
@@ -30,7 +33,8 @@ constexpr Tile16 tile16(int dk) {
 template <typename T, int DK, bool CAUSAL, bool PRESCALE>
 hipError_t launch_dk(const FwdParams& p, hipStream_t s) {
   constexpr Tile16 tt = tile16(DK);
-  return launch_mfma16_cfg<T, DK, tt.nw, tt.qb, tt.bk, tt.occ, CAUSAL, PRESCALE>(p, s);
+  // OPT 1: s_setprio(1) around the MFMA blocks (padded LDS rows, max-first rescale)
+  return launch_mfma16_cfg<T, DK, tt.nw, tt.qb, tt.bk, tt.occ, CAUSAL, PRESCALE, 1>(p, s);
 }
 
 template <typename T, bool CAUSAL, bool PRESCALE>
@@ -51,6 +55,10 @@ hipError_t launch_bucket(const FwdParams& p, int dk, hipStream_t s) {
 
 }  // namespace
 
+bool pipe16_applies(const FwdParams& p, int dk);
+hipError_t launch_pipe16(const FwdParams& p, int dk, bool bf16, bool causal, bool prescale, hipStream_t s);
+void describe_pipe16(int dk, int Sq, char* buf, int len);
+
 int mfma16_bucket(int D) {
   for (int dk : kMfma16Dk)
     if (D <= dk) return dk;
@@ -64,6 +72,7 @@ static bool use_prescale(const FwdParams& p, bool bf16) { return !bf16 && p.c <=
 hipError_t launch_mfma16(const FwdParams& p, bool bf16, bool causal, hipStream_t s) {
   const int dk = mfma16_bucket(p.D);
   if (dk < 0) return hipErrorInvalidValue;
+  if (pipe16_applies(p, dk)) return launch_pipe16(p, dk, bf16, causal, use_prescale(p, bf16), s);
   if (bf16)
     return causal ? launch_bucket<__bf16, true, false>(p, dk, s)
                   : launch_bucket<__bf16, false, false>(p, dk, s);
@@ -76,8 +85,15 @@ hipError_t launch_mfma16(const FwdParams& p, bool bf16, bool causal, hipStream_t
 
 int mfma16_max_bk() { return 64; }
 
-void describe_mfma16(int D, int Sq, char* buf, int len) {
+void describe_mfma16(int D, int Sq, int Sk, char* buf, int len) {
   const int dk = mfma16_bucket(D);
+  FwdParams p = {};
+  p.Sk = Sk;
+  p.k_s = p.v_s = D;
+  if (pipe16_applies(p, dk)) {
+    describe_pipe16(dk, Sq, buf, len);
+    return;
+  }
   const Tile16 t = tile16(dk);
   const int bq = t.nw * t.qb * 32;
   snprintf(buf, len,
