@@ -56,21 +56,28 @@ def _traffic_from_profile(workload: str):
 
 
 def time_kernel(fn, steps: int, warmup: int):
-    """(wall seconds for `steps` calls, mean per-call device seconds from events)."""
+    """(wall seconds for `steps` calls, mean per-call device seconds).
+
+    The device time comes from one pair of HIP events on the launching stream
+    around the `steps` back-to-back launches (the op launches on torch's
+    current stream), divided by `steps`: an event pair around every launch
+    would add a marker packet and its dispatch gap to each measurement, which
+    the profiler's per-kernel duration does not contain.
+    """
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    start = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    end = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    for i in range(steps):
-        start[i].record()
+    start.record()
+    for _ in range(steps):
         fn()
-        end[i].record()
+    end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    dev = sum(s.elapsed_time(e) for s, e in zip(start, end)) / steps / 1e3
+    dev = start.elapsed_time(end) / steps / 1e3
     return wall, dev
 
 

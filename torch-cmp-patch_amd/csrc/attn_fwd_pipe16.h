@@ -127,7 +127,9 @@ attn_fwd_pipe16(const FwdParams p) {
   for (int db = 0; db < NDB; ++db) oacc[db] = (f32x16){};
   f32x16 bias = (f32x16){};
   float mb = 0.f, lsum = 0.f;
-  bool first = true;
+  // rescale threshold on the tile's row max over the offset: -inf until the
+  // row has seen a live key (the first live tile sets the offset), then 8
+  float thr = -INFINITY;
   const float c = p.c;
 
   // ---- K/V tiles are fetched with raw buffer loads over this head's rows:
@@ -299,7 +301,7 @@ attn_fwd_pipe16(const FwdParams p) {
   // t+1's.  The loop below alternates the two arrays so that nothing is
   // copied between iterations.
   auto step = [&](int t, f32x16 (&sc)[NKB], f32x16 (&sn)[NKB], u32x4 (&kr)[KLD], u32x4 (&vr)[VLD]) {
-    // every wave is done reading K(t) and V(t-1); K(t+1) and V(t) are visible
+    // every wave is done reading K(t) and V(t-1); K(t+1), V(t) are visible
     lds_barrier();
     u32x4 kf[NKB][NKS];
     read_kf(t + 1, kf);  // stale data on the last tile; those scores are dropped
@@ -312,25 +314,30 @@ attn_fwd_pipe16(const FwdParams p) {
     load_k(t + 4, kr);
     load_v(t + 3, vr);
 
-    // ---- rescale decision for tile t: raise the offset when the row max
-    // exceeds it by more than 8 (log2 units), or on the first live tile
+    // Raise the offset to the row max mx (never lower it once a live key was
+    // seen) and rescale O and l; returns the shift applied to the scores.
+    auto rescale = [&](float mx) {
+      const bool fst = thr == -INFINITY;
+      float delta = fst ? mx : fmaxf(mx, 0.f);
+      if (mx == -INFINITY) delta = 0.f;
+      const float alpha = fast_exp2(-delta);
+      mb += delta;
+      lsum *= alpha;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) oacc[db] *= alpha;
+      if (PRESCALE) bias -= delta;  // stays exactly -mb
+      if (!(fst && mx == -INFINITY)) thr = 8.f;
+      return delta;
+    };
+
+    // ---- rescale decision for tile t: the row max exceeds the offset by
+    // more than 8 (log2 units), or this is the first live tile
     {
       const float mx = xhalf_max(mq);
-      const bool need = first ? (mx > -INFINITY) : (mx > 8.f);
-      if (__builtin_amdgcn_ballot_w64(need)) {
-        float delta = first ? mx : fmaxf(mx, 0.f);
-        if (mx == -INFINITY) delta = 0.f;
-        const float alpha = fast_exp2(-delta);
-        mb += delta;
-        lsum *= alpha;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) oacc[db] *= alpha;
+      if (__builtin_amdgcn_ballot_w64(mx > thr)) {
+        const float delta = rescale(mx);
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) sc[kb] -= delta;
-        if (PRESCALE) bias -= delta;  // stays exactly -mb
-        first = first && (mx == -INFINITY);
-      } else {
-        first = false;
       }
     }
 
@@ -368,6 +375,7 @@ attn_fwd_pipe16(const FwdParams p) {
       for (int u = i * UA / NQK; u < (i + 1) * UA / NQK; ++u) exp_unit(u);
       if (!(OPT & 4)) __builtin_amdgcn_sched_barrier(0);
     }
+
     float mpart = -INFINITY;
     auto piece = [&](int j) {  // 8 scores of the next tile: scale, then max
       const int kb = j >> 1, r0 = 8 * (j & 1);
@@ -396,6 +404,7 @@ attn_fwd_pipe16(const FwdParams p) {
     mq = mpart;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) sn[kb] = acc[kb];
+
 
     if (t + 1 < nt2 && tile_needs_mask(t + 1)) {
       mask(t + 1, sn);

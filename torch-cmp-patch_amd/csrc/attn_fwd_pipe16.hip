@@ -52,6 +52,10 @@ bool pipe16_applies(const FwdParams& p, int dk) {
   return (int64_t)(p.Sk + kPipeBk) * rs * 2 < (int64_t(1) << 31);
 }
 
+// `prescale` applies to fp16 (Q * scale * log2(e) must stay finite).  bf16
+// never pre-scales: rounding Q*c to 8 mantissa bits moves each score by up to
+// 2^-9 of its size, which at scale 1 (scores of tens of log2 units) breaks
+// the 2e-2 bf16 bar, so bf16 scores get one FMA each instead.
 hipError_t launch_pipe16(const FwdParams& p, int dk, bool bf16, bool causal, bool prescale, hipStream_t s) {
   if (bf16)
     return causal ? launch_bucket<__bf16, true, false>(p, dk, s) : launch_bucket<__bf16, false, false>(p, dk, s);
