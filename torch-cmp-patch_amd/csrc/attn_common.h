@@ -52,6 +52,29 @@ __device__ __forceinline__ int xcd_remap(int wg, int n) {
   return x * base + (x < rem ? x : rem) + j;
 }
 
+// Which (batch*head, query block) workgroup `wg` computes.  Non-causal: the
+// xcd_remap ranges, so the query blocks of one head share an XCD's L2.
+// Causal: query block j scans j+1 key blocks, so the start order matters.
+// When the heads split evenly over the XCDs, XCD x owns heads x, x+8, ... and
+// starts their query blocks longest first across those heads; an XCD starts
+// its workgroups in order as slots free up, so this is longest-first list
+// scheduling per XCD.  Otherwise each head's blocks run longest first inside
+// the contiguous range.
+__device__ __forceinline__ void wg_tile(int wg, const FwdParams& p, bool causal, int& bh, int& qblk) {
+  const int BH = p.B * p.H;
+  if (causal && BH % kNumXcd == 0) {
+    const int x = wg % kNumXcd, i = wg / kNumXcd, hx = BH / kNumXcd;
+    const int r = i / hx;  // query blocks handed out so far on this XCD, per head
+    bh = x + kNumXcd * (i - r * hx);
+    qblk = p.n_qblk - 1 - r;
+    return;
+  }
+  const int tile = xcd_remap(wg, p.n_wg);
+  bh = tile / p.n_qblk;
+  qblk = tile - bh * p.n_qblk;
+  if (causal) qblk = p.n_qblk - 1 - qblk;
+}
+
 // max / sum of a value with its partner 32 lanes away (v_permlane32_swap):
 // lane L receives {x[L mod 32], x[32 + L mod 32]} in the two results.
 __device__ __forceinline__ float xhalf_max(float x) {

@@ -157,10 +157,8 @@ attn_fwd_mfma16(const FwdParams p) {
   const int hh = lane >> 5;
 
   // ---- which (batch, head, query block) this workgroup owns
-  const int tile = xcd_remap(blockIdx.x, p.n_wg);
-  const int bh = tile / p.n_qblk;
-  int qblk = tile - bh * p.n_qblk;
-  if (CAUSAL) qblk = p.n_qblk - 1 - qblk;  // longest key sweeps first
+  int bh, qblk;
+  wg_tile(blockIdx.x, p, CAUSAL, bh, qblk);
   const int b = bh / p.H;
   const int h = bh - b * p.H;
   const int q0 = qblk * BQ;

@@ -53,10 +53,8 @@ attn_fwd_mfma32(const FwdParams p) {
   const int l16 = lane & 15;
   const int g = lane >> 4;
 
-  const int tile = xcd_remap(blockIdx.x, p.n_wg);
-  const int bh = tile / p.n_qblk;
-  int qblk = tile - bh * p.n_qblk;
-  if (CAUSAL) qblk = p.n_qblk - 1 - qblk;
+  int bh, qblk;
+  wg_tile(blockIdx.x, p, CAUSAL, bh, qblk);
   const int b = bh / p.H;
   const int h = bh - b * p.H;
   const int q0 = qblk * BQ;

@@ -79,10 +79,8 @@ attn_fwd_pipe16(const FwdParams p) {
   const int l32 = lane & 31;
   const int hh = lane >> 5;
 
-  const int tile = xcd_remap(blockIdx.x, p.n_wg);
-  const int bh = tile / p.n_qblk;
-  int qblk = tile - bh * p.n_qblk;
-  if (CAUSAL) qblk = p.n_qblk - 1 - qblk;  // longest key sweeps first
+  int bh, qblk;
+  wg_tile(blockIdx.x, p, CAUSAL, bh, qblk);
   const int b = bh / p.H;
   const int h = bh - b * p.H;
   const int q0 = qblk * BQ;
