@@ -251,8 +251,12 @@ attn_fwd_mfma32(const FwdParams p) {
 
 template <int DK, bool CAUSAL>
 hipError_t launch_mfma32_inst(const FwdParams& p0, hipStream_t stream) {
+  // One 16-row query block per wave: measured on MI355X, two per wave only
+  // lengthen each wave's dependency chain (1.6x slower on [1,8,1024,1024,64],
+  // 19% slower causal, equal on [2,8,4096,4096,40]), and 64-row workgroups
+  // fill more CUs on small grids.
   constexpr int NW = 4;
-  constexpr int NQB = (DK <= 128) ? 2 : 1;
+  constexpr int NQB = 1;
   constexpr int BK = (DK <= 128) ? 32 : 16;
   constexpr int BQ = NW * 16 * NQB;
   FwdParams p = p0;
@@ -298,7 +302,7 @@ hipError_t launch_mfma32(const FwdParams& p, bool causal, hipStream_t s) {
 
 void describe_mfma32(int D, int Sq, char* buf, int len) {
   const int dk = mfma32_bucket(D);
-  const int bq = dk <= 128 ? 128 : 64;
+  const int bq = 64;
   snprintf(buf, len, "mfma32 16x16x4f32 S^T-form: DK=%d DPV=%d waves=4 BQ=%d BK=%d qblocks=%d", dk,
            (dk + 15) / 16 * 16, bq, dk <= 128 ? 32 : 16, (Sq + bq - 1) / bq);
 }
