@@ -124,7 +124,10 @@ attn_fwd_pipe16(const FwdParams p) {
 #pragma unroll
   for (int db = 0; db < NDB; ++db) oacc[db] = (f32x16){};
   f32x16 bias = (f32x16){};
-  float mb = 0.f, lsum = 0.f;
+  float mb = 0.f;
+  // row sum of P over this lane's half of the keys, as two interleaved v_dot2
+  // chains carried across iterations (no per-iteration reduction to wait on)
+  float ls0 = 0.f, ls1 = 0.f;
   // rescale threshold on the tile's row max over the offset: -inf until the
   // row has seen a live key (the first live tile sets the offset), then 8
   float thr = -INFINITY;
@@ -320,7 +323,8 @@ attn_fwd_pipe16(const FwdParams p) {
       if (mx == -INFINITY) delta = 0.f;
       const float alpha = fast_exp2(-delta);
       mb += delta;
-      lsum *= alpha;
+      ls0 *= alpha;
+      ls1 *= alpha;
 #pragma unroll
       for (int db = 0; db < NDB; ++db) oacc[db] *= alpha;
       if (PRESCALE) bias -= delta;  // stays exactly -mb
@@ -346,7 +350,6 @@ attn_fwd_pipe16(const FwdParams p) {
     if (OPT & 1) __builtin_amdgcn_s_setprio(1);
     u32x4 pf[NCH];
     u32x4 vfr[NPV];
-    float ls0 = 0.f, ls1 = 0.f;
     const uint16_t* vs = vbase + (t & 1) * VTILE;
     auto exp_unit = [&](int u) {
       const int ch = u >> 2, e = u & 3, kb = ch >> 1, cc = ch & 1;
@@ -396,9 +399,6 @@ attn_fwd_pipe16(const FwdParams p) {
 #pragma unroll
     for (int j = NPV - (NU - UA) > 0 ? NPV - (NU - UA) : 0; j < NPC; ++j) piece(j);
     if (OPT & 1) __builtin_amdgcn_s_setprio(0);
-    // keep the row-sum chains inside this block (not sunk past the branch)
-    asm volatile("" ::"v"(ls0), "v"(ls1));
-    lsum += ls0 + ls1;
     mq = mpart;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) sn[kb] = acc[kb];
@@ -420,7 +420,7 @@ attn_fwd_pipe16(const FwdParams p) {
   }
 
   // ---- epilogue: combine the two halves' partial sums, normalise, store
-  const float inv = 1.f / xhalf_sum(lsum);
+  const float inv = 1.f / xhalf_sum(ls0 + ls1);
   if (qrow < Sq) {
     uint16_t* orow = og + (int64_t)qrow * p.o_s;
 #pragma unroll
