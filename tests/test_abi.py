@@ -64,6 +64,23 @@ def test_describe_baseline_configs():
         assert ("causal" in text) == w.causal
 
 
+def test_describe_key_split_plan():
+    """Without a visible device the plan assumes MI355X's 256 CUs.  SDXL
+    self-attention: 640 blocks of 128 queries = 2 whole rounds + 128 blocks
+    cut in 2 key ranges (one part per CU); 2*4*32 = 256 blocks fill whole
+    rounds; causal launches and short key sweeps never split; 4 blocks of
+    2048 keys (64 tiles) get 8 parts of 8 tiles."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("plan depends on the visible device's CU count")
+    f16 = abi.DTYPE_F16
+    assert "key-split: 512 whole + 128 x 2 parts" in abi.describe(f16, 2, 10, 4096, 4096, 64)[1]
+    assert "key-split" not in abi.describe(f16, 2, 4, 4096, 4096, 64)[1]
+    assert "key-split" not in abi.describe(f16, 2, 10, 4096, 4096, 64, True)[1]
+    assert "key-split" not in abi.describe(f16, 1, 2, 256, 300, 64)[1]
+    assert "key-split: 0 whole + 4 x 8 parts" in abi.describe(f16, 1, 2, 256, 2048, 64)[1]
+
+
 def _call(q=16, k=16, v=16, o=16, dtype=abi.DTYPE_F16, B=1, H=1, Sq=8, Sk=8, D=64,
           strides=(512, 512, 64), scale=0.125):
     st = (ctypes.c_int64 * 3)(*strides)

@@ -1,0 +1,110 @@
+"""GPU parity of the key-split launches of the pipelined fp16/bf16 kernel.
+
+When the query blocks do not fill whole rounds of the chip, the blocks past the
+last whole round run as several workgroups over disjoint key ranges, and the
+last one of a block to finish merges the partial (O, m, l) of the others.
+These cases drive that path (describe() must name the split) with the same
+bar as every other parity test: max |kernel - oracle| <= 1e-2 fp16, 2e-2 bf16,
+oracle = float64 SDPA on the CPU over the same rounded inputs.
+
+Shapes: fewer blocks than CUs (every block split, up to 8 parts), one whole
+round plus a remainder, ragged key counts whose parts get odd tile counts
+(a masked padding tile inside a part), scores spread over tens of log2 units
+(parts settle on different offsets before the merge), and back-to-back
+launches of different plans (the per-wave counters must come back to zero).
+"""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from cmpext3 import abi
+from cmpext3 import workloads as W
+from oracle import sdpa_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL = orc.TOLERANCE
+
+
+def _inputs(dtype, B, H, Sq, Sk, D, seed=0):
+    return W.Workload("split", dtype, B, H, Sq, Sk, D, seed=seed).make_inputs("cuda")
+
+
+def _split_text(q, B, H, Sq, Sk, D, causal=False):
+    return abi.describe(abi.dtype_code(q.dtype), B, H, Sq, Sk, D, causal)[1]
+
+
+def _check(q, k, v, scale, causal, dtype):
+    out = abi.attn_fwd(q, k, v, scale, causal)
+    torch.cuda.synchronize()
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), scale, causal)
+    err = orc.max_abs_err(out.cpu(), ref)
+    assert err <= TOL[dtype], f"max abs err {err:.3e}"
+    return out
+
+
+SPLIT = [
+    # dtype, B, H, Sq, Sk, D: blocks of 128 queries, 32-key tiles
+    ("fp16", 1, 2, 256, 2048, 64),    # 4 blocks, 8 parts each
+    ("bf16", 1, 2, 256, 2048, 64),
+    ("fp16", 1, 1, 100, 1024, 128),   # one ragged block, 4 parts
+    ("bf16", 2, 3, 130, 2000, 96),    # ragged Sq and Sk: parts of 15 and 16 tiles
+    ("fp16", 1, 3, 64, 777, 40),      # D below the bucket, odd Sk
+    ("fp16", 1, 17, 2048, 512, 64),   # one whole round + 16 blocks in 2 parts
+    ("bf16", 1, 17, 2048, 512, 128),
+]
+
+
+@pytest.mark.parametrize("case", SPLIT, ids=[f"{c[0]}-B{c[1]}H{c[2]}-q{c[3]}k{c[4]}d{c[5]}" for c in SPLIT])
+def test_split_parity(case):
+    dtype, B, H, Sq, Sk, D = case
+    q, k, v = _inputs(dtype, B, H, Sq, Sk, D, seed=Sq + Sk + D)
+    text = _split_text(q, B, H, Sq, Sk, D)
+    assert "key-split" in text, text
+    _check(q, k, v, 1.0 / math.sqrt(D), False, dtype)
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_split_wide_scores(dtype):
+    """Q scaled by 6 (scores with a standard deviation near 9 log2 units):
+    each part rescales on its own and ends on its own offset; the merge must
+    bring them to a common one."""
+    B, H, Sq, Sk, D = 1, 2, 200, 1500, 64
+    q, k, v = _inputs(dtype, B, H, Sq, Sk, D, seed=77)
+    q = (q.float() * 6).to(q.dtype)
+    assert "key-split" in _split_text(q, B, H, Sq, Sk, D)
+    _check(q, k, v, 0.125, False, dtype)
+
+
+def test_split_back_to_back_plans():
+    """Different split plans in a row on one stream share the exchange buffer;
+    a rerun of the first must reproduce it bit for bit."""
+    a = _inputs("fp16", 1, 2, 256, 2048, 64, seed=1)
+    b = _inputs("fp16", 1, 17, 2048, 512, 64, seed=2)
+    c = _inputs("bf16", 1, 1, 100, 1024, 128, seed=3)
+    out_a1 = _check(*a, 0.125, False, "fp16")
+    _check(*b, 0.125, False, "fp16")
+    _check(*c, 128 ** -0.5, False, "bf16")
+    out_a2 = _check(*a, 0.125, False, "fp16")
+    assert torch.equal(out_a1, out_a2)
+
+
+def test_split_bshd_views():
+    """[B,S,H,D]-memory views through the split path."""
+    wl = W.Workload("v", "fp16", 1, 3, 200, 1200, 64, seed=8)
+    q, k, v = wl.make_inputs("cuda", layout="bshd")
+    assert not q.is_contiguous()
+    assert "key-split" in _split_text(q, 1, 3, 200, 1200, 64)
+    _check(q, k, v, 0.125, False, "fp16")
+
+
+def test_causal_and_whole_rounds_do_not_split():
+    q = torch.empty(1, dtype=torch.float16)
+    assert "key-split" not in _split_text(q, 1, 2, 256, 2048, 64, causal=True)
+    # 2 x 4 x 32 blocks = exactly one block per CU on a 256-CU MI355X
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert "key-split" not in _split_text(q, 2, 4, 4096, 4096, 64)
+        assert "key-split" in _split_text(q, 2, 10, 4096, 4096, 64)

@@ -57,7 +57,7 @@ hipError_t launch_bucket(const FwdParams& p, int dk, hipStream_t s) {
 
 bool pipe16_applies(const FwdParams& p, int dk);
 hipError_t launch_pipe16(const FwdParams& p, int dk, bool bf16, bool causal, bool prescale, hipStream_t s);
-void describe_pipe16(int dk, int Sq, char* buf, int len);
+void describe_pipe16(int dk, int B, int H, int Sq, int Sk, bool causal, char* buf, int len);
 
 int mfma16_bucket(int D) {
   for (int dk : kMfma16Dk)
@@ -85,13 +85,13 @@ hipError_t launch_mfma16(const FwdParams& p, bool bf16, bool causal, hipStream_t
 
 int mfma16_max_bk() { return 64; }
 
-void describe_mfma16(int D, int Sq, int Sk, char* buf, int len) {
+void describe_mfma16(int D, int B, int H, int Sq, int Sk, bool causal, char* buf, int len) {
   const int dk = mfma16_bucket(D);
   FwdParams p = {};
   p.Sk = Sk;
   p.k_s = p.v_s = D;
   if (pipe16_applies(p, dk)) {
-    describe_pipe16(dk, Sq, buf, len);
+    describe_pipe16(dk, B, H, Sq, Sk, causal, buf, len);
     return;
   }
   const Tile16 t = tile16(dk);

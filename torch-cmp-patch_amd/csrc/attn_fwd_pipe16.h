@@ -1,29 +1,45 @@
 // Software-pipelined fused attention forward for fp16 / bf16 on gfx950
 // (v_mfma_f32_32x32x16_{f16,bf16}).
 //
-// Same math and register layout as attn_fwd_mfma16.h (S^T = K Q^T so that a
-// lane owns one query row, O^T = V^T P^T, bit-permuted K feed, V^T fragments
-// through ds_read_b64_tr_b16, optional Q pre-scaling with -m carried in the
-// accumulator, max-first lazy rescale).  One wave owns 32 query rows; a
-// workgroup of NW waves owns NW * 32.
+// Same register layout as attn_fwd_mfma16.h (S^T = K Q^T so that a lane owns
+// one query row, O^T = V^T P^T, bit-permuted K feed, V^T fragments through
+// ds_read_b64_tr_b16, optional Q pre-scaling with -m carried in the
+// accumulator).  One wave owns 32 query rows; a workgroup of NW waves owns
+// NW * 32.
 //
-// The difference is the schedule.  In attn_fwd_mfma16 a wave's tile is a
-// dependency chain (scores -> max -> exp -> PV), so the MFMA pipe and the VALU
-// only overlap across waves.  Here K runs one tile ahead of V:
+// Schedule.  K runs one tile ahead of V, and a tile's exponentials are split
+// over two iterations:
 //
 //   iteration t:  barrier
 //                 read K(t+1) fragments; store K(t+2), V(t+1) to LDS;
 //                 issue global loads of K(t+4), V(t+3)
-//                 rescale decision for tile t (max computed last iteration)
-//                 [ QK(t+1) MFMAs | exp/pack/row-sum of tile t ]
-//                 [ PV(t) MFMAs   | row max of tile t+1        ]
+//                 [ QK(t+1) MFMAs | exp/pack/row-sum, late half of tile t  ]
+//                 check tile t (below)
+//                 [ PV(t) MFMAs   | exp/pack/row-sum, early half of t+1   ]
 //
-// so that every MFMA of the tile has independent VALU work next to it in the
-// same wave.  The bracketed part is one basic block issued in a fixed order
-// (sched_barrier fences between MFMA-sized steps).  LDS holds two K and two V tiles; K(t+2) goes into
-// the buffer K(t) left, V(t+1) into the one V(t-1) left, and the single
+// so that every MFMA has independent VALU work beside it in the same wave.
+// Each bracketed part is issued in a fixed order (sched_barrier fences
+// between MFMA-sized steps).  LDS holds two K and two V tiles; K(t+2) goes
+// into the buffer K(t) left, V(t+1) into the one V(t-1) left, and the single
 // barrier per iteration orders those writes after the previous iteration's
 // reads.
+//
+// Softmax without a per-tile max.  Tile 0 sets the row offset m from its max;
+// later tiles are exponentiated as exp2(s*c - m) straight away.  The row sum
+// of a lane's probabilities bounds every one of them, so a sum at most 2^8
+// proves they all are, exactly what the max-first rule (rescale when the tile
+// max exceeds m by more than 8 log2 units) would have accepted without a
+// rescale.  A larger sum (rare) sends the wave to the exact path: tile max,
+// rescale of O and l if it exceeds m + 8, tile redone.  Results equal the
+// max-first scheme's; the per-score max and the cross-lane reduction leave
+// the common path.
+//
+// Key split.  When the query blocks do not fill whole rounds of the chip
+// (e.g. 640 blocks on 256 CUs x 3 slots: 128 CUs would run 3 and 128 run 2),
+// the blocks past the last whole round are cut into key ranges run by
+// separate workgroups, so that every CU ends with the same work.  Each part
+// leaves (O, m, l) in a workspace; the last part of a block to finish merges
+// (per-wave counter, no waiting) and writes the output.
 //
 // Reference algorithm: src/cuda/fp16_flash_attention_hfma2.cu:72-243.
 #pragma once
@@ -31,6 +47,20 @@
 #include "attn_fwd_mfma16.h"
 
 namespace cmpext3 {
+
+// Key split of the last query blocks: workgroups [0, nfull) take whole
+// blocks; the next (n_blocks - nfull) * nparts take one key range each of the
+// remaining blocks.  Per (split block, wave) the parts leave their partial O,
+// offset and row sum in ws; the last to arrive (counter in cnt) merges and
+// puts the counter back to zero.  nparts == 1: no split, ws/cnt unused.
+struct SplitArgs {
+  int nfull, nparts;
+  f32x4* ws;  // split blocks * nparts * NW * (DP / 8 + 1) * 64 float4
+  int* cnt;   // split blocks * NW counters, zero between launches
+};
+
+// float4 vectors each lane leaves per part: its O fragments, then (m, l)
+constexpr int split_vectors(int dp) { return dp / 8 + 1; }
 
 // Raw buffer resource over [base, base + bytes) (gfx9 dword3: 32-bit raw
 // reads).  The fields go through readfirstlane so that the compiler keeps the
@@ -49,7 +79,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base,
 // dim is not a multiple of 16 (D < DK), so K columns past D are zeroed.
 template <typename T, int DK, int DP, int NW, int BK, int OCC, bool CAUSAL, bool PRESCALE, int OPT = 0>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
-attn_fwd_pipe16(const FwdParams p) {
+attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   constexpr int NT = NW * 64;
   constexpr int BQ = NW * 32;
   constexpr bool SWZ = (OPT & 2) && (DK == DP) && (DK == 32 || DK == 64 || DK == 128);
@@ -79,8 +109,15 @@ attn_fwd_pipe16(const FwdParams p) {
   const int l32 = lane & 31;
   const int hh = lane >> 5;
 
+  int lb = blockIdx.x, part = 0, nparts = 1;
+  if (lb >= sa.nfull) {
+    const int r = lb - sa.nfull;
+    nparts = sa.nparts;
+    lb = sa.nfull + r / nparts;
+    part = r - (lb - sa.nfull) * nparts;
+  }
   int bh, qblk;
-  wg_tile(blockIdx.x, p, CAUSAL, bh, qblk);
+  wg_tile(lb, p, CAUSAL, bh, qblk);
   const int b = bh / p.H;
   const int h = bh - b * p.H;
   const int q0 = qblk * BQ;
@@ -96,8 +133,12 @@ attn_fwd_pipe16(const FwdParams p) {
 
   int kend = Sk;
   if (CAUSAL) kend = min(Sk, q0 + BQ);
-  const int ntiles = (kend + BK - 1) / BK;
+  const int ntall = (kend + BK - 1) / BK;
+  const int tbase = part * ntall / nparts;
+  const int ntiles = (part + 1) * ntall / nparts - tbase;
   if (ntiles <= 0) return;  // Sk == 0 is rejected by the host
+  // end of this workgroup's key range: the padding tile past it is masked
+  const int kpe = min(kend, (tbase + ntiles) * BK);
   const int nt2 = (ntiles + 1) & ~1;  // iterations run (even)
 
   // ---- Q as the B operand of S^T = K Q^T
@@ -161,21 +202,21 @@ attn_fwd_pipe16(const FwdParams p) {
   }
   // tile j (clamped to the last one) into a register set
   auto load_k = [&](int j, u32x4 (&kr)[KLD]) {
-    const int so = min(j, ntiles - 1) * BK * ks_b;
+    const int so = (tbase + min(j, ntiles - 1)) * BK * ks_b;
 #pragma unroll
     for (int it = 0; it < KLD; ++it)
       kr[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, kvo[it], so, 0));
   };
   auto load_v = [&](int j, u32x4 (&vr)[VLD]) {
-    const int so = min(j, ntiles - 1) * BK * vs_b;
+    const int so = (tbase + min(j, ntiles - 1)) * BK * vs_b;
 #pragma unroll
     for (int it = 0; it < VLD; ++it)
       vr[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vvo[it], so, 0));
   };
   // K columns past D are zeroed (Q is zero there, and 0 * finite = 0 keeps
   // the padded k-steps exact); V columns past D only feed discarded outputs.
-  auto store_k = [&](int j, const u32x4 (&kr)[KLD]) {
-    uint16_t* dst = kbase + (j & 1) * KTILE;
+  auto store_k = [&](int slot, const u32x4 (&kr)[KLD]) {
+    uint16_t* dst = kbase + slot * KTILE;
 #pragma unroll
     for (int it = 0; it < KLD; ++it)
       if (KFULL || it * NT + tid < BK * KCH) {
@@ -210,8 +251,8 @@ attn_fwd_pipe16(const FwdParams p) {
       v_rd[db][half] = r * RSV + (SWZ ? 8 * ((col >> 3) ^ lds_swz<DP>(r)) + (col & 7) : col);
     }
 
-  auto read_kf = [&](int j, u32x4 (&kf)[NKB][NKS]) {
-    const uint16_t* ks = kbase + (j & 1) * KTILE;
+  auto read_kf = [&](int slot, u32x4 (&kf)[NKB][NKS]) {
+    const uint16_t* ks = kbase + slot * KTILE;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
@@ -236,17 +277,17 @@ attn_fwd_pipe16(const FwdParams p) {
     }
   };
   auto tile_needs_mask = [&](int j) {
-    const int k0 = j * BK;
-    return (k0 + BK > Sk) || (CAUSAL && k0 + BK - 1 > qlo);
+    const int k0 = (tbase + j) * BK;
+    return (k0 + BK > kpe) || (CAUSAL && k0 + BK - 1 > qlo);
   };
   auto mask = [&](int j, f32x16 (&sc)[NKB]) {
-    const int k0 = j * BK;
+    const int k0 = (tbase + j) * BK;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = k0 + 32 * kb + acc_key(r, hh);
-        if (key >= Sk || (CAUSAL && key > qrow)) sc[kb][r] = -INFINITY;
+        if (key >= kpe || (CAUSAL && key > qrow)) sc[kb][r] = -INFINITY;
       }
   };
   // this lane's half of the row max (the two halves meet at the decision)
@@ -276,88 +317,84 @@ attn_fwd_pipe16(const FwdParams p) {
   load_k(3, kB);
   load_v(2, vB);
   lds_barrier();
-  f32x16 sA[NKB], sB[NKB];
-  {
-    u32x4 kf[NKB][NKS];
-    read_kf(0, kf);
-    qk(kf, sA);
-  }
-  to_exp2(sA);
-  if (tile_needs_mask(0)) mask(0, sA);
-  float mq = row_max(sA);
-
   constexpr int NQK = NKB * NKS;  // score MFMAs per tile
   constexpr int NPV = NCH * NDB;  // PV MFMAs per tile
   constexpr int NU = NCH * 4;     // exp units (2 exp + pack + row-sum step) per tile
-  // Units placed beside the score MFMAs; the rest go beside the PV MFMAs,
-  // unit UA + i after PV MFMA i.  Unit u feeds 16-key chunk u / 4, whose
-  // first PV MFMA has index NDB * (u / 4), so the last unit must land in an
-  // earlier step.  With 3/4 of the units up front that holds when NDB >= 2;
-  // with a single output block every unit goes up front.
-  constexpr int UA = NDB > 1 ? (3 * NU) / 4 : NU;
-  static_assert(NU - 1 - UA < (NU - 1) / 4 * NDB, "an exp unit would follow its PV MFMA");
-  constexpr int NPC = 2 * NKB;    // 8-score pieces of the next tile's max
+  constexpr int NE = NU / 2;      // early units (first half of the chunks), done one iteration ahead
+  static_assert(NCH % 2 == 0, "chunk split");
 
-  // One iteration; sc holds tile t's exp2-domain scores, sn receives tile
-  // t+1's.  The loop below alternates the two arrays so that nothing is
-  // copied between iterations.
-  auto step = [&](int t, f32x16 (&sc)[NKB], f32x16 (&sn)[NKB], u32x4 (&kr)[KLD], u32x4 (&vr)[VLD]) {
+  // Raise the offset to the row max mx (never lower it once a live key was
+  // seen) and rescale O and l; returns the shift applied to the scores.
+  auto rescale = [&](float mx) {
+    const bool fst = thr == -INFINITY;
+    float delta = fst ? mx : fmaxf(mx, 0.f);
+    if (mx == -INFINITY) delta = 0.f;
+    const float alpha = fast_exp2(-delta);
+    mb += delta;
+    ls0 *= alpha;
+    ls1 *= alpha;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) oacc[db] *= alpha;
+    if (PRESCALE) bias -= delta;  // stays exactly -mb
+    if (!(fst && mx == -INFINITY)) thr = 8.f;
+    return delta;
+  };
+  // exp unit u of a tile: two probabilities, packed, into the tile's row sum
+  auto unit = [&](int u, const f32x16 (&sc)[NKB], u32x4 (&pc)[NCH], float& t0, float& t1) {
+    const int ch = u >> 2, e = u & 3, kb = ch >> 1, cc = ch & 1;
+    const uint32_t w = Elt<T>::pack(fast_exp2(sc[kb][8 * cc + 2 * e]), fast_exp2(sc[kb][8 * cc + 2 * e + 1]));
+    pc[ch][e] = w;
+    if (e & 1) t1 = Elt<T>::sum2(w, t1);
+    else t0 = Elt<T>::sum2(w, t0);
+  };
+  // bf16 path: the two scores of unit u into the exp2 domain
+  auto conv = [&](int u, f32x16 (&sc)[NKB]) {
+    if (!PRESCALE) {
+      const int ch = u >> 2, e = u & 3, kb = ch >> 1, cc = ch & 1;
+      sc[kb][8 * cc + 2 * e] = __builtin_fmaf(sc[kb][8 * cc + 2 * e], c, -mb);
+      sc[kb][8 * cc + 2 * e + 1] = __builtin_fmaf(sc[kb][8 * cc + 2 * e + 1], c, -mb);
+    }
+  };
+
+  // tile 0 always sets the offset from its max
+  f32x16 sA[NKB], sB[NKB];
+  u32x4 pA[NCH], pB[NCH];
+  float tA0 = 0.f, tA1 = 0.f, tB0 = 0.f, tB1 = 0.f;
+  {
+    u32x4 kf0[NKB][NKS];
+    read_kf(0, kf0);
+    qk(kf0, sA);
+  }
+  to_exp2(sA);
+  if (tile_needs_mask(0)) mask(0, sA);
+  {
+    const float mx = xhalf_max(row_max(sA));
+    const float delta = rescale(mx);
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) sA[kb] -= delta;
+  }
+#pragma unroll
+  for (int u = 0; u < NE; ++u) unit(u, sA, pA, tA0, tA1);
+
+  // One iteration.  On entry sc holds tile t's exp2-domain scores, pc the
+  // early half of its probabilities and tc0/tc1 their row sums.
+  auto step = [&](int t, f32x16 (&sc)[NKB], f32x16 (&sn)[NKB], u32x4 (&pc)[NCH], u32x4 (&pn)[NCH],
+                  float& tc0, float& tc1, float& tn0, float& tn1, u32x4 (&kr)[KLD], u32x4 (&vr)[VLD]) {
     // every wave is done reading K(t) and V(t-1); K(t+1), V(t) are visible
     lds_barrier();
     u32x4 kf[NKB][NKS];
-    read_kf(t + 1, kf);  // stale data on the last tile; those scores are dropped
+    read_kf((t + 1) & 1, kf);  // stale data on the last tile; those scores are dropped
     // this iteration's register set holds K(t+2), V(t+1) (loaded two
     // iterations ago) and is refilled with K(t+4), V(t+3).  Past the last
     // tile the set holds a clamped copy that lands in a buffer no later
     // iteration reads, so the stores need no condition.
-    store_k(t + 2, kr);
+    store_k(t & 1, kr);
     store_v(t + 1, vr);
     load_k(t + 4, kr);
     load_v(t + 3, vr);
 
-    // Raise the offset to the row max mx (never lower it once a live key was
-    // seen) and rescale O and l; returns the shift applied to the scores.
-    auto rescale = [&](float mx) {
-      const bool fst = thr == -INFINITY;
-      float delta = fst ? mx : fmaxf(mx, 0.f);
-      if (mx == -INFINITY) delta = 0.f;
-      const float alpha = fast_exp2(-delta);
-      mb += delta;
-      ls0 *= alpha;
-      ls1 *= alpha;
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) oacc[db] *= alpha;
-      if (PRESCALE) bias -= delta;  // stays exactly -mb
-      if (!(fst && mx == -INFINITY)) thr = 8.f;
-      return delta;
-    };
-
-    // ---- rescale decision for tile t: the row max exceeds the offset by
-    // more than 8 (log2 units), or this is the first live tile
-    {
-      const float mx = xhalf_max(mq);
-      if (__builtin_amdgcn_ballot_w64(mx > thr)) {
-        const float delta = rescale(mx);
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) sc[kb] -= delta;
-      }
-    }
-
-    // ---- one basic block, issued in a fixed order (sched_barrier fences):
-    // stage A: score MFMAs of tile t+1, each beside V fragment reads of
-    // tile t and a share of tile t's exp units; stage B: PV MFMAs of tile
-    // t beside the remaining exp units and the pieces of tile t+1's max.
-    if (OPT & 1) __builtin_amdgcn_s_setprio(1);
-    u32x4 pf[NCH];
     u32x4 vfr[NPV];
     const uint16_t* vs = vbase + (t & 1) * VTILE;
-    auto exp_unit = [&](int u) {
-      const int ch = u >> 2, e = u & 3, kb = ch >> 1, cc = ch & 1;
-      const uint32_t w = Elt<T>::pack(fast_exp2(sc[kb][8 * cc + 2 * e]), fast_exp2(sc[kb][8 * cc + 2 * e + 1]));
-      pf[ch][e] = w;
-      if (e & 1) ls1 = Elt<T>::sum2(w, ls1);
-      else ls0 = Elt<T>::sum2(w, ls0);
-    };
     auto read_vfr = [&](int i) {
       const int ch = i / NDB, db = i - ch * NDB;
       const uint16_t* vp = vs + 16 * ch * RSV;
@@ -365,6 +402,9 @@ attn_fwd_pipe16(const FwdParams p) {
       const uint2 hi = lds_tr16_b64(vp + v_rd[db][1]);
       vfr[i] = (u32x4){lo.x, lo.y, hi.x, hi.y};
     };
+    // ---- stage A: score MFMAs of tile t+1 beside the V fragment reads of
+    // tile t and the late half of tile t's exp units
+    if (OPT & 1) __builtin_amdgcn_s_setprio(1);
     f32x16 acc[NKB];
 #pragma unroll
     for (int i = 0; i < NQK; ++i) {
@@ -373,54 +413,111 @@ attn_fwd_pipe16(const FwdParams p) {
       for (int v = i * NPV / NQK; v < (i + 1) * NPV / NQK; ++v) read_vfr(v);
       acc[kb] = Elt<T>::mma(kf[kb][s], qf[s], s == 0 ? (PRESCALE ? bias : (f32x16){}) : acc[kb]);
 #pragma unroll
-      for (int u = i * UA / NQK; u < (i + 1) * UA / NQK; ++u) exp_unit(u);
+      for (int u = i * NE / NQK; u < (i + 1) * NE / NQK; ++u) unit(NE + u, sc, pc, tc0, tc1);
       if (!(OPT & 4)) __builtin_amdgcn_sched_barrier(0);
     }
-
-    float mpart = -INFINITY;
-    auto piece = [&](int j) {  // 8 scores of the next tile: scale, then max
-      const int kb = j >> 1, r0 = 8 * (j & 1);
-#pragma unroll
-      for (int r = r0; r < r0 + 8; ++r) {
-        float x = acc[kb][r];
-        if (!PRESCALE) x = __builtin_fmaf(x, c, -mb);
-        acc[kb][r] = x;
-        mpart = fmaxf(mpart, x);
-      }
-    };
-#pragma unroll
-    for (int i = 0; i < NPV; ++i) {
-      const int ch = i / NDB, db = i - ch * NDB;
-      oacc[db] = Elt<T>::mma(vfr[i], pf[ch], oacc[db]);
-      if (i < NU - UA) exp_unit(UA + i);
-      else if (i - (NU - UA) < NPC) piece(i - (NU - UA));
-      if (!(OPT & 4)) __builtin_amdgcn_sched_barrier(0);
-    }
-#pragma unroll
-    for (int j = NPV - (NU - UA) > 0 ? NPV - (NU - UA) : 0; j < NPC; ++j) piece(j);
     if (OPT & 1) __builtin_amdgcn_s_setprio(0);
-    mq = mpart;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) sn[kb] = acc[kb];
 
-
-    if (t + 1 < nt2 && tile_needs_mask(t + 1)) {
-      mask(t + 1, sn);
-      mq = row_max(sn);
+    // ---- tile t is exponentiated against the running offset without its
+    // own max.  A lane row sum above 2^8 (always true if some probability
+    // exceeds 2^8) sends the wave to the exact path: the tile max decides a
+    // rescale as in the max-first scheme, and the tile is redone.
+    if (__builtin_amdgcn_ballot_w64(thr == -INFINITY || tc0 + tc1 > 256.f)) {
+      const float mx = xhalf_max(row_max(sc));
+      if (__builtin_amdgcn_ballot_w64(mx > thr)) {
+        const float delta = rescale(mx);
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) sc[kb] -= delta;
+        if (PRESCALE) {
+#pragma unroll
+          for (int kb = 0; kb < NKB; ++kb) sn[kb] -= delta;  // scored with the old offset
+        }
+        tc0 = 0.f;
+        tc1 = 0.f;
+#pragma unroll
+        for (int u = 0; u < NU; ++u) unit(u, sc, pc, tc0, tc1);
+      }
     }
+    ls0 += tc0;
+    ls1 += tc1;
+    if (t + 1 < nt2 && tile_needs_mask(t + 1)) mask(t + 1, sn);
+
+    // ---- stage B: PV MFMAs of tile t beside the K(t+2) fragment reads and
+    // the early half of tile t+1's exp units
+    if (OPT & 1) __builtin_amdgcn_s_setprio(1);
+    tn0 = 0.f;
+    tn1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < NPV; ++i) {
+      const int ch = i / NDB, db = i - ch * NDB;
+      oacc[db] = Elt<T>::mma(vfr[i], pc[ch], oacc[db]);
+#pragma unroll
+      for (int u = i * NE / NPV; u < (i + 1) * NE / NPV; ++u) {
+        conv(u, sn);
+        unit(u, sn, pn, tn0, tn1);
+      }
+      if (!(OPT & 4)) __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int u = NE; u < NU; ++u) conv(u, sn);
+    if (OPT & 1) __builtin_amdgcn_s_setprio(0);
   };
 
   // An even number of iterations keeps the loop body free of a mid-loop
   // exit, which would make the compiler wait for every prefetch at the top.
   // With an odd tile count the extra tile is a clamped copy of the last one
-  // whose keys all lie past kend: fully masked, it adds exactly zero.
+  // whose keys all lie past kpe: fully masked, it adds exactly zero.  The
+  // last iteration's early units work on stale scores nobody reads.
   for (int t = 0; t < nt2; t += 2) {
-    step(t, sA, sB, kA, vA);
-    step(t + 1, sB, sA, kB, vB);
+    step(t, sA, sB, pA, pB, tA0, tA1, tB0, tB1, kA, vA);
+    step(t + 1, sB, sA, pB, pA, tB0, tB1, tA0, tA1, kB, vB);
   }
 
-  // ---- epilogue: combine the two halves' partial sums, normalise, store
-  const float inv = 1.f / xhalf_sum(ls0 + ls1);
+  // ---- epilogue
+  float lsum = xhalf_sum(ls0 + ls1);
+  if (nparts > 1) {
+    // Leave this part's state, then let the last part of the block merge.
+    // Device-scope (sc1) stores and loads keep the exchange coherent across
+    // the XCDs' L2s without cache-wide write-back or invalidation.
+    constexpr int NV = split_vectors(DP);
+    static_assert(NV == NDB * 4 + 1, "O fragments + (m, l)");
+    const int sb = lb - sa.nfull;
+    const __amdgpu_buffer_rsrc_t wsr = uniform_rsrc(sa.ws, (int64_t)(sb + 1) * nparts * NW * NV * 64 * 16);
+    auto voff = [&](int q, int k) { return ((((sb * nparts + q) * NW + wave) * NV + k) * 64 + lane) * 16; };
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            (f32x4){oacc[db][4 * g], oacc[db][4 * g + 1], oacc[db][4 * g + 2], oacc[db][4 * g + 3]}, wsr,
+            voff(part, db * 4 + g), 0, 16);
+    __builtin_amdgcn_raw_buffer_store_b128((f32x4){mb, lsum, 0.f, 0.f}, wsr, voff(part, NDB * 4), 0, 16);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    int old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(sa.cnt + sb * NW + wave, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old != nparts - 1) return;
+    if (lane == 0) __hip_atomic_store(sa.cnt + sb * NW + wave, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int q = 0; q < nparts; ++q) {
+      if (q == part) continue;
+      const f32x4 ml = __builtin_amdgcn_raw_buffer_load_b128(wsr, voff(q, NDB * 4), 0, 16);
+      const float m = fmaxf(mb, ml[0]);
+      const float a = fast_exp2(mb - m), bq = fast_exp2(ml[0] - m);
+      lsum = lsum * a + ml[1] * bq;
+      mb = m;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 x = __builtin_amdgcn_raw_buffer_load_b128(wsr, voff(q, db * 4 + g), 0, 16);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) oacc[db][4 * g + i] = oacc[db][4 * g + i] * a + x[i] * bq;
+        }
+    }
+  }
+  const float inv = 1.f / lsum;
   if (qrow < Sq) {
     uint16_t* orow = og + (int64_t)qrow * p.o_s;
 #pragma unroll
@@ -439,7 +536,7 @@ attn_fwd_pipe16(const FwdParams p) {
 }
 
 template <typename T, int DK, int NW, int BK, int OCC, bool CAUSAL, bool PRESCALE, int OPT = 0>
-hipError_t launch_pipe16_cfg(const FwdParams& p0, hipStream_t stream) {
+hipError_t launch_pipe16_cfg(const FwdParams& p0, const SplitArgs& sa, hipStream_t stream) {
   constexpr int DP = (DK + 31) / 32 * 32;
   constexpr int BQ = NW * 32;
   FwdParams p = p0;
@@ -449,8 +546,9 @@ hipError_t launch_pipe16_cfg(const FwdParams& p0, hipStream_t stream) {
   // buffer offsets of the K/V tiles are 32-bit
   const int64_t rs = p.k_s > p.v_s ? p.k_s : p.v_s;
   if ((int64_t)(p.Sk + BK) * rs * 2 >= (int64_t(1) << 31)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((attn_fwd_pipe16<T, DK, DP, NW, BK, OCC, CAUSAL, PRESCALE, OPT>), dim3(p.n_wg),
-                     dim3(NW * 64), 0, stream, p);
+  const int nwg = sa.nfull + (p.n_wg - sa.nfull) * sa.nparts;
+  hipLaunchKernelGGL((attn_fwd_pipe16<T, DK, DP, NW, BK, OCC, CAUSAL, PRESCALE, OPT>), dim3(nwg),
+                     dim3(NW * 64), 0, stream, p, sa);
   return hipGetLastError();
 }
 

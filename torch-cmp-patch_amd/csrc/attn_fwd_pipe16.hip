@@ -1,12 +1,22 @@
-// Instantiations and tile table of the software-pipelined fp16/bf16 kernel
-// (template in attn_fwd_pipe16.h), used for head dims up to 128.
+// Instantiations, tile table and key-split plan of the software-pipelined
+// fp16/bf16 kernel (template in attn_fwd_pipe16.h), used for head dims up to
+// 128.
 //
 // Like the v2 table in attn_fwd_mfma16.hip this replaces the reference's
 // per-head-dim template table (src/cuda/fp16_flash_attention_hfma2.cu:278-285);
 // entries come from an offline sweep on an MI355X.  All buckets use 4-wave
 // workgroups and 32-key tiles; the waves per SIMD are the most the registers
 // allow without spilling (D = 32: 4, D <= 64: 3, D <= 128: 2).
+//
+// The key split (no counterpart in the reference) needs a small exchange
+// buffer per (device, stream), allocated on first use and kept for the life
+// of the process.  Where it cannot be had (a stream under graph capture, an
+// allocation failure, too many streams) the launch simply runs unsplit.
 #include <stdio.h>
+
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "attn_fwd_pipe16.h"
 
@@ -18,25 +28,121 @@ constexpr int kPipeNw = 4;
 constexpr int kPipeBk = 32;
 constexpr int pipe_occ(int dk) { return dk <= 32 ? 4 : dk <= 64 ? 3 : 2; }
 
+// Split plan limits: a part scans at least kMinPartTiles key tiles (shorter
+// parts spend more on their prologue and merge than they save), and at most
+// kMaxStreams streams per device get an exchange buffer.
+constexpr int kMinPartTiles = 8;
+constexpr int kMaxStreams = 16;
+constexpr int kMi355xCus = 256;  // used by describe() when no device is visible
+
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return kMi355xCus;
+  }
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+      (void)hipGetLastError();
+      return kMi355xCus;
+    }
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// Exchange buffer sized for the largest plan on this device: at most one part
+// per CU (split blocks * parts <= CUs), kPipeNw waves, DP <= 128.
+struct Exchange {
+  f32x4* ws;
+  int* cnt;
+};
+
+size_t exchange_ws_bytes(int cus) { return (size_t)cus * kPipeNw * split_vectors(128) * 64 * sizeof(f32x4); }
+size_t exchange_cnt_bytes(int cus) { return (size_t)cus * kPipeNw * sizeof(int); }
+
+bool exchange_for(hipStream_t s, int cus, Exchange& out) {
+  static std::mutex mu;
+  static std::map<std::pair<int, hipStream_t>, Exchange> cache;
+  static int per_dev[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return false;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_pair(dev, s);
+  auto it = cache.find(key);
+  if (it != cache.end()) {
+    out = it->second;
+    return true;
+  }
+  if (per_dev[dev] >= kMaxStreams) return false;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();
+    return false;
+  }
+  const size_t wsb = exchange_ws_bytes(cus), cb = exchange_cnt_bytes(cus);
+  void* mem = nullptr;
+  if (hipMalloc(&mem, wsb + cb) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  Exchange e{(f32x4*)mem, (int*)((char*)mem + wsb)};
+  // the counters start at zero; every merge puts its counter back
+  if (hipMemsetAsync(e.cnt, 0, cb, s) != hipSuccess) {
+    (void)hipGetLastError();
+    (void)hipFree(mem);
+    return false;
+  }
+  cache[key] = e;
+  ++per_dev[dev];
+  out = e;
+  return true;
+}
+
+// Which blocks run whole and how the rest are cut.  n blocks on `cus` CUs at
+// `occ` workgroups per CU; the dispatcher hands workgroup i to CU i mod cus
+// while all of them fit, so after the whole rounds each CU takes exactly one
+// part.  Causal launches keep their longest-first order and never split.
+SplitArgs split_plan(int n, int ntiles, int occ, int cus, bool causal) {
+  SplitArgs sa = {n, 1, nullptr, nullptr};
+  if (causal || cus <= 0) return sa;
+  const int full = n / cus, rem = n - full * cus;
+  if (rem == 0 || full + 1 > occ) return sa;  // whole rounds, or more than fits at once
+  int parts = cus / rem;
+  if (parts > ntiles / kMinPartTiles) parts = ntiles / kMinPartTiles;
+  if (parts < 2) return sa;
+  sa.nfull = full * cus;
+  sa.nparts = parts;
+  return sa;
+}
+
 template <typename T, int DK, bool CAUSAL, bool PRESCALE>
-hipError_t launch_dk(const FwdParams& p, hipStream_t s) {
-  // OPT 1: s_setprio around the MFMA block; OPT 8: zero K columns past D
-  if (p.D == DK) return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, pipe_occ(DK), CAUSAL, PRESCALE, 1>(p, s);
-  return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, pipe_occ(DK), CAUSAL, PRESCALE, 1 | 8>(p, s);
+hipError_t launch_dk(const FwdParams& p, const SplitArgs& sa, hipStream_t s) {
+  // OPT 1: s_setprio around the MFMA blocks; OPT 8: zero K columns past D
+  if (p.D == DK) return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, pipe_occ(DK), CAUSAL, PRESCALE, 1>(p, sa, s);
+  return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, pipe_occ(DK), CAUSAL, PRESCALE, 1 | 8>(p, sa, s);
 }
 
 template <typename T, bool CAUSAL, bool PRESCALE>
-hipError_t launch_bucket(const FwdParams& p, int dk, hipStream_t s) {
+hipError_t launch_bucket(const FwdParams& p, const SplitArgs& sa, int dk, hipStream_t s) {
   switch (dk) {
-    case 32: return launch_dk<T, 32, CAUSAL, PRESCALE>(p, s);
-    case 48: return launch_dk<T, 48, CAUSAL, PRESCALE>(p, s);
-    case 64: return launch_dk<T, 64, CAUSAL, PRESCALE>(p, s);
-    case 80: return launch_dk<T, 80, CAUSAL, PRESCALE>(p, s);
-    case 96: return launch_dk<T, 96, CAUSAL, PRESCALE>(p, s);
-    case 128: return launch_dk<T, 128, CAUSAL, PRESCALE>(p, s);
+    case 32: return launch_dk<T, 32, CAUSAL, PRESCALE>(p, sa, s);
+    case 48: return launch_dk<T, 48, CAUSAL, PRESCALE>(p, sa, s);
+    case 64: return launch_dk<T, 64, CAUSAL, PRESCALE>(p, sa, s);
+    case 80: return launch_dk<T, 80, CAUSAL, PRESCALE>(p, sa, s);
+    case 96: return launch_dk<T, 96, CAUSAL, PRESCALE>(p, sa, s);
+    case 128: return launch_dk<T, 128, CAUSAL, PRESCALE>(p, sa, s);
   }
   return hipErrorNotSupported;
 }
+
+int n_blocks(int B, int H, int Sq) { return B * H * ((Sq + kPipeNw * 32 - 1) / (kPipeNw * 32)); }
+int n_key_tiles(int Sk) { return (Sk + kPipeBk - 1) / kPipeBk; }
 
 }  // namespace
 
@@ -56,20 +162,41 @@ bool pipe16_applies(const FwdParams& p, int dk) {
 // never pre-scales: rounding Q*c to 8 mantissa bits moves each score by up to
 // 2^-9 of its size, which at scale 1 (scores of tens of log2 units) breaks
 // the 2e-2 bf16 bar, so bf16 scores get one FMA each instead.
-hipError_t launch_pipe16(const FwdParams& p, int dk, bool bf16, bool causal, bool prescale, hipStream_t s) {
+hipError_t launch_pipe16(const FwdParams& p0, int dk, bool bf16, bool causal, bool prescale, hipStream_t s) {
+  FwdParams p = p0;
+  // Without pre-scaling, masked keys enter as raw -inf and meet the multiplier
+  // c in one FMA; scale 0 would make that 0 * -inf.  A multiplier of 1e-30
+  // instead leaves every finite score's exp2 argument within 1e-22 of -m,
+  // which rounds to the same probability as scale 0 gives, and keeps -inf.
+  if (!prescale && p.c == 0.f) p.c = 1e-30f;
+  const int cus = device_cus();
+  SplitArgs sa = split_plan(n_blocks(p.B, p.H, p.Sq), n_key_tiles(p.Sk), pipe_occ(dk), cus, causal);
+  if (sa.nparts > 1) {
+    Exchange e;
+    if (exchange_for(s, cus, e)) {
+      sa.ws = e.ws;
+      sa.cnt = e.cnt;
+    } else {
+      sa = SplitArgs{n_blocks(p.B, p.H, p.Sq), 1, nullptr, nullptr};
+    }
+  }
   if (bf16)
-    return causal ? launch_bucket<__bf16, true, false>(p, dk, s) : launch_bucket<__bf16, false, false>(p, dk, s);
+    return causal ? launch_bucket<__bf16, true, false>(p, sa, dk, s) : launch_bucket<__bf16, false, false>(p, sa, dk, s);
   if (prescale)
-    return causal ? launch_bucket<_Float16, true, true>(p, dk, s) : launch_bucket<_Float16, false, true>(p, dk, s);
-  return causal ? launch_bucket<_Float16, true, false>(p, dk, s) : launch_bucket<_Float16, false, false>(p, dk, s);
+    return causal ? launch_bucket<_Float16, true, true>(p, sa, dk, s) : launch_bucket<_Float16, false, true>(p, sa, dk, s);
+  return causal ? launch_bucket<_Float16, true, false>(p, sa, dk, s) : launch_bucket<_Float16, false, false>(p, sa, dk, s);
 }
 
-void describe_pipe16(int dk, int Sq, char* buf, int len) {
+void describe_pipe16(int dk, int B, int H, int Sq, int Sk, bool causal, char* buf, int len) {
   const int bq = kPipeNw * 32;
+  const int n = n_blocks(B, H, Sq);
+  const SplitArgs sa = split_plan(n, n_key_tiles(Sk), pipe_occ(dk), device_cus(), causal);
+  char split[64] = "";
+  if (sa.nparts > 1) snprintf(split, sizeof split, " key-split: %d whole + %d x %d parts", sa.nfull, n - sa.nfull, sa.nparts);
   snprintf(buf, len,
            "pipe16 mfma 32x32x16 S^T-form, K one tile ahead of V: DK=%d DP=%d waves=%d BQ=%d BK=%d "
-           "waves/SIMD=%d qtiles=%d",
-           dk, (dk + 31) / 32 * 32, kPipeNw, bq, kPipeBk, pipe_occ(dk), (Sq + bq - 1) / bq);
+           "waves/SIMD=%d qtiles=%d%s",
+           dk, (dk + 31) / 32 * 32, kPipeNw, bq, kPipeBk, pipe_occ(dk), (Sq + bq - 1) / bq, split);
 }
 
 }  // namespace cmpext3
