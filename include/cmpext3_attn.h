@@ -2,9 +2,15 @@
  * cmpext3_attn.h -- C ABI of the MI355X (gfx950) fused attention forward.
  *
  * One entry point computes O = softmax(scale * Q K^T [+ causal mask]) V for
- * [B, H, S, D] tensors that already live in device memory.  It allocates
- * nothing: the caller owns every buffer, including the output.  All launches
- * go on the stream the caller passes.
+ * [B, H, S, D] tensors that already live in device memory.  The caller owns
+ * every input and output buffer.  The library itself keeps one exchange
+ * buffer per (device, stream) for launches that split key ranges across
+ * workgroups (fp16/bf16, non-causal, D <= 128, when the query blocks do not
+ * fill whole rounds of the GPU): allocated with hipMalloc on the first such
+ * launch on that stream (about 70 KB per CU), kept until the process ends.
+ * On a stream under graph capture, after a failed allocation, or past 16
+ * streams per device those launches run without the split, with the same
+ * results.  All launches go on the stream the caller passes.
  *
  * Reference interfaces this replaces (WifiLast/torch-cmp-patch):
  *   - launch_flash_attention_hfma2(q, k, v, o, B, H, Sq, Sk, D, qs, ks, vs, os,
@@ -62,7 +68,8 @@ extern "C" {
  *
  * Returns CMPEXT3_OK, or one of the CMPEXT3_E_* codes above, in which case
  * nothing was launched except for CMPEXT3_E_LAUNCH.  B*H*Sq == 0 is a no-op.
- * Thread-safe; no host synchronisation.
+ * Thread-safe; no host synchronisation (the first split launch on a stream
+ * allocates its exchange buffer and queues a clear of its counters on it).
  */
 int cmpext3_attn_fwd(const void* q, const void* k, const void* v, void* o,
                      int dtype, int B, int H, int Sq, int Sk, int D,
