@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define CMPEXT3_ATTN_ABI_VERSION 1
+#define CMPEXT3_ATTN_ABI_VERSION 2
 
 /* dtype codes */
 #define CMPEXT3_DTYPE_F16  0
@@ -76,6 +76,24 @@ int cmpext3_attn_fwd(const void* q, const void* k, const void* v, void* o,
                      const int64_t q_str[3], const int64_t k_str[3],
                      const int64_t v_str[3], const int64_t o_str[3],
                      float scale, int causal, hipStream_t stream);
+
+/*
+ * Grouped-query attention: as cmpext3_attn_fwd, with k and v holding H_kv
+ * heads ([B, H_kv, Sk, D]) shared by groups of H / H_kv consecutive query
+ * heads (query head h reads K/V head h / (H / H_kv)), the torch
+ * scaled_dot_product_attention(..., enable_gqa=True) semantics.  H_kv must
+ * divide H (else CMPEXT3_E_INVALID); H_kv == H is cmpext3_attn_fwd.
+ *
+ * Reference: the reference's patch hands enable_gqa only to stock torch
+ * (cmpext3/__init__.py:632-633) and its kernels require equal head counts
+ * (src/main.cpp:1603-1774), so GQA calls always left the native path; this
+ * entry point keeps them on it without repeating K/V per query head.
+ */
+int cmpext3_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o,
+                         int dtype, int B, int H, int H_kv, int Sq, int Sk, int D,
+                         const int64_t q_str[3], const int64_t k_str[3],
+                         const int64_t v_str[3], const int64_t o_str[3],
+                         float scale, int causal, hipStream_t stream);
 
 /* Human-readable text for a return code (static storage). */
 const char* cmpext3_attn_strerror(int code);

@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version_and_messages():
-    assert abi.lib().cmpext3_attn_abi_version() == 1
+    assert abi.lib().cmpext3_attn_abi_version() == 2
     for code in range(8):
         assert abi.strerror(code) and abi.strerror(code) != "unknown error code"
     assert abi.strerror(99) == "unknown error code"
@@ -106,3 +106,22 @@ def test_rejections_before_launch():
 def test_empty_problem_is_a_noop_even_without_pointers():
     assert _call(q=0, k=0, v=0, o=0, Sq=0) == abi.OK
     assert _call(q=0, k=0, v=0, o=0, B=0) == abi.OK
+
+
+def _call_gqa(H=4, H_kv=2, q=16, dtype=abi.DTYPE_F16, B=1, Sq=8, Sk=8, D=64):
+    st = (ctypes.c_int64 * 3)(2048, 512, 64)
+    return abi.lib().cmpext3_attn_fwd_gqa(ctypes.c_void_p(q), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                          ctypes.c_void_p(16), dtype, B, H, H_kv, Sq, Sk, D,
+                                          st, st, st, st, ctypes.c_float(0.125), 0, None)
+
+
+def test_gqa_head_counts_are_checked_before_launch():
+    """K/V head count must divide the query head count; checked after the
+    shape checks and before any launch (fake addresses, no GPU touched)."""
+    assert _call_gqa(H=4, H_kv=3, q=0) == abi.E_INVALID
+    assert _call_gqa(H=4, H_kv=3) == abi.E_INVALID
+    assert _call_gqa(H=4, H_kv=0) == abi.E_INVALID
+    assert _call_gqa(H=4, H_kv=8) == abi.E_INVALID
+    assert _call_gqa(H=4, H_kv=-1) == abi.E_INVALID
+    assert _call_gqa(H=4, H_kv=2, dtype=9) == abi.E_DTYPE
+    assert _call_gqa(H=4, H_kv=2, Sq=0, q=0) == abi.OK   # empty problem

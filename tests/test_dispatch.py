@@ -202,6 +202,21 @@ class TestScaledDotProductAttention:
         q, k, v = _qkv(1, 2, 3, 4)
         assert F.scaled_dot_product_attention(q, k, v).shape == q.shape
 
+    def test_gqa_runs_native_only_with_enable_gqa(self, patched, native, monkeypatch):
+        """K/V with fewer heads than Q: native (positional call, the kernel reads
+        the grouping from the shapes) under enable_gqa=True; stock otherwise,
+        where torch raises its own head-count error."""
+        force_eligible(monkeypatch)
+        q = torch.randn(1, 4, 3, 8)
+        k, v = torch.randn(1, 2, 3, 8), torch.randn(1, 2, 3, 8)
+        native.attention.return_value = "native-result"
+        assert F.scaled_dot_product_attention(q, k, v, enable_gqa=True) == "native-result"
+        _called_once_with_tensors(native.attention, q, k, v, None, False)
+        native.attention.reset_mock()
+        with pytest.raises(RuntimeError):
+            F.scaled_dot_product_attention(q, k, v)
+        native.attention.assert_not_called()
+
     def test_extra_kwargs_reach_only_stock(self, patched, native, monkeypatch):
         force_eligible(monkeypatch)
         native.attention.side_effect = RuntimeError("gqa head count")

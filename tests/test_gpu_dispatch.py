@@ -96,11 +96,12 @@ def test_reference_fallbacks_do_not_reach_native(patched, counting_native):
 
 def test_native_rejections_fall_back_to_correct_stock_results(patched):
     q = torch.randn(1, 4, 32, 64, dtype=torch.float16, device="cuda")
-    kv = torch.randn(1, 2, 32, 64, dtype=torch.float16, device="cuda")
+    k = torch.randn(1, 4, 32, 64, dtype=torch.float16, device="cuda")
+    v32 = torch.randn(1, 4, 32, 32, dtype=torch.float16, device="cuda")
     with torch.inference_mode():
-        out = F.scaled_dot_product_attention(q, kv, kv, enable_gqa=True)   # H_kv < H
-        want = cmpext3._ORIGINALS[(F, "scaled_dot_product_attention")](q, kv, kv, enable_gqa=True)
-        assert torch.allclose(out, want)
+        out = F.scaled_dot_product_attention(q, k, v32)                     # Dv != D
+        want = cmpext3._ORIGINALS[(F, "scaled_dot_product_attention")](q, k, v32)
+        assert torch.equal(out, want)
         empty = torch.randn(1, 4, 0, 64, dtype=torch.float16, device="cuda")
         out = F.scaled_dot_product_attention(q, empty, empty)                # Sk = 0
         assert torch.count_nonzero(out) == 0

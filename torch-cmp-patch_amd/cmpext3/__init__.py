@@ -142,9 +142,11 @@ def _patched_sdpa(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=Fa
     """F.scaled_dot_product_attention replacement (reference: cmpext3/__init__.py:609-633).
 
     Bails to stock for attn_mask, dropout, non-4D query, live autograd and
-    non-GPU / unsupported dtypes.  Extra keyword arguments (e.g. enable_gqa)
-    reach only the stock call; the native op sees (q, k, v, scale, is_causal)
-    positionally and rejects shapes it does not support.
+    non-GPU / unsupported dtypes.  Extra keyword arguments reach only the stock
+    call; the native op sees (q, k, v, scale, is_causal) positionally and
+    rejects shapes it does not support.  Grouped-query calls (K/V with fewer
+    heads than Q) run natively only under enable_gqa=True, as torch requires;
+    without it they go to stock, which raises torch's own error.
     """
     orig = _ORIGINALS[(F, "scaled_dot_product_attention")]
 
@@ -156,6 +158,9 @@ def _patched_sdpa(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=Fa
             or not isinstance(query, torch.Tensor) or query.dim() != 4
             or not _grad_safe(query, key, value)
             or not _usable(query, key, value)):
+        return stock()
+    if (isinstance(key, torch.Tensor) and key.dim() == 4 and key.shape[1] != query.shape[1]
+            and not kwargs.get("enable_gqa", False)):
         return stock()
     return _dispatch("attention", query,
                      (query.shape, query.dtype, key.shape, value.shape, scale, is_causal),

@@ -13,8 +13,8 @@ from typing import Optional
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcmpext3_attn.so")
 
 # Every function include/cmpext3_attn.h declares.
-SYMBOLS = ("cmpext3_attn_fwd", "cmpext3_attn_strerror", "cmpext3_attn_abi_version",
-           "cmpext3_attn_describe")
+SYMBOLS = ("cmpext3_attn_fwd", "cmpext3_attn_fwd_gqa", "cmpext3_attn_strerror",
+           "cmpext3_attn_abi_version", "cmpext3_attn_describe")
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
 OK, E_INVALID, E_DTYPE, E_HEAD_DIM, E_ALIGN, E_EMPTY_KEYS, E_LAUNCH, E_TOO_LARGE = range(8)
@@ -34,6 +34,9 @@ def lib() -> ctypes.CDLL:
         L.cmpext3_attn_fwd.argtypes = [vp, vp, vp, vp, ci, ci, ci, ci, ci, ci,
                                        i64p, i64p, i64p, i64p, ctypes.c_float, ci, vp]
         L.cmpext3_attn_fwd.restype = ci
+        L.cmpext3_attn_fwd_gqa.argtypes = [vp, vp, vp, vp, ci, ci, ci, ci, ci, ci, ci,
+                                           i64p, i64p, i64p, i64p, ctypes.c_float, ci, vp]
+        L.cmpext3_attn_fwd_gqa.restype = ci
         L.cmpext3_attn_strerror.argtypes = [ci]
         L.cmpext3_attn_strerror.restype = ctypes.c_char_p
         L.cmpext3_attn_abi_version.argtypes = []
@@ -66,7 +69,8 @@ def _strides(t):
 
 def attn_fwd_raw(q, k, v, o, scale: float, causal: bool = False, stream=None,
                  D: Optional[int] = None) -> int:
-    """Call cmpext3_attn_fwd on [B,H,S,D] tensors (any strides with unit last stride).
+    """Call cmpext3_attn_fwd on [B,H,S,D] tensors (any strides with unit last stride),
+    or cmpext3_attn_fwd_gqa when k/v hold fewer heads than q (grouped-query).
     Returns the C return code; launches on `stream` (a torch.cuda.Stream, a raw
     handle, or None for the current stream)."""
     import torch
@@ -77,12 +81,15 @@ def attn_fwd_raw(q, k, v, o, scale: float, causal: bool = False, stream=None,
     else:
         handle = stream.cuda_stream
     B, H, Sq, Dq = q.shape
-    return lib().cmpext3_attn_fwd(
-        ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()),
-        ctypes.c_void_p(v.data_ptr()), ctypes.c_void_p(o.data_ptr()),
-        dtype_code(q.dtype), B, H, Sq, k.shape[2], Dq if D is None else D,
-        _strides(q), _strides(k), _strides(v), _strides(o),
-        ctypes.c_float(scale), int(causal), ctypes.c_void_p(handle))
+    ptrs = (ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()),
+            ctypes.c_void_p(v.data_ptr()), ctypes.c_void_p(o.data_ptr()))
+    tail = (_strides(q), _strides(k), _strides(v), _strides(o),
+            ctypes.c_float(scale), int(causal), ctypes.c_void_p(handle))
+    Dx = Dq if D is None else D
+    if k.shape[1] != H:
+        return lib().cmpext3_attn_fwd_gqa(*ptrs, dtype_code(q.dtype), B, H, k.shape[1], Sq,
+                                          k.shape[2], Dx, *tail)
+    return lib().cmpext3_attn_fwd(*ptrs, dtype_code(q.dtype), B, H, Sq, k.shape[2], Dx, *tail)
 
 
 def attn_fwd(q, k, v, scale: Optional[float] = None, causal: bool = False, stream=None):

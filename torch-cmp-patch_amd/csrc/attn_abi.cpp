@@ -107,15 +107,24 @@ int cmpext3_attn_fwd(const void* q, const void* k, const void* v, void* o, int d
                      int Sq, int Sk, int D, const int64_t q_str[3], const int64_t k_str[3],
                      const int64_t v_str[3], const int64_t o_str[3], float scale, int causal,
                      hipStream_t stream) {
+  return cmpext3_attn_fwd_gqa(q, k, v, o, dtype, B, H, H, Sq, Sk, D, q_str, k_str, v_str, o_str, scale,
+                              causal, stream);
+}
+
+int cmpext3_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o, int dtype, int B,
+                         int H, int H_kv, int Sq, int Sk, int D, const int64_t q_str[3],
+                         const int64_t k_str[3], const int64_t v_str[3], const int64_t o_str[3],
+                         float scale, int causal, hipStream_t stream) {
   int rc = check_shape(dtype, B, H, Sq, Sk, D);
   if (rc != CMPEXT3_OK) return rc;
   if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;
+  if (H_kv < 1 || H_kv > H || H % H_kv != 0) return CMPEXT3_E_INVALID;
   if (!q || !k || !v || !o || !q_str || !k_str || !v_str || !o_str) return CMPEXT3_E_INVALID;
   if (!isfinite(scale)) return CMPEXT3_E_INVALID;
   const int es = elem_size(dtype);
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return CMPEXT3_E_ALIGN;
-  if (!stride_ok(q_str, B, H, Sq, es) || !stride_ok(k_str, B, H, Sk, es) ||
-      !stride_ok(v_str, B, H, Sk, es) || !stride_ok(o_str, B, H, Sq, es))
+  if (!stride_ok(q_str, B, H, Sq, es) || !stride_ok(k_str, B, H_kv, Sk, es) ||
+      !stride_ok(v_str, B, H_kv, Sk, es) || !stride_ok(o_str, B, H, Sq, es))
     return CMPEXT3_E_ALIGN;
   // the fp16/bf16 kernel addresses one K/V tile with 32-bit element offsets
   if (dtype != CMPEXT3_DTYPE_F32 &&
@@ -130,6 +139,7 @@ int cmpext3_attn_fwd(const void* q, const void* k, const void* v, void* o, int d
   p.v_b = v_str[0]; p.v_h = v_str[1]; p.v_s = v_str[2];
   p.o_b = o_str[0]; p.o_h = o_str[1]; p.o_s = o_str[2];
   p.B = B; p.H = H; p.Sq = Sq; p.Sk = Sk; p.D = D;
+  p.kv_group = H / H_kv;  // query head h reads K/V head h / kv_group
   // exp2-domain multiplier; a negative scale is folded into Q's sign bits
   p.c = fabsf(scale) * cmpext3::kLog2e;
   p.q_sign = (scale < 0.f) ? (dtype == CMPEXT3_DTYPE_F32 ? 0x80000000u : 0x80008000u) : 0u;

@@ -25,6 +25,7 @@ struct FwdParams {
   int64_t v_b, v_h, v_s;
   int64_t o_b, o_h, o_s;
   int B, H, Sq, Sk, D;
+  int kv_group;     // query heads per K/V head (grouped-query attention; 1 = none)
   int n_qblk;       // query blocks per (batch, head)
   int n_wg;         // workgroups launched = B * H * n_qblk
   float c;          // |scale| * log2(e): scores enter exp2 as s * c - m

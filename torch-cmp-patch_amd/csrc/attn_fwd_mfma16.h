@@ -164,8 +164,8 @@ attn_fwd_mfma16(const FwdParams p) {
   const int q0 = qblk * BQ;
 
   const uint16_t* __restrict__ qg = (const uint16_t*)p.q + b * p.q_b + h * p.q_h;
-  const uint16_t* kg = (const uint16_t*)p.k + b * p.k_b + h * p.k_h;
-  const uint16_t* vg = (const uint16_t*)p.v + b * p.v_b + h * p.v_h;
+  const uint16_t* kg = (const uint16_t*)p.k + b * p.k_b + (h / p.kv_group) * p.k_h;
+  const uint16_t* vg = (const uint16_t*)p.v + b * p.v_b + (h / p.kv_group) * p.v_h;
   uint16_t* __restrict__ og = (uint16_t*)p.o + b * p.o_b + h * p.o_h;
 
   const int Sq = p.Sq, Sk = p.Sk, D = p.D;

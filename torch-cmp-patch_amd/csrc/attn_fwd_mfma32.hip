@@ -60,8 +60,8 @@ attn_fwd_mfma32(const FwdParams p) {
   const int q0 = qblk * BQ;
 
   const float* __restrict__ qg = (const float*)p.q + b * p.q_b + h * p.q_h;
-  const float* __restrict__ kg = (const float*)p.k + b * p.k_b + h * p.k_h;
-  const float* __restrict__ vg = (const float*)p.v + b * p.v_b + h * p.v_h;
+  const float* __restrict__ kg = (const float*)p.k + b * p.k_b + (h / p.kv_group) * p.k_h;
+  const float* __restrict__ vg = (const float*)p.v + b * p.v_b + (h / p.kv_group) * p.v_h;
   float* __restrict__ og = (float*)p.o + b * p.o_b + h * p.o_h;
 
   const int Sq = p.Sq, Sk = p.Sk, D = p.D;

@@ -30,9 +30,9 @@
 // proves they all are, exactly what the max-first rule (rescale when the tile
 // max exceeds m by more than 8 log2 units) would have accepted without a
 // rescale.  A larger sum (rare) sends the wave to the exact path: tile max,
-// rescale of O and l if it exceeds m + 8, tile redone.  Results equal the
-// max-first scheme's; the per-score max and the cross-lane reduction leave
-// the common path.
+// rescale of O and l if it exceeds m + 8, tile redone.  Every rescale
+// decision equals the max-first scheme's; the per-score max and the
+// cross-lane reduction leave the common path.
 //
 // Key split.  When the query blocks do not fill whole rounds of the chip
 // (e.g. 640 blocks on 256 CUs x 3 slots: 128 CUs would run 3 and 128 run 2),
@@ -123,8 +123,8 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   const int q0 = qblk * BQ;
 
   const uint16_t* __restrict__ qg = (const uint16_t*)p.q + b * p.q_b + h * p.q_h;
-  const uint16_t* kg = (const uint16_t*)p.k + b * p.k_b + h * p.k_h;
-  const uint16_t* vg = (const uint16_t*)p.v + b * p.v_b + h * p.v_h;
+  const uint16_t* kg = (const uint16_t*)p.k + b * p.k_b + (h / p.kv_group) * p.k_h;
+  const uint16_t* vg = (const uint16_t*)p.v + b * p.v_b + (h / p.kv_group) * p.v_h;
   uint16_t* __restrict__ og = (uint16_t*)p.o + b * p.o_b + h * p.o_h;
 
   const int Sq = p.Sq, Sk = p.Sk, D = p.D;
@@ -477,7 +477,7 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
 
   // ---- epilogue
   float lsum = xhalf_sum(ls0 + ls1);
-  if (nparts > 1) {
+  if (!CAUSAL && nparts > 1) {  // causal launches never split
     // Leave this part's state, then let the last part of the block merge.
     // Device-scope (sc1) stores and loads keep the exchange coherent across
     // the XCDs' L2s without cache-wide write-back or invalidation.
@@ -486,34 +486,44 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
     const int sb = lb - sa.nfull;
     const __amdgpu_buffer_rsrc_t wsr = uniform_rsrc(sa.ws, (int64_t)(sb + 1) * nparts * NW * NV * 64 * 16);
     auto voff = [&](int q, int k) { return ((((sb * nparts + q) * NW + wave) * NV + k) * 64 + lane) * 16; };
+    // device-scope (aux 16 = sc1) 16-byte accesses; the builtins move dwords, so the
+    // fp32 values go through explicit bit casts
+    auto st_ws = [&](f32x4 x, int off) {
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), wsr, off, 0, 16);
+    };
+    auto ld_ws = [&](int off) { return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wsr, off, 0, 16)); };
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int g = 0; g < 4; ++g)
-        __builtin_amdgcn_raw_buffer_store_b128(
-            (f32x4){oacc[db][4 * g], oacc[db][4 * g + 1], oacc[db][4 * g + 2], oacc[db][4 * g + 3]}, wsr,
-            voff(part, db * 4 + g), 0, 16);
-    __builtin_amdgcn_raw_buffer_store_b128((f32x4){mb, lsum, 0.f, 0.f}, wsr, voff(part, NDB * 4), 0, 16);
+        st_ws((f32x4){oacc[db][4 * g], oacc[db][4 * g + 1], oacc[db][4 * g + 2], oacc[db][4 * g + 3]},
+              voff(part, db * 4 + g));
+    st_ws((f32x4){mb, lsum, 0.f, 0.f}, voff(part, NDB * 4));
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     int old = 0;
     if (lane == 0) old = __hip_atomic_fetch_add(sa.cnt + sb * NW + wave, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     old = __builtin_amdgcn_readfirstlane(old);
     if (old != nparts - 1) return;
     if (lane == 0) __hip_atomic_store(sa.cnt + sb * NW + wave, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Merge every part, this one included, from the exchange buffer in part
+    // order: the same instructions on the same values whichever part arrives
+    // last, so a rerun is bit-identical.
+    float mt = -INFINITY;
+    for (int q = 0; q < nparts; ++q) mt = fmaxf(mt, ld_ws(voff(q, NDB * 4))[0]);
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) oacc[db] = (f32x16){};
+    lsum = 0.f;
     for (int q = 0; q < nparts; ++q) {
-      if (q == part) continue;
-      const f32x4 ml = __builtin_amdgcn_raw_buffer_load_b128(wsr, voff(q, NDB * 4), 0, 16);
-      const float m = fmaxf(mb, ml[0]);
-      const float a = fast_exp2(mb - m), bq = fast_exp2(ml[0] - m);
-      lsum = lsum * a + ml[1] * bq;
-      mb = m;
+      const f32x4 ml = ld_ws(voff(q, NDB * 4));
+      const float a = fast_exp2(ml[0] - mt);
+      lsum = __builtin_fmaf(ml[1], a, lsum);
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const f32x4 x = __builtin_amdgcn_raw_buffer_load_b128(wsr, voff(q, db * 4 + g), 0, 16);
+          const f32x4 x = ld_ws(voff(q, db * 4 + g));
 #pragma unroll
-          for (int i = 0; i < 4; ++i) oacc[db][4 * g + i] = oacc[db][4 * g + i] * a + x[i] * bq;
+          for (int i = 0; i < 4; ++i) oacc[db][4 * g + i] = __builtin_fmaf(x[i], a, oacc[db][4 * g + i]);
         }
     }
   }

@@ -43,9 +43,9 @@ int launch(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& 
   const int64_t os[3] = {o.stride(0), o.stride(1), o.stride(2)};
   if (q.stride(3) != 1 || k.stride(3) != 1 || v.stride(3) != 1 || o.stride(3) != 1)
     return CMPEXT3_E_ALIGN;
-  return cmpext3_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dtype,
-                          (int)q.size(0), (int)q.size(1), (int)q.size(2), (int)k.size(2), D, qs,
-                          ks, vs, os, scale, causal ? 1 : 0, stream);
+  return cmpext3_attn_fwd_gqa(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dtype,
+                              (int)q.size(0), (int)q.size(1), (int)k.size(1), (int)q.size(2),
+                              (int)k.size(2), D, qs, ks, vs, os, scale, causal ? 1 : 0, stream);
 }
 
 bool is_bshd_view(const torch::Tensor& t) {
@@ -72,10 +72,13 @@ torch::Tensor attention(torch::Tensor query, torch::Tensor key, torch::Tensor va
   TORCH_CHECK(dtype >= 0, "cmpext3 attention: unsupported dtype ", query.scalar_type());
 
   const int64_t B = query.size(0), H = query.size(1), Sq = query.size(2), D = query.size(3);
-  const int64_t Sk = key.size(2);
-  TORCH_CHECK(key.size(0) == B && key.size(1) == H && key.size(3) == D,
+  const int64_t Sk = key.size(2), Hkv = key.size(1);
+  // K/V may hold fewer heads than Q when that count divides H (grouped-query
+  // attention, torch's enable_gqa semantics: query head h uses K/V head
+  // h / (H / Hkv)); the Python patch only sends such calls with enable_gqa.
+  TORCH_CHECK(key.size(0) == B && key.size(3) == D && (Hkv == H || (Hkv >= 1 && H % Hkv == 0)),
               "cmpext3 attention: key shape mismatch");
-  TORCH_CHECK(value.size(0) == B && value.size(1) == H && value.size(2) == Sk && value.size(3) == D,
+  TORCH_CHECK(value.size(0) == B && value.size(1) == Hkv && value.size(2) == Sk && value.size(3) == D,
               "cmpext3 attention: value shape mismatch");
   TORCH_CHECK(D >= 1 && D <= 256, "cmpext3 attention: head dim ", D, " outside 1..256");
   TORCH_CHECK(Sk > 0 || B * H * Sq == 0, "cmpext3 attention: empty key sequence");
