@@ -38,12 +38,13 @@
 extern "C" {
 #endif
 
-#define CMPEXT3_ATTN_ABI_VERSION 2
+#define CMPEXT3_ATTN_ABI_VERSION 3
 
-/* dtype codes */
+/* dtype codes (CMPEXT3_DTYPE_BOOL: attention masks only) */
 #define CMPEXT3_DTYPE_F16  0
 #define CMPEXT3_DTYPE_BF16 1
 #define CMPEXT3_DTYPE_F32  2
+#define CMPEXT3_DTYPE_BOOL 3
 
 /* return codes */
 #define CMPEXT3_OK                 0
@@ -54,6 +55,7 @@ extern "C" {
 #define CMPEXT3_E_EMPTY_KEYS       5  /* Sk == 0 with Sq > 0: softmax over nothing */
 #define CMPEXT3_E_LAUNCH           6  /* the HIP launch itself failed */
 #define CMPEXT3_E_TOO_LARGE        7  /* a size does not fit the kernel's index arithmetic */
+#define CMPEXT3_E_MASK             8  /* attention mask with fp32 q, D > 128 or causal */
 
 /*
  * Fused attention forward.
@@ -94,6 +96,36 @@ int cmpext3_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o,
                          const int64_t q_str[3], const int64_t k_str[3],
                          const int64_t v_str[3], const int64_t o_str[3],
                          float scale, int causal, hipStream_t stream);
+
+/*
+ * Attention with an explicit mask: as cmpext3_attn_fwd_gqa, plus torch's
+ * scaled_dot_product_attention attn_mask.
+ *
+ *   mask       : device pointer, 16-byte aligned.
+ *   mask_dtype : CMPEXT3_DTYPE_BOOL (one byte per element; non-zero keeps the
+ *                (query, key) pair, zero drops it) or CMPEXT3_DTYPE_F16 /
+ *                _BF16 / _F32 (added to scale * Q K^T, -inf drops the pair);
+ *                -1 means no mask (then mask and mask_str are ignored).
+ *   mask_str[3]: element strides of the mask over {batch, head, query}
+ *                (0 = broadcast, otherwise multiples of 4); keys are
+ *                contiguous (stride 1).  Element (b, h, i, j) lives at
+ *                mask + b*mask_str[0] + h*mask_str[1] + i*mask_str[2] + j.
+ *                Keys are read in runs of 8: every row must be readable up
+ *                to Sk rounded up to a multiple of 8 (values past Sk are
+ *                ignored).
+ * A query row whose keys are all dropped gives zeros (torch's result).
+ * Supported for f16/bf16 q/k/v with D <= 128 and causal == 0; other calls
+ * return CMPEXT3_E_MASK and launch nothing.
+ *
+ * Reference: the reference never ran masks natively: _patched_sdpa sends
+ * any attn_mask to stock torch (cmpext3/__init__.py:624).
+ */
+int cmpext3_attn_fwd_masked(const void* q, const void* k, const void* v, void* o,
+                            int dtype, int B, int H, int H_kv, int Sq, int Sk, int D,
+                            const int64_t q_str[3], const int64_t k_str[3],
+                            const int64_t v_str[3], const int64_t o_str[3],
+                            const void* mask, int mask_dtype, const int64_t mask_str[3],
+                            float scale, int causal, hipStream_t stream);
 
 /* Human-readable text for a return code (static storage). */
 const char* cmpext3_attn_strerror(int code);

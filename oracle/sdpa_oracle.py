@@ -20,7 +20,14 @@ Reference behaviour restated (WifiLast/torch-cmp-patch):
   - causal for Sq != Sk is top-left aligned (key j visible to query i iff
     j <= i), which is torch's is_causal convention;
   - max-abs error bar and the fp32-upcast oracle: tools/dev_flash_attn.py:24-27.
-Rows with no visible key (Sk == 0) give zeros, as torch's math SDPA does.
+Rows with no visible key (Sk == 0, or every key masked out) give zeros, as
+torch's math SDPA does (torch 2.10 CPU, pinned in tests/test_oracle.py).
+
+attn_mask (sdpa_np, sdpa_loops): torch's scaled_dot_product_attention rule --
+a bool mask keeps the (query, key) pairs where it is True, a float mask is
+added to scale * Q K^T; either broadcasts to [B, H, Sq, Sk].  The reference
+never ran masks natively (cmpext3/__init__.py:624 sends them to stock torch),
+so the restated behaviour is torch's.
 """
 from __future__ import annotations
 
@@ -56,8 +63,35 @@ def causal_visible(sq: int, sk: int) -> np.ndarray:
     return np.tril(np.ones((sq, sk), dtype=bool))
 
 
+def _mask_4d(mask, B, H, Sq, Sk):
+    """attn_mask as a read-only [B, H, Sq, Sk] view: bool (keep where True) or
+    float64 (additive), broadcast like torch's SDPA."""
+    if mask is None:
+        return None
+    try:
+        import torch
+        if isinstance(mask, torch.Tensor):
+            mask = (mask.detach().cpu().numpy() if mask.dtype == torch.bool
+                    else mask.detach().to("cpu", torch.float64).numpy())
+    except ImportError:  # pragma: no cover
+        pass
+    mask = np.asarray(mask)
+    if mask.dtype != np.bool_:
+        mask = mask.astype(np.float64)
+    return np.broadcast_to(mask, (B, H, Sq, Sk))
+
+
+def _apply_mask(s, m):
+    """scores s with mask slice m (bool keep / float additive)."""
+    if m is None:
+        return s
+    if m.dtype == np.bool_:
+        return np.where(m, s, -np.inf)
+    return s + m
+
+
 def sdpa_np(q, k, v, scale: Optional[float] = None, causal: bool = False,
-            block: int = 512) -> np.ndarray:
+            block: int = 512, attn_mask=None) -> np.ndarray:
     """float64 SDPA over [B, H, S, D] arrays or tensors, blocked over query rows."""
     q, k, v = _as_f64(q), _as_f64(k), _as_f64(v)
     B, H, Sq, D = q.shape
@@ -69,6 +103,7 @@ def sdpa_np(q, k, v, scale: Optional[float] = None, causal: bool = False,
     if Sk == 0:
         out[...] = 0.0
         return out
+    mask = _mask_4d(attn_mask, B, H, Sq, Sk)
     for b in range(B):
         for h in range(H):
             kt = k[b, h].T
@@ -78,10 +113,16 @@ def sdpa_np(q, k, v, scale: Optional[float] = None, causal: bool = False,
                 if causal:
                     vis = causal_visible(Sq, Sk)[i0:i1]
                     s = np.where(vis, s, -np.inf)
+                if mask is not None:
+                    s = _apply_mask(s, mask[b, h, i0:i1])
                 m = s.max(axis=1, keepdims=True)
+                dead = ~np.isfinite(m) & (m < 0)          # no visible key in the row
+                m = np.where(dead, 0.0, m)
                 with np.errstate(invalid="ignore"):
                     e = np.exp(s - m)
-                    out[b, h, i0:i1] = (e @ v[b, h]) / e.sum(axis=1, keepdims=True)
+                    z = e.sum(axis=1, keepdims=True)
+                    o = (e @ v[b, h]) / np.where(dead, 1.0, z)
+                out[b, h, i0:i1] = np.where(dead, 0.0, o)
     return out
 
 
@@ -128,22 +169,30 @@ def sdpa_c(q, k, v, scale: Optional[float] = None, causal: bool = False) -> np.n
     return out
 
 
-def sdpa_loops(q, k, v, scale: Optional[float] = None, causal: bool = False) -> np.ndarray:
+def sdpa_loops(q, k, v, scale: Optional[float] = None, causal: bool = False,
+               attn_mask=None) -> np.ndarray:
     """Pure-Python brute force (tiny inputs only)."""
     q, k, v = _as_f64(q), _as_f64(k), _as_f64(v)
     B, H, Sq, D = q.shape
     Sk, Dv = k.shape[2], v.shape[3]
     if scale is None:
         scale = default_scale(D)
+    mask = _mask_4d(attn_mask, B, H, Sq, Sk)
     out = np.empty((B, H, Sq, Dv), dtype=np.float64)
     for b in range(B):
         for h in range(H):
             for i in range(Sq):
-                keys = [j for j in range(Sk) if not causal or j <= i]
+                def add(j):
+                    if mask is None or mask.dtype == np.bool_:
+                        return 0.0
+                    return float(mask[b, h, i, j])
+                keys = [j for j in range(Sk) if (not causal or j <= i)
+                        and (mask is None or mask.dtype != np.bool_ or bool(mask[b, h, i, j]))
+                        and add(j) != -math.inf]
                 if not keys:
                     out[b, h, i, :] = 0.0
                     continue
-                s = [scale * sum(float(q[b, h, i, d]) * float(k[b, h, j, d]) for d in range(D))
+                s = [scale * sum(float(q[b, h, i, d]) * float(k[b, h, j, d]) for d in range(D)) + add(j)
                      for j in keys]
                 m = max(s)
                 w = [math.exp(x - m) for x in s]

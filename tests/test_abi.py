@@ -38,8 +38,8 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version_and_messages():
-    assert abi.lib().cmpext3_attn_abi_version() == 2
-    for code in range(8):
+    assert abi.lib().cmpext3_attn_abi_version() == 3
+    for code in range(9):
         assert abi.strerror(code) and abi.strerror(code) != "unknown error code"
     assert abi.strerror(99) == "unknown error code"
 

@@ -153,12 +153,23 @@ class TestScaledDotProductAttention:
         assert F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=0.3) == "native-result"
         _called_once_with_tensors(native.attention, q, k, v, 0.3, True)
 
-    def test_falls_back_when_attn_mask_given(self, patched, native, monkeypatch):
+    def test_attn_mask_goes_native_as_sixth_argument(self, patched, native, monkeypatch):
+        """The reference sent every attn_mask to stock (its cmpext3/__init__.py:624);
+        here bool/float masks without is_causal reach the kernel, positionally."""
         force_eligible(monkeypatch)
         q, k, v = _qkv(1, 2, 3, 4)
-        out = F.scaled_dot_product_attention(q, k, v, attn_mask=torch.zeros(3, 3, dtype=torch.bool))
+        mask = torch.zeros(3, 3, dtype=torch.bool)
+        native.attention.return_value = "native-result"
+        assert F.scaled_dot_product_attention(q, k, v, attn_mask=mask) == "native-result"
+        _called_once_with_tensors(native.attention, q, k, v, None, False, mask)
+
+    def test_falls_back_for_mask_with_causal(self, patched, native, monkeypatch):
+        force_eligible(monkeypatch)
+        q, k, v = _qkv(1, 2, 3, 4)
+        mask = torch.ones(3, 3, dtype=torch.bool)
+        out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, is_causal=True)
         native.attention.assert_not_called()
-        assert out.shape == q.shape
+        assert torch.allclose(out, STOCK_SDPA(q, k, v, attn_mask=mask, is_causal=True))
 
     def test_falls_back_when_dropout_nonzero(self, patched, native, monkeypatch):
         force_eligible(monkeypatch)

@@ -1,0 +1,163 @@
+"""GPU parity of attention with an explicit attn_mask (torch SDPA semantics).
+
+A bool mask keeps the (query, key) pairs where it is True; a float mask
+(f16/bf16/f32) is added to scale * Q K^T, -inf dropping the pair; masks
+broadcast to [B, H, Sq, Sk]; a row whose keys are all dropped gives zeros.
+Checked through the C ABI (cmpext3_attn_fwd_masked) and through
+F.scaled_dot_product_attention against the float64 oracle with the same mask
+(oracle/sdpa_oracle.py sdpa_np, pinned to torch in tests/test_oracle.py), at
+the usual bar: max abs error <= 1e-2 fp16, 2e-2 bf16.
+
+Shapes cover short key sweeps (the pipelined kernel takes every masked call),
+odd tile counts, the key split (parts of a row merge masked partials, some of
+them empty), grouped-query K/V, head dims below their bucket, and mask
+layouts the ABI cannot read in place (transposed, key count not a multiple
+of 4), which the bindings copy.  Unsupported masked calls (fp32, D > 128,
+mask with causal) are rejected by the ABI and fall back to stock in the patch.
+"""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import cmpext3
+from cmpext3 import abi
+from cmpext3 import workloads as W
+from oracle import sdpa_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL = orc.TOLERANCE
+TDT = {"fp16": torch.float16, "bf16": torch.bfloat16}
+
+
+def _inputs(dtype, B, H, Sq, Sk, D, seed, Hkv=None):
+    q = W.Workload("mq", dtype, B, H, Sq, Sk, D, seed=seed).make_inputs("cuda")[0]
+    _, k, v = W.Workload("mk", dtype, B, Hkv or H, Sq, Sk, D, seed=seed + 1).make_inputs("cuda")
+    return q, k, v
+
+
+def _mask(kind, dtype, B, H, Sq, Sk, seed):
+    g = torch.Generator().manual_seed(seed)
+    if kind == "bool_pad":                    # key padding, [B,1,1,Sk]
+        m = torch.ones(B, 1, 1, Sk, dtype=torch.bool)
+        for b in range(B):
+            m[b, ..., Sk - 1 - (17 * (b + 1)) % Sk:] = False
+    elif kind == "bool_full":                 # per (b, h, query), one row fully dropped
+        m = torch.rand(B, H, Sq, Sk, generator=g) > 0.3
+        m[0, 0, min(5, Sq - 1)] = False
+    elif kind == "add_heads":                 # additive, per head, query dtype, some -inf
+        m = (torch.randn(1, H, Sq, Sk, generator=g) * 2).to(TDT[dtype])
+        m[..., ::7] = -math.inf
+    elif kind == "add_2d_f32":                # additive fp32 [Sq, Sk], causal-like -inf band
+        m = torch.randn(Sq, Sk, generator=g)
+        m = m.masked_fill(torch.ones(Sq, Sk, dtype=torch.bool).triu(Sk // 2 + 1), -math.inf)
+    else:
+        raise ValueError(kind)
+    return m.cuda()
+
+
+CASES = [
+    # dtype, B, H, Sq, Sk, D
+    ("fp16", 2, 3, 100, 77, 64),      # short keys
+    ("bf16", 1, 2, 130, 300, 128),    # odd tile count
+    ("fp16", 1, 2, 256, 2048, 64),    # key split, 8 parts
+    ("bf16", 2, 2, 200, 1000, 40),    # D below its bucket, key split
+]
+KINDS = ["bool_pad", "bool_full", "add_heads", "add_2d_f32"]
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}-B{c[1]}H{c[2]}-q{c[3]}k{c[4]}d{c[5]}" for c in CASES])
+def test_mask_parity(case, kind):
+    dtype, B, H, Sq, Sk, D = case
+    q, k, v = _inputs(dtype, B, H, Sq, Sk, D, seed=Sq + Sk)
+    m = _mask(kind, dtype, B, H, Sq, Sk, seed=D)
+    scale = 1.0 / math.sqrt(D)
+    out = abi.attn_fwd(q, k, v, scale, False, attn_mask=m)
+    torch.cuda.synchronize()
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), scale, attn_mask=m.cpu())
+    assert orc.max_abs_err(out.cpu(), ref) <= TOL[dtype]
+
+
+def test_fully_masked_rows_are_zero():
+    q, k, v = _inputs("fp16", 1, 2, 64, 600, 64, seed=3)
+    m = torch.ones(1, 2, 64, 600, dtype=torch.bool, device="cuda")
+    m[:, :, 10] = False                    # whole row dropped (every key-split part empty)
+    m[:, 1, 20, :300] = False              # first half dropped: one part empty, one not
+    out = abi.attn_fwd(q, k, v, 0.125, False, attn_mask=m)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out[:, :, 10]) == 0
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), 0.125, attn_mask=m.cpu())
+    assert orc.max_abs_err(out.cpu(), ref) <= TOL["fp16"]
+
+
+def test_mask_with_grouped_query_heads():
+    q, k, v = _inputs("bf16", 1, 8, 128, 512, 64, seed=9, Hkv=2)
+    m = _mask("bool_full", "bf16", 1, 8, 128, 512, seed=4)
+    out = abi.attn_fwd(q, k, v, 0.125, False, attn_mask=m)
+    torch.cuda.synchronize()
+    kr, vr = k.cpu().repeat_interleave(4, dim=1), v.cpu().repeat_interleave(4, dim=1)
+    ref = orc.sdpa_np(q.cpu(), kr, vr, 0.125, attn_mask=m.cpu())
+    assert orc.max_abs_err(out.cpu(), ref) <= TOL["bf16"]
+
+
+def test_mask_layouts_that_need_a_copy():
+    """A transposed mask view and a key count that is not a multiple of 4."""
+    q, k, v = _inputs("fp16", 1, 2, 96, 301, 64, seed=12)
+    base = torch.randn(2, 301, 96, device="cuda").to(torch.float16)
+    m = base.transpose(1, 2)[None]           # [1, 2, 96, 301], key stride 96
+    assert m.stride(-1) != 1
+    out = abi.attn_fwd(q, k, v, 0.125, False, attn_mask=m)
+    torch.cuda.synchronize()
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), 0.125, attn_mask=m.cpu())
+    assert orc.max_abs_err(out.cpu(), ref) <= TOL["fp16"]
+
+
+def test_unsupported_masked_calls_are_rejected():
+    m = torch.ones(64, 64, dtype=torch.bool, device="cuda")
+    q32 = torch.randn(1, 2, 64, 64, device="cuda")
+    assert abi.attn_fwd_raw(q32, q32, q32, torch.empty_like(q32), 0.125, attn_mask=m) == abi.E_MASK
+    q160 = torch.randn(1, 2, 64, 160, device="cuda").half()
+    assert abi.attn_fwd_raw(q160, q160, q160, torch.empty_like(q160), 0.125, attn_mask=m) == abi.E_MASK
+    q64 = torch.randn(1, 2, 64, 64, device="cuda").half()
+    assert abi.attn_fwd_raw(q64, q64, q64, torch.empty_like(q64), 0.125, True, attn_mask=m) == abi.E_MASK
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_masked_sdpa_runs_native(patched, dtype):
+    q, k, v = _inputs(dtype, 2, 4, 200, 333, 64, seed=21)
+    m = _mask("bool_pad", dtype, 2, 4, 200, 333, seed=1)
+    calls = {"n": 0}
+    real = cmpext3._C
+
+    class Counting:
+        @staticmethod
+        def attention(*args):
+            calls["n"] += 1
+            return real.attention(*args)
+
+    old = cmpext3._C
+    cmpext3._C = Counting
+    try:
+        with torch.inference_mode():
+            out = F.scaled_dot_product_attention(q, k, v, attn_mask=m)
+    finally:
+        cmpext3._C = old
+    torch.cuda.synchronize()
+    assert calls["n"] == 1
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), None, attn_mask=m.cpu())
+    assert orc.max_abs_err(out.cpu(), ref) <= TOL[dtype]
+
+
+def test_unsupported_masked_sdpa_falls_back(patched):
+    """fp32 with a mask: the native op rejects it, stock computes it."""
+    q, k, v = (torch.randn(1, 2, 50, 64, device="cuda") for _ in range(3))
+    m = torch.rand(50, 50, device="cuda") > 0.5
+    with torch.inference_mode():
+        out = F.scaled_dot_product_attention(q, k, v, attn_mask=m)
+        want = cmpext3._ORIGINALS[(F, "scaled_dot_product_attention")](q, k, v, attn_mask=m)
+    assert torch.equal(out, want)

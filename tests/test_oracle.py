@@ -208,3 +208,68 @@ def _pins_pass(fn) -> bool:
 def test_planted_mistakes_are_caught(kind):
     assert _pins_pass(_mutant("none"))          # the unmutated restatement passes
     assert not _pins_pass(_mutant(kind))
+
+
+# ---------------------------------------------------------------------------
+# attn_mask (torch's SDPA rule: bool keeps where True, float is added to the
+# scaled scores; broadcast to [B, H, Sq, Sk]; rows with no visible key -> 0).
+# ---------------------------------------------------------------------------
+
+def _torch_math_masked(q, k, v, scale, mask):
+    with sdpa_kernel(SDPBackend.MATH):
+        return F.scaled_dot_product_attention(q, k, v, attn_mask=mask, scale=scale).numpy()
+
+
+def _masks(B, H, Sq, Sk, seed):
+    g = torch.Generator().manual_seed(seed)
+    full = torch.rand(B, H, Sq, Sk, generator=g) > 0.4
+    full[0, 0, 1] = False                                   # one row sees no key at all
+    pad = torch.ones(B, 1, 1, Sk, dtype=torch.bool)
+    pad[..., Sk // 2:] = False                              # key-padding mask
+    add = torch.randn(1, H, Sq, Sk, generator=g, dtype=torch.float64) * 3
+    add[..., 0] = -math.inf                                 # -inf entries in a float mask
+    rows = torch.randn(Sq, Sk, generator=g, dtype=torch.float64)
+    return {"bool_full": full, "bool_pad": pad, "float_heads": add, "float_2d": rows}
+
+
+@pytest.mark.parametrize("kind", ["bool_full", "bool_pad", "float_heads", "float_2d"])
+def test_masked_oracle_matches_torch_math(kind):
+    q, k, v = _rand(2, 3, 9, 13, 8, seed=41)
+    mask = _masks(2, 3, 9, 13, seed=42)[kind]
+    want = _torch_math_masked(q, k, v, 0.3, mask)
+    assert orc.max_abs_err(orc.sdpa_np(q, k, v, 0.3, attn_mask=mask), want) < 1e-12
+    assert orc.max_abs_err(orc.sdpa_loops(q, k, v, 0.3, attn_mask=mask), want) < 1e-12
+
+
+def test_fully_masked_rows_give_zeros_like_torch():
+    q, k, v = _rand(1, 1, 4, 6, 8, seed=5)
+    mask = torch.ones(4, 6, dtype=torch.bool)
+    mask[2] = False
+    out = orc.sdpa_np(q, k, v, 0.5, attn_mask=mask)
+    assert np.array_equal(out[0, 0, 2], np.zeros(8))
+    assert np.array_equal(out[0, 0, 2], _torch_math_masked(q, k, v, 0.5, mask)[0, 0, 2])
+
+
+def test_mask_identities():
+    """An all-True bool mask or an all-zero float mask changes nothing; a mask
+    that keeps only key j returns V[j]; a constant added to a row's float mask
+    changes nothing."""
+    q, k, v = _rand(1, 2, 5, 7, 8, seed=6)
+    base = orc.sdpa_np(q, k, v, 0.4)
+    assert orc.max_abs_err(orc.sdpa_np(q, k, v, 0.4, attn_mask=torch.ones(5, 7, dtype=torch.bool)), base) < 1e-14
+    assert orc.max_abs_err(orc.sdpa_np(q, k, v, 0.4, attn_mask=torch.zeros(5, 7)), base) < 1e-14
+    only3 = torch.zeros(5, 7, dtype=torch.bool)
+    only3[:, 3] = True
+    got = orc.sdpa_np(q, k, v, 0.4, attn_mask=only3)
+    assert np.allclose(got, np.broadcast_to(v.numpy()[:, :, 3:4], got.shape), atol=1e-14)
+    shift = torch.randn(5, 1, dtype=torch.float64) * 10
+    assert orc.max_abs_err(orc.sdpa_np(q, k, v, 0.4, attn_mask=shift.expand(5, 7)), base) < 1e-12
+
+
+def test_planted_mask_polarity_mistake_is_caught():
+    """Applying a bool mask inverted (keeping where False) fails the torch pin."""
+    q, k, v = _rand(1, 2, 6, 9, 8, seed=8)
+    mask = _masks(1, 2, 6, 9, seed=9)["bool_full"]
+    want = _torch_math_masked(q, k, v, 0.3, mask)
+    assert orc.max_abs_err(orc.sdpa_np(q, k, v, 0.3, attn_mask=mask), want) < 1e-12
+    assert orc.max_abs_err(orc.sdpa_np(q, k, v, 0.3, attn_mask=~mask), want) > 1e-3

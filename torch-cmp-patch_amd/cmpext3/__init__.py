@@ -113,6 +113,8 @@ def _restore(target: Any, name: str) -> None:
 
 
 _DTYPE_TAG = {torch.float16: "fp16", torch.float32: "fp32", torch.bfloat16: "bf16"}
+# attn_mask dtypes the native op takes (bool keeps, floats are added)
+_MASK_DTYPES = (torch.bool, torch.float16, torch.bfloat16, torch.float32)
 
 
 def _dispatch(op: str, ref: torch.Tensor, key: tuple,
@@ -141,12 +143,15 @@ def _patched_sdpa(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=Fa
                   scale=None, **kwargs):
     """F.scaled_dot_product_attention replacement (reference: cmpext3/__init__.py:609-633).
 
-    Bails to stock for attn_mask, dropout, non-4D query, live autograd and
-    non-GPU / unsupported dtypes.  Extra keyword arguments reach only the stock
-    call; the native op sees (q, k, v, scale, is_causal) positionally and
-    rejects shapes it does not support.  Grouped-query calls (K/V with fewer
-    heads than Q) run natively only under enable_gqa=True, as torch requires;
-    without it they go to stock, which raises torch's own error.
+    Bails to stock for dropout, non-4D query, live autograd and non-GPU /
+    unsupported dtypes.  Extra keyword arguments reach only the stock call;
+    the native op sees (q, k, v, scale, is_causal) positionally (plus the mask
+    as a sixth argument when one is given) and rejects what it does not
+    support.  Grouped-query calls (K/V with fewer heads than Q) run natively
+    only under enable_gqa=True, as torch requires; without it they go to
+    stock, which raises torch's own error.  An attn_mask (bool or float
+    tensor) runs natively when is_causal is False; mask and is_causal
+    together go to stock.
     """
     orig = _ORIGINALS[(F, "scaled_dot_product_attention")]
 
@@ -154,17 +159,26 @@ def _patched_sdpa(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=Fa
         return orig(query, key, value, attn_mask=attn_mask, dropout_p=dropout_p,
                     is_causal=is_causal, scale=scale, **kwargs)
 
-    if (attn_mask is not None or dropout_p != 0.0
+    if (dropout_p != 0.0
             or not isinstance(query, torch.Tensor) or query.dim() != 4
-            or not _grad_safe(query, key, value)
+            or not _grad_safe(query, key, value, attn_mask)
             or not _usable(query, key, value)):
         return stock()
     if (isinstance(key, torch.Tensor) and key.dim() == 4 and key.shape[1] != query.shape[1]
             and not kwargs.get("enable_gqa", False)):
         return stock()
+    if attn_mask is None:
+        return _dispatch("attention", query,
+                         (query.shape, query.dtype, key.shape, value.shape, scale, is_causal),
+                         lambda: _C.attention(query, key, value, scale, is_causal),
+                         stock)
+    if (is_causal or not isinstance(attn_mask, torch.Tensor)
+            or attn_mask.dtype not in _MASK_DTYPES):
+        return stock()
     return _dispatch("attention", query,
-                     (query.shape, query.dtype, key.shape, value.shape, scale, is_causal),
-                     lambda: _C.attention(query, key, value, scale, is_causal),
+                     (query.shape, query.dtype, key.shape, value.shape, scale, is_causal,
+                      tuple(attn_mask.shape), attn_mask.dtype, attn_mask.stride()),
+                     lambda: _C.attention(query, key, value, scale, is_causal, attn_mask),
                      stock)
 
 

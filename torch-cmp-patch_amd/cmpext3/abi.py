@@ -13,11 +13,11 @@ from typing import Optional
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcmpext3_attn.so")
 
 # Every function include/cmpext3_attn.h declares.
-SYMBOLS = ("cmpext3_attn_fwd", "cmpext3_attn_fwd_gqa", "cmpext3_attn_strerror",
-           "cmpext3_attn_abi_version", "cmpext3_attn_describe")
+SYMBOLS = ("cmpext3_attn_fwd", "cmpext3_attn_fwd_gqa", "cmpext3_attn_fwd_masked",
+           "cmpext3_attn_strerror", "cmpext3_attn_abi_version", "cmpext3_attn_describe")
 
-DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
-OK, E_INVALID, E_DTYPE, E_HEAD_DIM, E_ALIGN, E_EMPTY_KEYS, E_LAUNCH, E_TOO_LARGE = range(8)
+DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_BOOL = 0, 1, 2, 3
+OK, E_INVALID, E_DTYPE, E_HEAD_DIM, E_ALIGN, E_EMPTY_KEYS, E_LAUNCH, E_TOO_LARGE, E_MASK = range(9)
 
 _lib = None
 
@@ -37,6 +37,10 @@ def lib() -> ctypes.CDLL:
         L.cmpext3_attn_fwd_gqa.argtypes = [vp, vp, vp, vp, ci, ci, ci, ci, ci, ci, ci,
                                            i64p, i64p, i64p, i64p, ctypes.c_float, ci, vp]
         L.cmpext3_attn_fwd_gqa.restype = ci
+        L.cmpext3_attn_fwd_masked.argtypes = [vp, vp, vp, vp, ci, ci, ci, ci, ci, ci, ci,
+                                              i64p, i64p, i64p, i64p, vp, ci, i64p,
+                                              ctypes.c_float, ci, vp]
+        L.cmpext3_attn_fwd_masked.restype = ci
         L.cmpext3_attn_strerror.argtypes = [ci]
         L.cmpext3_attn_strerror.restype = ctypes.c_char_p
         L.cmpext3_attn_abi_version.argtypes = []
@@ -59,7 +63,26 @@ def describe(dtype: int, B: int, H: int, Sq: int, Sk: int, D: int, causal: bool 
 
 def dtype_code(dtype) -> int:
     import torch
-    return {torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16, torch.float32: DTYPE_F32}[dtype]
+    return {torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16, torch.float32: DTYPE_F32,
+            torch.bool: DTYPE_BOOL}[dtype]
+
+
+def prepare_mask(mask, B: int, H: int, Sq: int, Sk: int):
+    """attn_mask broadcast to [B,H,Sq,Sk] in the layout the C ABI takes (unit key
+    stride, other strides multiples of 4 elements, rows readable up to a multiple
+    of 8 keys, 16-byte aligned base): a view when the given tensor already fits,
+    else a compact copy with rows zero-padded to a multiple of 8."""
+    import torch
+    m = mask.expand(B, H, Sq, Sk)
+    fits = (m.stride(3) == 1 and Sk % 8 == 0 and all(m.stride(i) % 4 == 0 for i in range(3))
+            and m.data_ptr() % 16 == 0)
+    if not fits:
+        cb, ch, cq = (1 if m.stride(0) == 0 else B), (1 if m.stride(1) == 0 else H), \
+                     (1 if m.stride(2) == 0 else Sq)
+        c = torch.zeros(cb, ch, cq, (Sk + 7) // 8 * 8, dtype=m.dtype, device=m.device)
+        c[..., :Sk].copy_(m[:cb, :ch, :cq])
+        m = c[..., :Sk].expand(B, H, Sq, Sk)
+    return m
 
 
 def _strides(t):
@@ -68,7 +91,7 @@ def _strides(t):
 
 
 def attn_fwd_raw(q, k, v, o, scale: float, causal: bool = False, stream=None,
-                 D: Optional[int] = None) -> int:
+                 D: Optional[int] = None, attn_mask=None) -> int:
     """Call cmpext3_attn_fwd on [B,H,S,D] tensors (any strides with unit last stride),
     or cmpext3_attn_fwd_gqa when k/v hold fewer heads than q (grouped-query).
     Returns the C return code; launches on `stream` (a torch.cuda.Stream, a raw
@@ -86,20 +109,28 @@ def attn_fwd_raw(q, k, v, o, scale: float, causal: bool = False, stream=None,
     tail = (_strides(q), _strides(k), _strides(v), _strides(o),
             ctypes.c_float(scale), int(causal), ctypes.c_void_p(handle))
     Dx = Dq if D is None else D
+    if attn_mask is not None:
+        m = prepare_mask(attn_mask, B, H, Sq, k.shape[2])
+        mstr = (ctypes.c_int64 * 3)(m.stride(0), m.stride(1), m.stride(2))
+        rc = lib().cmpext3_attn_fwd_masked(*ptrs, dtype_code(q.dtype), B, H, k.shape[1], Sq,
+                                           k.shape[2], Dx, *tail[:4], ctypes.c_void_p(m.data_ptr()),
+                                           dtype_code(m.dtype), mstr, *tail[4:])
+        return rc
     if k.shape[1] != H:
         return lib().cmpext3_attn_fwd_gqa(*ptrs, dtype_code(q.dtype), B, H, k.shape[1], Sq,
                                           k.shape[2], Dx, *tail)
     return lib().cmpext3_attn_fwd(*ptrs, dtype_code(q.dtype), B, H, Sq, k.shape[2], Dx, *tail)
 
 
-def attn_fwd(q, k, v, scale: Optional[float] = None, causal: bool = False, stream=None):
+def attn_fwd(q, k, v, scale: Optional[float] = None, causal: bool = False, stream=None,
+             attn_mask=None):
     """Allocate O like q (contiguous [B,H,Sq,D]) and run the kernel through the C ABI.
     Raises RuntimeError with the library's message on a non-zero return code."""
     import torch
     o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     if scale is None:
         scale = q.shape[-1] ** -0.5
-    rc = attn_fwd_raw(q, k, v, o, scale, causal, stream)
+    rc = attn_fwd_raw(q, k, v, o, scale, causal, stream, attn_mask=attn_mask)
     if rc != OK:
         raise RuntimeError(f"cmpext3_attn_fwd: {strerror(rc)} (code {rc})")
     return o

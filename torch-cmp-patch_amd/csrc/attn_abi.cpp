@@ -79,6 +79,8 @@ const char* cmpext3_attn_strerror(int code) {
     case CMPEXT3_E_EMPTY_KEYS: return "key/value sequence is empty";
     case CMPEXT3_E_LAUNCH: return "HIP kernel launch failed";
     case CMPEXT3_E_TOO_LARGE: return "problem too large for 32-bit tile indexing";
+    case CMPEXT3_E_MASK:
+      return "attention mask not supported here (needs f16/bf16 q, head dim <= 128, non-causal)";
   }
   return "unknown error code";
 }
@@ -115,10 +117,32 @@ int cmpext3_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o, i
                          int H, int H_kv, int Sq, int Sk, int D, const int64_t q_str[3],
                          const int64_t k_str[3], const int64_t v_str[3], const int64_t o_str[3],
                          float scale, int causal, hipStream_t stream) {
+  return cmpext3_attn_fwd_masked(q, k, v, o, dtype, B, H, H_kv, Sq, Sk, D, q_str, k_str, v_str, o_str,
+                                 nullptr, -1, nullptr, scale, causal, stream);
+}
+
+int cmpext3_attn_fwd_masked(const void* q, const void* k, const void* v, void* o, int dtype, int B,
+                            int H, int H_kv, int Sq, int Sk, int D, const int64_t q_str[3],
+                            const int64_t k_str[3], const int64_t v_str[3], const int64_t o_str[3],
+                            const void* mask, int mask_dtype, const int64_t mask_str[3], float scale,
+                            int causal, hipStream_t stream) {
   int rc = check_shape(dtype, B, H, Sq, Sk, D);
   if (rc != CMPEXT3_OK) return rc;
   if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;
   if (H_kv < 1 || H_kv > H || H % H_kv != 0) return CMPEXT3_E_INVALID;
+  const bool masked = mask_dtype != -1;
+  if (masked) {
+    if (mask_dtype < CMPEXT3_DTYPE_F16 || mask_dtype > CMPEXT3_DTYPE_BOOL) return CMPEXT3_E_DTYPE;
+    if (!mask || !mask_str) return CMPEXT3_E_INVALID;
+    // masks run on the pipelined fp16/bf16 kernel only, without causal masking
+    if (dtype == CMPEXT3_DTYPE_F32 || D > 128 || causal) return CMPEXT3_E_MASK;
+    // every 4-key run of a row is one aligned 4/8/16-byte load
+    if (((uintptr_t)mask & 15u) != 0) return CMPEXT3_E_ALIGN;
+    for (int i = 0; i < 3; ++i)
+      if (mask_str[i] < 0 || mask_str[i] % 4 != 0) return CMPEXT3_E_ALIGN;
+    const int mes = mask_dtype == CMPEXT3_DTYPE_BOOL ? 1 : mask_dtype == CMPEXT3_DTYPE_F32 ? 4 : 2;
+    if (((int64_t)(Sq - 1) * mask_str[2] + Sk + 64) * mes >= INT32_MAX) return CMPEXT3_E_TOO_LARGE;
+  }
   if (!q || !k || !v || !o || !q_str || !k_str || !v_str || !o_str) return CMPEXT3_E_INVALID;
   if (!isfinite(scale)) return CMPEXT3_E_INVALID;
   const int es = elem_size(dtype);
@@ -140,6 +164,14 @@ int cmpext3_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o, i
   p.o_b = o_str[0]; p.o_h = o_str[1]; p.o_s = o_str[2];
   p.B = B; p.H = H; p.Sq = Sq; p.Sk = Sk; p.D = D;
   p.kv_group = H / H_kv;  // query head h reads K/V head h / kv_group
+  p.mask_kind = cmpext3::MASK_NONE;
+  if (masked) {
+    p.mask = mask;
+    p.m_b = mask_str[0]; p.m_h = mask_str[1]; p.m_q = mask_str[2];
+    p.mask_kind = mask_dtype == CMPEXT3_DTYPE_BOOL ? cmpext3::MASK_BOOL
+                  : mask_dtype == CMPEXT3_DTYPE_F32 ? cmpext3::MASK_F32
+                  : mask_dtype == CMPEXT3_DTYPE_BF16 ? cmpext3::MASK_BF16 : cmpext3::MASK_F16;
+  }
   // exp2-domain multiplier; a negative scale is folded into Q's sign bits
   p.c = fabsf(scale) * cmpext3::kLog2e;
   p.q_sign = (scale < 0.f) ? (dtype == CMPEXT3_DTYPE_F32 ? 0x80000000u : 0x80008000u) : 0u;

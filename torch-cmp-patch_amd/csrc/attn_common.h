@@ -30,7 +30,19 @@ struct FwdParams {
   int n_wg;         // workgroups launched = B * H * n_qblk
   float c;          // |scale| * log2(e): scores enter exp2 as s * c - m
   uint32_t q_sign;  // sign mask XORed into Q words when scale < 0
+  // optional attention mask (torch SDPA attn_mask), element strides for
+  // {batch, head, query}; unit stride along keys; kind: MASK_* below
+  const void* mask;
+  int64_t m_b, m_h, m_q;
+  int mask_kind;
 };
+
+// attention-mask element kinds (FwdParams::mask_kind)
+constexpr int MASK_NONE = -1;
+constexpr int MASK_F16 = 0;   // additive, fp16
+constexpr int MASK_BF16 = 1;  // additive, bf16
+constexpr int MASK_F32 = 2;   // additive, fp32
+constexpr int MASK_BOOL = 3;  // one byte per element, non-zero keeps the pair
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));

@@ -90,6 +90,7 @@ void describe_mfma16(int D, int B, int H, int Sq, int Sk, bool causal, char* buf
   FwdParams p = {};
   p.Sk = Sk;
   p.k_s = p.v_s = D;
+  p.mask_kind = MASK_NONE;
   if (pipe16_applies(p, dk)) {
     describe_pipe16(dk, B, H, Sq, Sk, causal, buf, len);
     return;

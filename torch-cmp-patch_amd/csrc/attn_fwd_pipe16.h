@@ -77,12 +77,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base,
 // XOR-swizzled LDS rows (DK == DP in {32, 64, 128}).  OPT bit 2: leave the
 // interleave to the compiler (no sched_barrier fences).  OPT bit 3: the head
 // dim is not a multiple of 16 (D < DK), so K columns past D are zeroed.
+// OPT bit 4: an attention mask (p.mask, non-causal launches) is applied to
+// every tile's scores before the exponentials.
 template <typename T, int DK, int DP, int NW, int BK, int OCC, bool CAUSAL, bool PRESCALE, int OPT = 0>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
 attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   constexpr int NT = NW * 64;
   constexpr int BQ = NW * 32;
   constexpr bool SWZ = (OPT & 2) && (DK == DP) && (DK == 32 || DK == 64 || DK == 128);
+  constexpr bool MASK = (OPT & 16) != 0;
+  static_assert(!(MASK && CAUSAL), "masked launches are non-causal");
   constexpr int RSK = SWZ ? DK : DK + 8;  // K tile row stride (halves)
   constexpr int RSV = SWZ ? DP : DP + 8;  // V tile row stride (halves)
   constexpr int KTILE = BK * RSK;
@@ -290,6 +294,51 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
         if (key >= kpe || (CAUSAL && key > qrow)) sc[kb][r] = -INFINITY;
       }
   };
+  // attention mask of tile j added to (bool: applied to) exp2-domain scores.
+  // A lane's 16 keys per 32-key block are 2 runs of 8 consecutive keys
+  // (acc_key: 16j + 8hh + 0..7), so each run is one 8/16/32-byte read; rows
+  // past Sq use the last row (their output is never stored).  The last row is
+  // readable up to Sk rounded up to 8 (the ABI's contract); reads past that
+  // return zero, and every key at or past Sk is masked by the key-range rule
+  // afterwards.
+  const int mes = p.mask_kind == MASK_BOOL ? 1 : p.mask_kind == MASK_F32 ? 4 : 2;
+  const __amdgpu_buffer_rsrc_t mrs =
+      uniform_rsrc(MASK ? (const void*)((const char*)p.mask + (b * p.m_b + h * p.m_h) * mes) : p.q,
+                   MASK ? ((int64_t)(Sq - 1) * p.m_q + (Sk + 7) / 8 * 8) * mes : 0);
+  const int mrow_off = MASK ? (int)((int64_t)min(qrow, Sq - 1) * p.m_q * mes) : 0;
+  auto add_mask = [&](int j, f32x16 (&sc)[NKB]) {
+    const int k0 = (tbase + j) * BK;
+    const int kind = p.mask_kind;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int run = 0; run < 2; ++run) {
+        const int key = k0 + 32 * kb + 16 * run + 8 * hh;  // first of 8 consecutive keys
+        const int r0 = 8 * run;
+        if (kind == MASK_BOOL) {
+          const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(mrs, mrow_off + key, 0, 0));
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            if (((w[i >> 2] >> (8 * (i & 3))) & 0xffu) == 0u) sc[kb][r0 + i] = -INFINITY;
+        } else if (kind == MASK_F32) {
+#pragma unroll
+          for (int hv = 0; hv < 2; ++hv) {
+            const f32x4 a = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(mrs, mrow_off + 4 * (key + 4 * hv), 0, 0));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[kb][r0 + 4 * hv + i] = __builtin_fmaf(a[i], kLog2e, sc[kb][r0 + 4 * hv + i]);
+          }
+        } else {
+          const u32x4 w = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(mrs, mrow_off + 2 * key, 0, 0));
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const f32x2 a = kind == MASK_F16 ? Elt<_Float16>::unpack(w[i]) : Elt<__bf16>::unpack(w[i]);
+            sc[kb][r0 + 2 * i] = __builtin_fmaf(a[0], kLog2e, sc[kb][r0 + 2 * i]);
+            sc[kb][r0 + 2 * i + 1] = __builtin_fmaf(a[1], kLog2e, sc[kb][r0 + 2 * i + 1]);
+          }
+        }
+      }
+  };
   // this lane's half of the row max (the two halves meet at the decision)
   auto row_max = [&](const f32x16 (&sc)[NKB]) {
     float m = -INFINITY;
@@ -349,7 +398,7 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   };
   // bf16 path: the two scores of unit u into the exp2 domain
   auto conv = [&](int u, f32x16 (&sc)[NKB]) {
-    if (!PRESCALE) {
+    if (!PRESCALE && !MASK) {
       const int ch = u >> 2, e = u & 3, kb = ch >> 1, cc = ch & 1;
       sc[kb][8 * cc + 2 * e] = __builtin_fmaf(sc[kb][8 * cc + 2 * e], c, -mb);
       sc[kb][8 * cc + 2 * e + 1] = __builtin_fmaf(sc[kb][8 * cc + 2 * e + 1], c, -mb);
@@ -366,6 +415,7 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
     qk(kf0, sA);
   }
   to_exp2(sA);
+  if (MASK) add_mask(0, sA);
   if (tile_needs_mask(0)) mask(0, sA);
   {
     const float mx = xhalf_max(row_max(sA));
@@ -442,7 +492,17 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
     }
     ls0 += tc0;
     ls1 += tc1;
-    if (t + 1 < nt2 && tile_needs_mask(t + 1)) mask(t + 1, sn);
+    if (MASK) {
+      // the mask is added in the exp2 domain, so masked bf16 tiles are
+      // converted here rather than unit by unit in stage B
+      if (t + 1 < nt2) {
+        to_exp2(sn);
+        add_mask(t + 1, sn);
+        if (tile_needs_mask(t + 1)) mask(t + 1, sn);
+      }
+    } else if (t + 1 < nt2 && tile_needs_mask(t + 1)) {
+      mask(t + 1, sn);
+    }
 
     // ---- stage B: PV MFMAs of tile t beside the K(t+2) fragment reads and
     // the early half of tile t+1's exp units
@@ -498,7 +558,8 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
       for (int g = 0; g < 4; ++g)
         st_ws((f32x4){oacc[db][4 * g], oacc[db][4 * g + 1], oacc[db][4 * g + 2], oacc[db][4 * g + 3]},
               voff(part, db * 4 + g));
-    st_ws((f32x4){mb, lsum, 0.f, 0.f}, voff(part, NDB * 4));
+    // a part whose keys are all masked for this row holds nothing: offset -inf
+    st_ws((f32x4){lsum > 0.f ? mb : -INFINITY, lsum, 0.f, 0.f}, voff(part, NDB * 4));
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     int old = 0;
     if (lane == 0) old = __hip_atomic_fetch_add(sa.cnt + sb * NW + wave, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -515,7 +576,7 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
     lsum = 0.f;
     for (int q = 0; q < nparts; ++q) {
       const f32x4 ml = ld_ws(voff(q, NDB * 4));
-      const float a = fast_exp2(ml[0] - mt);
+      const float a = ml[0] == -INFINITY ? 0.f : fast_exp2(ml[0] - mt);
       lsum = __builtin_fmaf(ml[1], a, lsum);
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
@@ -527,7 +588,8 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
         }
     }
   }
-  const float inv = 1.f / lsum;
+  // a row that saw no key at all (every key masked) gives zeros, as torch does
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
   if (qrow < Sq) {
     uint16_t* orow = og + (int64_t)qrow * p.o_s;
 #pragma unroll

@@ -27,6 +27,8 @@ namespace {
 constexpr int kPipeNw = 4;
 constexpr int kPipeBk = 32;
 constexpr int pipe_occ(int dk) { return dk <= 32 ? 4 : dk <= 64 ? 3 : 2; }
+// masked launches need a few more registers: D = 32 drops to 3 waves per SIMD
+constexpr int pipe_occ_masked(int dk) { return dk <= 64 ? 3 : 2; }
 
 // Split plan limits: a part scans at least kMinPartTiles key tiles (shorter
 // parts spend more on their prologue and merge than they save), and at most
@@ -121,22 +123,24 @@ SplitArgs split_plan(int n, int ntiles, int occ, int cus, bool causal) {
   return sa;
 }
 
-template <typename T, int DK, bool CAUSAL, bool PRESCALE>
+template <typename T, int DK, bool CAUSAL, bool PRESCALE, int MOPT>
 hipError_t launch_dk(const FwdParams& p, const SplitArgs& sa, hipStream_t s) {
-  // OPT 1: s_setprio around the MFMA blocks; OPT 8: zero K columns past D
-  if (p.D == DK) return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, pipe_occ(DK), CAUSAL, PRESCALE, 1>(p, sa, s);
-  return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, pipe_occ(DK), CAUSAL, PRESCALE, 1 | 8>(p, sa, s);
+  // OPT 1: s_setprio around the MFMA blocks; OPT 8: zero K columns past D;
+  // OPT 16 (MOPT): attention mask
+  constexpr int occ = MOPT ? pipe_occ_masked(DK) : pipe_occ(DK);
+  if (p.D == DK) return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, occ, CAUSAL, PRESCALE, 1 | MOPT>(p, sa, s);
+  return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, occ, CAUSAL, PRESCALE, 1 | 8 | MOPT>(p, sa, s);
 }
 
-template <typename T, bool CAUSAL, bool PRESCALE>
+template <typename T, bool CAUSAL, bool PRESCALE, int MOPT = 0>
 hipError_t launch_bucket(const FwdParams& p, const SplitArgs& sa, int dk, hipStream_t s) {
   switch (dk) {
-    case 32: return launch_dk<T, 32, CAUSAL, PRESCALE>(p, sa, s);
-    case 48: return launch_dk<T, 48, CAUSAL, PRESCALE>(p, sa, s);
-    case 64: return launch_dk<T, 64, CAUSAL, PRESCALE>(p, sa, s);
-    case 80: return launch_dk<T, 80, CAUSAL, PRESCALE>(p, sa, s);
-    case 96: return launch_dk<T, 96, CAUSAL, PRESCALE>(p, sa, s);
-    case 128: return launch_dk<T, 128, CAUSAL, PRESCALE>(p, sa, s);
+    case 32: return launch_dk<T, 32, CAUSAL, PRESCALE, MOPT>(p, sa, s);
+    case 48: return launch_dk<T, 48, CAUSAL, PRESCALE, MOPT>(p, sa, s);
+    case 64: return launch_dk<T, 64, CAUSAL, PRESCALE, MOPT>(p, sa, s);
+    case 80: return launch_dk<T, 80, CAUSAL, PRESCALE, MOPT>(p, sa, s);
+    case 96: return launch_dk<T, 96, CAUSAL, PRESCALE, MOPT>(p, sa, s);
+    case 128: return launch_dk<T, 128, CAUSAL, PRESCALE, MOPT>(p, sa, s);
   }
   return hipErrorNotSupported;
 }
@@ -148,12 +152,13 @@ int n_key_tiles(int Sk) { return (Sk + kPipeBk - 1) / kPipeBk; }
 
 // True when the pipelined kernel takes this problem: head-dim bucket <= 128,
 // a key sweep long enough for its prologue (four tiles in flight) to pay off
-// (SDXL cross-attention, Sk = 77, is faster on the v2 kernel), and K/V tiles
+// (SDXL cross-attention, Sk = 77, is faster on the v2 kernel) unless an
+// attention mask is given (only this kernel applies masks), and K/V tiles
 // addressable with 32-bit buffer offsets.
 constexpr int kPipeMinSk = 256;
 
 bool pipe16_applies(const FwdParams& p, int dk) {
-  if (dk > 128 || p.Sk < kPipeMinSk) return false;
+  if (dk > 128 || (p.Sk < kPipeMinSk && p.mask_kind == MASK_NONE)) return false;
   const int64_t rs = p.k_s > p.v_s ? p.k_s : p.v_s;
   return (int64_t)(p.Sk + kPipeBk) * rs * 2 < (int64_t(1) << 31);
 }
@@ -170,7 +175,8 @@ hipError_t launch_pipe16(const FwdParams& p0, int dk, bool bf16, bool causal, bo
   // which rounds to the same probability as scale 0 gives, and keeps -inf.
   if (!prescale && p.c == 0.f) p.c = 1e-30f;
   const int cus = device_cus();
-  SplitArgs sa = split_plan(n_blocks(p.B, p.H, p.Sq), n_key_tiles(p.Sk), pipe_occ(dk), cus, causal);
+  const int occ = p.mask_kind != MASK_NONE ? pipe_occ_masked(dk) : pipe_occ(dk);
+  SplitArgs sa = split_plan(n_blocks(p.B, p.H, p.Sq), n_key_tiles(p.Sk), occ, cus, causal);
   if (sa.nparts > 1) {
     Exchange e;
     if (exchange_for(s, cus, e)) {
@@ -179,6 +185,12 @@ hipError_t launch_pipe16(const FwdParams& p0, int dk, bool bf16, bool causal, bo
     } else {
       sa = SplitArgs{n_blocks(p.B, p.H, p.Sq), 1, nullptr, nullptr};
     }
+  }
+  if (p.mask_kind != MASK_NONE) {  // masked launches are non-causal (checked by the caller)
+    if (causal) return hipErrorNotSupported;
+    if (bf16) return launch_bucket<__bf16, false, false, 16>(p, sa, dk, s);
+    return prescale ? launch_bucket<_Float16, false, true, 16>(p, sa, dk, s)
+                    : launch_bucket<_Float16, false, false, 16>(p, sa, dk, s);
   }
   if (bf16)
     return causal ? launch_bucket<__bf16, true, false>(p, sa, dk, s) : launch_bucket<__bf16, false, false>(p, sa, dk, s);

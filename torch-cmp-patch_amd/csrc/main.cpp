@@ -1,6 +1,6 @@
 // cmpext3._native -- torch binding of the fused attention forward.
 //
-// attention(query, key, value, scale=None, causal=False) -> Tensor
+// attention(query, key, value, scale=None, causal=False, attn_mask=None) -> Tensor
 //   Same signature and error convention as the reference's binding
 //   (src/main.cpp:2353-2358 -> custom_attention_forward, :1603-1774): every
 //   unsupported input raises RuntimeError (TORCH_CHECK) so that the Python
@@ -15,7 +15,11 @@
 //     view (the reference's HFMA2 path does this for fp16, :1652);
 //   * head dims that are not a whole number of 16-byte chunks, and tensors
 //     whose base pointer or row strides are not 16-byte aligned, are repacked
-//     into zero-padded contiguous copies instead of being rejected.
+//     into zero-padded contiguous copies instead of being rejected;
+//   * K/V may hold fewer heads than Q (grouped-query attention);
+//   * attn_mask (bool or additive f16/bf16/f32, broadcast like torch's SDPA)
+//     runs natively for f16/bf16 with D <= 128 and causal=False (the
+//     reference sent every mask to stock torch, cmpext3/__init__.py:624).
 #include <cmath>
 
 #include <torch/extension.h>
@@ -35,17 +39,62 @@ int dtype_code(at::ScalarType t) {
   }
 }
 
+// attention mask in the form the C ABI takes: [B,H,Sq,Sk] view, unit key
+// stride, other strides multiples of 4 elements (0 = broadcast)
+struct Mask {
+  torch::Tensor t;
+  int dtype = -1;
+};
+
 int launch(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v,
-           torch::Tensor& o, int dtype, int D, float scale, bool causal, hipStream_t stream) {
+           torch::Tensor& o, int dtype, int D, float scale, bool causal, const Mask& mask,
+           hipStream_t stream) {
   const int64_t qs[3] = {q.stride(0), q.stride(1), q.stride(2)};
   const int64_t ks[3] = {k.stride(0), k.stride(1), k.stride(2)};
   const int64_t vs[3] = {v.stride(0), v.stride(1), v.stride(2)};
   const int64_t os[3] = {o.stride(0), o.stride(1), o.stride(2)};
   if (q.stride(3) != 1 || k.stride(3) != 1 || v.stride(3) != 1 || o.stride(3) != 1)
     return CMPEXT3_E_ALIGN;
-  return cmpext3_attn_fwd_gqa(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dtype,
-                              (int)q.size(0), (int)q.size(1), (int)k.size(1), (int)q.size(2),
-                              (int)k.size(2), D, qs, ks, vs, os, scale, causal ? 1 : 0, stream);
+  int64_t ms[3] = {0, 0, 0};
+  if (mask.dtype >= 0) {
+    ms[0] = mask.t.stride(0); ms[1] = mask.t.stride(1); ms[2] = mask.t.stride(2);
+  }
+  return cmpext3_attn_fwd_masked(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dtype,
+                                 (int)q.size(0), (int)q.size(1), (int)k.size(1), (int)q.size(2),
+                                 (int)k.size(2), D, qs, ks, vs, os,
+                                 mask.dtype >= 0 ? mask.t.data_ptr() : nullptr, mask.dtype, ms,
+                                 scale, causal ? 1 : 0, stream);
+}
+
+// torch's attn_mask broadcast to [B,H,Sq,Sk]; copied into a compact buffer
+// (broadcast dims kept at size 1, rows padded to a multiple of 8 keys) when
+// its layout does not fit the ABI.
+Mask prepare_mask(const torch::Tensor& m0, const torch::Tensor& query, int64_t B, int64_t H,
+                  int64_t Sq, int64_t Sk) {
+  TORCH_CHECK(m0.device() == query.device(), "cmpext3 attention: attn_mask on another device");
+  TORCH_CHECK(m0.dim() <= 4, "cmpext3 attention: attn_mask has more than 4 dims");
+  Mask mk;
+  switch (m0.scalar_type()) {
+    case at::kBool: mk.dtype = CMPEXT3_DTYPE_BOOL; break;
+    case at::kHalf: mk.dtype = CMPEXT3_DTYPE_F16; break;
+    case at::kBFloat16: mk.dtype = CMPEXT3_DTYPE_BF16; break;
+    case at::kFloat: mk.dtype = CMPEXT3_DTYPE_F32; break;
+    default: TORCH_CHECK(false, "cmpext3 attention: unsupported attn_mask dtype ", m0.scalar_type());
+  }
+  torch::Tensor m = m0.expand({B, H, Sq, Sk});
+  // in place only if rows can be read in runs of 8 keys without leaving the
+  // tensor: unit key stride and Sk a multiple of 8
+  const bool fits = m.stride(3) == 1 && Sk % 8 == 0 && m.stride(0) % 4 == 0 && m.stride(1) % 4 == 0 &&
+                    m.stride(2) % 4 == 0 && ((uintptr_t)m.data_ptr() & 15u) == 0;
+  if (!fits) {
+    const int64_t cb = m.stride(0) == 0 ? 1 : B, ch = m.stride(1) == 0 ? 1 : H;
+    const int64_t cq = m.stride(2) == 0 ? 1 : Sq, skp = (Sk + 7) / 8 * 8;
+    torch::Tensor c = torch::zeros({cb, ch, cq, skp}, m.options());
+    c.narrow(3, 0, Sk).copy_(m.narrow(0, 0, cb).narrow(1, 0, ch).narrow(2, 0, cq));
+    m = c.narrow(3, 0, Sk).expand({B, H, Sq, Sk});
+  }
+  mk.t = m;
+  return mk;
 }
 
 bool is_bshd_view(const torch::Tensor& t) {
@@ -58,7 +107,8 @@ bool is_bshd_view(const torch::Tensor& t) {
 }  // namespace
 
 torch::Tensor attention(torch::Tensor query, torch::Tensor key, torch::Tensor value,
-                        c10::optional<double> scale_arg, bool causal) {
+                        c10::optional<double> scale_arg, bool causal,
+                        c10::optional<torch::Tensor> attn_mask) {
   TORCH_CHECK(query.dim() == 4, "cmpext3 attention: query must be 4D [B, H, S, D]");
   TORCH_CHECK(key.dim() == 4, "cmpext3 attention: key must be 4D");
   TORCH_CHECK(value.dim() == 4, "cmpext3 attention: value must be 4D");
@@ -90,12 +140,18 @@ torch::Tensor attention(torch::Tensor query, torch::Tensor key, torch::Tensor va
   const at::hip::HIPGuardMasqueradingAsCUDA guard(query.device());
   hipStream_t stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA(query.device().index()).stream();
 
+  Mask mask;
+  if (attn_mask.has_value() && attn_mask->defined()) {
+    TORCH_CHECK(!causal, "cmpext3 attention: attn_mask together with causal runs on stock torch");
+    mask = prepare_mask(*attn_mask, query, B, H, Sq, Sk);
+  }
+
   torch::Tensor out = is_bshd_view(query)
                           ? torch::empty({B, Sq, H, D}, query.options()).transpose(1, 2)
                           : torch::empty({B, H, Sq, D}, query.options());
   if (out.numel() == 0) return out;
 
-  int rc = launch(query, key, value, out, dtype, (int)D, scale, causal, stream);
+  int rc = launch(query, key, value, out, dtype, (int)D, scale, causal, mask, stream);
   if (rc == CMPEXT3_E_ALIGN || rc == CMPEXT3_E_HEAD_DIM) {
     // Repack into contiguous copies zero-padded to whole 16-byte chunks.
     // Zero columns add nothing to Q K^T, and the padded V columns only produce
@@ -109,7 +165,7 @@ torch::Tensor attention(torch::Tensor query, torch::Tensor key, torch::Tensor va
     };
     torch::Tensor qp = pad(query), kp = pad(key), vp = pad(value);
     torch::Tensor op = torch::empty({B, H, Sq, Dp}, query.options());
-    rc = launch(qp, kp, vp, op, dtype, (int)Dp, scale, causal, stream);
+    rc = launch(qp, kp, vp, op, dtype, (int)Dp, scale, causal, mask, stream);
     if (rc == CMPEXT3_OK) out = (Dp == D) ? op : op.narrow(3, 0, D).contiguous();
   }
   TORCH_CHECK(rc == CMPEXT3_OK, "cmpext3 attention: ", cmpext3_attn_strerror(rc));
@@ -128,7 +184,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "cmpext3 native ops for MI355X (gfx950): fused attention forward";
   m.def("attention", &attention, "Fused SDPA forward (fp16/bf16/fp32, causal or not)",
         py::arg("query"), py::arg("key"), py::arg("value"), py::arg("scale") = py::none(),
-        py::arg("causal") = false);
+        py::arg("causal") = false, py::arg("attn_mask") = py::none());
   m.def("describe", &describe, "Kernel/tile choice for a problem (host only)", py::arg("dtype"),
         py::arg("B"), py::arg("H"), py::arg("Sq"), py::arg("Sk"), py::arg("D"),
         py::arg("causal") = false);
