@@ -126,5 +126,8 @@ def test_autoselect_probe_on_gpu(patched, autoselecting):
 def test_describe_names_the_kernel():
     text = cmpext3.ops.describe(0, 2, 10, 4096, 4096, 64, False)
     assert "pipe16" in text and "DK=64" in text
+    # SDXL cross-attention (77 keys): all of K/V in LDS, one pass per row
+    assert "short16" in cmpext3.ops.describe(0, 2, 10, 4096, 77, 64, False)
+    assert "short16" not in cmpext3.ops.describe(0, 2, 10, 4096, 77, 64, True)
     assert "mfma16" in cmpext3.ops.describe(0, 2, 10, 4096, 4096, 256, False)
     assert "mfma32" in cmpext3.ops.describe(2, 2, 8, 4096, 4096, 40, False)

@@ -56,6 +56,9 @@ hipError_t launch_bucket(const FwdParams& p, int dk, hipStream_t s) {
 }  // namespace
 
 bool pipe16_applies(const FwdParams& p, int dk);
+bool short16_applies(const FwdParams& p, int dk, bool causal);
+hipError_t launch_short16(const FwdParams& p, int dk, bool bf16, hipStream_t s);
+void describe_short16(int dk, int Sq, int Sk, char* buf, int len);
 hipError_t launch_pipe16(const FwdParams& p, int dk, bool bf16, bool causal, bool prescale, hipStream_t s);
 void describe_pipe16(int dk, int B, int H, int Sq, int Sk, bool causal, char* buf, int len);
 
@@ -72,6 +75,7 @@ static bool use_prescale(const FwdParams& p, bool bf16) { return !bf16 && p.c <=
 hipError_t launch_mfma16(const FwdParams& p, bool bf16, bool causal, hipStream_t s) {
   const int dk = mfma16_bucket(p.D);
   if (dk < 0) return hipErrorInvalidValue;
+  if (short16_applies(p, dk, causal)) return launch_short16(p, dk, bf16, s);
   if (pipe16_applies(p, dk)) return launch_pipe16(p, dk, bf16, causal, use_prescale(p, bf16), s);
   if (bf16)
     return causal ? launch_bucket<__bf16, true, false>(p, dk, s)
@@ -91,6 +95,10 @@ void describe_mfma16(int D, int B, int H, int Sq, int Sk, bool causal, char* buf
   p.Sk = Sk;
   p.k_s = p.v_s = D;
   p.mask_kind = MASK_NONE;
+  if (short16_applies(p, dk, causal)) {
+    describe_short16(dk, Sq, Sk, buf, len);
+    return;
+  }
   if (pipe16_applies(p, dk)) {
     describe_pipe16(dk, B, H, Sq, Sk, causal, buf, len);
     return;
