@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define CMPEXT3_ATTN_ABI_VERSION 3
+#define CMPEXT3_ATTN_ABI_VERSION 4
 
 /* dtype codes (CMPEXT3_DTYPE_BOOL: attention masks only) */
 #define CMPEXT3_DTYPE_F16  0
@@ -56,6 +56,7 @@ extern "C" {
 #define CMPEXT3_E_LAUNCH           6  /* the HIP launch itself failed */
 #define CMPEXT3_E_TOO_LARGE        7  /* a size does not fit the kernel's index arithmetic */
 #define CMPEXT3_E_MASK             8  /* attention mask with fp32 q, D > 128 or causal */
+#define CMPEXT3_E_TRAINING         9  /* training entry point with fp32 or D > 128 */
 
 /*
  * Fused attention forward.
@@ -126,6 +127,52 @@ int cmpext3_attn_fwd_masked(const void* q, const void* k, const void* v, void* o
                             const int64_t v_str[3], const int64_t o_str[3],
                             const void* mask, int mask_dtype, const int64_t mask_str[3],
                             float scale, int causal, hipStream_t stream);
+
+/*
+ * Training forward: as cmpext3_attn_fwd (H_kv == H, no mask), and also writes
+ *
+ *   lse : [B, H, Sq] fp32, contiguous (element (b, h, i) at lse[(b*H + h)*Sq + i]),
+ *         the natural-log log-sum-exp over the visible keys of row i of
+ *         scale * Q K^T -- what cmpext3_attn_bwd needs to rebuild the softmax.
+ *
+ * Supported for f16/bf16 with D <= 128 (else CMPEXT3_E_TRAINING, nothing
+ * launched).  Every such call runs the pipelined kernel, whatever Sk.
+ *
+ * Reference: none.  The reference is forward-only: its patch hands every
+ * call with live autograd to stock torch (cmpext3/__init__.py:115-125).
+ */
+int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, float* lse,
+                         int dtype, int B, int H, int Sq, int Sk, int D,
+                         const int64_t q_str[3], const int64_t k_str[3],
+                         const int64_t v_str[3], const int64_t o_str[3],
+                         float scale, int causal, hipStream_t stream);
+
+/*
+ * Backward of the attention above: given q, k, v, the forward output o, its
+ * gradient dout and the forward's lse, writes the gradients
+ *
+ *   dq : [B, H, Sq, D]   dk, dv : [B, H, Sk, D]   (all `dtype`, overwritten)
+ *
+ * of sum(o * dout), with the same scale and causal flag as the forward.
+ *   delta : caller-owned fp32 workspace of B*H*Sq elements (4-byte aligned;
+ *           receives sum_d dout * o per row).
+ *   *_str[3] : element strides over {batch, head, seq} as in cmpext3_attn_fwd.
+ * Three kernels on `stream`: Delta, dK/dV (one workgroup per 128 keys), dQ
+ * (one per 128 queries); each gradient row is written by exactly one
+ * workgroup, so results are bit-identical from run to run.  B*H*Sq == 0 is a
+ * no-op (dk and dv are then left untouched).  f16/bf16 with D <= 128 only
+ * (else CMPEXT3_E_TRAINING).
+ *
+ * Reference: none (forward-only reference, cmpext3/__init__.py:115-125).
+ */
+int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
+                     const void* dout, const float* lse, void* dq, void* dk, void* dv,
+                     float* delta, int dtype, int B, int H, int Sq, int Sk, int D,
+                     const int64_t q_str[3], const int64_t k_str[3],
+                     const int64_t v_str[3], const int64_t o_str[3],
+                     const int64_t do_str[3], const int64_t dq_str[3],
+                     const int64_t dk_str[3], const int64_t dv_str[3],
+                     float scale, int causal, hipStream_t stream);
 
 /* Human-readable text for a return code (static storage). */
 const char* cmpext3_attn_strerror(int code);

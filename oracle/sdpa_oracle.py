@@ -28,6 +28,17 @@ a bool mask keeps the (query, key) pairs where it is True, a float mask is
 added to scale * Q K^T; either broadcasts to [B, H, Sq, Sk].  The reference
 never ran masks natively (cmpext3/__init__.py:624 sends them to stock torch),
 so the restated behaviour is torch's.
+
+Backward (sdpa_lse_np, sdpa_bwd_np): the gradient of the same forward.  The
+reference is forward-only (its patch sends every call with live autograd to
+stock torch, cmpext3/__init__.py:115-125), so there is no reference code to
+follow; the restatement is the calculus of softmax attention, with
+P = softmax(S), S = scale * Q K^T (causal: invisible pairs at -inf):
+  dV = P^T dO,  dP = dO V^T,  Delta_i = sum_d dO_id O_id = sum_j P_ij dP_ij,
+  dS = P * (dP - Delta),  dQ = scale * dS K,  dK = scale * dS^T Q,
+and lse_i = log sum_j exp(S_ij) (natural log).  Pinned in
+tests/test_oracle_bwd.py against torch autograd in float64, central finite
+differences and closed forms.
 """
 from __future__ import annotations
 
@@ -124,6 +135,63 @@ def sdpa_np(q, k, v, scale: Optional[float] = None, causal: bool = False,
                     o = (e @ v[b, h]) / np.where(dead, 1.0, z)
                 out[b, h, i0:i1] = np.where(dead, 0.0, o)
     return out
+
+
+def sdpa_lse_np(q, k, scale: Optional[float] = None, causal: bool = False,
+                block: int = 512) -> np.ndarray:
+    """float64 [B, H, Sq] natural-log logsumexp over keys of scale * Q K^T
+    (causal: visible keys only)."""
+    q, k = _as_f64(q), _as_f64(k)
+    B, H, Sq, D = q.shape
+    Sk = k.shape[2]
+    if scale is None:
+        scale = default_scale(D)
+    out = np.empty((B, H, Sq), dtype=np.float64)
+    for b in range(B):
+        for h in range(H):
+            kt = k[b, h].T
+            for i0 in range(0, Sq, block):
+                i1 = min(Sq, i0 + block)
+                s = (q[b, h, i0:i1] @ kt) * scale
+                if causal:
+                    s = np.where(causal_visible(Sq, Sk)[i0:i1], s, -np.inf)
+                m = s.max(axis=1, keepdims=True)
+                out[b, h, i0:i1] = (m + np.log(np.exp(s - m).sum(axis=1, keepdims=True)))[:, 0]
+    return out
+
+
+def sdpa_bwd_np(q, k, v, do, scale: Optional[float] = None, causal: bool = False,
+                block: int = 512):
+    """float64 gradients (dq, dk, dv) of sum(O * dO) for O = sdpa(q, k, v),
+    blocked over query rows (every query row sees at least key 0)."""
+    q, k, v, do = _as_f64(q), _as_f64(k), _as_f64(v), _as_f64(do)
+    B, H, Sq, D = q.shape
+    Sk = k.shape[2]
+    if scale is None:
+        scale = default_scale(D)
+    dq = np.zeros_like(q)
+    dk = np.zeros_like(k)
+    dv = np.zeros_like(v)
+    for b in range(B):
+        for h in range(H):
+            kt = k[b, h].T
+            for i0 in range(0, Sq, block):
+                i1 = min(Sq, i0 + block)
+                s = (q[b, h, i0:i1] @ kt) * scale
+                if causal:
+                    s = np.where(causal_visible(Sq, Sk)[i0:i1], s, -np.inf)
+                m = s.max(axis=1, keepdims=True)
+                e = np.exp(s - m)
+                p = e / e.sum(axis=1, keepdims=True)               # [rows, Sk]
+                g = do[b, h, i0:i1]
+                o = p @ v[b, h]
+                dv[b, h] += p.T @ g
+                dp = g @ v[b, h].T
+                delta = (g * o).sum(axis=1, keepdims=True)
+                ds = p * (dp - delta)
+                dq[b, h, i0:i1] = scale * (ds @ k[b, h])
+                dk[b, h] += scale * (ds.T @ q[b, h, i0:i1])
+    return dq, dk, dv
 
 
 def _load_c():

@@ -38,8 +38,8 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version_and_messages():
-    assert abi.lib().cmpext3_attn_abi_version() == 3
-    for code in range(9):
+    assert abi.lib().cmpext3_attn_abi_version() == 4
+    for code in range(10):
         assert abi.strerror(code) and abi.strerror(code) != "unknown error code"
     assert abi.strerror(99) == "unknown error code"
 
@@ -125,3 +125,40 @@ def test_gqa_head_counts_are_checked_before_launch():
     assert _call_gqa(H=4, H_kv=-1) == abi.E_INVALID
     assert _call_gqa(H=4, H_kv=2, dtype=9) == abi.E_DTYPE
     assert _call_gqa(H=4, H_kv=2, Sq=0, q=0) == abi.OK   # empty problem
+
+
+def _call_lse(lse=16, dtype=abi.DTYPE_F16, D=64, q=16, Sq=8, Sk=8, scale=0.125):
+    st = (ctypes.c_int64 * 3)(512, 512, 64)
+    vp = ctypes.c_void_p
+    return abi.lib().cmpext3_attn_fwd_lse(vp(q), vp(16), vp(16), vp(16), vp(lse), dtype, 1, 1, Sq, Sk, D,
+                                          st, st, st, st, ctypes.c_float(scale), 0, None)
+
+
+def _call_bwd(delta=16, lse=16, dtype=abi.DTYPE_F16, D=64, dq=16, Sq=8, Sk=8, scale=0.125,
+              strides=(512, 512, 64)):
+    st = (ctypes.c_int64 * 3)(*strides)
+    vp = ctypes.c_void_p
+    return abi.lib().cmpext3_attn_bwd(vp(16), vp(16), vp(16), vp(16), vp(16), vp(lse), vp(dq), vp(16),
+                                      vp(16), vp(delta), dtype, 1, 1, Sq, Sk, D,
+                                      *([st] * 8), ctypes.c_float(scale), 1, None)
+
+
+def test_training_entry_points_reject_before_launch():
+    """Fake device addresses: each case must be turned down on the host."""
+    assert _call_lse(dtype=abi.DTYPE_F32, D=64) == abi.E_TRAINING
+    assert _call_lse(D=160) == abi.E_TRAINING
+    assert _call_lse(lse=0) == abi.E_INVALID
+    assert _call_lse(lse=18) == abi.E_INVALID
+    assert _call_lse(q=24) == abi.E_ALIGN
+    assert _call_lse(Sk=0) == abi.E_EMPTY_KEYS
+    assert _call_lse(lse=0, q=0, Sq=0) == abi.OK          # empty problem
+    assert _call_bwd(dtype=abi.DTYPE_F32) == abi.E_TRAINING
+    assert _call_bwd(D=136) == abi.E_TRAINING
+    assert _call_bwd(delta=0) == abi.E_INVALID
+    assert _call_bwd(lse=0) == abi.E_INVALID
+    assert _call_bwd(delta=18) == abi.E_ALIGN
+    assert _call_bwd(dq=24) == abi.E_ALIGN
+    assert _call_bwd(strides=(512, 512, 60)) == abi.E_ALIGN
+    assert _call_bwd(scale=float("nan")) == abi.E_INVALID
+    assert _call_bwd(strides=(1 << 40, 1 << 40, 1 << 26)) == abi.E_TOO_LARGE
+    assert _call_bwd(delta=0, Sq=0) == abi.OK

@@ -1,0 +1,187 @@
+"""GPU parity of the training pair: the forward that keeps the row
+log-sum-exp (cmpext3_attn_fwd_lse) and the backward (cmpext3_attn_bwd), both
+through the C ABI, plus the autograd Function and the opt-in SDPA route.
+
+Oracle: float64 restatements in oracle/sdpa_oracle.py (sdpa_np, sdpa_lse_np,
+sdpa_bwd_np), pinned to torch autograd, finite differences and closed forms in
+tests/test_oracle_bwd.py.  Bars, written here:
+  * forward output: max abs error <= 1e-2 fp16, 2e-2 bf16 (the forward's bar);
+  * log-sum-exp: max abs error <= 1e-2 fp16, 2e-2 bf16 (natural log);
+  * gradients: max abs error <= 1e-2 (fp16) / 2e-2 (bf16) times max |oracle|
+    of that gradient (at least 1e-3), i.e. the same numbers relative to each
+    gradient's own scale (gradients, unlike attention outputs, are not bounded
+    by the values of V; the floor covers gradients that are exactly zero, such
+    as dQ and dK with a single key).
+"""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import cmpext3
+from cmpext3 import abi
+from oracle import sdpa_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"fp16": 1e-2, "bf16": 2e-2}
+TDT = {"fp16": torch.float16, "bf16": torch.bfloat16}
+
+
+def _inputs(dtype, B, H, Sq, Sk, D, seed, amp=1.0):
+    g = torch.Generator().manual_seed(seed)
+    mk = lambda S: (torch.randn(B, H, S, D, generator=g) * amp).to(TDT[dtype]).cuda()
+    q, k, v = mk(Sq), mk(Sk), mk(Sk)
+    do = torch.randn(B, H, Sq, D, generator=g).to(TDT[dtype]).cuda()
+    return q, k, v, do
+
+
+def _rel_err(got, want):
+    want = torch.as_tensor(want)
+    return orc.max_abs_err(got.cpu(), want) / max(float(want.abs().max()), 1e-3)
+
+
+CASES = [
+    # dtype, B, H, Sq, Sk, D, causal, scale (None = 1/sqrt(D))
+    ("fp16", 1, 2, 128, 128, 64, False, None),
+    ("fp16", 2, 2, 200, 300, 64, True, None),     # ragged, causal Sq < Sk
+    ("bf16", 1, 2, 300, 130, 64, True, None),     # causal Sq > Sk
+    ("fp16", 1, 2, 256, 77, 128, False, None),    # short keys, D = 128
+    ("bf16", 1, 3, 333, 257, 96, False, None),    # D below its 128 bucket
+    ("fp16", 1, 1, 100, 500, 40, True, None),     # D = 40 (padded to 48 by the binding)
+    ("fp16", 1, 2, 64, 1024, 64, False, -0.2),    # negative scale, key split in the forward
+    ("bf16", 2, 1, 1, 33, 128, False, None),      # one query row
+    ("fp16", 1, 1, 37, 1, 64, True, None),        # one key
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}-q{c[3]}k{c[4]}d{c[5]}{'c' if c[6] else ''}"
+                                             f"{'' if c[7] is None else 's' + str(c[7])}" for c in CASES])
+def test_fwd_lse_and_bwd_parity(case):
+    dtype, B, H, Sq, Sk, D, causal, scale = case
+    q, k, v, do = _inputs(dtype, B, H, Sq, Sk, D, seed=Sq * 7 + Sk)
+    s = D ** -0.5 if scale is None else scale
+    if D % 8 == 0:   # the C ABI itself (the binding pads other head dims)
+        out, lse = abi.attn_fwd_lse(q, k, v, s, causal)
+        dq, dk, dv = abi.attn_bwd(q, k, v, out, do, lse, s, causal)
+    else:
+        out, lse = cmpext3.ops.attention_fwd_lse(q, k, v, s, causal)
+        dq, dk, dv = cmpext3.ops.attention_bwd(q, k, v, out, do, lse, s, causal)
+    torch.cuda.synchronize()
+    qc, kc, vc, dc = (t.cpu() for t in (q, k, v, do))
+    assert orc.max_abs_err(out.cpu(), orc.sdpa_np(qc, kc, vc, s, causal)) <= TOL[dtype]
+    assert orc.max_abs_err(lse.cpu(), orc.sdpa_lse_np(qc, kc, s, causal)) <= TOL[dtype]
+    want = orc.sdpa_bwd_np(qc, kc, vc, dc, s, causal)
+    for name, got, ref in zip(("dq", "dk", "dv"), (dq, dk, dv), want):
+        assert _rel_err(got, ref) <= TOL[dtype], name
+
+
+def test_bwd_wide_scores():
+    """Scores spread over tens of log2 units: P spans many orders of magnitude."""
+    q, k, v, do = _inputs("fp16", 1, 2, 160, 700, 64, seed=5, amp=2.5)
+    out, lse = abi.attn_fwd_lse(q, k, v, 0.125, False)
+    dq, dk, dv = abi.attn_bwd(q, k, v, out, do, lse, 0.125, False)
+    torch.cuda.synchronize()
+    want = orc.sdpa_bwd_np(q.cpu(), k.cpu(), v.cpu(), do.cpu(), 0.125, False)
+    for got, ref in zip((dq, dk, dv), want):
+        assert _rel_err(got, ref) <= TOL["fp16"]
+
+
+def test_bwd_is_deterministic():
+    q, k, v, do = _inputs("bf16", 2, 2, 300, 600, 64, seed=9)
+    out, lse = abi.attn_fwd_lse(q, k, v, 0.125, True)
+    first = abi.attn_bwd(q, k, v, out, do, lse, 0.125, True)
+    second = abi.attn_bwd(q, k, v, out, do, lse, 0.125, True)
+    torch.cuda.synchronize()
+    for a, b in zip(first, second):
+        assert torch.equal(a, b)
+
+
+def test_bwd_strided_views():
+    """[B,S,H,D] memory viewed as [B,H,S,D] for every operand and gradient."""
+    B, S, H, D = 1, 192, 4, 64
+    g = torch.Generator().manual_seed(3)
+    mk = lambda: torch.randn(B, S, H, D, generator=g).half().cuda().transpose(1, 2)
+    q, k, v, do = mk(), mk(), mk(), mk()
+    assert not q.is_contiguous()
+    out, lse = abi.attn_fwd_lse(q, k, v, 0.125, True)
+    dq, dk, dv = (torch.empty(B, S, H, D, dtype=torch.float16, device="cuda").transpose(1, 2)
+                  for _ in range(3))
+    delta = torch.empty(B, H, S, device="cuda")
+    assert abi.attn_bwd_raw(q, k, v, out, do, lse, dq, dk, dv, delta, 0.125, True) == abi.OK
+    torch.cuda.synchronize()
+    want = orc.sdpa_bwd_np(q.cpu(), k.cpu(), v.cpu(), do.cpu(), 0.125, True)
+    for got, ref in zip((dq, dk, dv), want):
+        assert _rel_err(got, ref) <= TOL["fp16"]
+
+
+def test_bwd_headline_shape_heads_and_identities():
+    """SDXL self-attention shape [2,10,4096,64] fp16: two heads against the
+    oracle, and over every head the identities the mathematics fixes (the dK
+    rows sum to zero, the dV rows sum to the dO rows)."""
+    q, k, v, do = _inputs("fp16", 2, 10, 4096, 4096, 64, seed=1)
+    out, lse = abi.attn_fwd_lse(q, k, v, 0.125, False)
+    dq, dk, dv = abi.attn_bwd(q, k, v, out, do, lse, 0.125, False)
+    torch.cuda.synchronize()
+    for b, h in ((0, 0), (1, 9)):
+        sl = lambda t: t[b:b + 1, h:h + 1].cpu()
+        want = orc.sdpa_bwd_np(sl(q), sl(k), sl(v), sl(do), 0.125, False)
+        for got, ref in zip((dq, dk, dv), want):
+            assert _rel_err(sl(got), ref) <= TOL["fp16"]
+    # each identity's violation relative to the L1 mass of the summed rows
+    # (rounding noise leaves ~1e-3; a wrong Delta or P transpose leaves O(1))
+    dk64, dv64, do64 = dk.double(), dv.double(), do.double()
+    assert float((dk64.sum(dim=2).abs() / dk64.abs().sum(dim=2)).max()) <= 1e-2
+    assert float(((dv64.sum(dim=2) - do64.sum(dim=2)).abs() / dv64.abs().sum(dim=2)).max()) <= 1e-2
+
+
+def test_autograd_function_matches_oracle():
+    q, k, v, do = _inputs("bf16", 1, 2, 150, 220, 64, seed=4)
+    q, k, v = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out = cmpext3.attention(q, k, v, None, True)
+    out.backward(do)
+    torch.cuda.synchronize()
+    want = orc.sdpa_bwd_np(q.detach().cpu(), k.detach().cpu(), v.detach().cpu(), do.cpu(), None, True)
+    for got, ref in zip((q.grad, k.grad, v.grad), want):
+        assert _rel_err(got, ref) <= TOL["bf16"]
+
+
+def test_sdpa_training_route(patched):
+    """With enable_backward(), SDPA with live autograd runs the native pair;
+    without it, stock (the reference's behaviour)."""
+    q, k, v, do = _inputs("fp16", 2, 2, 128, 256, 64, seed=6)
+    calls = {"fwd": 0, "bwd": 0}
+    real = cmpext3._C
+
+    class Counting:
+        attention = staticmethod(real.attention)
+
+        @staticmethod
+        def attention_fwd_lse(*a):
+            calls["fwd"] += 1
+            return real.attention_fwd_lse(*a)
+
+        @staticmethod
+        def attention_bwd(*a):
+            calls["bwd"] += 1
+            return real.attention_bwd(*a)
+
+    old, was = cmpext3._C, cmpext3.backward_enabled()
+    cmpext3._C = Counting
+    try:
+        for flag in (False, True):
+            cmpext3.enable_backward(flag)
+            qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+            out = F.scaled_dot_product_attention(qq, kk, vv, is_causal=True)
+            out.backward(do)
+            torch.cuda.synchronize()
+            assert calls == ({"fwd": 1, "bwd": 1} if flag else {"fwd": 0, "bwd": 0})
+            want = orc.sdpa_bwd_np(q.cpu(), k.cpu(), v.cpu(), do.cpu(), None, True)
+            for got, ref in zip((qq.grad, kk.grad, vv.grad), want):
+                assert _rel_err(got, ref) <= TOL["fp16"]
+    finally:
+        cmpext3._C = old
+        cmpext3.enable_backward(was)

@@ -23,6 +23,14 @@ What runs where:
     argument the native op rejects (RuntimeError/TypeError), e.g. GQA head
     counts or an empty key sequence.
 
+Training (no counterpart in the reference, which is forward-only): with
+``CMPEXT3_BACKWARD=1`` in the environment, or after ``enable_backward()``,
+SDPA calls with live autograd on fp16/bf16 GPU tensors with D <= 128, equal
+head counts, no mask and no dropout run the native forward and backward
+kernels (``attention`` below, a torch.autograd.Function); everything else
+with live autograd still goes to stock.  Off by default, so the default
+behaviour is the reference's.
+
 Only the attention op of the reference is in this package: its other patched
 ops (linear, conv, norms, activations, ...) and its NVML clock/power side
 effect are deliberately absent.
@@ -49,7 +57,8 @@ ops = _C
 
 from . import autoselect  # noqa: E402
 
-__all__ = ["enable", "disable", "is_enabled", "autoselect_report", "ops", "autoselect"]
+__all__ = ["enable", "disable", "is_enabled", "autoselect_report", "ops", "autoselect",
+           "attention", "enable_backward", "backward_enabled"]
 
 _SUPPORTED_DTYPES = (torch.float16, torch.float32, torch.bfloat16)
 _ORIGINALS: dict[tuple[Any, str], Callable] = {}
@@ -117,6 +126,57 @@ _DTYPE_TAG = {torch.float16: "fp16", torch.float32: "fp32", torch.bfloat16: "bf1
 _MASK_DTYPES = (torch.bool, torch.float16, torch.bfloat16, torch.float32)
 
 
+_TRAIN_DTYPES = (torch.float16, torch.bfloat16)
+_BACKWARD = os.environ.get("CMPEXT3_BACKWARD", "0") == "1"
+
+
+def enable_backward(flag: bool = True) -> None:
+    """Send SDPA calls with live autograd to the native forward/backward pair
+    (where it applies) instead of stock torch."""
+    global _BACKWARD
+    _BACKWARD = bool(flag)
+
+
+def backward_enabled() -> bool:
+    return _BACKWARD
+
+
+class _Attention(torch.autograd.Function):
+    """softmax(scale * Q K^T [causal]) V with the native backward: the forward
+    keeps the row log-sum-exp, the backward recomputes P from it (three
+    kernels: Delta, dK/dV, dQ; no atomics)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, scale, causal):
+        out, lse = _C.attention_fwd_lse(q, k, v, scale, causal)
+        ctx.save_for_backward(q, k, v, out, lse)
+        ctx.scale, ctx.causal = scale, causal
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        q, k, v, out, lse = ctx.saved_tensors
+        dq, dk, dv = _C.attention_bwd(q, k, v, out, grad_out, lse, ctx.scale, ctx.causal)
+        return dq, dk, dv, None, None
+
+
+def attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+              scale: float | None = None, causal: bool = False) -> torch.Tensor:
+    """Differentiable native attention (fp16/bf16 GPU tensors [B, H, S, D],
+    D <= 128, K/V with Q's head count).  Raises RuntimeError for anything else."""
+    return _Attention.apply(query, key, value, scale, causal)
+
+
+def _training_applies(query, key, value, attn_mask, dropout_p) -> bool:
+    return (_BACKWARD and attn_mask is None and dropout_p == 0.0
+            and all(isinstance(t, torch.Tensor) and t.is_cuda and t.dim() == 4
+                    and t.dtype == query.dtype for t in (query, key, value))
+            and query.dtype in _TRAIN_DTYPES
+            and key.shape[0] == query.shape[0] and key.shape[1] == query.shape[1]
+            and key.shape[3] == query.shape[3] and value.shape == key.shape
+            and 1 <= query.shape[3] <= 128 and key.shape[2] > 0)
+
+
 def _dispatch(op: str, ref: torch.Tensor, key: tuple,
               native_call: Callable, stock_call: Callable) -> Any:
     """Serve one call from the native kernel or stock torch.
@@ -159,6 +219,12 @@ def _patched_sdpa(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=Fa
         return orig(query, key, value, attn_mask=attn_mask, dropout_p=dropout_p,
                     is_causal=is_causal, scale=scale, **kwargs)
 
+    if (isinstance(query, torch.Tensor) and not _grad_safe(query, key, value, attn_mask)
+            and _training_applies(query, key, value, attn_mask, dropout_p)):
+        try:
+            return _Attention.apply(query, key, value, scale, is_causal)
+        except (RuntimeError, TypeError):
+            return stock()
     if (dropout_p != 0.0
             or not isinstance(query, torch.Tensor) or query.dim() != 4
             or not _grad_safe(query, key, value, attn_mask)

@@ -14,10 +14,12 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcmpext3_
 
 # Every function include/cmpext3_attn.h declares.
 SYMBOLS = ("cmpext3_attn_fwd", "cmpext3_attn_fwd_gqa", "cmpext3_attn_fwd_masked",
+           "cmpext3_attn_fwd_lse", "cmpext3_attn_bwd",
            "cmpext3_attn_strerror", "cmpext3_attn_abi_version", "cmpext3_attn_describe")
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_BOOL = 0, 1, 2, 3
-OK, E_INVALID, E_DTYPE, E_HEAD_DIM, E_ALIGN, E_EMPTY_KEYS, E_LAUNCH, E_TOO_LARGE, E_MASK = range(9)
+(OK, E_INVALID, E_DTYPE, E_HEAD_DIM, E_ALIGN, E_EMPTY_KEYS, E_LAUNCH, E_TOO_LARGE, E_MASK,
+ E_TRAINING) = range(10)
 
 _lib = None
 
@@ -41,6 +43,11 @@ def lib() -> ctypes.CDLL:
                                               i64p, i64p, i64p, i64p, vp, ci, i64p,
                                               ctypes.c_float, ci, vp]
         L.cmpext3_attn_fwd_masked.restype = ci
+        L.cmpext3_attn_fwd_lse.argtypes = [vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci,
+                                           i64p, i64p, i64p, i64p, ctypes.c_float, ci, vp]
+        L.cmpext3_attn_fwd_lse.restype = ci
+        L.cmpext3_attn_bwd.argtypes = [vp] * 10 + [ci] * 6 + [i64p] * 8 + [ctypes.c_float, ci, vp]
+        L.cmpext3_attn_bwd.restype = ci
         L.cmpext3_attn_strerror.argtypes = [ci]
         L.cmpext3_attn_strerror.restype = ctypes.c_char_p
         L.cmpext3_attn_abi_version.argtypes = []
@@ -134,3 +141,59 @@ def attn_fwd(q, k, v, scale: Optional[float] = None, causal: bool = False, strea
     if rc != OK:
         raise RuntimeError(f"cmpext3_attn_fwd: {strerror(rc)} (code {rc})")
     return o
+
+
+def _handle(t, stream):
+    import torch
+    if stream is None:
+        return torch.cuda.current_stream(t.device).cuda_stream
+    return stream if isinstance(stream, int) else stream.cuda_stream
+
+
+def attn_fwd_lse(q, k, v, scale: Optional[float] = None, causal: bool = False, stream=None):
+    """Training forward through cmpext3_attn_fwd_lse: returns (O, lse) with
+    lse the fp32 [B,H,Sq] natural-log row log-sum-exp.  Raises RuntimeError on
+    a non-zero return code."""
+    import torch
+    B, H, Sq, D = q.shape
+    o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    lse = torch.empty(B, H, Sq, dtype=torch.float32, device=q.device)
+    if scale is None:
+        scale = D ** -0.5
+    rc = lib().cmpext3_attn_fwd_lse(
+        ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()),
+        ctypes.c_void_p(o.data_ptr()), ctypes.c_void_p(lse.data_ptr()), dtype_code(q.dtype),
+        B, H, Sq, k.shape[2], D, _strides(q), _strides(k), _strides(v), _strides(o),
+        ctypes.c_float(scale), int(causal), ctypes.c_void_p(_handle(q, stream)))
+    if rc != OK:
+        raise RuntimeError(f"cmpext3_attn_fwd_lse: {strerror(rc)} (code {rc})")
+    return o, lse
+
+
+def attn_bwd_raw(q, k, v, o, do, lse, dq, dk, dv, delta, scale: float, causal: bool = False,
+                 stream=None) -> int:
+    """Call cmpext3_attn_bwd on caller-allocated tensors; returns the C code."""
+    B, H, Sq, D = q.shape
+    vp = ctypes.c_void_p
+    return lib().cmpext3_attn_bwd(
+        *(vp(t.data_ptr()) for t in (q, k, v, o, do, lse, dq, dk, dv, delta)),
+        dtype_code(q.dtype), B, H, Sq, k.shape[2], D,
+        *(_strides(t) for t in (q, k, v, o, do, dq, dk, dv)),
+        ctypes.c_float(scale), int(causal), vp(_handle(q, stream)))
+
+
+def attn_bwd(q, k, v, o, do, lse, scale: Optional[float] = None, causal: bool = False, stream=None):
+    """Gradients (dq, dk, dv) through cmpext3_attn_bwd (outputs contiguous, a
+    delta workspace allocated here).  Raises RuntimeError on a non-zero code."""
+    import torch
+    B, H, Sq, D = q.shape
+    dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+    dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+    delta = torch.empty(B, H, Sq, dtype=torch.float32, device=q.device)
+    if scale is None:
+        scale = D ** -0.5
+    rc = attn_bwd_raw(q, k, v, o, do, lse, dq, dk, dv, delta, scale, causal, stream)
+    if rc != OK:
+        raise RuntimeError(f"cmpext3_attn_bwd: {strerror(rc)} (code {rc})")
+    return dq, dk, dv

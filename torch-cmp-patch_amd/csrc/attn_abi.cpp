@@ -14,7 +14,10 @@
 #include "../../include/cmpext3_attn.h"
 #include "attn_common.h"
 
+#include "attn_bwd16.h"
+
 namespace cmpext3 {
+hipError_t launch_bwd16(const BwdParams& p, bool bf16, bool causal, hipStream_t s);
 hipError_t launch_mfma16(const FwdParams& p, bool bf16, bool causal, hipStream_t s);
 hipError_t launch_mfma32(const FwdParams& p, bool causal, hipStream_t s);
 int mfma16_bucket(int D);
@@ -81,6 +84,8 @@ const char* cmpext3_attn_strerror(int code) {
     case CMPEXT3_E_TOO_LARGE: return "problem too large for 32-bit tile indexing";
     case CMPEXT3_E_MASK:
       return "attention mask not supported here (needs f16/bf16 q, head dim <= 128, non-causal)";
+    case CMPEXT3_E_TRAINING:
+      return "not supported by the training entry points (need f16/bf16 and head dim <= 128)";
   }
   return "unknown error code";
 }
@@ -121,11 +126,15 @@ int cmpext3_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o, i
                                  nullptr, -1, nullptr, scale, causal, stream);
 }
 
-int cmpext3_attn_fwd_masked(const void* q, const void* k, const void* v, void* o, int dtype, int B,
-                            int H, int H_kv, int Sq, int Sk, int D, const int64_t q_str[3],
-                            const int64_t k_str[3], const int64_t v_str[3], const int64_t o_str[3],
-                            const void* mask, int mask_dtype, const int64_t mask_str[3], float scale,
-                            int causal, hipStream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// Forward with every option; lse (may be null) receives the row log-sum-exp.
+int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, int dtype, int B, int H,
+             int H_kv, int Sq, int Sk, int D, const int64_t q_str[3], const int64_t k_str[3],
+             const int64_t v_str[3], const int64_t o_str[3], const void* mask, int mask_dtype,
+             const int64_t mask_str[3], float scale, int causal, hipStream_t stream) {
   int rc = check_shape(dtype, B, H, Sq, Sk, D);
   if (rc != CMPEXT3_OK) return rc;
   if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;
@@ -165,6 +174,7 @@ int cmpext3_attn_fwd_masked(const void* q, const void* k, const void* v, void* o
   p.B = B; p.H = H; p.Sq = Sq; p.Sk = Sk; p.D = D;
   p.kv_group = H / H_kv;  // query head h reads K/V head h / kv_group
   p.mask_kind = cmpext3::MASK_NONE;
+  p.lse = lse;
   if (masked) {
     p.mask = mask;
     p.m_b = mask_str[0]; p.m_h = mask_str[1]; p.m_q = mask_str[2];
@@ -181,6 +191,88 @@ int cmpext3_attn_fwd_masked(const void* q, const void* k, const void* v, void* o
     err = cmpext3::launch_mfma32(p, causal != 0, stream);
   else
     err = cmpext3::launch_mfma16(p, dtype == CMPEXT3_DTYPE_BF16, causal != 0, stream);
+  return err == hipSuccess ? CMPEXT3_OK : CMPEXT3_E_LAUNCH;
+}
+
+// Row offsets of one 32-row tile past the last row stay below 2^31 bytes.
+bool tile_offsets_fit(int S, int64_t s0, int64_t s1) {
+  const int64_t rs = s0 > s1 ? s0 : s1;
+  return (int64_t)(S + 64) * rs * 2 < INT32_MAX;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cmpext3_attn_fwd_masked(const void* q, const void* k, const void* v, void* o, int dtype, int B,
+                            int H, int H_kv, int Sq, int Sk, int D, const int64_t q_str[3],
+                            const int64_t k_str[3], const int64_t v_str[3], const int64_t o_str[3],
+                            const void* mask, int mask_dtype, const int64_t mask_str[3], float scale,
+                            int causal, hipStream_t stream) {
+  return fwd_impl(q, k, v, o, nullptr, dtype, B, H, H_kv, Sq, Sk, D, q_str, k_str, v_str, o_str, mask,
+                  mask_dtype, mask_str, scale, causal, stream);
+}
+
+int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, float* lse, int dtype,
+                         int B, int H, int Sq, int Sk, int D, const int64_t q_str[3],
+                         const int64_t k_str[3], const int64_t v_str[3], const int64_t o_str[3],
+                         float scale, int causal, hipStream_t stream) {
+  const int rc = check_shape(dtype, B, H, Sq, Sk, D);
+  if (rc != CMPEXT3_OK) return rc;
+  if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;
+  if (dtype == CMPEXT3_DTYPE_F32 || D > 128) return CMPEXT3_E_TRAINING;
+  if (!lse || ((uintptr_t)lse & 3u) != 0) return CMPEXT3_E_INVALID;
+  if (!k_str || !v_str) return CMPEXT3_E_INVALID;
+  // the pipelined kernel (the one that writes the log-sum-exp) addresses K/V
+  // tiles with 32-bit buffer offsets
+  if (!tile_offsets_fit(Sk, k_str[2], v_str[2])) return CMPEXT3_E_TOO_LARGE;
+  return fwd_impl(q, k, v, o, lse, dtype, B, H, H, Sq, Sk, D, q_str, k_str, v_str, o_str, nullptr, -1,
+                  nullptr, scale, causal, stream);
+}
+
+int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                     const float* lse, void* dq, void* dk, void* dv, float* delta, int dtype, int B,
+                     int H, int Sq, int Sk, int D, const int64_t q_str[3], const int64_t k_str[3],
+                     const int64_t v_str[3], const int64_t o_str[3], const int64_t do_str[3],
+                     const int64_t dq_str[3], const int64_t dk_str[3], const int64_t dv_str[3],
+                     float scale, int causal, hipStream_t stream) {
+  const int rc = check_shape(dtype, B, H, Sq, Sk, D);
+  if (rc != CMPEXT3_OK) return rc;
+  if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;
+  if (dtype == CMPEXT3_DTYPE_F32 || D > 128) return CMPEXT3_E_TRAINING;
+  if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv || !delta) return CMPEXT3_E_INVALID;
+  if (!q_str || !k_str || !v_str || !o_str || !do_str || !dq_str || !dk_str || !dv_str)
+    return CMPEXT3_E_INVALID;
+  if (!isfinite(scale)) return CMPEXT3_E_INVALID;
+  if (((uintptr_t)lse & 3u) != 0 || ((uintptr_t)delta & 3u) != 0) return CMPEXT3_E_ALIGN;
+  const void* ptrs[] = {q, k, v, o, dout, dq, dk, dv};
+  for (const void* ptr : ptrs)
+    if (!aligned16(ptr)) return CMPEXT3_E_ALIGN;
+  if (!stride_ok(q_str, B, H, Sq, 2) || !stride_ok(o_str, B, H, Sq, 2) || !stride_ok(do_str, B, H, Sq, 2) ||
+      !stride_ok(dq_str, B, H, Sq, 2) || !stride_ok(k_str, B, H, Sk, 2) || !stride_ok(v_str, B, H, Sk, 2) ||
+      !stride_ok(dk_str, B, H, Sk, 2) || !stride_ok(dv_str, B, H, Sk, 2))
+    return CMPEXT3_E_ALIGN;
+  // Q/dO tiles (dK/dV kernel) and K/V tiles (dQ kernel) use 32-bit buffer offsets
+  if (!tile_offsets_fit(Sq, q_str[2], do_str[2]) || !tile_offsets_fit(Sk, k_str[2], v_str[2]))
+    return CMPEXT3_E_TOO_LARGE;
+
+  cmpext3::BwdParams p;
+  memset(&p, 0, sizeof p);
+  p.q = q; p.k = k; p.v = v; p.o = o; p.dout = dout; p.lse = lse;
+  p.dq = dq; p.dk = dk; p.dv = dv; p.delta = delta;
+  p.q_b = q_str[0]; p.q_h = q_str[1]; p.q_s = q_str[2];
+  p.k_b = k_str[0]; p.k_h = k_str[1]; p.k_s = k_str[2];
+  p.v_b = v_str[0]; p.v_h = v_str[1]; p.v_s = v_str[2];
+  p.o_b = o_str[0]; p.o_h = o_str[1]; p.o_s = o_str[2];
+  p.do_b = do_str[0]; p.do_h = do_str[1]; p.do_s = do_str[2];
+  p.dq_b = dq_str[0]; p.dq_h = dq_str[1]; p.dq_s = dq_str[2];
+  p.dk_b = dk_str[0]; p.dk_h = dk_str[1]; p.dk_s = dk_str[2];
+  p.dv_b = dv_str[0]; p.dv_h = dv_str[1]; p.dv_s = dv_str[2];
+  p.B = B; p.H = H; p.Sq = Sq; p.Sk = Sk; p.D = D;
+  p.c = fabsf(scale) * cmpext3::kLog2e;
+  p.scale = scale;
+  p.sign = scale < 0.f ? 0x80008000u : 0u;
+  const hipError_t err = cmpext3::launch_bwd16(p, dtype == CMPEXT3_DTYPE_BF16, causal != 0, stream);
   return err == hipSuccess ? CMPEXT3_OK : CMPEXT3_E_LAUNCH;
 }
 

@@ -1,0 +1,445 @@
+// Backward pass of the fused attention, fp16 / bf16 on gfx950
+// (v_mfma_f32_32x32x16_{f16,bf16}), head-dim buckets 64 and 128.
+//
+// Given Q, K, V, the forward output O, its gradient dO and the forward's row
+// log-sum-exp (natural log, written by the forward's training variant), with
+// P = softmax(S), S = scale * Q K^T (causal: top-left, key j visible to
+// query i iff j <= i):
+//   Delta_i = sum_d dO_id O_id                     (attn_bwd_delta)
+//   dV = P^T dO,  dK = scale * dS^T Q              (attn_bwd_dkdv, per key block)
+//   dQ = scale * dS K                              (attn_bwd_dq, per query block)
+//   with dP = dO V^T and dS = P * (dP - Delta).
+// P is recomputed from the scores and the saved log-sum-exp, so nothing of
+// size Sq x Sk is stored.  The two gradient kernels each own their output rows
+// outright (no atomics, no accumulation across workgroups), so the results are
+// bit-identical from run to run.  The reference is forward-only (its patch
+// hands calls with live autograd to stock torch, cmpext3/__init__.py:115-125);
+// this is the gradient of the same forward, checked against the float64
+// restatement in oracle/sdpa_oracle.py (sdpa_bwd_np).
+//
+// Layout: one 32 x 32 MFMA accumulator holds scores for 32 queries x 32 keys.
+// The dK/dV kernel keeps lane = key: S = Q K^T and dP = dO V^T take their B
+// operand (8 head-dim values of the lane's key) from registers loaded once,
+// their A operand (query rows) from the LDS tile; P and dS then sit in the
+// lanes exactly as the B operand of dV^T = dO^T P and dK^T = Q^T dS needs them
+// (8 consecutive queries per lane, thanks to the bit-permuted row feed), and
+// dO^T / Q^T come from the same LDS tiles through ds_read_b64_tr_b16.  The dQ
+// kernel mirrors the forward: lane = query, S^T = K Q^T, dP^T = V dO^T,
+// dQ^T = K^T dS^T.  A negative scale is folded into the sign of the operand
+// held in registers (K in dK/dV, Q in dQ), and the signed scale multiplies the
+// result.
+#pragma once
+
+#include "attn_fwd_pipe16.h"
+
+namespace cmpext3 {
+
+struct BwdParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;
+  const void* dout;
+  const float* lse;  // [B*H, Sq] row log-sum-exp of scale * Q K^T (natural log)
+  void* dq;
+  void* dk;
+  void* dv;
+  float* delta;      // [B*H, Sq] workspace: sum_d dO * O per row
+  // element strides of dims {batch, head, seq}; head-dim stride is 1
+  int64_t q_b, q_h, q_s, k_b, k_h, k_s, v_b, v_h, v_s, o_b, o_h, o_s, do_b, do_h, do_s;
+  int64_t dq_b, dq_h, dq_s, dk_b, dk_h, dk_s, dv_b, dv_h, dv_s;
+  int B, H, Sq, Sk, D;
+  int n_blk;        // key blocks (dK/dV) or query blocks (dQ) per (batch, head)
+  int n_wg;         // workgroups launched = B * H * n_blk
+  float c;          // |scale| * log2(e)
+  float scale;      // signed scale: dK = scale * dS^T Q, dQ = scale * dS K
+  uint32_t sign;    // 0x80008000 when scale < 0 (XORed into K or Q words), else 0
+};
+
+// ---- Delta_i = sum_d dO_id * O_id (fp32), 8 lanes per row
+template <typename T>
+__global__ void __launch_bounds__(256) attn_bwd_delta(const BwdParams p) {
+  const int sub = threadIdx.x & 7;
+  const int64_t g = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);  // row over B*H*Sq
+  const bool live = g < (int64_t)p.B * p.H * p.Sq;
+  float acc = 0.f;
+  if (live) {
+    const int64_t bh = g / p.Sq;
+    const int i = (int)(g - bh * p.Sq);
+    const int b = (int)(bh / p.H), h = (int)(bh - (int64_t)b * p.H);
+    const uint16_t* orow = (const uint16_t*)p.o + b * p.o_b + h * p.o_h + (int64_t)i * p.o_s;
+    const uint16_t* drow = (const uint16_t*)p.dout + b * p.do_b + h * p.do_h + (int64_t)i * p.do_s;
+    for (int c8 = sub; 8 * c8 < p.D; c8 += 8) {
+      const u32x4 a = *(const u32x4*)(orow + 8 * c8);
+      const u32x4 d = *(const u32x4*)(drow + 8 * c8);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const f32x2 x = Elt<T>::unpack(a[w]), y = Elt<T>::unpack(d[w]);
+        acc = __builtin_fmaf(x[0], y[0], acc);
+        acc = __builtin_fmaf(x[1], y[1], acc);
+      }
+    }
+  }
+  acc += __shfl_xor(acc, 1, 8);
+  acc += __shfl_xor(acc, 2, 8);
+  acc += __shfl_xor(acc, 4, 8);
+  if (live && sub == 0) p.delta[g] = acc;
+}
+
+// One 32-row tile (rows r0.., DK columns) of a [rows, D] matrix into registers,
+// 16-byte chunks spread over the 256 threads; rows past `nrows` read as zero
+// (buffer bounds), chunks past D are zeroed.
+template <int DK>
+struct TileLoader {
+  static constexpr int KCH = DK / 8;
+  static constexpr int N = 32 * KCH / 256;  // chunks per thread
+  static_assert(32 * KCH % 256 == 0, "whole chunks per thread");
+  int voff[N], loff[N];
+  bool zero[N];
+  __device__ __forceinline__ void init(int tid, int64_t row_stride, int D, int RS) {
+#pragma unroll
+    for (int it = 0; it < N; ++it) {
+      const int ci = it * 256 + tid, r = ci / KCH, c8 = ci - r * KCH;
+      voff[it] = (int)(r * row_stride * 2) + 16 * c8;
+      loff[it] = r * RS + 8 * c8;
+      zero[it] = 8 * c8 >= D;
+    }
+  }
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, int soff, u32x4 (&x)[N]) const {
+#pragma unroll
+    for (int it = 0; it < N; ++it)
+      x[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff[it], soff, 0));
+  }
+  __device__ __forceinline__ void store(uint16_t* dst, const u32x4 (&x)[N]) const {
+#pragma unroll
+    for (int it = 0; it < N; ++it) *(u32x4*)(dst + loff[it]) = zero[it] ? (u32x4){0u, 0u, 0u, 0u} : x[it];
+  }
+};
+
+// A-operand fragment of X^T for a 16-row slice of a row-major LDS tile
+// (row = query or key, column = head dim): 8 consecutive rows of one column.
+__device__ __forceinline__ u32x4 tr_frag(const uint16_t* base, int off0, int off1) {
+  const uint2 lo = lds_tr16_b64(base + off0);
+  const uint2 hi = lds_tr16_b64(base + off1);
+  return (u32x4){lo.x, lo.y, hi.x, hi.y};
+}
+
+// Store a [32 rows x DP] accumulator set (C layout: lane = row l32, register
+// 4g + j of block db = column 32 db + 8 g + 4 hh + j) times `mul` as T.
+template <typename T, int NDB>
+__device__ __forceinline__ void store_rows(uint16_t* base, int64_t row_stride, int row, int nrows, int D, int hh,
+                                           const f32x16 (&acc)[NDB], float mul) {
+  if (row >= nrows) return;
+  uint16_t* dst = base + (int64_t)row * row_stride;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = 32 * db + 8 * g + 4 * hh;
+      if (d < D) {
+        u32x2 w;
+        w[0] = Elt<T>::pack(acc[db][4 * g + 0] * mul, acc[db][4 * g + 1] * mul);
+        w[1] = Elt<T>::pack(acc[db][4 * g + 2] * mul, acc[db][4 * g + 3] * mul);
+        *(u32x2*)(dst + d) = w;
+      }
+    }
+}
+
+// ---- dK, dV for one block of 128 keys (4 waves x 32 keys), sweeping the
+// query tiles (32 rows of Q, dO, lse, Delta) through double-buffered LDS.
+template <typename T, int DK, bool CAUSAL>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DK <= 64 ? 2 : 1)))
+attn_bwd_dkdv(const BwdParams p) {
+  constexpr int BQ = 32, BKV = 128;
+  constexpr int RS = DK + 8;  // LDS row stride (halves)
+  constexpr int NKS = DK / 16, NDB = DK / 32;
+  static_assert(DK % 32 == 0, "head-dim bucket");
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 2 * BQ * RS];  // [slot][Q, dO][row][col]
+  __shared__ __attribute__((aligned(16))) float lsd[2][2][BQ];            // [slot][lse2, Delta][row]
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  // key blocks in order (causal: the first blocks see the most queries, so
+  // they start first); XCD-contiguous ranges share Q/dO in L2
+  const int tile = xcd_remap(blockIdx.x, p.n_wg);
+  const int bh = tile / p.n_blk, kb = tile - bh * p.n_blk;
+  const int b = bh / p.H, h = bh - b * p.H;
+  const int Sq = p.Sq, Sk = p.Sk, D = p.D;
+  const int kw0 = kb * BKV + wave * 32;  // first key of this wave
+  const int key = kw0 + l32;             // this lane's key
+
+  // B operands held for the whole sweep: 8 head-dim values of this lane's key
+  const uint16_t* kg = (const uint16_t*)p.k + b * p.k_b + h * p.k_h;
+  const uint16_t* vg = (const uint16_t*)p.v + b * p.v_b + h * p.v_h;
+  u32x4 kf[NKS], vf[NKS];
+#pragma unroll
+  for (int s = 0; s < NKS; ++s) {
+    const int d = 16 * s + 8 * hh;
+    u32x4 x = {0u, 0u, 0u, 0u}, y = {0u, 0u, 0u, 0u};
+    if (key < Sk && d < D) {
+      x = *(const u32x4*)(kg + (int64_t)key * p.k_s + d);
+      y = *(const u32x4*)(vg + (int64_t)key * p.v_s + d);
+    }
+    kf[s] = x ^ p.sign;
+    vf[s] = y;
+  }
+
+  const uint16_t* qg = (const uint16_t*)p.q + b * p.q_b + h * p.q_h;
+  const uint16_t* dog = (const uint16_t*)p.dout + b * p.do_b + h * p.do_h;
+  const __amdgpu_buffer_rsrc_t qrs = uniform_rsrc(qg, ((int64_t)(Sq - 1) * p.q_s + D) * 2);
+  const __amdgpu_buffer_rsrc_t dors = uniform_rsrc(dog, ((int64_t)(Sq - 1) * p.do_s + D) * 2);
+  TileLoader<DK> lq, ldo;
+  lq.init(tid, p.q_s, D, RS);
+  ldo.init(tid, p.do_s, D, RS);
+  const float* lse_g = p.lse + (int64_t)bh * Sq;
+  const float* dlt_g = p.delta + (int64_t)bh * Sq;
+
+  // fragment read offsets: A = query rows (bit-permuted), A = X^T slices
+  int a_rd[NKS];
+  {
+    const int r = perm_row(l32);
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) a_rd[s] = r * RS + 16 * s + 8 * hh;
+  }
+  const int jj = lane & 15, gg = lane >> 4;
+  int t_rd[NDB][2];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+      t_rd[db][half] = (8 * (gg >> 1) + (jj >> 2) + 4 * half) * RS + 32 * db + 16 * (gg & 1) + 4 * (jj & 3);
+
+  f32x16 dva[NDB], dka[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) dva[db] = dka[db] = (f32x16){};
+
+  const int t0 = CAUSAL ? kb * (BKV / BQ) : 0;  // query tiles before the block see none of its keys
+  const int t1 = (Sq + BQ - 1) / BQ;
+  u32x4 xq[TileLoader<DK>::N], xd[TileLoader<DK>::N];
+  float xl = INFINITY, xdl = 0.f;
+  auto fetch = [&](int t) {
+    const int q0 = t * BQ;
+    lq.load(qrs, (int)(q0 * p.q_s * 2), xq);
+    ldo.load(dors, (int)(q0 * p.do_s * 2), xd);
+    if (tid < BQ) {
+      const int row = q0 + tid;
+      xl = row < Sq ? lse_g[row] * kLog2e : INFINITY;  // rows past Sq: P = 0
+      xdl = row < Sq ? dlt_g[row] : 0.f;
+    }
+  };
+  auto put = [&](int slot) {
+    uint16_t* base = lds + slot * 2 * BQ * RS;
+    lq.store(base, xq);
+    ldo.store(base + BQ * RS, xd);
+    if (tid < BQ) {
+      lsd[slot][0][tid] = xl;
+      lsd[slot][1][tid] = xdl;
+    }
+  };
+
+  const float c = p.c;
+  if (t0 < t1) {
+    fetch(t0);
+    put(0);
+  }
+  lds_barrier();
+  for (int t = t0; t < t1; ++t) {
+    const int slot = (t - t0) & 1;
+    if (t + 1 < t1) fetch(t + 1);
+    const int q0 = t * BQ;
+    // causal: a tile whose last query precedes this wave's first key adds nothing
+    if (!CAUSAL || q0 + BQ - 1 >= kw0) {
+      const uint16_t* qs = lds + slot * 2 * BQ * RS;
+      const uint16_t* dos = qs + BQ * RS;
+      f32x16 s = (f32x16){}, dp = (f32x16){};
+#pragma unroll
+      for (int st = 0; st < NKS; ++st) s = Elt<T>::mma(*(const u32x4*)(qs + a_rd[st]), kf[st], s);
+#pragma unroll
+      for (int st = 0; st < NKS; ++st) dp = Elt<T>::mma(*(const u32x4*)(dos + a_rd[st]), vf[st], dp);
+      // register r holds query q0 + acc_key(r, hh): two runs of 8 consecutive rows
+      float l2[16], dl[16];
+#pragma unroll
+      for (int run = 0; run < 2; ++run) {
+        const f32x4 a0 = *(const f32x4*)&lsd[slot][0][16 * run + 8 * hh];
+        const f32x4 a1 = *(const f32x4*)&lsd[slot][0][16 * run + 8 * hh + 4];
+        const f32x4 d0 = *(const f32x4*)&lsd[slot][1][16 * run + 8 * hh];
+        const f32x4 d1 = *(const f32x4*)&lsd[slot][1][16 * run + 8 * hh + 4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          l2[8 * run + i] = a0[i];
+          l2[8 * run + 4 + i] = a1[i];
+          dl[8 * run + i] = d0[i];
+          dl[8 * run + 4 + i] = d1[i];
+        }
+      }
+      const bool diag = CAUSAL && q0 < kw0 + 31;
+      float pr[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = __builtin_fmaf(s[r], c, -l2[r]);
+        if (diag && key > q0 + acc_key(r, hh)) x = -INFINITY;
+        pr[r] = fast_exp2(x);
+      }
+      u32x4 pp[2], ps[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 8 * ks + 2 * e;
+          pp[ks][e] = Elt<T>::pack(pr[r], pr[r + 1]);
+          ps[ks][e] = Elt<T>::pack(pr[r] * (dp[r] - dl[r]), pr[r + 1] * (dp[r + 1] - dl[r + 1]));
+        }
+      // dV^T += dO^T P, dK^T += Q^T dS (16 queries per k-step)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const uint16_t* dsl = dos + 16 * ks * RS;
+          dva[db] = Elt<T>::mma(tr_frag(dsl, t_rd[db][0], t_rd[db][1]), pp[ks], dva[db]);
+          const uint16_t* qsl = qs + 16 * ks * RS;
+          dka[db] = Elt<T>::mma(tr_frag(qsl, t_rd[db][0], t_rd[db][1]), ps[ks], dka[db]);
+        }
+    }
+    if (t + 1 < t1) put(slot ^ 1);
+    lds_barrier();
+  }
+
+  // lane = key, registers = head-dim columns
+  uint16_t* dkg = (uint16_t*)p.dk + b * p.dk_b + h * p.dk_h;
+  uint16_t* dvg = (uint16_t*)p.dv + b * p.dv_b + h * p.dv_h;
+  store_rows<T, NDB>(dvg, p.dv_s, key, Sk, D, hh, dva, 1.f);
+  store_rows<T, NDB>(dkg, p.dk_s, key, Sk, D, hh, dka, p.scale);
+}
+
+// ---- dQ for one block of 128 queries (4 waves x 32 queries), sweeping the
+// key tiles (32 rows of K and V) through double-buffered LDS.
+template <typename T, int DK, bool CAUSAL>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DK <= 64 ? 3 : 2)))
+attn_bwd_dq(const BwdParams p) {
+  constexpr int BQ = 128, BK = 32;
+  constexpr int RS = DK + 8;
+  constexpr int NKS = DK / 16, NDB = DK / 32;
+  static_assert(DK % 32 == 0, "head-dim bucket");
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 2 * BK * RS];  // [slot][K, V][row][col]
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  int bh, qblk;
+  {
+    FwdParams fp;
+    fp.B = p.B; fp.H = p.H; fp.n_qblk = p.n_blk; fp.n_wg = p.n_wg;
+    wg_tile(blockIdx.x, fp, CAUSAL, bh, qblk);  // causal: longest key sweeps first
+  }
+  const int b = bh / p.H, h = bh - b * p.H;
+  const int Sq = p.Sq, Sk = p.Sk, D = p.D;
+  const int qrow = qblk * BQ + wave * 32 + l32;  // this lane's query
+
+  // B operands held for the whole sweep: 8 head-dim values of this lane's query
+  const uint16_t* qg = (const uint16_t*)p.q + b * p.q_b + h * p.q_h;
+  const uint16_t* dog = (const uint16_t*)p.dout + b * p.do_b + h * p.do_h;
+  u32x4 qf[NKS], dof[NKS];
+#pragma unroll
+  for (int s = 0; s < NKS; ++s) {
+    const int d = 16 * s + 8 * hh;
+    u32x4 x = {0u, 0u, 0u, 0u}, y = {0u, 0u, 0u, 0u};
+    if (qrow < Sq && d < D) {
+      x = *(const u32x4*)(qg + (int64_t)qrow * p.q_s + d);
+      y = *(const u32x4*)(dog + (int64_t)qrow * p.do_s + d);
+    }
+    qf[s] = x ^ p.sign;
+    dof[s] = y;
+  }
+  const float l2 = qrow < Sq ? p.lse[(int64_t)bh * Sq + qrow] * kLog2e : INFINITY;  // past Sq: P = 0
+  const float dl = qrow < Sq ? p.delta[(int64_t)bh * Sq + qrow] : 0.f;
+
+  const uint16_t* kg = (const uint16_t*)p.k + b * p.k_b + h * p.k_h;
+  const uint16_t* vg = (const uint16_t*)p.v + b * p.v_b + h * p.v_h;
+  const __amdgpu_buffer_rsrc_t krs = uniform_rsrc(kg, ((int64_t)(Sk - 1) * p.k_s + D) * 2);
+  const __amdgpu_buffer_rsrc_t vrs = uniform_rsrc(vg, ((int64_t)(Sk - 1) * p.v_s + D) * 2);
+  TileLoader<DK> lk, lv;
+  lk.init(tid, p.k_s, D, RS);
+  lv.init(tid, p.v_s, D, RS);
+
+  int a_rd[NKS];
+  {
+    const int r = perm_row(l32);
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) a_rd[s] = r * RS + 16 * s + 8 * hh;
+  }
+  const int jj = lane & 15, gg = lane >> 4;
+  int t_rd[NDB][2];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+      t_rd[db][half] = (8 * (gg >> 1) + (jj >> 2) + 4 * half) * RS + 32 * db + 16 * (gg & 1) + 4 * (jj & 3);
+
+  f32x16 dqa[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) dqa[db] = (f32x16){};
+
+  const int kend = CAUSAL ? min(Sk, qblk * BQ + BQ) : Sk;  // keys any row of the block sees
+  const int nt = (kend + BK - 1) / BK;
+  const int wlast = qblk * BQ + wave * 32 + 31;            // this wave's last query
+  u32x4 xk[TileLoader<DK>::N], xv[TileLoader<DK>::N];
+  auto fetch = [&](int t) {
+    lk.load(krs, (int)(t * BK * p.k_s * 2), xk);
+    lv.load(vrs, (int)(t * BK * p.v_s * 2), xv);
+  };
+  auto put = [&](int slot) {
+    uint16_t* base = lds + slot * 2 * BK * RS;
+    lk.store(base, xk);
+    lv.store(base + BK * RS, xv);
+  };
+
+  const float c = p.c;
+  if (nt > 0) {
+    fetch(0);
+    put(0);
+  }
+  lds_barrier();
+  for (int t = 0; t < nt; ++t) {
+    const int slot = t & 1;
+    if (t + 1 < nt) fetch(t + 1);
+    const int k0 = t * BK;
+    if (!CAUSAL || k0 <= wlast) {  // causal: tiles past this wave's last query add nothing
+      const uint16_t* ks = lds + slot * 2 * BK * RS;
+      const uint16_t* vs = ks + BK * RS;
+      f32x16 s = (f32x16){}, dp = (f32x16){};
+#pragma unroll
+      for (int st = 0; st < NKS; ++st) s = Elt<T>::mma(*(const u32x4*)(ks + a_rd[st]), qf[st], s);
+#pragma unroll
+      for (int st = 0; st < NKS; ++st) dp = Elt<T>::mma(*(const u32x4*)(vs + a_rd[st]), dof[st], dp);
+      const bool edge = k0 + BK > Sk || (CAUSAL && k0 + BK - 1 > qblk * BQ + wave * 32);
+      u32x4 ps[2];
+#pragma unroll
+      for (int ks2 = 0; ks2 < 2; ++ks2)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float pv[2];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int r = 8 * ks2 + 2 * e + u;
+            float x = __builtin_fmaf(s[r], c, -l2);
+            if (edge) {
+              const int kk = k0 + acc_key(r, hh);
+              if (kk >= Sk || (CAUSAL && kk > qrow)) x = -INFINITY;
+            }
+            pv[u] = fast_exp2(x) * (dp[r] - dl);
+          }
+          ps[ks2][e] = Elt<T>::pack(pv[0], pv[1]);
+        }
+      // dQ^T += K^T dS^T (16 keys per k-step)
+#pragma unroll
+      for (int ks2 = 0; ks2 < 2; ++ks2)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+          dqa[db] = Elt<T>::mma(tr_frag(ks + 16 * ks2 * RS, t_rd[db][0], t_rd[db][1]), ps[ks2], dqa[db]);
+    }
+    if (t + 1 < nt) put(slot ^ 1);
+    lds_barrier();
+  }
+
+  uint16_t* dqg = (uint16_t*)p.dq + b * p.dq_b + h * p.dq_h;
+  store_rows<T, NDB>(dqg, p.dq_s, qrow, Sq, D, hh, dqa, p.scale);
+}
+
+}  // namespace cmpext3

@@ -35,6 +35,10 @@ struct FwdParams {
   const void* mask;
   int64_t m_b, m_h, m_q;
   int mask_kind;
+  // optional [B*H, Sq] fp32 output: natural-log log-sum-exp of each query
+  // row's scale * Q K^T over its visible keys (what a backward pass needs to
+  // rebuild P); null = not written.  Written by the pipelined kernel only.
+  float* lse;
 };
 
 // attention-mask element kinds (FwdParams::mask_kind)

@@ -78,7 +78,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base,
 // interleave to the compiler (no sched_barrier fences).  OPT bit 3: the head
 // dim is not a multiple of 16 (D < DK), so K columns past D are zeroed.
 // OPT bit 4: an attention mask (p.mask, non-causal launches) is applied to
-// every tile's scores before the exponentials.
+// every tile's scores before the exponentials.  OPT bit 5: each row's
+// log-sum-exp goes to p.lse (the training forward).
 template <typename T, int DK, int DP, int NW, int BK, int OCC, bool CAUSAL, bool PRESCALE, int OPT = 0>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
 attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
@@ -537,6 +538,7 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
 
   // ---- epilogue
   float lsum = xhalf_sum(ls0 + ls1);
+  float moff = mb;  // exp2-domain offset of lsum
   if (!CAUSAL && nparts > 1) {  // causal launches never split
     // Leave this part's state, then let the last part of the block merge.
     // Device-scope (sc1) stores and loads keep the exchange coherent across
@@ -571,6 +573,7 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
     // last, so a rerun is bit-identical.
     float mt = -INFINITY;
     for (int q = 0; q < nparts; ++q) mt = fmaxf(mt, ld_ws(voff(q, NDB * 4))[0]);
+    moff = mt;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) oacc[db] = (f32x16){};
     lsum = 0.f;
@@ -590,6 +593,12 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   }
   // a row that saw no key at all (every key masked) gives zeros, as torch does
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  // log-sum-exp in natural log: (offset + log2 of the sum) * ln 2
+  if constexpr ((OPT & 32) != 0) {
+    if (qrow < Sq && hh == 0)
+      p.lse[(int64_t)bh * Sq + qrow] =
+          lsum > 0.f ? (moff + __builtin_amdgcn_logf(lsum)) * 0.6931471805599453f : -INFINITY;
+  }
   if (qrow < Sq) {
     uint16_t* orow = og + (int64_t)qrow * p.o_s;
 #pragma unroll

@@ -132,6 +132,20 @@ hipError_t launch_dk(const FwdParams& p, const SplitArgs& sa, hipStream_t s) {
   return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, occ, CAUSAL, PRESCALE, 1 | 8 | MOPT>(p, sa, s);
 }
 
+// Training forward (OPT 32: write the row log-sum-exp): buckets 64 and 128 only.
+template <typename T, bool CAUSAL, bool PRESCALE>
+hipError_t launch_lse(const FwdParams& p, const SplitArgs& sa, int dk, hipStream_t s) {
+  if (dk == 64) {
+    if (p.D == 64) return launch_pipe16_cfg<T, 64, kPipeNw, kPipeBk, pipe_occ(64), CAUSAL, PRESCALE, 1 | 32>(p, sa, s);
+    return launch_pipe16_cfg<T, 64, kPipeNw, kPipeBk, pipe_occ(64), CAUSAL, PRESCALE, 1 | 8 | 32>(p, sa, s);
+  }
+  if (dk == 128) {
+    if (p.D == 128) return launch_pipe16_cfg<T, 128, kPipeNw, kPipeBk, pipe_occ(128), CAUSAL, PRESCALE, 1 | 32>(p, sa, s);
+    return launch_pipe16_cfg<T, 128, kPipeNw, kPipeBk, pipe_occ(128), CAUSAL, PRESCALE, 1 | 8 | 32>(p, sa, s);
+  }
+  return hipErrorNotSupported;
+}
+
 template <typename T, bool CAUSAL, bool PRESCALE, int MOPT = 0>
 hipError_t launch_bucket(const FwdParams& p, const SplitArgs& sa, int dk, hipStream_t s) {
   switch (dk) {
@@ -152,13 +166,13 @@ int n_key_tiles(int Sk) { return (Sk + kPipeBk - 1) / kPipeBk; }
 
 // True when the pipelined kernel takes this problem: head-dim bucket <= 128,
 // a key sweep long enough for its prologue (four tiles in flight) to pay off
-// (SDXL cross-attention, Sk = 77, is faster on the v2 kernel) unless an
-// attention mask is given (only this kernel applies masks), and K/V tiles
-// addressable with 32-bit buffer offsets.
+// (shorter sweeps run faster on the short-key and v2 kernels) unless an
+// attention mask or the log-sum-exp output is asked for (only this kernel
+// has them), and K/V tiles addressable with 32-bit buffer offsets.
 constexpr int kPipeMinSk = 256;
 
 bool pipe16_applies(const FwdParams& p, int dk) {
-  if (dk > 128 || (p.Sk < kPipeMinSk && p.mask_kind == MASK_NONE)) return false;
+  if (dk > 128 || (p.Sk < kPipeMinSk && p.mask_kind == MASK_NONE && !p.lse)) return false;
   const int64_t rs = p.k_s > p.v_s ? p.k_s : p.v_s;
   return (int64_t)(p.Sk + kPipeBk) * rs * 2 < (int64_t(1) << 31);
 }
@@ -167,8 +181,10 @@ bool pipe16_applies(const FwdParams& p, int dk) {
 // never pre-scales: rounding Q*c to 8 mantissa bits moves each score by up to
 // 2^-9 of its size, which at scale 1 (scores of tens of log2 units) breaks
 // the 2e-2 bf16 bar, so bf16 scores get one FMA each instead.
-hipError_t launch_pipe16(const FwdParams& p0, int dk, bool bf16, bool causal, bool prescale, hipStream_t s) {
+hipError_t launch_pipe16(const FwdParams& p0, int dk0, bool bf16, bool causal, bool prescale, hipStream_t s) {
   FwdParams p = p0;
+  // the training forward has the 64 and 128 buckets only
+  const int dk = p.lse ? (dk0 <= 64 ? 64 : 128) : dk0;
   // Without pre-scaling, masked keys enter as raw -inf and meet the multiplier
   // c in one FMA; scale 0 would make that 0 * -inf.  A multiplier of 1e-30
   // instead leaves every finite score's exp2 argument within 1e-22 of -m,
@@ -185,6 +201,12 @@ hipError_t launch_pipe16(const FwdParams& p0, int dk, bool bf16, bool causal, bo
     } else {
       sa = SplitArgs{n_blocks(p.B, p.H, p.Sq), 1, nullptr, nullptr};
     }
+  }
+  if (p.lse) {  // training forward: unmasked (checked by the caller)
+    if (bf16) return causal ? launch_lse<__bf16, true, false>(p, sa, dk, s) : launch_lse<__bf16, false, false>(p, sa, dk, s);
+    if (prescale)
+      return causal ? launch_lse<_Float16, true, true>(p, sa, dk, s) : launch_lse<_Float16, false, true>(p, sa, dk, s);
+    return causal ? launch_lse<_Float16, true, false>(p, sa, dk, s) : launch_lse<_Float16, false, false>(p, sa, dk, s);
   }
   if (p.mask_kind != MASK_NONE) {  // masked launches are non-causal (checked by the caller)
     if (causal) return hipErrorNotSupported;

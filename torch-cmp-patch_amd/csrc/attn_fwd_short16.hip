@@ -37,7 +37,7 @@ int key_blocks(int Sk) { return Sk <= 64 ? 2 : Sk <= 96 ? 3 : 4; }
 }  // namespace
 
 bool short16_applies(const FwdParams& p, int dk, bool causal) {
-  if (causal || p.mask_kind != MASK_NONE || dk > 128 || p.Sk > 128) return false;
+  if (causal || p.mask_kind != MASK_NONE || p.lse || dk > 128 || p.Sk > 128) return false;
   const int64_t rs = p.k_s > p.v_s ? p.k_s : p.v_s;
   return (int64_t)128 * rs * 2 < (int64_t(1) << 31);
 }

@@ -20,7 +20,12 @@
 //   * attn_mask (bool or additive f16/bf16/f32, broadcast like torch's SDPA)
 //     runs natively for f16/bf16 with D <= 128 and causal=False (the
 //     reference sent every mask to stock torch, cmpext3/__init__.py:624).
+//
+// attention_fwd_lse / attention_bwd: the training pair (no reference
+// counterpart: the reference is forward-only, cmpext3/__init__.py:115-125),
+// used by cmpext3's autograd Function.
 #include <cmath>
+#include <vector>
 
 #include <torch/extension.h>
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
@@ -172,6 +177,124 @@ torch::Tensor attention(torch::Tensor query, torch::Tensor key, torch::Tensor va
   return out;
 }
 
+namespace {
+
+// Shared checks of the training entry points: 4-D GPU f16/bf16 tensors of one
+// dtype and device, equal head counts, head dim <= 128.
+int training_dtype(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v) {
+  TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4, "cmpext3 attention: q, k, v must be 4D");
+  TORCH_CHECK(q.is_cuda() && q.device() == k.device() && q.device() == v.device(),
+              "cmpext3 attention: tensors must be on one GPU");
+  TORCH_CHECK(q.scalar_type() == k.scalar_type() && q.scalar_type() == v.scalar_type(),
+              "cmpext3 attention: q, k, v must share one dtype");
+  const int dtype = dtype_code(q.scalar_type());
+  TORCH_CHECK(dtype == CMPEXT3_DTYPE_F16 || dtype == CMPEXT3_DTYPE_BF16,
+              "cmpext3 attention: the training path takes fp16/bf16 only");
+  TORCH_CHECK(k.size(0) == q.size(0) && k.size(1) == q.size(1) && k.size(3) == q.size(3) &&
+                  v.sizes() == k.sizes(),
+              "cmpext3 attention: the training path needs K/V of Q's batch, heads and head dim");
+  TORCH_CHECK(q.size(3) >= 1 && q.size(3) <= 128, "cmpext3 attention: the training path needs D <= 128");
+  TORCH_CHECK(k.size(2) > 0 || q.size(0) * q.size(1) * q.size(2) == 0,
+              "cmpext3 attention: empty key sequence");
+  return dtype;
+}
+
+// The ABI's layout: unit head-dim stride, 16-byte aligned base and row strides,
+// head dim a multiple of 8 (zero-padded to Dp otherwise).
+torch::Tensor abi_layout(const torch::Tensor& t, int64_t Dp) {
+  const int64_t D = t.size(3);
+  if (Dp != D) return at::constant_pad_nd(t, {0, Dp - D}, 0).contiguous();
+  const bool ok = t.stride(3) == 1 && ((uintptr_t)t.data_ptr() & 15u) == 0 && t.stride(0) % 8 == 0 &&
+                  t.stride(1) % 8 == 0 && t.stride(2) % 8 == 0;
+  return ok ? t : t.contiguous();
+}
+
+void strides3(const torch::Tensor& t, int64_t s[3]) {
+  s[0] = t.stride(0); s[1] = t.stride(1); s[2] = t.stride(2);
+}
+
+float resolve_scale(c10::optional<double> scale_arg, int64_t D) {
+  const float scale = scale_arg.has_value() ? (float)scale_arg.value() : 1.0f / std::sqrt((float)D);
+  TORCH_CHECK(std::isfinite(scale), "cmpext3 attention: non-finite scale");
+  return scale;
+}
+
+}  // namespace
+
+// Training forward: (out, lse), lse = [B, H, Sq] fp32 natural-log row
+// log-sum-exp, the state attention_bwd needs.
+std::vector<torch::Tensor> attention_fwd_lse(torch::Tensor query, torch::Tensor key, torch::Tensor value,
+                                             c10::optional<double> scale_arg, bool causal) {
+  const int dtype = training_dtype(query, key, value);
+  const int64_t B = query.size(0), H = query.size(1), Sq = query.size(2), D = query.size(3);
+  const int64_t Sk = key.size(2), Dp = (D + 7) / 8 * 8;
+  const float scale = resolve_scale(scale_arg, D);
+  const at::hip::HIPGuardMasqueradingAsCUDA guard(query.device());
+  hipStream_t stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA(query.device().index()).stream();
+
+  torch::Tensor lse = torch::empty({B, H, Sq}, query.options().dtype(at::kFloat));
+  torch::Tensor out = torch::empty({B, H, Sq, Dp}, query.options());
+  if (out.numel() == 0) return {Dp == D ? out : out.narrow(3, 0, D), lse};
+  const torch::Tensor q = abi_layout(query, Dp), k = abi_layout(key, Dp), v = abi_layout(value, Dp);
+  int64_t qs[3], ks[3], vs[3], os[3];
+  strides3(q, qs); strides3(k, ks); strides3(v, vs); strides3(out, os);
+  const int rc = cmpext3_attn_fwd_lse(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                      lse.data_ptr<float>(), dtype, (int)B, (int)H, (int)Sq, (int)Sk,
+                                      (int)Dp, qs, ks, vs, os, scale, causal ? 1 : 0, stream);
+  TORCH_CHECK(rc == CMPEXT3_OK, "cmpext3 attention: ", cmpext3_attn_strerror(rc));
+  return {Dp == D ? out : out.narrow(3, 0, D).contiguous(), lse};
+}
+
+// Training backward: (dq, dk, dv) of sum(out * grad_out) for out =
+// attention_fwd_lse(query, key, value, scale, causal)[0].
+std::vector<torch::Tensor> attention_bwd(torch::Tensor query, torch::Tensor key, torch::Tensor value,
+                                         torch::Tensor out, torch::Tensor grad_out, torch::Tensor lse,
+                                         c10::optional<double> scale_arg, bool causal) {
+  const int dtype = training_dtype(query, key, value);
+  const int64_t B = query.size(0), H = query.size(1), Sq = query.size(2), D = query.size(3);
+  const int64_t Sk = key.size(2), Dp = (D + 7) / 8 * 8;
+  TORCH_CHECK(out.sizes() == query.sizes() && grad_out.sizes() == query.sizes() &&
+                  out.scalar_type() == query.scalar_type() && grad_out.scalar_type() == query.scalar_type(),
+              "cmpext3 attention: out / grad_out must match query");
+  TORCH_CHECK(lse.scalar_type() == at::kFloat && lse.dim() == 3 && lse.size(0) == B && lse.size(1) == H &&
+                  lse.size(2) == Sq,
+              "cmpext3 attention: lse must be fp32 [B, H, Sq]");
+  TORCH_CHECK(out.device() == query.device() && grad_out.device() == query.device() &&
+                  lse.device() == query.device(),
+              "cmpext3 attention: tensors must be on one GPU");
+  const float scale = resolve_scale(scale_arg, D);
+  const at::hip::HIPGuardMasqueradingAsCUDA guard(query.device());
+  hipStream_t stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA(query.device().index()).stream();
+
+  torch::Tensor dq = torch::empty({B, H, Sq, Dp}, query.options());
+  torch::Tensor dk = torch::empty({B, H, Sk, Dp}, query.options());
+  torch::Tensor dv = torch::empty({B, H, Sk, Dp}, query.options());
+  if (B * H * Sq == 0) {  // no query: nothing reaches K or V
+    dk.zero_();
+    dv.zero_();
+  } else {
+    const torch::Tensor q = abi_layout(query, Dp), k = abi_layout(key, Dp), v = abi_layout(value, Dp);
+    const torch::Tensor o = abi_layout(out, Dp), g = abi_layout(grad_out, Dp);
+    const torch::Tensor l = lse.contiguous();
+    torch::Tensor delta = torch::empty({B, H, Sq}, query.options().dtype(at::kFloat));
+    int64_t qs[3], ks[3], vs[3], os[3], gs[3], dqs[3], dks[3], dvs[3];
+    strides3(q, qs); strides3(k, ks); strides3(v, vs); strides3(o, os); strides3(g, gs);
+    strides3(dq, dqs); strides3(dk, dks); strides3(dv, dvs);
+    const int rc = cmpext3_attn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), g.data_ptr(),
+                                    l.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                    delta.data_ptr<float>(), dtype, (int)B, (int)H, (int)Sq, (int)Sk,
+                                    (int)Dp, qs, ks, vs, os, gs, dqs, dks, dvs, scale, causal ? 1 : 0,
+                                    stream);
+    TORCH_CHECK(rc == CMPEXT3_OK, "cmpext3 attention backward: ", cmpext3_attn_strerror(rc));
+  }
+  if (Dp != D) {
+    dq = dq.narrow(3, 0, D).contiguous();
+    dk = dk.narrow(3, 0, D).contiguous();
+    dv = dv.narrow(3, 0, D).contiguous();
+  }
+  return {dq, dk, dv};
+}
+
 std::string describe(int64_t dtype, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
                      bool causal) {
   char buf[256];
@@ -188,5 +311,14 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("describe", &describe, "Kernel/tile choice for a problem (host only)", py::arg("dtype"),
         py::arg("B"), py::arg("H"), py::arg("Sq"), py::arg("Sk"), py::arg("D"),
         py::arg("causal") = false);
+  m.def("attention_fwd_lse", &attention_fwd_lse,
+        "Training forward (fp16/bf16, D <= 128): returns (out, lse), lse = fp32 [B,H,Sq] row "
+        "log-sum-exp (natural log)",
+        py::arg("query"), py::arg("key"), py::arg("value"), py::arg("scale") = py::none(),
+        py::arg("causal") = false);
+  m.def("attention_bwd", &attention_bwd,
+        "Training backward: (dq, dk, dv) from q, k, v, out, grad_out and the forward's lse",
+        py::arg("query"), py::arg("key"), py::arg("value"), py::arg("out"), py::arg("grad_out"),
+        py::arg("lse"), py::arg("scale") = py::none(), py::arg("causal") = false);
   m.def("abi_version", &cmpext3_attn_abi_version, "C ABI version of libcmpext3_attn.so");
 }
