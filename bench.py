@@ -18,8 +18,14 @@ line.
                tensors), same workload and dtype, bounded to ~10 s
   configs      the same kernel timing for every BASELINE config (informational)
 
+--backward times a training step instead: the forward that keeps the row
+log-sum-exp plus the backward (Delta, dK/dV and dQ kernels), FLOPs counted as
+4*B*H*Sq*Sk*D forward + 2.5x that backward (the five matrix products of the
+gradient; the kernels recompute S and dP once more, which is not counted);
+causal workloads count the visible pairs only.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
-                       [--no-cpu-baseline] [--no-configs]
+                       [--no-cpu-baseline] [--no-configs] [--backward]
 """
 from __future__ import annotations
 
@@ -107,6 +113,93 @@ def cpu_baseline(wl, budget_s: float = 10.0):
     }
 
 
+def cpu_baseline_training(wl, budget_s: float = 20.0):
+    """Stock torch SDPA forward + backward on host CPU tensors (fp32 when the
+    CPU kernels reject the workload dtype), bounded to ~budget_s."""
+    import torch
+    import torch.nn.functional as F
+    torch.set_num_threads(os.cpu_count() or 1)
+    q, k, v = wl.make_inputs("cpu")
+    dt_used = wl.dtype
+
+    def step(q, k, v):
+        qq, kk, vv = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+        out = F.scaled_dot_product_attention(qq, kk, vv, is_causal=wl.causal, scale=wl.eff_scale)
+        out.backward(torch.ones_like(out))
+
+    try:
+        t0 = time.perf_counter()
+        step(q, k, v)
+    except RuntimeError:
+        q, k, v = (t.float() for t in (q, k, v))
+        dt_used = "fp32"
+        t0 = time.perf_counter()
+        step(q, k, v)
+    one = time.perf_counter() - t0
+    n = max(1, min(5, int(budget_s / max(one, 1e-3))))
+    t0 = time.perf_counter()
+    for _ in range(n):
+        step(q, k, v)
+    dt = (time.perf_counter() - t0) / n
+    return {
+        "value": round(3.5 * wl.flops() / dt / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "reference",
+        "sample": (f"stock torch SDPA forward+backward on host CPU tensors, full {wl.name} workload "
+                   f"{list(wl.shapes()[0])} {dt_used}, 1 warmup + {n} timed steps, "
+                   f"{dt * 1e3:.1f} ms/step"),
+    }
+
+
+def bench_training(wl, args) -> dict:
+    import torch
+    import cmpext3
+    g = torch.Generator().manual_seed(1)
+    q, k, v = wl.make_inputs("cuda")
+    do = torch.randn(q.shape, generator=g).to(q.dtype).to("cuda")
+    ops, sc, ca = cmpext3.ops, wl.eff_scale, wl.causal
+    out, lse = ops.attention_fwd_lse(q, k, v, sc, ca)
+    fwd = lambda: ops.attention_fwd_lse(q, k, v, sc, ca)  # noqa: E731
+    bwd = lambda: ops.attention_bwd(q, k, v, out, do, lse, sc, ca)  # noqa: E731
+
+    def step():
+        fwd()
+        bwd()
+
+    wall, dev_step = time_kernel(step, args.steps, args.warmup)
+    _, dev_fwd = time_kernel(fwd, args.steps, 3)
+    _, dev_bwd = time_kernel(bwd, args.steps, 3)
+    f_fwd, f_bwd = wl.flops(), 2.5 * wl.flops()
+    peak = 2516.6 if wl.dtype in ("fp16", "bf16") else 157.3
+    return {
+        "metric": "attention training step (fwd with lse + bwd) TFLOP/s, % of MI355X MFMA peak",
+        "value": round((f_fwd + f_bwd) * args.steps / wall / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"fp16": "f16", "bf16": "bf16"}[wl.dtype],
+        "data": "synthetic (seeded N(0,1) Q/K/V/dO, CPU generator -> device)",
+        "config": {"workload": wl.name, "B": wl.B, "H": wl.H, "Sq": wl.Sq, "Sk": wl.Sk, "D": wl.D,
+                   "causal": wl.causal, "scale": sc,
+                   "entry": "cmpext3.ops.attention_fwd_lse + attention_bwd -> cmpext3_attn_fwd_lse, "
+                            "cmpext3_attn_bwd"},
+        "roofline": {"bound": "mfma", "achieved": round(f_bwd / dev_bwd / 1e12, 3), "peak": peak,
+                     "unit": "TFLOP/s", "frac": round(f_bwd / dev_bwd / 1e12 / peak, 4), "traffic": None,
+                     "kernel_us": round(dev_bwd * 1e6, 3), "flops_per_launch": f_bwd,
+                     "what": "backward call (Delta + dK/dV + dQ kernels) as one unit"},
+        "forward_lse": {"kernel_us": round(dev_fwd * 1e6, 3),
+                        "tflops": round(f_fwd / dev_fwd / 1e12, 3)},
+        "step_device_us": round(dev_step * 1e6, 3),
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline_training(wl),
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -115,6 +208,8 @@ def main() -> int:
     ap.add_argument("--workload", default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
+    ap.add_argument("--backward", action="store_true",
+                    help="time a training step (forward with lse + backward) instead")
     ap.add_argument("--calibrate-copy-mb", type=int, default=0,
                     help="after the timed loop, run 3 plain elementwise copies (fp32, out = in*1) "
                          "of this many MiB: the known-traffic kernel that scales rocprofv3 "
@@ -137,6 +232,9 @@ def main() -> int:
         return 1
     wl = W.BY_NAME[args.workload] if args.workload else W.HEADLINE
     torch.manual_seed(0)
+    if args.backward:
+        print(json.dumps(bench_training(wl, args)), flush=True)
+        return 0
     q, k, v = wl.make_inputs("cuda")
     fn = lambda: cmpext3.ops.attention(q, k, v, wl.eff_scale, wl.causal)  # noqa: E731
 
