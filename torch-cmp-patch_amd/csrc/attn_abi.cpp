@@ -269,7 +269,9 @@ int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
   p.dk_b = dk_str[0]; p.dk_h = dk_str[1]; p.dk_s = dk_str[2];
   p.dv_b = dv_str[0]; p.dv_h = dv_str[1]; p.dv_s = dv_str[2];
   p.B = B; p.H = H; p.Sq = Sq; p.Sk = Sk; p.D = D;
-  p.c = fabsf(scale) * cmpext3::kLog2e;
+  // scale 0: the dK/dV kernel divides by c; c = 1e-30 puts every finite score
+  // within 1e-22 of the exp2 argument scale 0 gives, and keeps -lse2 / c finite
+  p.c = scale == 0.f ? 1e-30f : fabsf(scale) * cmpext3::kLog2e;
   p.scale = scale;
   p.sign = scale < 0.f ? 0x80008000u : 0u;
   const hipError_t err = cmpext3::launch_bwd16(p, dtype == CMPEXT3_DTYPE_BF16, causal != 0, stream);

@@ -147,15 +147,20 @@ __device__ __forceinline__ void store_rows(uint16_t* base, int64_t row_stride, i
 
 // ---- dK, dV for one block of 128 keys (4 waves x 32 keys), sweeping the
 // query tiles (32 rows of Q, dO, lse, Delta) through double-buffered LDS.
+// Waves per SIMD: the most the registers allow without spilling (D <= 64:
+// 3, 2 causal; D <= 128: 1, its K/V operands and dK/dV accumulators alone
+// take 192 registers).
 template <typename T, int DK, bool CAUSAL>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DK <= 64 ? 2 : 1)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DK <= 64 ? (CAUSAL ? 2 : 3) : 1)))
 attn_bwd_dkdv(const BwdParams p) {
   constexpr int BQ = 32, BKV = 128;
   constexpr int RS = DK + 8;  // LDS row stride (halves)
   constexpr int NKS = DK / 16, NDB = DK / 32;
   static_assert(DK % 32 == 0, "head-dim bucket");
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 2 * BQ * RS];  // [slot][Q, dO][row][col]
-  __shared__ __attribute__((aligned(16))) float lsd[2][2][BQ];            // [slot][lse2, Delta][row]
+  // [slot][-lse2 / c, -Delta][row]: the starting values of the S and dP
+  // accumulators, so that the MFMAs leave S - lse2 / c and dP - Delta
+  __shared__ __attribute__((aligned(16))) float lsd[2][2][BQ];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   // key blocks in order (causal: the first blocks see the most queries, so
@@ -215,15 +220,16 @@ attn_bwd_dkdv(const BwdParams p) {
   const int t0 = CAUSAL ? kb * (BKV / BQ) : 0;  // query tiles before the block see none of its keys
   const int t1 = (Sq + BQ - 1) / BQ;
   u32x4 xq[TileLoader<DK>::N], xd[TileLoader<DK>::N];
-  float xl = INFINITY, xdl = 0.f;
+  float xl = -INFINITY, xdl = 0.f;
+  const float inv_c = 1.f / p.c;  // c > 0 (the caller substitutes a tiny c for scale 0)
   auto fetch = [&](int t) {
     const int q0 = t * BQ;
     lq.load(qrs, (int)(q0 * p.q_s * 2), xq);
     ldo.load(dors, (int)(q0 * p.do_s * 2), xd);
     if (tid < BQ) {
       const int row = q0 + tid;
-      xl = row < Sq ? lse_g[row] * kLog2e : INFINITY;  // rows past Sq: P = 0
-      xdl = row < Sq ? dlt_g[row] : 0.f;
+      xl = row < Sq ? -(lse_g[row] * kLog2e) * inv_c : -INFINITY;  // rows past Sq: P = 0
+      xdl = row < Sq ? -dlt_g[row] : 0.f;
     }
   };
   auto put = [&](int slot) {
@@ -250,43 +256,41 @@ attn_bwd_dkdv(const BwdParams p) {
     if (!CAUSAL || q0 + BQ - 1 >= kw0) {
       const uint16_t* qs = lds + slot * 2 * BQ * RS;
       const uint16_t* dos = qs + BQ * RS;
-      f32x16 s = (f32x16){}, dp = (f32x16){};
+      // register r holds query q0 + acc_key(r, hh): two runs of 8 consecutive rows
+      f32x16 s, dp;
+#pragma unroll
+      for (int run = 0; run < 2; ++run)
+#pragma unroll
+        for (int h4 = 0; h4 < 2; ++h4) {
+          const f32x4 a = *(const f32x4*)&lsd[slot][0][16 * run + 8 * hh + 4 * h4];
+          const f32x4 d = *(const f32x4*)&lsd[slot][1][16 * run + 8 * hh + 4 * h4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            s[8 * run + 4 * h4 + i] = a[i];
+            dp[8 * run + 4 * h4 + i] = d[i];
+          }
+        }
 #pragma unroll
       for (int st = 0; st < NKS; ++st) s = Elt<T>::mma(*(const u32x4*)(qs + a_rd[st]), kf[st], s);
 #pragma unroll
       for (int st = 0; st < NKS; ++st) dp = Elt<T>::mma(*(const u32x4*)(dos + a_rd[st]), vf[st], dp);
-      // register r holds query q0 + acc_key(r, hh): two runs of 8 consecutive rows
-      float l2[16], dl[16];
-#pragma unroll
-      for (int run = 0; run < 2; ++run) {
-        const f32x4 a0 = *(const f32x4*)&lsd[slot][0][16 * run + 8 * hh];
-        const f32x4 a1 = *(const f32x4*)&lsd[slot][0][16 * run + 8 * hh + 4];
-        const f32x4 d0 = *(const f32x4*)&lsd[slot][1][16 * run + 8 * hh];
-        const f32x4 d1 = *(const f32x4*)&lsd[slot][1][16 * run + 8 * hh + 4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          l2[8 * run + i] = a0[i];
-          l2[8 * run + 4 + i] = a1[i];
-          dl[8 * run + i] = d0[i];
-          dl[8 * run + 4 + i] = d1[i];
-        }
-      }
+      // s = S - lse2 / c, dp = dP - Delta
       const bool diag = CAUSAL && q0 < kw0 + 31;
-      float pr[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = __builtin_fmaf(s[r], c, -l2[r]);
-        if (diag && key > q0 + acc_key(r, hh)) x = -INFINITY;
-        pr[r] = fast_exp2(x);
-      }
       u32x4 pp[2], ps[2];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int r = 8 * ks + 2 * e;
-          pp[ks][e] = Elt<T>::pack(pr[r], pr[r + 1]);
-          ps[ks][e] = Elt<T>::pack(pr[r] * (dp[r] - dl[r]), pr[r + 1] * (dp[r + 1] - dl[r + 1]));
+          float pv[2];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int r = 8 * ks + 2 * e + u;
+            float x = s[r] * c;
+            if (diag && key > q0 + acc_key(r, hh)) x = -INFINITY;
+            pv[u] = fast_exp2(x);
+          }
+          pp[ks][e] = Elt<T>::pack(pv[0], pv[1]);
+          ps[ks][e] = Elt<T>::pack(pv[0] * dp[8 * ks + 2 * e], pv[1] * dp[8 * ks + 2 * e + 1]);
         }
       // dV^T += dO^T P, dK^T += Q^T dS (16 queries per k-step)
 #pragma unroll
