@@ -129,7 +129,7 @@ int cmpext3_attn_fwd_masked(const void* q, const void* k, const void* v, void* o
                             float scale, int causal, hipStream_t stream);
 
 /*
- * Training forward: as cmpext3_attn_fwd (H_kv == H, no mask), and also writes
+ * Training forward: as cmpext3_attn_fwd_gqa (no mask), and also writes
  *
  *   lse : [B, H, Sq] fp32, contiguous (element (b, h, i) at lse[(b*H + h)*Sq + i]),
  *         the natural-log log-sum-exp over the visible keys of row i of
@@ -142,7 +142,7 @@ int cmpext3_attn_fwd_masked(const void* q, const void* k, const void* v, void* o
  * call with live autograd to stock torch (cmpext3/__init__.py:115-125).
  */
 int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, float* lse,
-                         int dtype, int B, int H, int Sq, int Sk, int D,
+                         int dtype, int B, int H, int H_kv, int Sq, int Sk, int D,
                          const int64_t q_str[3], const int64_t k_str[3],
                          const int64_t v_str[3], const int64_t o_str[3],
                          float scale, int causal, hipStream_t stream);
@@ -151,13 +151,16 @@ int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, f
  * Backward of the attention above: given q, k, v, the forward output o, its
  * gradient dout and the forward's lse, writes the gradients
  *
- *   dq : [B, H, Sq, D]   dk, dv : [B, H, Sk, D]   (all `dtype`, overwritten)
+ *   dq : [B, H, Sq, D]   dk, dv : [B, H_kv, Sk, D]   (all `dtype`, overwritten)
  *
- * of sum(o * dout), with the same scale and causal flag as the forward.
+ * of sum(o * dout), with the same scale, causal flag and K/V head count as
+ * the forward (H_kv must divide H; query head h uses K/V head h / (H / H_kv),
+ * and dk, dv sum the contributions of every query head of the group).
  *   delta : caller-owned fp32 workspace of B*H*Sq elements (4-byte aligned;
  *           receives sum_d dout * o per row).
  *   *_str[3] : element strides over {batch, head, seq} as in cmpext3_attn_fwd.
- * Three kernels on `stream`: Delta, dK/dV (one workgroup per 128 keys), dQ
+ * Three kernels on `stream`: Delta, dK/dV (one workgroup per 128 keys of a
+ * K/V head), dQ
  * (one per 128 queries); each gradient row is written by exactly one
  * workgroup, so results are bit-identical from run to run.  B*H*Sq == 0 is a
  * no-op (dk and dv are then left untouched).  f16/bf16 with D <= 128 only
@@ -167,7 +170,7 @@ int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, f
  */
 int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
                      const void* dout, const float* lse, void* dq, void* dk, void* dv,
-                     float* delta, int dtype, int B, int H, int Sq, int Sk, int D,
+                     float* delta, int dtype, int B, int H, int H_kv, int Sq, int Sk, int D,
                      const int64_t q_str[3], const int64_t k_str[3],
                      const int64_t v_str[3], const int64_t o_str[3],
                      const int64_t do_str[3], const int64_t dq_str[3],

@@ -130,16 +130,16 @@ def test_gqa_head_counts_are_checked_before_launch():
 def _call_lse(lse=16, dtype=abi.DTYPE_F16, D=64, q=16, Sq=8, Sk=8, scale=0.125):
     st = (ctypes.c_int64 * 3)(512, 512, 64)
     vp = ctypes.c_void_p
-    return abi.lib().cmpext3_attn_fwd_lse(vp(q), vp(16), vp(16), vp(16), vp(lse), dtype, 1, 1, Sq, Sk, D,
-                                          st, st, st, st, ctypes.c_float(scale), 0, None)
+    return abi.lib().cmpext3_attn_fwd_lse(vp(q), vp(16), vp(16), vp(16), vp(lse), dtype, 1, 1, 1, Sq, Sk,
+                                          D, st, st, st, st, ctypes.c_float(scale), 0, None)
 
 
 def _call_bwd(delta=16, lse=16, dtype=abi.DTYPE_F16, D=64, dq=16, Sq=8, Sk=8, scale=0.125,
-              strides=(512, 512, 64)):
+              strides=(512, 512, 64), H=1, H_kv=1):
     st = (ctypes.c_int64 * 3)(*strides)
     vp = ctypes.c_void_p
     return abi.lib().cmpext3_attn_bwd(vp(16), vp(16), vp(16), vp(16), vp(16), vp(lse), vp(dq), vp(16),
-                                      vp(16), vp(delta), dtype, 1, 1, Sq, Sk, D,
+                                      vp(16), vp(delta), dtype, 1, H, H_kv, Sq, Sk, D,
                                       *([st] * 8), ctypes.c_float(scale), 1, None)
 
 
@@ -162,3 +162,5 @@ def test_training_entry_points_reject_before_launch():
     assert _call_bwd(scale=float("nan")) == abi.E_INVALID
     assert _call_bwd(strides=(1 << 40, 1 << 40, 1 << 26)) == abi.E_TOO_LARGE
     assert _call_bwd(delta=0, Sq=0) == abi.OK
+    assert _call_bwd(H=4, H_kv=3) == abi.E_INVALID
+    assert _call_bwd(H=4, H_kv=0) == abi.E_INVALID

@@ -185,3 +185,67 @@ def test_sdpa_training_route(patched):
     finally:
         cmpext3._C = old
         cmpext3.enable_backward(was)
+
+
+GQA_CASES = [
+    # dtype, B, H, Hkv, Sq, Sk, D, causal
+    ("fp16", 1, 8, 2, 256, 256, 64, False),
+    ("bf16", 2, 6, 3, 300, 200, 128, True),
+    ("fp16", 1, 4, 1, 130, 700, 64, True),    # multi-query, causal Sq < Sk
+]
+
+
+@pytest.mark.parametrize("case", GQA_CASES, ids=[f"{c[0]}-H{c[2]}of{c[3]}-q{c[4]}k{c[5]}d{c[6]}"
+                                                 f"{'c' if c[7] else ''}" for c in GQA_CASES])
+def test_bwd_grouped_query(case):
+    """K/V with fewer heads: dK/dV sum every query head of the group; the
+    oracle runs on K/V repeated per query head and sums the repeats."""
+    dtype, B, H, Hkv, Sq, Sk, D, causal = case
+    g = torch.Generator().manual_seed(H * Sq + Sk)
+    mk = lambda h, S: torch.randn(B, h, S, D, generator=g).to(TDT[dtype]).cuda()
+    q, k, v, do = mk(H, Sq), mk(Hkv, Sk), mk(Hkv, Sk), mk(H, Sq)
+    s = D ** -0.5
+    out, lse = abi.attn_fwd_lse(q, k, v, s, causal)
+    dq, dk, dv = abi.attn_bwd(q, k, v, out, do, lse, s, causal)
+    torch.cuda.synchronize()
+    grp = H // Hkv
+    kr, vr = (t.cpu().repeat_interleave(grp, dim=1) for t in (k, v))
+    qc, dc = q.cpu(), do.cpu()
+    assert orc.max_abs_err(out.cpu(), orc.sdpa_np(qc, kr, vr, s, causal)) <= TOL[dtype]
+    dq_r, dk_r, dv_r = orc.sdpa_bwd_np(qc, kr, vr, dc, s, causal)
+    dk_r = dk_r.reshape(B, Hkv, grp, Sk, D).sum(axis=2)
+    dv_r = dv_r.reshape(B, Hkv, grp, Sk, D).sum(axis=2)
+    for name, got, ref in zip(("dq", "dk", "dv"), (dq, dk, dv), (dq_r, dk_r, dv_r)):
+        assert _rel_err(got, ref) <= TOL[dtype], name
+
+
+def test_sdpa_training_route_grouped_query(patched):
+    """enable_gqa=True with live autograd stays native under enable_backward()."""
+    g = torch.Generator().manual_seed(8)
+    q = torch.randn(1, 8, 192, 64, generator=g).half().cuda().requires_grad_(True)
+    k = torch.randn(1, 2, 192, 64, generator=g).half().cuda().requires_grad_(True)
+    v = torch.randn(1, 2, 192, 64, generator=g).half().cuda().requires_grad_(True)
+    do = torch.randn(1, 8, 192, 64, generator=g).half().cuda()
+    was = cmpext3.backward_enabled()
+    cmpext3.enable_backward(True)
+    try:
+        out = F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True)
+        assert out.grad_fn is not None and "_Attention" in type(out.grad_fn).__name__
+        out.backward(do)
+    finally:
+        cmpext3.enable_backward(was)
+    torch.cuda.synchronize()
+    kr, vr = (t.detach().cpu().repeat_interleave(4, dim=1) for t in (k, v))
+    dq_r, dk_r, dv_r = orc.sdpa_bwd_np(q.detach().cpu(), kr, vr, do.cpu(), None, True)
+    assert _rel_err(q.grad, dq_r) <= TOL["fp16"]
+    assert _rel_err(k.grad, dk_r.reshape(1, 2, 4, 192, 64).sum(axis=2)) <= TOL["fp16"]
+    assert _rel_err(v.grad, dv_r.reshape(1, 2, 4, 192, 64).sum(axis=2)) <= TOL["fp16"]
+
+
+def test_double_backward_is_refused():
+    q, k, v, do = _inputs("fp16", 1, 1, 64, 64, 64, seed=2)
+    q, k, v = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out = cmpext3.attention(q, k, v)
+    (gq,) = torch.autograd.grad(out, q, do, create_graph=True)
+    with pytest.raises(RuntimeError):
+        gq.sum().backward()

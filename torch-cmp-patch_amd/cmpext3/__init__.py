@@ -26,7 +26,8 @@ What runs where:
 Training (no counterpart in the reference, which is forward-only): with
 ``CMPEXT3_BACKWARD=1`` in the environment, or after ``enable_backward()``,
 SDPA calls with live autograd on fp16/bf16 GPU tensors with D <= 128, equal
-head counts, no mask and no dropout run the native forward and backward
+head counts (or grouped-query K/V under enable_gqa=True), no mask and no
+dropout run the native forward and backward
 kernels (``attention`` below, a torch.autograd.Function); everything else
 with live autograd still goes to stock.  Off by default, so the default
 behaviour is the reference's.
@@ -154,6 +155,7 @@ class _Attention(torch.autograd.Function):
         return out
 
     @staticmethod
+    @torch.autograd.function.once_differentiable
     def backward(ctx, grad_out):
         q, k, v, out, lse = ctx.saved_tensors
         dq, dk, dv = _C.attention_bwd(q, k, v, out, grad_out, lse, ctx.scale, ctx.causal)
@@ -163,18 +165,21 @@ class _Attention(torch.autograd.Function):
 def attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
               scale: float | None = None, causal: bool = False) -> torch.Tensor:
     """Differentiable native attention (fp16/bf16 GPU tensors [B, H, S, D],
-    D <= 128, K/V with Q's head count).  Raises RuntimeError for anything else."""
+    D <= 128; K/V may hold fewer heads than Q when that count divides H, with
+    torch's enable_gqa meaning).  Raises RuntimeError for anything else."""
     return _Attention.apply(query, key, value, scale, causal)
 
 
-def _training_applies(query, key, value, attn_mask, dropout_p) -> bool:
-    return (_BACKWARD and attn_mask is None and dropout_p == 0.0
+def _training_applies(query, key, value, attn_mask, dropout_p, enable_gqa) -> bool:
+    if not (_BACKWARD and attn_mask is None and dropout_p == 0.0
             and all(isinstance(t, torch.Tensor) and t.is_cuda and t.dim() == 4
                     and t.dtype == query.dtype for t in (query, key, value))
-            and query.dtype in _TRAIN_DTYPES
-            and key.shape[0] == query.shape[0] and key.shape[1] == query.shape[1]
-            and key.shape[3] == query.shape[3] and value.shape == key.shape
-            and 1 <= query.shape[3] <= 128 and key.shape[2] > 0)
+            and query.dtype in _TRAIN_DTYPES):
+        return False
+    hq, hkv = query.shape[1], key.shape[1]
+    heads_ok = hkv == hq or (enable_gqa and hkv >= 1 and hq % hkv == 0)
+    return (heads_ok and key.shape[0] == query.shape[0] and key.shape[3] == query.shape[3]
+            and value.shape == key.shape and 1 <= query.shape[3] <= 128 and key.shape[2] > 0)
 
 
 def _dispatch(op: str, ref: torch.Tensor, key: tuple,
@@ -220,7 +225,8 @@ def _patched_sdpa(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=Fa
                     is_causal=is_causal, scale=scale, **kwargs)
 
     if (isinstance(query, torch.Tensor) and not _grad_safe(query, key, value, attn_mask)
-            and _training_applies(query, key, value, attn_mask, dropout_p)):
+            and _training_applies(query, key, value, attn_mask, dropout_p,
+                                  bool(kwargs.get("enable_gqa", False)))):
         try:
             return _Attention.apply(query, key, value, scale, is_causal)
         except (RuntimeError, TypeError):

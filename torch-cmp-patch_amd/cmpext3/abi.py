@@ -43,10 +43,10 @@ def lib() -> ctypes.CDLL:
                                               i64p, i64p, i64p, i64p, vp, ci, i64p,
                                               ctypes.c_float, ci, vp]
         L.cmpext3_attn_fwd_masked.restype = ci
-        L.cmpext3_attn_fwd_lse.argtypes = [vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci,
+        L.cmpext3_attn_fwd_lse.argtypes = [vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci, ci,
                                            i64p, i64p, i64p, i64p, ctypes.c_float, ci, vp]
         L.cmpext3_attn_fwd_lse.restype = ci
-        L.cmpext3_attn_bwd.argtypes = [vp] * 10 + [ci] * 6 + [i64p] * 8 + [ctypes.c_float, ci, vp]
+        L.cmpext3_attn_bwd.argtypes = [vp] * 10 + [ci] * 7 + [i64p] * 8 + [ctypes.c_float, ci, vp]
         L.cmpext3_attn_bwd.restype = ci
         L.cmpext3_attn_strerror.argtypes = [ci]
         L.cmpext3_attn_strerror.restype = ctypes.c_char_p
@@ -152,8 +152,8 @@ def _handle(t, stream):
 
 def attn_fwd_lse(q, k, v, scale: Optional[float] = None, causal: bool = False, stream=None):
     """Training forward through cmpext3_attn_fwd_lse: returns (O, lse) with
-    lse the fp32 [B,H,Sq] natural-log row log-sum-exp.  Raises RuntimeError on
-    a non-zero return code."""
+    lse the fp32 [B,H,Sq] natural-log row log-sum-exp (k, v may hold fewer
+    heads than q: grouped-query).  Raises RuntimeError on a non-zero code."""
     import torch
     B, H, Sq, D = q.shape
     o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
@@ -163,7 +163,7 @@ def attn_fwd_lse(q, k, v, scale: Optional[float] = None, causal: bool = False, s
     rc = lib().cmpext3_attn_fwd_lse(
         ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()),
         ctypes.c_void_p(o.data_ptr()), ctypes.c_void_p(lse.data_ptr()), dtype_code(q.dtype),
-        B, H, Sq, k.shape[2], D, _strides(q), _strides(k), _strides(v), _strides(o),
+        B, H, k.shape[1], Sq, k.shape[2], D, _strides(q), _strides(k), _strides(v), _strides(o),
         ctypes.c_float(scale), int(causal), ctypes.c_void_p(_handle(q, stream)))
     if rc != OK:
         raise RuntimeError(f"cmpext3_attn_fwd_lse: {strerror(rc)} (code {rc})")
@@ -177,7 +177,7 @@ def attn_bwd_raw(q, k, v, o, do, lse, dq, dk, dv, delta, scale: float, causal: b
     vp = ctypes.c_void_p
     return lib().cmpext3_attn_bwd(
         *(vp(t.data_ptr()) for t in (q, k, v, o, do, lse, dq, dk, dv, delta)),
-        dtype_code(q.dtype), B, H, Sq, k.shape[2], D,
+        dtype_code(q.dtype), B, H, k.shape[1], Sq, k.shape[2], D,
         *(_strides(t) for t in (q, k, v, o, do, dq, dk, dv)),
         ctypes.c_float(scale), int(causal), vp(_handle(q, stream)))
 

@@ -214,7 +214,7 @@ int cmpext3_attn_fwd_masked(const void* q, const void* k, const void* v, void* o
 }
 
 int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, float* lse, int dtype,
-                         int B, int H, int Sq, int Sk, int D, const int64_t q_str[3],
+                         int B, int H, int H_kv, int Sq, int Sk, int D, const int64_t q_str[3],
                          const int64_t k_str[3], const int64_t v_str[3], const int64_t o_str[3],
                          float scale, int causal, hipStream_t stream) {
   const int rc = check_shape(dtype, B, H, Sq, Sk, D);
@@ -226,13 +226,13 @@ int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, f
   // the pipelined kernel (the one that writes the log-sum-exp) addresses K/V
   // tiles with 32-bit buffer offsets
   if (!tile_offsets_fit(Sk, k_str[2], v_str[2])) return CMPEXT3_E_TOO_LARGE;
-  return fwd_impl(q, k, v, o, lse, dtype, B, H, H, Sq, Sk, D, q_str, k_str, v_str, o_str, nullptr, -1,
+  return fwd_impl(q, k, v, o, lse, dtype, B, H, H_kv, Sq, Sk, D, q_str, k_str, v_str, o_str, nullptr, -1,
                   nullptr, scale, causal, stream);
 }
 
 int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
                      const float* lse, void* dq, void* dk, void* dv, float* delta, int dtype, int B,
-                     int H, int Sq, int Sk, int D, const int64_t q_str[3], const int64_t k_str[3],
+                     int H, int H_kv, int Sq, int Sk, int D, const int64_t q_str[3], const int64_t k_str[3],
                      const int64_t v_str[3], const int64_t o_str[3], const int64_t do_str[3],
                      const int64_t dq_str[3], const int64_t dk_str[3], const int64_t dv_str[3],
                      float scale, int causal, hipStream_t stream) {
@@ -240,6 +240,7 @@ int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
   if (rc != CMPEXT3_OK) return rc;
   if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;
   if (dtype == CMPEXT3_DTYPE_F32 || D > 128) return CMPEXT3_E_TRAINING;
+  if (H_kv < 1 || H_kv > H || H % H_kv != 0) return CMPEXT3_E_INVALID;
   if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv || !delta) return CMPEXT3_E_INVALID;
   if (!q_str || !k_str || !v_str || !o_str || !do_str || !dq_str || !dk_str || !dv_str)
     return CMPEXT3_E_INVALID;
@@ -249,8 +250,8 @@ int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
   for (const void* ptr : ptrs)
     if (!aligned16(ptr)) return CMPEXT3_E_ALIGN;
   if (!stride_ok(q_str, B, H, Sq, 2) || !stride_ok(o_str, B, H, Sq, 2) || !stride_ok(do_str, B, H, Sq, 2) ||
-      !stride_ok(dq_str, B, H, Sq, 2) || !stride_ok(k_str, B, H, Sk, 2) || !stride_ok(v_str, B, H, Sk, 2) ||
-      !stride_ok(dk_str, B, H, Sk, 2) || !stride_ok(dv_str, B, H, Sk, 2))
+      !stride_ok(dq_str, B, H, Sq, 2) || !stride_ok(k_str, B, H_kv, Sk, 2) || !stride_ok(v_str, B, H_kv, Sk, 2) ||
+      !stride_ok(dk_str, B, H_kv, Sk, 2) || !stride_ok(dv_str, B, H_kv, Sk, 2))
     return CMPEXT3_E_ALIGN;
   // Q/dO tiles (dK/dV kernel) and K/V tiles (dQ kernel) use 32-bit buffer offsets
   if (!tile_offsets_fit(Sq, q_str[2], do_str[2]) || !tile_offsets_fit(Sk, k_str[2], v_str[2]))
@@ -269,6 +270,8 @@ int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
   p.dk_b = dk_str[0]; p.dk_h = dk_str[1]; p.dk_s = dk_str[2];
   p.dv_b = dv_str[0]; p.dv_h = dv_str[1]; p.dv_s = dv_str[2];
   p.B = B; p.H = H; p.Sq = Sq; p.Sk = Sk; p.D = D;
+  p.Hkv = H_kv;
+  p.group = H / H_kv;
   // scale 0: the dK/dV kernel divides by c; c = 1e-30 puts every finite score
   // within 1e-22 of the exp2 argument scale 0 gives, and keeps -lse2 / c finite
   p.c = scale == 0.f ? 1e-30f : fabsf(scale) * cmpext3::kLog2e;

@@ -27,7 +27,9 @@
 // kernel mirrors the forward: lane = query, S^T = K Q^T, dP^T = V dO^T,
 // dQ^T = K^T dS^T.  A negative scale is folded into the sign of the operand
 // held in registers (K in dK/dV, Q in dQ), and the signed scale multiplies the
-// result.
+// result.  Grouped-query K/V (Hkv heads shared by H / Hkv query heads each):
+// a dK/dV workgroup sweeps the query tiles of every query head of its group,
+// so the group's contributions are summed in registers.
 #pragma once
 
 #include "attn_fwd_pipe16.h"
@@ -49,7 +51,9 @@ struct BwdParams {
   int64_t q_b, q_h, q_s, k_b, k_h, k_s, v_b, v_h, v_s, o_b, o_h, o_s, do_b, do_h, do_s;
   int64_t dq_b, dq_h, dq_s, dk_b, dk_h, dk_s, dv_b, dv_h, dv_s;
   int B, H, Sq, Sk, D;
-  int n_blk;        // key blocks (dK/dV) or query blocks (dQ) per (batch, head)
+  int Hkv;          // K/V heads (dk, dv have Hkv heads); query head h uses K/V head h / group
+  int group;        // H / Hkv
+  int n_blk;        // key blocks (dK/dV, per K/V head) or query blocks (dQ, per query head)
   int n_wg;         // workgroups launched = B * H * n_blk
   float c;          // |scale| * log2(e)
   float scale;      // signed scale: dK = scale * dS^T Q, dQ = scale * dS K
@@ -166,15 +170,15 @@ attn_bwd_dkdv(const BwdParams p) {
   // key blocks in order (causal: the first blocks see the most queries, so
   // they start first); XCD-contiguous ranges share Q/dO in L2
   const int tile = xcd_remap(blockIdx.x, p.n_wg);
-  const int bh = tile / p.n_blk, kb = tile - bh * p.n_blk;
-  const int b = bh / p.H, h = bh - b * p.H;
+  const int bhk = tile / p.n_blk, kb = tile - bhk * p.n_blk;  // (batch, K/V head), key block
+  const int b = bhk / p.Hkv, hk = bhk - b * p.Hkv;
   const int Sq = p.Sq, Sk = p.Sk, D = p.D;
   const int kw0 = kb * BKV + wave * 32;  // first key of this wave
   const int key = kw0 + l32;             // this lane's key
 
   // B operands held for the whole sweep: 8 head-dim values of this lane's key
-  const uint16_t* kg = (const uint16_t*)p.k + b * p.k_b + h * p.k_h;
-  const uint16_t* vg = (const uint16_t*)p.v + b * p.v_b + h * p.v_h;
+  const uint16_t* kg = (const uint16_t*)p.k + b * p.k_b + hk * p.k_h;
+  const uint16_t* vg = (const uint16_t*)p.v + b * p.v_b + hk * p.v_h;
   u32x4 kf[NKS], vf[NKS];
 #pragma unroll
   for (int s = 0; s < NKS; ++s) {
@@ -188,15 +192,9 @@ attn_bwd_dkdv(const BwdParams p) {
     vf[s] = y;
   }
 
-  const uint16_t* qg = (const uint16_t*)p.q + b * p.q_b + h * p.q_h;
-  const uint16_t* dog = (const uint16_t*)p.dout + b * p.do_b + h * p.do_h;
-  const __amdgpu_buffer_rsrc_t qrs = uniform_rsrc(qg, ((int64_t)(Sq - 1) * p.q_s + D) * 2);
-  const __amdgpu_buffer_rsrc_t dors = uniform_rsrc(dog, ((int64_t)(Sq - 1) * p.do_s + D) * 2);
   TileLoader<DK> lq, ldo;
   lq.init(tid, p.q_s, D, RS);
   ldo.init(tid, p.do_s, D, RS);
-  const float* lse_g = p.lse + (int64_t)bh * Sq;
-  const float* dlt_g = p.delta + (int64_t)bh * Sq;
 
   // fragment read offsets: A = query rows (bit-permuted), A = X^T slices
   int a_rd[NKS];
@@ -217,19 +215,37 @@ attn_bwd_dkdv(const BwdParams p) {
 #pragma unroll
   for (int db = 0; db < NDB; ++db) dva[db] = dka[db] = (f32x16){};
 
+  // The sweep: query tiles t0 .. t1-1 of each query head of the group, as one
+  // sequence j = g * nt + (t - t0).
   const int t0 = CAUSAL ? kb * (BKV / BQ) : 0;  // query tiles before the block see none of its keys
   const int t1 = (Sq + BQ - 1) / BQ;
+  const int nt = t1 > t0 ? t1 - t0 : 0;
+  const int nj = nt * p.group;
   u32x4 xq[TileLoader<DK>::N], xd[TileLoader<DK>::N];
   float xl = -INFINITY, xdl = 0.f;
   const float inv_c = 1.f / p.c;  // c > 0 (the caller substitutes a tiny c for scale 0)
-  auto fetch = [&](int t) {
+  auto fetch = [&](int j) {
+    const int g = j / nt, t = t0 + (j - g * nt);
+    const int h = hk * p.group + g;
+    const uint16_t* qg = (const uint16_t*)p.q + b * p.q_b + h * p.q_h;
+    const uint16_t* dog = (const uint16_t*)p.dout + b * p.do_b + h * p.do_h;
+    const __amdgpu_buffer_rsrc_t qrs = uniform_rsrc(qg, ((int64_t)(Sq - 1) * p.q_s + D) * 2);
+    const __amdgpu_buffer_rsrc_t dors = uniform_rsrc(dog, ((int64_t)(Sq - 1) * p.do_s + D) * 2);
     const int q0 = t * BQ;
     lq.load(qrs, (int)(q0 * p.q_s * 2), xq);
     ldo.load(dors, (int)(q0 * p.do_s * 2), xd);
+    // this head's lse / Delta rows: a wave-uniform base (kept in SGPRs) plus
+    // the 32-bit row index
+    const int64_t hoff = ((int64_t)b * p.H + h) * Sq;
+    const int hlo = __builtin_amdgcn_readfirstlane((int)(uint32_t)hoff);
+    const int hhi = __builtin_amdgcn_readfirstlane((int)(uint32_t)(hoff >> 32));
+    const int64_t hoff_u = ((int64_t)(uint32_t)hhi << 32) | (uint32_t)hlo;
+    const float* lse_h = p.lse + hoff_u;
+    const float* dlt_h = p.delta + hoff_u;
     if (tid < BQ) {
       const int row = q0 + tid;
-      xl = row < Sq ? -(lse_g[row] * kLog2e) * inv_c : -INFINITY;  // rows past Sq: P = 0
-      xdl = row < Sq ? -dlt_g[row] : 0.f;
+      xl = row < Sq ? -(lse_h[row] * kLog2e) * inv_c : -INFINITY;  // rows past Sq: P = 0
+      xdl = row < Sq ? -dlt_h[row] : 0.f;
     }
   };
   auto put = [&](int slot) {
@@ -243,15 +259,15 @@ attn_bwd_dkdv(const BwdParams p) {
   };
 
   const float c = p.c;
-  if (t0 < t1) {
-    fetch(t0);
+  if (nj > 0) {
+    fetch(0);
     put(0);
   }
   lds_barrier();
-  for (int t = t0; t < t1; ++t) {
-    const int slot = (t - t0) & 1;
-    if (t + 1 < t1) fetch(t + 1);
-    const int q0 = t * BQ;
+  for (int j = 0; j < nj; ++j) {
+    const int slot = j & 1;
+    if (j + 1 < nj) fetch(j + 1);
+    const int q0 = (t0 + j % nt) * BQ;
     // causal: a tile whose last query precedes this wave's first key adds nothing
     if (!CAUSAL || q0 + BQ - 1 >= kw0) {
       const uint16_t* qs = lds + slot * 2 * BQ * RS;
@@ -303,13 +319,13 @@ attn_bwd_dkdv(const BwdParams p) {
           dka[db] = Elt<T>::mma(tr_frag(qsl, t_rd[db][0], t_rd[db][1]), ps[ks], dka[db]);
         }
     }
-    if (t + 1 < t1) put(slot ^ 1);
+    if (j + 1 < nj) put(slot ^ 1);
     lds_barrier();
   }
 
   // lane = key, registers = head-dim columns
-  uint16_t* dkg = (uint16_t*)p.dk + b * p.dk_b + h * p.dk_h;
-  uint16_t* dvg = (uint16_t*)p.dv + b * p.dv_b + h * p.dv_h;
+  uint16_t* dkg = (uint16_t*)p.dk + b * p.dk_b + hk * p.dk_h;
+  uint16_t* dvg = (uint16_t*)p.dv + b * p.dv_b + hk * p.dv_h;
   store_rows<T, NDB>(dvg, p.dv_s, key, Sk, D, hh, dva, 1.f);
   store_rows<T, NDB>(dkg, p.dk_s, key, Sk, D, hh, dka, p.scale);
 }
@@ -354,8 +370,9 @@ attn_bwd_dq(const BwdParams p) {
   const float l2 = qrow < Sq ? p.lse[(int64_t)bh * Sq + qrow] * kLog2e : INFINITY;  // past Sq: P = 0
   const float dl = qrow < Sq ? p.delta[(int64_t)bh * Sq + qrow] : 0.f;
 
-  const uint16_t* kg = (const uint16_t*)p.k + b * p.k_b + h * p.k_h;
-  const uint16_t* vg = (const uint16_t*)p.v + b * p.v_b + h * p.v_h;
+  const int hk = h / p.group;
+  const uint16_t* kg = (const uint16_t*)p.k + b * p.k_b + hk * p.k_h;
+  const uint16_t* vg = (const uint16_t*)p.v + b * p.v_b + hk * p.v_h;
   const __amdgpu_buffer_rsrc_t krs = uniform_rsrc(kg, ((int64_t)(Sk - 1) * p.k_s + D) * 2);
   const __amdgpu_buffer_rsrc_t vrs = uniform_rsrc(vg, ((int64_t)(Sk - 1) * p.v_s + D) * 2);
   TileLoader<DK> lk, lv;

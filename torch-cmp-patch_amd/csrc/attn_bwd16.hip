@@ -14,7 +14,7 @@ hipError_t launch_bwd_t(const BwdParams& p0, hipStream_t s) {
   const int64_t rows = (int64_t)p.B * p.H * p.Sq;
   hipLaunchKernelGGL(attn_bwd_delta<T>, dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, s, p);
   p.n_blk = (p.Sk + 127) / 128;
-  p.n_wg = p.B * p.H * p.n_blk;
+  p.n_wg = p.B * p.Hkv * p.n_blk;
   hipLaunchKernelGGL((attn_bwd_dkdv<T, DK, CAUSAL>), dim3(p.n_wg), dim3(256), 0, s, p);
   p.n_blk = (p.Sq + 127) / 128;
   p.n_wg = p.B * p.H * p.n_blk;

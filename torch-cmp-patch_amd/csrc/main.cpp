@@ -180,7 +180,7 @@ torch::Tensor attention(torch::Tensor query, torch::Tensor key, torch::Tensor va
 namespace {
 
 // Shared checks of the training entry points: 4-D GPU f16/bf16 tensors of one
-// dtype and device, equal head counts, head dim <= 128.
+// dtype and device, K/V heads dividing the query heads, head dim <= 128.
 int training_dtype(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v) {
   TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4, "cmpext3 attention: q, k, v must be 4D");
   TORCH_CHECK(q.is_cuda() && q.device() == k.device() && q.device() == v.device(),
@@ -190,9 +190,10 @@ int training_dtype(const torch::Tensor& q, const torch::Tensor& k, const torch::
   const int dtype = dtype_code(q.scalar_type());
   TORCH_CHECK(dtype == CMPEXT3_DTYPE_F16 || dtype == CMPEXT3_DTYPE_BF16,
               "cmpext3 attention: the training path takes fp16/bf16 only");
-  TORCH_CHECK(k.size(0) == q.size(0) && k.size(1) == q.size(1) && k.size(3) == q.size(3) &&
-                  v.sizes() == k.sizes(),
-              "cmpext3 attention: the training path needs K/V of Q's batch, heads and head dim");
+  TORCH_CHECK(k.size(0) == q.size(0) && k.size(1) >= 1 && q.size(1) % k.size(1) == 0 &&
+                  k.size(3) == q.size(3) && v.sizes() == k.sizes(),
+              "cmpext3 attention: the training path needs K/V of Q's batch and head dim, with a "
+              "head count dividing Q's");
   TORCH_CHECK(q.size(3) >= 1 && q.size(3) <= 128, "cmpext3 attention: the training path needs D <= 128");
   TORCH_CHECK(k.size(2) > 0 || q.size(0) * q.size(1) * q.size(2) == 0,
               "cmpext3 attention: empty key sequence");
@@ -227,7 +228,7 @@ std::vector<torch::Tensor> attention_fwd_lse(torch::Tensor query, torch::Tensor 
                                              c10::optional<double> scale_arg, bool causal) {
   const int dtype = training_dtype(query, key, value);
   const int64_t B = query.size(0), H = query.size(1), Sq = query.size(2), D = query.size(3);
-  const int64_t Sk = key.size(2), Dp = (D + 7) / 8 * 8;
+  const int64_t Sk = key.size(2), Hkv = key.size(1), Dp = (D + 7) / 8 * 8;
   const float scale = resolve_scale(scale_arg, D);
   const at::hip::HIPGuardMasqueradingAsCUDA guard(query.device());
   hipStream_t stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA(query.device().index()).stream();
@@ -239,8 +240,8 @@ std::vector<torch::Tensor> attention_fwd_lse(torch::Tensor query, torch::Tensor 
   int64_t qs[3], ks[3], vs[3], os[3];
   strides3(q, qs); strides3(k, ks); strides3(v, vs); strides3(out, os);
   const int rc = cmpext3_attn_fwd_lse(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                                      lse.data_ptr<float>(), dtype, (int)B, (int)H, (int)Sq, (int)Sk,
-                                      (int)Dp, qs, ks, vs, os, scale, causal ? 1 : 0, stream);
+                                      lse.data_ptr<float>(), dtype, (int)B, (int)H, (int)Hkv, (int)Sq,
+                                      (int)Sk, (int)Dp, qs, ks, vs, os, scale, causal ? 1 : 0, stream);
   TORCH_CHECK(rc == CMPEXT3_OK, "cmpext3 attention: ", cmpext3_attn_strerror(rc));
   return {Dp == D ? out : out.narrow(3, 0, D).contiguous(), lse};
 }
@@ -252,7 +253,7 @@ std::vector<torch::Tensor> attention_bwd(torch::Tensor query, torch::Tensor key,
                                          c10::optional<double> scale_arg, bool causal) {
   const int dtype = training_dtype(query, key, value);
   const int64_t B = query.size(0), H = query.size(1), Sq = query.size(2), D = query.size(3);
-  const int64_t Sk = key.size(2), Dp = (D + 7) / 8 * 8;
+  const int64_t Sk = key.size(2), Hkv = key.size(1), Dp = (D + 7) / 8 * 8;
   TORCH_CHECK(out.sizes() == query.sizes() && grad_out.sizes() == query.sizes() &&
                   out.scalar_type() == query.scalar_type() && grad_out.scalar_type() == query.scalar_type(),
               "cmpext3 attention: out / grad_out must match query");
@@ -267,8 +268,8 @@ std::vector<torch::Tensor> attention_bwd(torch::Tensor query, torch::Tensor key,
   hipStream_t stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA(query.device().index()).stream();
 
   torch::Tensor dq = torch::empty({B, H, Sq, Dp}, query.options());
-  torch::Tensor dk = torch::empty({B, H, Sk, Dp}, query.options());
-  torch::Tensor dv = torch::empty({B, H, Sk, Dp}, query.options());
+  torch::Tensor dk = torch::empty({B, Hkv, Sk, Dp}, query.options());
+  torch::Tensor dv = torch::empty({B, Hkv, Sk, Dp}, query.options());
   if (B * H * Sq == 0) {  // no query: nothing reaches K or V
     dk.zero_();
     dv.zero_();
@@ -282,9 +283,9 @@ std::vector<torch::Tensor> attention_bwd(torch::Tensor query, torch::Tensor key,
     strides3(dq, dqs); strides3(dk, dks); strides3(dv, dvs);
     const int rc = cmpext3_attn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), g.data_ptr(),
                                     l.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                                    delta.data_ptr<float>(), dtype, (int)B, (int)H, (int)Sq, (int)Sk,
-                                    (int)Dp, qs, ks, vs, os, gs, dqs, dks, dvs, scale, causal ? 1 : 0,
-                                    stream);
+                                    delta.data_ptr<float>(), dtype, (int)B, (int)H, (int)Hkv, (int)Sq,
+                                    (int)Sk, (int)Dp, qs, ks, vs, os, gs, dqs, dks, dvs, scale,
+                                    causal ? 1 : 0, stream);
     TORCH_CHECK(rc == CMPEXT3_OK, "cmpext3 attention backward: ", cmpext3_attn_strerror(rc));
   }
   if (Dp != D) {
