@@ -106,3 +106,38 @@ def test_mismatched_heads_without_gqa_still_raise(patched):
     q, k, v = _gqa_inputs("fp16", 1, 4, 2, 32, 32, 64, seed=1)
     with pytest.raises(RuntimeError):
         F.scaled_dot_product_attention(q, k, v)
+
+
+PACKED = [
+    # dtype, B, H, Hkv, Sq, Sk, D: short query sweeps, packed G query heads per K/V head
+    ("bf16", 4, 32, 8, 1, 4096, 128),    # decode step, key split
+    ("fp16", 2, 16, 2, 5, 700, 64),      # ragged rows per head, 8 heads per group
+    ("fp16", 1, 8, 4, 64, 333, 64),      # the largest packed Sq
+    ("bf16", 1, 12, 3, 7, 2048, 96),     # head dim below its bucket
+    ("bf16", 1, 32, 8, 1, 32768, 128),   # long-context decode: 32 key parts, 3 of 4 waves rowless
+]
+
+
+@pytest.mark.parametrize("case", PACKED, ids=[f"{c[0]}-H{c[2]}of{c[3]}-q{c[4]}k{c[5]}d{c[6]}" for c in PACKED])
+def test_gqa_packed_query_heads(case):
+    """Grouped-query launches with short query sweeps pack each group's query
+    heads into the rows of one problem (K/V streamed once per group)."""
+    dtype, B, H, Hkv, Sq, Sk, D = case
+    q, k, v = _gqa_inputs(dtype, B, H, Hkv, Sq, Sk, D, seed=Sq * 3 + Sk)
+    scale = 1.0 / math.sqrt(D)
+    out = abi.attn_fwd(q, k, v, scale, False)
+    torch.cuda.synchronize()
+    assert orc.max_abs_err(out.cpu(), _oracle(q, k, v, scale, False)) <= TOL[dtype]
+
+
+def test_gqa_packed_strided_query_and_output():
+    """Packed rows with [B,S,H,D]-memory query and output views."""
+    B, H, Hkv, Sq, Sk, D = 2, 8, 2, 3, 640, 64
+    g = torch.Generator().manual_seed(17)
+    q = torch.randn(B, Sq, H, D, generator=g).half().cuda().transpose(1, 2)
+    k = torch.randn(B, Hkv, Sk, D, generator=g).half().cuda()
+    v = torch.randn(B, Hkv, Sk, D, generator=g).half().cuda()
+    o = torch.empty(B, Sq, H, D, dtype=torch.float16, device="cuda").transpose(1, 2)
+    assert abi.attn_fwd_raw(q, k, v, o, 0.125, False) == abi.OK
+    torch.cuda.synchronize()
+    assert orc.max_abs_err(o.cpu(), _oracle(q, k, v, 0.125, False)) <= TOL["fp16"]

@@ -39,6 +39,12 @@ struct FwdParams {
   // row's scale * Q K^T over its visible keys (what a backward pass needs to
   // rebuild P); null = not written.  Written by the pipelined kernel only.
   float* lse;
+  // grouped-query row packing (pipelined kernel, non-causal): when pack_sq > 0
+  // the launch runs over K/V heads, and row r of head hk is query position
+  // r % pack_sq of query head hk * G + r / pack_sq; q_h / o_h then step over a
+  // whole group of query heads and q_g / o_g over one query head
+  int pack_sq;
+  int64_t q_g, o_g;
 };
 
 // attention-mask element kinds (FwdParams::mask_kind)

@@ -135,6 +135,15 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   const int Sq = p.Sq, Sk = p.Sk, D = p.D;
   const int qlo = q0 + wave * 32;          // first query row of this wave
   const int qrow = qlo + l32;
+  // element offset of row r: packed grouped-query rows interleave the group's
+  // query heads (query head r / pack_sq, position r % pack_sq)
+  auto row_off = [&](int r, int64_t s_head, int64_t s_row) -> int64_t {
+    if (p.pack_sq > 0) {
+      const int g = r / p.pack_sq;
+      return g * s_head + (int64_t)(r - g * p.pack_sq) * s_row;
+    }
+    return (int64_t)r * s_row;
+  };
 
   int kend = Sk;
   if (CAUSAL) kend = min(Sk, q0 + BQ);
@@ -153,7 +162,7 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   for (int s = 0; s < NKS; ++s) {
     const int d = 16 * s + 8 * hh;
     u32x4 x = {0u, 0u, 0u, 0u};
-    if (qrow < Sq && d < D) x = *(const u32x4*)(qg + (int64_t)qrow * p.q_s + d);
+    if (qrow < Sq && d < D) x = *(const u32x4*)(qg + row_off(qrow, p.q_g, p.q_s) + d);
     if (PRESCALE) {
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
@@ -539,6 +548,9 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   // ---- epilogue
   float lsum = xhalf_sum(ls0 + ls1);
   float moff = mb;  // exp2-domain offset of lsum
+  // a wave whose rows all lie past Sq (short or packed query sweeps) has
+  // nothing to exchange or store; every part of the block agrees on that
+  if (qlo >= Sq) return;
   if (!CAUSAL && nparts > 1) {  // causal launches never split
     // Leave this part's state, then let the last part of the block merge.
     // Device-scope (sc1) stores and loads keep the exchange coherent across
@@ -600,7 +612,7 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
           lsum > 0.f ? (moff + __builtin_amdgcn_logf(lsum)) * 0.6931471805599453f : -INFINITY;
   }
   if (qrow < Sq) {
-    uint16_t* orow = og + (int64_t)qrow * p.o_s;
+    uint16_t* orow = og + row_off(qrow, p.o_g, p.o_s);
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll

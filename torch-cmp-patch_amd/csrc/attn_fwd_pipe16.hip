@@ -181,8 +181,33 @@ bool pipe16_applies(const FwdParams& p, int dk) {
 // never pre-scales: rounding Q*c to 8 mantissa bits moves each score by up to
 // 2^-9 of its size, which at scale 1 (scores of tens of log2 units) breaks
 // the 2e-2 bf16 bar, so bf16 scores get one FMA each instead.
+// Grouped-query launches whose query heads hold less than one block of rows
+// each (decode, short prefills) pack the G query heads of a K/V head into the
+// rows of one problem: the K/V of that head is then streamed once for all of
+// them, instead of once per query head with mostly empty blocks.  Non-causal,
+// unmasked, inference launches only (the row position then does not matter).
+constexpr int kPackMaxSq = 64;
+
+bool packs_query_heads(const FwdParams& p, bool causal) {
+  return !causal && p.kv_group > 1 && p.Sq <= kPackMaxSq && p.mask_kind == MASK_NONE && !p.lse &&
+         p.pack_sq == 0 && (int64_t)p.kv_group * p.Sq <= (int64_t)INT32_MAX / 2;
+}
+
+void pack_query_heads(FwdParams& p) {
+  const int G = p.kv_group;
+  p.pack_sq = p.Sq;
+  p.q_g = p.q_h;
+  p.o_g = p.o_h;
+  p.q_h *= G;  // packed head hk starts at query head hk * G
+  p.o_h *= G;
+  p.H /= G;
+  p.Sq *= G;
+  p.kv_group = 1;
+}
+
 hipError_t launch_pipe16(const FwdParams& p0, int dk0, bool bf16, bool causal, bool prescale, hipStream_t s) {
   FwdParams p = p0;
+  if (packs_query_heads(p, causal)) pack_query_heads(p);
   // the training forward has the 64 and 128 buckets only
   const int dk = p.lse ? (dk0 <= 64 ? 64 : 128) : dk0;
   // Without pre-scaling, masked keys enter as raw -inf and meet the multiplier
