@@ -93,13 +93,14 @@ def cpu_baseline(wl, budget_s: float = 10.0):
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     q, k, v = wl.make_inputs("cpu")
+    gqa = wl.kv_heads != wl.H
     t0 = time.perf_counter()
-    F.scaled_dot_product_attention(q, k, v, is_causal=wl.causal, scale=wl.eff_scale)  # warmup
+    F.scaled_dot_product_attention(q, k, v, is_causal=wl.causal, scale=wl.eff_scale, enable_gqa=gqa)
     one = time.perf_counter() - t0
     n = max(1, min(20, int(budget_s / max(one, 1e-3))))
     t0 = time.perf_counter()
     for _ in range(n):
-        F.scaled_dot_product_attention(q, k, v, is_causal=wl.causal, scale=wl.eff_scale)
+        F.scaled_dot_product_attention(q, k, v, is_causal=wl.causal, scale=wl.eff_scale, enable_gqa=gqa)
     dt = (time.perf_counter() - t0) / n
     return {
         "value": round(wl.flops() / dt / 1e12, 6),
@@ -124,7 +125,8 @@ def cpu_baseline_training(wl, budget_s: float = 20.0):
 
     def step(q, k, v):
         qq, kk, vv = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
-        out = F.scaled_dot_product_attention(qq, kk, vv, is_causal=wl.causal, scale=wl.eff_scale)
+        out = F.scaled_dot_product_attention(qq, kk, vv, is_causal=wl.causal, scale=wl.eff_scale,
+                                             enable_gqa=wl.kv_heads != wl.H)
         out.backward(torch.ones_like(out))
 
     try:
@@ -241,9 +243,19 @@ def main() -> int:
     wall, dev = time_kernel(fn, args.steps, args.warmup)
     ms = wall / args.steps * 1e3
     value = wl.flops() * args.steps / wall / 1e12
-    achieved = wl.flops() / dev / 1e12
     peak = W.PEAK_TFLOPS[wl.dtype]
     traffic = _traffic_from_profile(wl.name)
+    # below the ridge point (peak FLOP/s over peak HBM bytes/s) HBM bounds the kernel
+    hbm_bound = wl.flops() / wl.bytes() < peak * 1e12 / (W.PEAK_HBM_GBS * 1e9)
+    if hbm_bound:
+        roofline = {"bound": "hbm", "achieved": round(wl.bytes() / dev / 1e9, 1), "peak": W.PEAK_HBM_GBS,
+                    "unit": "GB/s", "frac": round(wl.bytes() / dev / 1e9 / W.PEAK_HBM_GBS, 4),
+                    "traffic": traffic, "kernel_us": round(dev * 1e6, 3), "bytes_per_launch": wl.bytes()}
+    else:
+        achieved = wl.flops() / dev / 1e12
+        roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": peak,
+                    "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
+                    "kernel_us": round(dev * 1e6, 3), "flops_per_launch": wl.flops()}
 
     if args.calibrate_copy_mb > 0:
         n = args.calibrate_copy_mb * (1 << 20) // 4
@@ -282,12 +294,10 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": {"fp16": "f16", "bf16": "bf16", "fp32": "f32"}[wl.dtype],
         "data": "synthetic (seeded N(0,1) Q/K/V, CPU generator -> device)",
-        "config": {"workload": wl.name, "B": wl.B, "H": wl.H, "Sq": wl.Sq, "Sk": wl.Sk,
-                   "D": wl.D, "causal": wl.causal, "scale": wl.eff_scale,
+        "config": {"workload": wl.name, "B": wl.B, "H": wl.H, "Hkv": wl.kv_heads, "Sq": wl.Sq,
+                   "Sk": wl.Sk, "D": wl.D, "causal": wl.causal, "scale": wl.eff_scale,
                    "entry": "cmpext3.ops.attention -> cmpext3_attn_fwd"},
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": peak,
-                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
-                     "kernel_us": round(dev * 1e6, 3), "flops_per_launch": wl.flops()},
+        "roofline": roofline,
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(wl),
         "configs": configs,
     }

@@ -1,5 +1,6 @@
-"""The five attention workloads this build is measured and checked on, and their
-seeded synthetic inputs.
+"""The five attention workloads this build is measured and checked on (plus a
+grouped-query decode step, outside BASELINE's list), and their seeded
+synthetic inputs.
 
 Inputs follow one recipe everywhere (bench, tests, smoke): a CPU
 torch.Generator seeded per workload draws fp32 N(0,1) for Q, then K, then V;
@@ -36,6 +37,7 @@ class Workload:
     kv_std: float = 1.0
     seed: int = 0
     note: str = field(default="", compare=False)
+    Hkv: Optional[int] = None  # K/V heads (grouped-query); None = H
 
     @property
     def torch_dtype(self) -> torch.dtype:
@@ -55,12 +57,16 @@ class Workload:
     def flops(self) -> int:
         return 4 * self.B * self.H * self.visible_pairs() * self.D
 
+    @property
+    def kv_heads(self) -> int:
+        return self.H if self.Hkv is None else self.Hkv
+
     def bytes(self) -> int:
         es = torch.tensor([], dtype=self.torch_dtype).element_size()
-        return es * self.B * self.H * self.D * (2 * self.Sq + 2 * self.Sk)
+        return es * self.B * self.D * (2 * self.H * self.Sq + 2 * self.kv_heads * self.Sk)
 
     def shapes(self):
-        return (self.B, self.H, self.Sq, self.D), (self.B, self.H, self.Sk, self.D)
+        return (self.B, self.H, self.Sq, self.D), (self.B, self.kv_heads, self.Sk, self.D)
 
     def make_inputs(self, device="cpu", seed: Optional[int] = None, layout: str = "bhsd"):
         """(q, k, v) with the recipe in the module docstring.  layout="bshd" returns
@@ -95,7 +101,13 @@ WORKLOADS = [
     Workload("sd15_self_fp32", "fp32", 2, 8, 4096, 4096, 40, scale=1 / math.sqrt(40), seed=5,
              note="SD1.5 UNet self-attention on the fp32 path, D=40"),
 ]
-BY_NAME = {w.name: w for w in WORKLOADS}
+# Measured beside BASELINE's configs (bench.py --workload NAME), not part of them.
+EXTRA_WORKLOADS = [
+    Workload("qwen3_decode_bf16", "bf16", 16, 16, 1, 4096, 128, scale=1 / math.sqrt(128), seed=6,
+             Hkv=8, note="Qwen3-0.6B-style decode step: 16 query heads over 8 K/V heads "
+                         "(native GQA), 4096-token KV cache, non-causal"),
+]
+BY_NAME = {w.name: w for w in WORKLOADS + EXTRA_WORKLOADS}
 
 # The workload the headline metric is quoted on.
 HEADLINE = BY_NAME["sdxl_self_fp16"]
