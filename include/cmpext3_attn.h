@@ -55,7 +55,7 @@ extern "C" {
 #define CMPEXT3_E_EMPTY_KEYS       5  /* Sk == 0 with Sq > 0: softmax over nothing */
 #define CMPEXT3_E_LAUNCH           6  /* the HIP launch itself failed */
 #define CMPEXT3_E_TOO_LARGE        7  /* a size does not fit the kernel's index arithmetic */
-#define CMPEXT3_E_MASK             8  /* attention mask with fp32 q, D > 128 or causal */
+#define CMPEXT3_E_MASK             8  /* attention mask with fp32 q or D > 128 */
 #define CMPEXT3_E_TRAINING         9  /* training entry point with fp32 or D > 128 */
 
 /*
@@ -115,8 +115,10 @@ int cmpext3_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o,
  *                to Sk rounded up to a multiple of 8 (values past Sk are
  *                ignored).
  * A query row whose keys are all dropped gives zeros (torch's result).
- * Supported for f16/bf16 q/k/v with D <= 128 and causal == 0; other calls
- * return CMPEXT3_E_MASK and launch nothing.
+ * With causal != 0 a pair is used only if it is causally visible AND the
+ * mask keeps it (torch's rule for attn_mask with is_causal).  Supported for
+ * f16/bf16 q/k/v with D <= 128; other calls return CMPEXT3_E_MASK and launch
+ * nothing.
  *
  * Reference: the reference never ran masks natively: _patched_sdpa sends
  * any attn_mask to stock torch (cmpext3/__init__.py:624).

@@ -163,13 +163,26 @@ class TestScaledDotProductAttention:
         assert F.scaled_dot_product_attention(q, k, v, attn_mask=mask) == "native-result"
         _called_once_with_tensors(native.attention, q, k, v, None, False, mask)
 
-    def test_falls_back_for_mask_with_causal(self, patched, native, monkeypatch):
+    def test_mask_with_causal_goes_native(self, patched, native, monkeypatch):
+        """attn_mask together with is_causal reaches the kernel (a pair must
+        pass both rules, torch's CPU behaviour)."""
         force_eligible(monkeypatch)
         q, k, v = _qkv(1, 2, 3, 4)
         mask = torch.ones(3, 3, dtype=torch.bool)
+        native.attention.return_value = "native-result"
         out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, is_causal=True)
+        assert out == "native-result"
+        _called_once_with_tensors(native.attention, q, k, v, None, True, mask)
+
+    def test_falls_back_for_unsupported_mask_dtype(self, patched, native, monkeypatch):
+        force_eligible(monkeypatch)
+        q, k, v = _qkv(1, 2, 3, 4)
+        mask = torch.zeros(3, 3, dtype=torch.float64)
+        try:
+            F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+        except RuntimeError:
+            pass   # stock's own error for a float64 mask on float32 q
         native.attention.assert_not_called()
-        assert torch.allclose(out, STOCK_SDPA(q, k, v, attn_mask=mask, is_causal=True))
 
     def test_falls_back_when_dropout_nonzero(self, patched, native, monkeypatch):
         force_eligible(monkeypatch)

@@ -85,11 +85,9 @@ def test_runs_on_the_callers_stream():
 
 
 def test_reference_fallbacks_do_not_reach_native(patched, counting_native):
-    """Dropout, live autograd and a mask combined with is_causal stay on stock
-    (plain attn_mask calls run natively: tests/test_gpu_mask.py)."""
+    """Dropout and live autograd stay on stock (attn_mask calls, with or
+    without is_causal, run natively: tests/test_gpu_mask.py)."""
     q, k, v = W.Workload("fb", "fp16", 1, 2, 64, 64, 64).make_inputs("cuda")
-    mask = torch.ones(64, 64, dtype=torch.bool, device="cuda").tril_()
-    F.scaled_dot_product_attention(q, k, v, attn_mask=mask, is_causal=True)
     F.scaled_dot_product_attention(q, k, v, dropout_p=0.5)
     qg = q.clone().requires_grad_(True)
     F.scaled_dot_product_attention(qg, k, v)

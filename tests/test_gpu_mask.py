@@ -12,8 +12,10 @@ Shapes cover short key sweeps (the pipelined kernel takes every masked call),
 odd tile counts, the key split (parts of a row merge masked partials, some of
 them empty), grouped-query K/V, head dims below their bucket, and mask
 layouts the ABI cannot read in place (transposed, key count not a multiple
-of 4), which the bindings copy.  Unsupported masked calls (fp32, D > 128,
-mask with causal) are rejected by the ABI and fall back to stock in the patch.
+of 4), which the bindings copy.  With is_causal a pair must be causally
+visible and kept by the mask (torch's CPU rule; the oracle is pinned to it in
+tests/test_oracle.py).  Unsupported masked calls (fp32, D > 128) are rejected
+by the ABI and fall back to stock in the patch.
 """
 from __future__ import annotations
 
@@ -70,16 +72,17 @@ CASES = [
 KINDS = ["bool_pad", "bool_full", "add_heads", "add_2d_f32"]
 
 
+@pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}-B{c[1]}H{c[2]}-q{c[3]}k{c[4]}d{c[5]}" for c in CASES])
-def test_mask_parity(case, kind):
+def test_mask_parity(case, kind, causal):
     dtype, B, H, Sq, Sk, D = case
     q, k, v = _inputs(dtype, B, H, Sq, Sk, D, seed=Sq + Sk)
     m = _mask(kind, dtype, B, H, Sq, Sk, seed=D)
     scale = 1.0 / math.sqrt(D)
-    out = abi.attn_fwd(q, k, v, scale, False, attn_mask=m)
+    out = abi.attn_fwd(q, k, v, scale, causal, attn_mask=m)
     torch.cuda.synchronize()
-    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), scale, attn_mask=m.cpu())
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), scale, causal=causal, attn_mask=m.cpu())
     assert orc.max_abs_err(out.cpu(), ref) <= TOL[dtype]
 
 
@@ -123,8 +126,6 @@ def test_unsupported_masked_calls_are_rejected():
     assert abi.attn_fwd_raw(q32, q32, q32, torch.empty_like(q32), 0.125, attn_mask=m) == abi.E_MASK
     q160 = torch.randn(1, 2, 64, 160, device="cuda").half()
     assert abi.attn_fwd_raw(q160, q160, q160, torch.empty_like(q160), 0.125, attn_mask=m) == abi.E_MASK
-    q64 = torch.randn(1, 2, 64, 64, device="cuda").half()
-    assert abi.attn_fwd_raw(q64, q64, q64, torch.empty_like(q64), 0.125, True, attn_mask=m) == abi.E_MASK
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])

@@ -241,6 +241,23 @@ def test_masked_oracle_matches_torch_math(kind):
     assert orc.max_abs_err(orc.sdpa_loops(q, k, v, 0.3, attn_mask=mask), want) < 1e-12
 
 
+@pytest.mark.parametrize("kind", ["bool_full", "bool_pad", "float_heads", "float_2d"])
+def test_masked_causal_oracle_matches_torch_cpu(kind):
+    """attn_mask with is_causal: torch's CPU SDPA (default dispatch; its MATH
+    backend refuses the pair) uses a (query, key) pair only if it is causally
+    visible and the mask keeps it (bool) / adds the mask to the visible pairs
+    (float).  Sq < Sk and Sq > Sk both checked."""
+    for sq, sk in ((9, 13), (13, 9)):
+        q, k, v = _rand(2, 3, sq, sk, 8, seed=43)
+        mask = _masks(2, 3, sq, sk, seed=44)[kind]
+        mask = mask if kind != "bool_full" else mask.clone()
+        if kind == "bool_full":
+            mask[..., 0] = True          # torch's CPU path gives NaN for rows with no visible key
+        want = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, is_causal=True, scale=0.3).numpy()
+        assert orc.max_abs_err(orc.sdpa_np(q, k, v, 0.3, causal=True, attn_mask=mask), want) < 1e-12
+        assert orc.max_abs_err(orc.sdpa_loops(q, k, v, 0.3, causal=True, attn_mask=mask), want) < 1e-12
+
+
 def test_fully_masked_rows_give_zeros_like_torch():
     q, k, v = _rand(1, 1, 4, 6, 8, seed=5)
     mask = torch.ones(4, 6, dtype=torch.bool)

@@ -215,8 +215,8 @@ def _patched_sdpa(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=Fa
     support.  Grouped-query calls (K/V with fewer heads than Q) run natively
     only under enable_gqa=True, as torch requires; without it they go to
     stock, which raises torch's own error.  An attn_mask (bool or float
-    tensor) runs natively when is_causal is False; mask and is_causal
-    together go to stock.
+    tensor) runs natively, also together with is_causal (a pair must pass
+    both, torch's rule).
     """
     orig = _ORIGINALS[(F, "scaled_dot_product_attention")]
 
@@ -244,8 +244,7 @@ def _patched_sdpa(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=Fa
                          (query.shape, query.dtype, key.shape, value.shape, scale, is_causal),
                          lambda: _C.attention(query, key, value, scale, is_causal),
                          stock)
-    if (is_causal or not isinstance(attn_mask, torch.Tensor)
-            or attn_mask.dtype not in _MASK_DTYPES):
+    if not isinstance(attn_mask, torch.Tensor) or attn_mask.dtype not in _MASK_DTYPES:
         return stock()
     return _dispatch("attention", query,
                      (query.shape, query.dtype, key.shape, value.shape, scale, is_causal,

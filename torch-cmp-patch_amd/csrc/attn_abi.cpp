@@ -83,7 +83,7 @@ const char* cmpext3_attn_strerror(int code) {
     case CMPEXT3_E_LAUNCH: return "HIP kernel launch failed";
     case CMPEXT3_E_TOO_LARGE: return "problem too large for 32-bit tile indexing";
     case CMPEXT3_E_MASK:
-      return "attention mask not supported here (needs f16/bf16 q, head dim <= 128, non-causal)";
+      return "attention mask not supported here (needs f16/bf16 q and head dim <= 128)";
     case CMPEXT3_E_TRAINING:
       return "not supported by the training entry points (need f16/bf16 and head dim <= 128)";
   }
@@ -143,8 +143,8 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
   if (masked) {
     if (mask_dtype < CMPEXT3_DTYPE_F16 || mask_dtype > CMPEXT3_DTYPE_BOOL) return CMPEXT3_E_DTYPE;
     if (!mask || !mask_str) return CMPEXT3_E_INVALID;
-    // masks run on the pipelined fp16/bf16 kernel only, without causal masking
-    if (dtype == CMPEXT3_DTYPE_F32 || D > 128 || causal) return CMPEXT3_E_MASK;
+    // masks run on the pipelined fp16/bf16 kernel only (causal or not)
+    if (dtype == CMPEXT3_DTYPE_F32 || D > 128) return CMPEXT3_E_MASK;
     // every 4-key run of a row is one aligned 4/8/16-byte load
     if (((uintptr_t)mask & 15u) != 0) return CMPEXT3_E_ALIGN;
     for (int i = 0; i < 3; ++i)

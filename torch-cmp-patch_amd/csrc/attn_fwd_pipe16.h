@@ -77,8 +77,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base,
 // XOR-swizzled LDS rows (DK == DP in {32, 64, 128}).  OPT bit 2: leave the
 // interleave to the compiler (no sched_barrier fences).  OPT bit 3: the head
 // dim is not a multiple of 16 (D < DK), so K columns past D are zeroed.
-// OPT bit 4: an attention mask (p.mask, non-causal launches) is applied to
-// every tile's scores before the exponentials.  OPT bit 5: each row's
+// OPT bit 4: an attention mask (p.mask) is applied to every tile's scores
+// before the exponentials (with CAUSAL, a pair must pass both).  OPT bit 5: each row's
 // log-sum-exp goes to p.lse (the training forward).
 template <typename T, int DK, int DP, int NW, int BK, int OCC, bool CAUSAL, bool PRESCALE, int OPT = 0>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
@@ -87,7 +87,6 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   constexpr int BQ = NW * 32;
   constexpr bool SWZ = (OPT & 2) && (DK == DP) && (DK == 32 || DK == 64 || DK == 128);
   constexpr bool MASK = (OPT & 16) != 0;
-  static_assert(!(MASK && CAUSAL), "masked launches are non-causal");
   constexpr int RSK = SWZ ? DK : DK + 8;  // K tile row stride (halves)
   constexpr int RSV = SWZ ? DP : DP + 8;  // V tile row stride (halves)
   constexpr int KTILE = BK * RSK;

@@ -233,11 +233,15 @@ hipError_t launch_pipe16(const FwdParams& p0, int dk0, bool bf16, bool causal, b
       return causal ? launch_lse<_Float16, true, true>(p, sa, dk, s) : launch_lse<_Float16, false, true>(p, sa, dk, s);
     return causal ? launch_lse<_Float16, true, false>(p, sa, dk, s) : launch_lse<_Float16, false, false>(p, sa, dk, s);
   }
-  if (p.mask_kind != MASK_NONE) {  // masked launches are non-causal (checked by the caller)
-    if (causal) return hipErrorNotSupported;
-    if (bf16) return launch_bucket<__bf16, false, false, 16>(p, sa, dk, s);
-    return prescale ? launch_bucket<_Float16, false, true, 16>(p, sa, dk, s)
-                    : launch_bucket<_Float16, false, false, 16>(p, sa, dk, s);
+  if (p.mask_kind != MASK_NONE) {  // with causal, a pair must pass both rules
+    if (bf16)
+      return causal ? launch_bucket<__bf16, true, false, 16>(p, sa, dk, s)
+                    : launch_bucket<__bf16, false, false, 16>(p, sa, dk, s);
+    if (prescale)
+      return causal ? launch_bucket<_Float16, true, true, 16>(p, sa, dk, s)
+                    : launch_bucket<_Float16, false, true, 16>(p, sa, dk, s);
+    return causal ? launch_bucket<_Float16, true, false, 16>(p, sa, dk, s)
+                  : launch_bucket<_Float16, false, false, 16>(p, sa, dk, s);
   }
   if (bf16)
     return causal ? launch_bucket<__bf16, true, false>(p, sa, dk, s) : launch_bucket<__bf16, false, false>(p, sa, dk, s);

@@ -18,8 +18,8 @@
 //     into zero-padded contiguous copies instead of being rejected;
 //   * K/V may hold fewer heads than Q (grouped-query attention);
 //   * attn_mask (bool or additive f16/bf16/f32, broadcast like torch's SDPA)
-//     runs natively for f16/bf16 with D <= 128 and causal=False (the
-//     reference sent every mask to stock torch, cmpext3/__init__.py:624).
+//     runs natively for f16/bf16 with D <= 128, alone or combined with causal
+//     (the reference sent every mask to stock torch, cmpext3/__init__.py:624).
 //
 // attention_fwd_lse / attention_bwd: the training pair (no reference
 // counterpart: the reference is forward-only, cmpext3/__init__.py:115-125),
@@ -147,7 +147,6 @@ torch::Tensor attention(torch::Tensor query, torch::Tensor key, torch::Tensor va
 
   Mask mask;
   if (attn_mask.has_value() && attn_mask->defined()) {
-    TORCH_CHECK(!causal, "cmpext3 attention: attn_mask together with causal runs on stock torch");
     mask = prepare_mask(*attn_mask, query, B, H, Sq, Sk);
   }
 
