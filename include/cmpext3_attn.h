@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define CMPEXT3_ATTN_ABI_VERSION 4
+#define CMPEXT3_ATTN_ABI_VERSION 5
 
 /* dtype codes (CMPEXT3_DTYPE_BOOL: attention masks only) */
 #define CMPEXT3_DTYPE_F16  0
@@ -131,11 +131,13 @@ int cmpext3_attn_fwd_masked(const void* q, const void* k, const void* v, void* o
                             float scale, int causal, hipStream_t stream);
 
 /*
- * Training forward: as cmpext3_attn_fwd_gqa (no mask), and also writes
+ * Training forward: as cmpext3_attn_fwd_masked (mask_dtype -1 = no mask), and
+ * also writes
  *
  *   lse : [B, H, Sq] fp32, contiguous (element (b, h, i) at lse[(b*H + h)*Sq + i]),
  *         the natural-log log-sum-exp over the visible keys of row i of
- *         scale * Q K^T -- what cmpext3_attn_bwd needs to rebuild the softmax.
+ *         scale * Q K^T (+ mask) -- what cmpext3_attn_bwd needs to rebuild the
+ *         softmax; -inf for a row whose keys are all dropped.
  *
  * Supported for f16/bf16 with D <= 128 (else CMPEXT3_E_TRAINING, nothing
  * launched).  Every such call runs the pipelined kernel, whatever Sk.
@@ -147,6 +149,7 @@ int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, f
                          int dtype, int B, int H, int H_kv, int Sq, int Sk, int D,
                          const int64_t q_str[3], const int64_t k_str[3],
                          const int64_t v_str[3], const int64_t o_str[3],
+                         const void* mask, int mask_dtype, const int64_t mask_str[3],
                          float scale, int causal, hipStream_t stream);
 
 /*
@@ -155,9 +158,11 @@ int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, f
  *
  *   dq : [B, H, Sq, D]   dk, dv : [B, H_kv, Sk, D]   (all `dtype`, overwritten)
  *
- * of sum(o * dout), with the same scale, causal flag and K/V head count as
+ * of sum(o * dout), with the same scale, causal flag, K/V head count and
+ * attention mask (same layout rules as cmpext3_attn_fwd_masked; -1 = none) as
  * the forward (H_kv must divide H; query head h uses K/V head h / (H / H_kv),
- * and dk, dv sum the contributions of every query head of the group).
+ * and dk, dv sum the contributions of every query head of the group).  A row
+ * whose keys were all dropped passes no gradient (its dq row is zero).
  *   delta : caller-owned fp32 workspace of B*H*Sq elements (4-byte aligned;
  *           receives sum_d dout * o per row).
  *   *_str[3] : element strides over {batch, head, seq} as in cmpext3_attn_fwd.
@@ -177,6 +182,7 @@ int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
                      const int64_t v_str[3], const int64_t o_str[3],
                      const int64_t do_str[3], const int64_t dq_str[3],
                      const int64_t dk_str[3], const int64_t dv_str[3],
+                     const void* mask, int mask_dtype, const int64_t mask_str[3],
                      float scale, int causal, hipStream_t stream);
 
 /* Human-readable text for a return code (static storage). */

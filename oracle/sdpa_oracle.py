@@ -36,9 +36,11 @@ follow; the restatement is the calculus of softmax attention, with
 P = softmax(S), S = scale * Q K^T (causal: invisible pairs at -inf):
   dV = P^T dO,  dP = dO V^T,  Delta_i = sum_d dO_id O_id = sum_j P_ij dP_ij,
   dS = P * (dP - Delta),  dQ = scale * dS K,  dK = scale * dS^T Q,
-and lse_i = log sum_j exp(S_ij) (natural log).  Pinned in
-tests/test_oracle_bwd.py against torch autograd in float64, central finite
-differences and closed forms.
+and lse_i = log sum_j exp(S_ij) (natural log).  attn_mask / causal act on S
+as in the forward (invisible pairs at -inf, float masks added); a row with no
+visible key has P = 0.  Pinned in tests/test_oracle_bwd.py against torch
+autograd in float64 (masks included), central finite differences and closed
+forms.
 """
 from __future__ import annotations
 
@@ -138,14 +140,16 @@ def sdpa_np(q, k, v, scale: Optional[float] = None, causal: bool = False,
 
 
 def sdpa_lse_np(q, k, scale: Optional[float] = None, causal: bool = False,
-                block: int = 512) -> np.ndarray:
+                block: int = 512, attn_mask=None) -> np.ndarray:
     """float64 [B, H, Sq] natural-log logsumexp over keys of scale * Q K^T
-    (causal: visible keys only)."""
+    (causal / attn_mask: visible keys only, float masks added; a row with no
+    visible key gives -inf)."""
     q, k = _as_f64(q), _as_f64(k)
     B, H, Sq, D = q.shape
     Sk = k.shape[2]
     if scale is None:
         scale = default_scale(D)
+    mask = _mask_4d(attn_mask, B, H, Sq, Sk)
     out = np.empty((B, H, Sq), dtype=np.float64)
     for b in range(B):
         for h in range(H):
@@ -155,20 +159,28 @@ def sdpa_lse_np(q, k, scale: Optional[float] = None, causal: bool = False,
                 s = (q[b, h, i0:i1] @ kt) * scale
                 if causal:
                     s = np.where(causal_visible(Sq, Sk)[i0:i1], s, -np.inf)
+                if mask is not None:
+                    s = _apply_mask(s, mask[b, h, i0:i1])
                 m = s.max(axis=1, keepdims=True)
-                out[b, h, i0:i1] = (m + np.log(np.exp(s - m).sum(axis=1, keepdims=True)))[:, 0]
+                dead = ~np.isfinite(m) & (m < 0)
+                m = np.where(dead, 0.0, m)
+                with np.errstate(divide="ignore"):
+                    lse = m + np.log(np.exp(s - m).sum(axis=1, keepdims=True))
+                out[b, h, i0:i1] = np.where(dead, -np.inf, lse)[:, 0]
     return out
 
 
 def sdpa_bwd_np(q, k, v, do, scale: Optional[float] = None, causal: bool = False,
-                block: int = 512):
+                block: int = 512, attn_mask=None):
     """float64 gradients (dq, dk, dv) of sum(O * dO) for O = sdpa(q, k, v),
-    blocked over query rows (every query row sees at least key 0)."""
+    blocked over query rows.  attn_mask as in sdpa_np; a row with no visible
+    key has O = 0 and passes no gradient."""
     q, k, v, do = _as_f64(q), _as_f64(k), _as_f64(v), _as_f64(do)
     B, H, Sq, D = q.shape
     Sk = k.shape[2]
     if scale is None:
         scale = default_scale(D)
+    mask = _mask_4d(attn_mask, B, H, Sq, Sk)
     dq = np.zeros_like(q)
     dk = np.zeros_like(k)
     dv = np.zeros_like(v)
@@ -180,9 +192,14 @@ def sdpa_bwd_np(q, k, v, do, scale: Optional[float] = None, causal: bool = False
                 s = (q[b, h, i0:i1] @ kt) * scale
                 if causal:
                     s = np.where(causal_visible(Sq, Sk)[i0:i1], s, -np.inf)
+                if mask is not None:
+                    s = _apply_mask(s, mask[b, h, i0:i1])
                 m = s.max(axis=1, keepdims=True)
+                dead = ~np.isfinite(m) & (m < 0)                    # no visible key
+                m = np.where(dead, 0.0, m)
                 e = np.exp(s - m)
-                p = e / e.sum(axis=1, keepdims=True)               # [rows, Sk]
+                z = e.sum(axis=1, keepdims=True)
+                p = np.where(dead, 0.0, e / np.where(dead, 1.0, z))  # [rows, Sk]
                 g = do[b, h, i0:i1]
                 o = p @ v[b, h]
                 dv[b, h] += p.T @ g

@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version_and_messages():
-    assert abi.lib().cmpext3_attn_abi_version() == 4
+    assert abi.lib().cmpext3_attn_abi_version() == 5
     for code in range(10):
         assert abi.strerror(code) and abi.strerror(code) != "unknown error code"
     assert abi.strerror(99) == "unknown error code"
@@ -131,16 +131,17 @@ def _call_lse(lse=16, dtype=abi.DTYPE_F16, D=64, q=16, Sq=8, Sk=8, scale=0.125):
     st = (ctypes.c_int64 * 3)(512, 512, 64)
     vp = ctypes.c_void_p
     return abi.lib().cmpext3_attn_fwd_lse(vp(q), vp(16), vp(16), vp(16), vp(lse), dtype, 1, 1, 1, Sq, Sk,
-                                          D, st, st, st, st, ctypes.c_float(scale), 0, None)
+                                          D, st, st, st, st, vp(0), -1, st, ctypes.c_float(scale), 0, None)
 
 
 def _call_bwd(delta=16, lse=16, dtype=abi.DTYPE_F16, D=64, dq=16, Sq=8, Sk=8, scale=0.125,
-              strides=(512, 512, 64), H=1, H_kv=1):
+              strides=(512, 512, 64), H=1, H_kv=1, mask=0, mask_dtype=-1, mask_str=(0, 0, 0)):
     st = (ctypes.c_int64 * 3)(*strides)
     vp = ctypes.c_void_p
     return abi.lib().cmpext3_attn_bwd(vp(16), vp(16), vp(16), vp(16), vp(16), vp(lse), vp(dq), vp(16),
                                       vp(16), vp(delta), dtype, 1, H, H_kv, Sq, Sk, D,
-                                      *([st] * 8), ctypes.c_float(scale), 1, None)
+                                      *([st] * 8), vp(mask), mask_dtype, (ctypes.c_int64 * 3)(*mask_str),
+                                      ctypes.c_float(scale), 1, None)
 
 
 def test_training_entry_points_reject_before_launch():
@@ -164,3 +165,7 @@ def test_training_entry_points_reject_before_launch():
     assert _call_bwd(delta=0, Sq=0) == abi.OK
     assert _call_bwd(H=4, H_kv=3) == abi.E_INVALID
     assert _call_bwd(H=4, H_kv=0) == abi.E_INVALID
+    assert _call_bwd(mask=0, mask_dtype=abi.DTYPE_BOOL) == abi.E_INVALID
+    assert _call_bwd(mask=16, mask_dtype=7) == abi.E_DTYPE
+    assert _call_bwd(mask=24, mask_dtype=abi.DTYPE_BOOL) == abi.E_ALIGN
+    assert _call_bwd(mask=16, mask_dtype=abi.DTYPE_BOOL, mask_str=(0, 0, 6)) == abi.E_ALIGN

@@ -249,3 +249,82 @@ def test_double_backward_is_refused():
     (gq,) = torch.autograd.grad(out, q, do, create_graph=True)
     with pytest.raises(RuntimeError):
         gq.sum().backward()
+
+
+def _train_mask(kind, B, H, Sq, Sk, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    if kind == "bool_pad":                    # key padding [B,1,1,Sk]
+        m = torch.ones(B, 1, 1, Sk, dtype=torch.bool)
+        for b in range(B):
+            m[b, ..., Sk - 1 - (13 * (b + 1)) % Sk:] = False
+    elif kind == "bool_full":                 # per (b, h, query), key 0 kept
+        m = torch.rand(B, H, Sq, Sk, generator=g) > 0.3
+        m[..., 0] = True
+    elif kind == "add_heads":                 # additive in the query dtype, -inf entries
+        m = (torch.randn(1, H, Sq, Sk, generator=g) * 2).to(TDT[dtype])
+        m[..., 1::5] = -math.inf
+    else:                                     # additive fp32 [Sq, Sk]
+        m = torch.randn(Sq, Sk, generator=g)
+    return m.cuda()
+
+
+MASK_TRAIN = [
+    # dtype, B, H, Sq, Sk, D
+    ("fp16", 2, 2, 160, 300, 64),
+    ("bf16", 1, 2, 200, 1100, 128),   # forward key split
+]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("kind", ["bool_pad", "bool_full", "add_heads", "add_2d_f32"])
+@pytest.mark.parametrize("case", MASK_TRAIN, ids=[f"{c[0]}-q{c[3]}k{c[4]}d{c[5]}" for c in MASK_TRAIN])
+def test_masked_training_pair(case, kind, causal):
+    dtype, B, H, Sq, Sk, D = case
+    q, k, v, do = _inputs(dtype, B, H, Sq, Sk, D, seed=Sq + Sk + D)
+    m = _train_mask(kind, B, H, Sq, Sk, dtype, seed=D)
+    s = D ** -0.5
+    out, lse = abi.attn_fwd_lse(q, k, v, s, causal, attn_mask=m)
+    dq, dk, dv = abi.attn_bwd(q, k, v, out, do, lse, s, causal, attn_mask=m)
+    torch.cuda.synchronize()
+    qc, kc, vc, dc, mc = (t.cpu() for t in (q, k, v, do, m))
+    assert orc.max_abs_err(out.cpu(), orc.sdpa_np(qc, kc, vc, s, causal, attn_mask=mc)) <= TOL[dtype]
+    assert orc.max_abs_err(lse.cpu(), orc.sdpa_lse_np(qc, kc, s, causal, attn_mask=mc)) <= TOL[dtype]
+    want = orc.sdpa_bwd_np(qc, kc, vc, dc, s, causal, attn_mask=mc)
+    for name, got, ref in zip(("dq", "dk", "dv"), (dq, dk, dv), want):
+        assert _rel_err(got, ref) <= TOL[dtype], name
+
+
+def test_masked_training_dead_rows():
+    """Rows whose keys are all dropped: output 0, lse -inf, no gradient."""
+    q, k, v, do = _inputs("fp16", 1, 2, 96, 200, 64, seed=77)
+    m = torch.ones(1, 2, 96, 200, dtype=torch.bool, device="cuda")
+    m[:, :, 7] = False
+    m[:, 1, 40, :100] = False
+    out, lse = abi.attn_fwd_lse(q, k, v, 0.125, False, attn_mask=m)
+    dq, dk, dv = abi.attn_bwd(q, k, v, out, do, lse, 0.125, False, attn_mask=m)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out[:, :, 7]) == 0
+    assert bool(torch.isneginf(lse[:, :, 7]).all())
+    assert torch.count_nonzero(dq[:, :, 7]) == 0
+    want = orc.sdpa_bwd_np(q.cpu(), k.cpu(), v.cpu(), do.cpu(), 0.125, False, attn_mask=m.cpu())
+    for got, ref in zip((dq, dk, dv), want):
+        assert _rel_err(got, ref) <= TOL["fp16"]
+
+
+def test_sdpa_training_route_with_mask(patched):
+    """enable_backward(): a masked SDPA call with live autograd stays native."""
+    q, k, v, do = _inputs("bf16", 2, 2, 128, 192, 64, seed=13)
+    m = _train_mask("bool_pad", 2, 2, 128, 192, "bf16", seed=2)
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    was = cmpext3.backward_enabled()
+    cmpext3.enable_backward(True)
+    try:
+        out = F.scaled_dot_product_attention(qq, kk, vv, attn_mask=m, is_causal=True)
+        assert "_Attention" in type(out.grad_fn).__name__
+        out.backward(do)
+    finally:
+        cmpext3.enable_backward(was)
+    torch.cuda.synchronize()
+    want = orc.sdpa_bwd_np(q.cpu(), k.cpu(), v.cpu(), do.cpu(), None, True, attn_mask=m.cpu())
+    for got, ref in zip((qq.grad, kk.grad, vv.grad), want):
+        assert _rel_err(got, ref) <= TOL["bf16"]

@@ -139,3 +139,48 @@ def test_planted_mistakes_fail(mistake):
         assert err <= 1e-10
     else:
         assert err > 1e-3
+
+
+def _masks(B, H, Sq, Sk, seed):
+    g = torch.Generator().manual_seed(seed)
+    keep = torch.rand(B, H, Sq, Sk, generator=g) > 0.3
+    keep[..., 0] = True                       # every row keeps key 0 (no dead rows for torch)
+    pad = torch.ones(B, 1, 1, Sk, dtype=torch.bool)
+    pad[..., Sk - 3:] = False
+    add = torch.randn(1, H, Sq, Sk, generator=g, dtype=torch.float64) * 2
+    add[..., 1::4] = -torch.inf
+    return {"bool": keep, "pad": pad, "add": add}
+
+
+@pytest.mark.parametrize("kind", ["bool", "pad", "add"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_masked_bwd_matches_torch_autograd_f64(kind, causal):
+    B, H, Sq, Sk, D = 2, 2, 11, 14, 8
+    q, k, v, do = _inputs(B, H, Sq, Sk, D, seed=31)
+    mask = _masks(B, H, Sq, Sk, seed=32)[kind]
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    o = F.scaled_dot_product_attention(qq, kk, vv, attn_mask=mask, is_causal=causal, scale=0.4)
+    o.backward(do)
+    got = orc.sdpa_bwd_np(q, k, v, do, 0.4, causal, block=5, attn_mask=mask)
+    for g, w in zip(got, (qq.grad, kk.grad, vv.grad)):
+        assert np.abs(g - w.numpy()).max() <= 1e-10
+    s = (q @ k.transpose(-1, -2)) * 0.4
+    if causal:
+        s = s.masked_fill(~torch.ones(Sq, Sk, dtype=torch.bool).tril(), -torch.inf)
+    s = s.masked_fill(~mask, -torch.inf) if mask.dtype == torch.bool else s + mask
+    want_lse = torch.logsumexp(s, dim=-1).numpy()
+    assert np.abs(orc.sdpa_lse_np(q, k, 0.4, causal, block=5, attn_mask=mask) - want_lse).max() <= 1e-12
+
+
+def test_masked_bwd_dead_rows_pass_no_gradient():
+    """A row whose keys are all dropped has O = 0 (torch's result): it adds
+    nothing to dK/dV and its dQ is zero; lse is -inf there."""
+    q, k, v, do = _inputs(1, 1, 6, 9, 8, seed=33)
+    keep = torch.ones(1, 1, 6, 9, dtype=torch.bool)
+    keep[0, 0, 2] = False
+    dq, dk, dv = orc.sdpa_bwd_np(q, k, v, do, 0.5, False, attn_mask=keep)
+    assert np.abs(dq[0, 0, 2]).max() == 0
+    rows = [i for i in range(6) if i != 2]
+    dq2, dk2, dv2 = orc.sdpa_bwd_np(q[:, :, rows], k, v, do[:, :, rows], 0.5, False)
+    assert np.abs(dk - dk2).max() <= 1e-12 and np.abs(dv - dv2).max() <= 1e-12
+    assert orc.sdpa_lse_np(q, k, 0.5, attn_mask=keep)[0, 0, 2] == -np.inf

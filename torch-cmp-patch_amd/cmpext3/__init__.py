@@ -26,8 +26,9 @@ What runs where:
 Training (no counterpart in the reference, which is forward-only): with
 ``CMPEXT3_BACKWARD=1`` in the environment, or after ``enable_backward()``,
 SDPA calls with live autograd on fp16/bf16 GPU tensors with D <= 128, equal
-head counts (or grouped-query K/V under enable_gqa=True), no mask and no
-dropout run the native forward and backward
+head counts (or grouped-query K/V under enable_gqa=True), an optional
+attn_mask that needs no gradient, and no dropout run the native forward and
+backward
 kernels (``attention`` below, a torch.autograd.Function); everything else
 with live autograd still goes to stock.  Off by default, so the default
 behaviour is the reference's.
@@ -148,30 +149,40 @@ class _Attention(torch.autograd.Function):
     kernels: Delta, dK/dV, dQ; no atomics)."""
 
     @staticmethod
-    def forward(ctx, q, k, v, scale, causal):
-        out, lse = _C.attention_fwd_lse(q, k, v, scale, causal)
-        ctx.save_for_backward(q, k, v, out, lse)
+    def forward(ctx, q, k, v, scale, causal, attn_mask):
+        if attn_mask is None:
+            out, lse = _C.attention_fwd_lse(q, k, v, scale, causal)
+        else:
+            out, lse = _C.attention_fwd_lse(q, k, v, scale, causal, attn_mask)
+        ctx.save_for_backward(q, k, v, out, lse, attn_mask)
         ctx.scale, ctx.causal = scale, causal
         return out
 
     @staticmethod
     @torch.autograd.function.once_differentiable
     def backward(ctx, grad_out):
-        q, k, v, out, lse = ctx.saved_tensors
-        dq, dk, dv = _C.attention_bwd(q, k, v, out, grad_out, lse, ctx.scale, ctx.causal)
-        return dq, dk, dv, None, None
+        q, k, v, out, lse, attn_mask = ctx.saved_tensors
+        if attn_mask is None:
+            dq, dk, dv = _C.attention_bwd(q, k, v, out, grad_out, lse, ctx.scale, ctx.causal)
+        else:
+            dq, dk, dv = _C.attention_bwd(q, k, v, out, grad_out, lse, ctx.scale, ctx.causal, attn_mask)
+        return dq, dk, dv, None, None, None
 
 
 def attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
-              scale: float | None = None, causal: bool = False) -> torch.Tensor:
+              scale: float | None = None, causal: bool = False,
+              attn_mask: torch.Tensor | None = None) -> torch.Tensor:
     """Differentiable native attention (fp16/bf16 GPU tensors [B, H, S, D],
     D <= 128; K/V may hold fewer heads than Q when that count divides H, with
-    torch's enable_gqa meaning).  Raises RuntimeError for anything else."""
-    return _Attention.apply(query, key, value, scale, causal)
+    torch's enable_gqa meaning; attn_mask as in SDPA, bool or additive, no
+    gradient taken for it).  Raises RuntimeError for anything else."""
+    return _Attention.apply(query, key, value, scale, causal, attn_mask)
 
 
 def _training_applies(query, key, value, attn_mask, dropout_p, enable_gqa) -> bool:
-    if not (_BACKWARD and attn_mask is None and dropout_p == 0.0
+    mask_ok = attn_mask is None or (isinstance(attn_mask, torch.Tensor) and attn_mask.is_cuda
+                                    and attn_mask.dtype in _MASK_DTYPES and not attn_mask.requires_grad)
+    if not (_BACKWARD and mask_ok and dropout_p == 0.0
             and all(isinstance(t, torch.Tensor) and t.is_cuda and t.dim() == 4
                     and t.dtype == query.dtype for t in (query, key, value))
             and query.dtype in _TRAIN_DTYPES):
@@ -228,7 +239,7 @@ def _patched_sdpa(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=Fa
             and _training_applies(query, key, value, attn_mask, dropout_p,
                                   bool(kwargs.get("enable_gqa", False)))):
         try:
-            return _Attention.apply(query, key, value, scale, is_causal)
+            return _Attention.apply(query, key, value, scale, is_causal, attn_mask)
         except (RuntimeError, TypeError):
             return stock()
     if (dropout_p != 0.0

@@ -44,9 +44,10 @@ def lib() -> ctypes.CDLL:
                                               ctypes.c_float, ci, vp]
         L.cmpext3_attn_fwd_masked.restype = ci
         L.cmpext3_attn_fwd_lse.argtypes = [vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci, ci,
-                                           i64p, i64p, i64p, i64p, ctypes.c_float, ci, vp]
+                                           i64p, i64p, i64p, i64p, vp, ci, i64p, ctypes.c_float, ci, vp]
         L.cmpext3_attn_fwd_lse.restype = ci
-        L.cmpext3_attn_bwd.argtypes = [vp] * 10 + [ci] * 7 + [i64p] * 8 + [ctypes.c_float, ci, vp]
+        L.cmpext3_attn_bwd.argtypes = ([vp] * 10 + [ci] * 7 + [i64p] * 8 + [vp, ci, i64p]
+                                       + [ctypes.c_float, ci, vp])
         L.cmpext3_attn_bwd.restype = ci
         L.cmpext3_attn_strerror.argtypes = [ci]
         L.cmpext3_attn_strerror.restype = ctypes.c_char_p
@@ -150,7 +151,17 @@ def _handle(t, stream):
     return stream if isinstance(stream, int) else stream.cuda_stream
 
 
-def attn_fwd_lse(q, k, v, scale: Optional[float] = None, causal: bool = False, stream=None):
+def _mask_args(attn_mask, B, H, Sq, Sk):
+    """(pointer, dtype code, strides, keep-alive tensor) for an optional mask."""
+    if attn_mask is None:
+        return ctypes.c_void_p(0), -1, (ctypes.c_int64 * 3)(0, 0, 0), None
+    m = prepare_mask(attn_mask, B, H, Sq, Sk)
+    return (ctypes.c_void_p(m.data_ptr()), dtype_code(m.dtype),
+            (ctypes.c_int64 * 3)(m.stride(0), m.stride(1), m.stride(2)), m)
+
+
+def attn_fwd_lse(q, k, v, scale: Optional[float] = None, causal: bool = False, stream=None,
+                 attn_mask=None):
     """Training forward through cmpext3_attn_fwd_lse: returns (O, lse) with
     lse the fp32 [B,H,Sq] natural-log row log-sum-exp (k, v may hold fewer
     heads than q: grouped-query).  Raises RuntimeError on a non-zero code."""
@@ -160,29 +171,32 @@ def attn_fwd_lse(q, k, v, scale: Optional[float] = None, causal: bool = False, s
     lse = torch.empty(B, H, Sq, dtype=torch.float32, device=q.device)
     if scale is None:
         scale = D ** -0.5
+    mp, mdt, mst, _keep = _mask_args(attn_mask, B, H, Sq, k.shape[2])
     rc = lib().cmpext3_attn_fwd_lse(
         ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()),
         ctypes.c_void_p(o.data_ptr()), ctypes.c_void_p(lse.data_ptr()), dtype_code(q.dtype),
         B, H, k.shape[1], Sq, k.shape[2], D, _strides(q), _strides(k), _strides(v), _strides(o),
-        ctypes.c_float(scale), int(causal), ctypes.c_void_p(_handle(q, stream)))
+        mp, mdt, mst, ctypes.c_float(scale), int(causal), ctypes.c_void_p(_handle(q, stream)))
     if rc != OK:
         raise RuntimeError(f"cmpext3_attn_fwd_lse: {strerror(rc)} (code {rc})")
     return o, lse
 
 
 def attn_bwd_raw(q, k, v, o, do, lse, dq, dk, dv, delta, scale: float, causal: bool = False,
-                 stream=None) -> int:
+                 stream=None, attn_mask=None) -> int:
     """Call cmpext3_attn_bwd on caller-allocated tensors; returns the C code."""
     B, H, Sq, D = q.shape
     vp = ctypes.c_void_p
+    mp, mdt, mst, _keep = _mask_args(attn_mask, B, H, Sq, k.shape[2])
     return lib().cmpext3_attn_bwd(
         *(vp(t.data_ptr()) for t in (q, k, v, o, do, lse, dq, dk, dv, delta)),
         dtype_code(q.dtype), B, H, k.shape[1], Sq, k.shape[2], D,
         *(_strides(t) for t in (q, k, v, o, do, dq, dk, dv)),
-        ctypes.c_float(scale), int(causal), vp(_handle(q, stream)))
+        mp, mdt, mst, ctypes.c_float(scale), int(causal), vp(_handle(q, stream)))
 
 
-def attn_bwd(q, k, v, o, do, lse, scale: Optional[float] = None, causal: bool = False, stream=None):
+def attn_bwd(q, k, v, o, do, lse, scale: Optional[float] = None, causal: bool = False, stream=None,
+             attn_mask=None):
     """Gradients (dq, dk, dv) through cmpext3_attn_bwd (outputs contiguous, a
     delta workspace allocated here).  Raises RuntimeError on a non-zero code."""
     import torch
@@ -193,7 +207,7 @@ def attn_bwd(q, k, v, o, do, lse, scale: Optional[float] = None, causal: bool = 
     delta = torch.empty(B, H, Sq, dtype=torch.float32, device=q.device)
     if scale is None:
         scale = D ** -0.5
-    rc = attn_bwd_raw(q, k, v, o, do, lse, dq, dk, dv, delta, scale, causal, stream)
+    rc = attn_bwd_raw(q, k, v, o, do, lse, dq, dk, dv, delta, scale, causal, stream, attn_mask)
     if rc != OK:
         raise RuntimeError(f"cmpext3_attn_bwd: {strerror(rc)} (code {rc})")
     return dq, dk, dv

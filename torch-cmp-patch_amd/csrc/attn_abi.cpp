@@ -54,6 +54,28 @@ int check_shape(int dtype, int B, int H, int Sq, int Sk, int D) {
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
+// attention-mask arguments (mask_dtype -1 = none): CMPEXT3_OK or an error code
+int check_mask(const void* mask, int mask_dtype, const int64_t mask_str[3], int dtype, int D, int Sq, int Sk) {
+  if (mask_dtype == -1) return CMPEXT3_OK;
+  if (mask_dtype < CMPEXT3_DTYPE_F16 || mask_dtype > CMPEXT3_DTYPE_BOOL) return CMPEXT3_E_DTYPE;
+  if (!mask || !mask_str) return CMPEXT3_E_INVALID;
+  // masks run on the pipelined fp16/bf16 kernels only (causal or not)
+  if (dtype == CMPEXT3_DTYPE_F32 || D > 128) return CMPEXT3_E_MASK;
+  // every 8-key run of a row is one aligned 8/16/32-byte load
+  if (((uintptr_t)mask & 15u) != 0) return CMPEXT3_E_ALIGN;
+  for (int i = 0; i < 3; ++i)
+    if (mask_str[i] < 0 || mask_str[i] % 4 != 0) return CMPEXT3_E_ALIGN;
+  const int mes = mask_dtype == CMPEXT3_DTYPE_BOOL ? 1 : mask_dtype == CMPEXT3_DTYPE_F32 ? 4 : 2;
+  if (((int64_t)(Sq - 1) * mask_str[2] + Sk + 64) * mes >= INT32_MAX) return CMPEXT3_E_TOO_LARGE;
+  return CMPEXT3_OK;
+}
+
+int mask_kind_of(int mask_dtype) {
+  return mask_dtype == CMPEXT3_DTYPE_BOOL ? cmpext3::MASK_BOOL
+         : mask_dtype == CMPEXT3_DTYPE_F32 ? cmpext3::MASK_F32
+         : mask_dtype == CMPEXT3_DTYPE_BF16 ? cmpext3::MASK_BF16 : cmpext3::MASK_F16;
+}
+
 // A stride only matters if its dimension has more than one index.
 bool stride_ok(const int64_t s[3], int n0, int n1, int n2, int es) {
   const int64_t n[3] = {n0, n1, n2};
@@ -140,18 +162,8 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
   if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;
   if (H_kv < 1 || H_kv > H || H % H_kv != 0) return CMPEXT3_E_INVALID;
   const bool masked = mask_dtype != -1;
-  if (masked) {
-    if (mask_dtype < CMPEXT3_DTYPE_F16 || mask_dtype > CMPEXT3_DTYPE_BOOL) return CMPEXT3_E_DTYPE;
-    if (!mask || !mask_str) return CMPEXT3_E_INVALID;
-    // masks run on the pipelined fp16/bf16 kernel only (causal or not)
-    if (dtype == CMPEXT3_DTYPE_F32 || D > 128) return CMPEXT3_E_MASK;
-    // every 4-key run of a row is one aligned 4/8/16-byte load
-    if (((uintptr_t)mask & 15u) != 0) return CMPEXT3_E_ALIGN;
-    for (int i = 0; i < 3; ++i)
-      if (mask_str[i] < 0 || mask_str[i] % 4 != 0) return CMPEXT3_E_ALIGN;
-    const int mes = mask_dtype == CMPEXT3_DTYPE_BOOL ? 1 : mask_dtype == CMPEXT3_DTYPE_F32 ? 4 : 2;
-    if (((int64_t)(Sq - 1) * mask_str[2] + Sk + 64) * mes >= INT32_MAX) return CMPEXT3_E_TOO_LARGE;
-  }
+  rc = check_mask(mask, mask_dtype, mask_str, dtype, D, Sq, Sk);
+  if (rc != CMPEXT3_OK) return rc;
   if (!q || !k || !v || !o || !q_str || !k_str || !v_str || !o_str) return CMPEXT3_E_INVALID;
   if (!isfinite(scale)) return CMPEXT3_E_INVALID;
   const int es = elem_size(dtype);
@@ -178,9 +190,7 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
   if (masked) {
     p.mask = mask;
     p.m_b = mask_str[0]; p.m_h = mask_str[1]; p.m_q = mask_str[2];
-    p.mask_kind = mask_dtype == CMPEXT3_DTYPE_BOOL ? cmpext3::MASK_BOOL
-                  : mask_dtype == CMPEXT3_DTYPE_F32 ? cmpext3::MASK_F32
-                  : mask_dtype == CMPEXT3_DTYPE_BF16 ? cmpext3::MASK_BF16 : cmpext3::MASK_F16;
+    p.mask_kind = mask_kind_of(mask_dtype);
   }
   // exp2-domain multiplier; a negative scale is folded into Q's sign bits
   p.c = fabsf(scale) * cmpext3::kLog2e;
@@ -216,7 +226,8 @@ int cmpext3_attn_fwd_masked(const void* q, const void* k, const void* v, void* o
 int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, float* lse, int dtype,
                          int B, int H, int H_kv, int Sq, int Sk, int D, const int64_t q_str[3],
                          const int64_t k_str[3], const int64_t v_str[3], const int64_t o_str[3],
-                         float scale, int causal, hipStream_t stream) {
+                         const void* mask, int mask_dtype, const int64_t mask_str[3], float scale,
+                         int causal, hipStream_t stream) {
   const int rc = check_shape(dtype, B, H, Sq, Sk, D);
   if (rc != CMPEXT3_OK) return rc;
   if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;
@@ -226,8 +237,8 @@ int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, f
   // the pipelined kernel (the one that writes the log-sum-exp) addresses K/V
   // tiles with 32-bit buffer offsets
   if (!tile_offsets_fit(Sk, k_str[2], v_str[2])) return CMPEXT3_E_TOO_LARGE;
-  return fwd_impl(q, k, v, o, lse, dtype, B, H, H_kv, Sq, Sk, D, q_str, k_str, v_str, o_str, nullptr, -1,
-                  nullptr, scale, causal, stream);
+  return fwd_impl(q, k, v, o, lse, dtype, B, H, H_kv, Sq, Sk, D, q_str, k_str, v_str, o_str, mask,
+                  mask_dtype, mask_str, scale, causal, stream);
 }
 
 int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
@@ -235,12 +246,15 @@ int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
                      int H, int H_kv, int Sq, int Sk, int D, const int64_t q_str[3], const int64_t k_str[3],
                      const int64_t v_str[3], const int64_t o_str[3], const int64_t do_str[3],
                      const int64_t dq_str[3], const int64_t dk_str[3], const int64_t dv_str[3],
-                     float scale, int causal, hipStream_t stream) {
-  const int rc = check_shape(dtype, B, H, Sq, Sk, D);
+                     const void* mask, int mask_dtype, const int64_t mask_str[3], float scale, int causal,
+                     hipStream_t stream) {
+  int rc = check_shape(dtype, B, H, Sq, Sk, D);
   if (rc != CMPEXT3_OK) return rc;
   if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;
   if (dtype == CMPEXT3_DTYPE_F32 || D > 128) return CMPEXT3_E_TRAINING;
   if (H_kv < 1 || H_kv > H || H % H_kv != 0) return CMPEXT3_E_INVALID;
+  rc = check_mask(mask, mask_dtype, mask_str, dtype, D, Sq, Sk);
+  if (rc != CMPEXT3_OK) return rc;
   if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv || !delta) return CMPEXT3_E_INVALID;
   if (!q_str || !k_str || !v_str || !o_str || !do_str || !dq_str || !dk_str || !dv_str)
     return CMPEXT3_E_INVALID;
@@ -272,6 +286,12 @@ int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
   p.B = B; p.H = H; p.Sq = Sq; p.Sk = Sk; p.D = D;
   p.Hkv = H_kv;
   p.group = H / H_kv;
+  p.mask_kind = cmpext3::MASK_NONE;
+  if (mask_dtype != -1) {
+    p.mask = mask;
+    p.m_b = mask_str[0]; p.m_h = mask_str[1]; p.m_q = mask_str[2];
+    p.mask_kind = mask_kind_of(mask_dtype);
+  }
   // scale 0: the dK/dV kernel divides by c; c = 1e-30 puts every finite score
   // within 1e-22 of the exp2 argument scale 0 gives, and keeps -lse2 / c finite
   p.c = scale == 0.f ? 1e-30f : fabsf(scale) * cmpext3::kLog2e;

@@ -58,7 +58,27 @@ struct BwdParams {
   float c;          // |scale| * log2(e)
   float scale;      // signed scale: dK = scale * dS^T Q, dQ = scale * dS K
   uint32_t sign;    // 0x80008000 when scale < 0 (XORed into K or Q words), else 0
+  // optional attention mask, as in FwdParams (element strides over {batch,
+  // head, query}, unit key stride, kind MASK_*; MASK_NONE = none)
+  const void* mask;
+  int64_t m_b, m_h, m_q;
+  int mask_kind;
 };
+
+// Mask element size in bytes.
+__device__ __forceinline__ int mask_bytes(int kind) { return kind == MASK_BOOL ? 1 : kind == MASK_F32 ? 4 : 2; }
+
+// One mask element as an exp2-domain addend: -inf for a dropped pair (bool
+// zero), value * log2(e) for additive masks.  `off` is a byte offset into the
+// descriptor's range (reads past it return zero).
+__device__ __forceinline__ float mask_elem(__amdgpu_buffer_rsrc_t rs, int off, int kind) {
+  if (kind == MASK_BOOL) return __builtin_amdgcn_raw_buffer_load_b8(rs, off, 0, 0) ? 0.f : -INFINITY;
+  if (kind == MASK_F32) return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0)) * kLog2e;
+  const uint32_t w = __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
+  const float f = kind == MASK_F16 ? (float)__builtin_bit_cast(_Float16, (uint16_t)w)
+                                   : __uint_as_float(w << 16);
+  return f * kLog2e;
+}
 
 // ---- Delta_i = sum_d dO_id * O_id (fp32), 8 lanes per row
 template <typename T>
@@ -154,8 +174,9 @@ __device__ __forceinline__ void store_rows(uint16_t* base, int64_t row_stride, i
 // Waves per SIMD: the most the registers allow without spilling (D <= 64:
 // 3, 2 causal; D <= 128: 1, its K/V operands and dK/dV accumulators alone
 // take 192 registers).
-template <typename T, int DK, bool CAUSAL>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DK <= 64 ? (CAUSAL ? 2 : 3) : 1)))
+template <typename T, int DK, bool CAUSAL, bool MASK>
+__global__ void __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(DK <= 64 ? (CAUSAL || MASK ? 2 : 3) : 1)))
 attn_bwd_dkdv(const BwdParams p) {
   constexpr int BQ = 32, BKV = 128;
   constexpr int RS = DK + 8;  // LDS row stride (halves)
@@ -244,7 +265,9 @@ attn_bwd_dkdv(const BwdParams p) {
     const float* dlt_h = p.delta + hoff_u;
     if (tid < BQ) {
       const int row = q0 + tid;
-      xl = row < Sq ? -(lse_h[row] * kLog2e) * inv_c : -INFINITY;  // rows past Sq: P = 0
+      // rows past Sq, and rows that saw no key in the forward (lse = -inf): P = 0
+      const float L = row < Sq ? lse_h[row] : -INFINITY;
+      xl = L > -INFINITY ? -(L * kLog2e) * inv_c : -INFINITY;
       xdl = row < Sq ? -dlt_h[row] : 0.f;
     }
   };
@@ -272,6 +295,19 @@ attn_bwd_dkdv(const BwdParams p) {
     if (!CAUSAL || q0 + BQ - 1 >= kw0) {
       const uint16_t* qs = lds + slot * 2 * BQ * RS;
       const uint16_t* dos = qs + BQ * RS;
+      // attention mask of this tile as exp2-domain addends, one element per
+      // (query row of register r, this lane's key); lanes of one half read
+      // consecutive keys of one row
+      float madd[16];
+      if (MASK) {
+        const int kind = p.mask_kind, mes = mask_bytes(kind);
+        const int h = hk * p.group + j / nt;
+        const __amdgpu_buffer_rsrc_t mrs = uniform_rsrc(
+            (const char*)p.mask + (b * p.m_b + h * p.m_h) * mes, ((int64_t)(Sq - 1) * p.m_q + (Sk + 7) / 8 * 8) * mes);
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          madd[r] = mask_elem(mrs, (int)(((int64_t)(q0 + acc_key(r, hh)) * p.m_q + key) * mes), kind);
+      }
       // register r holds query q0 + acc_key(r, hh): two runs of 8 consecutive rows
       f32x16 s, dp;
 #pragma unroll
@@ -301,7 +337,7 @@ attn_bwd_dkdv(const BwdParams p) {
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
             const int r = 8 * ks + 2 * e + u;
-            float x = s[r] * c;
+            float x = MASK ? __builtin_fmaf(s[r], c, madd[r]) : s[r] * c;
             if (diag && key > q0 + acc_key(r, hh)) x = -INFINITY;
             pv[u] = fast_exp2(x);
           }
@@ -332,8 +368,9 @@ attn_bwd_dkdv(const BwdParams p) {
 
 // ---- dQ for one block of 128 queries (4 waves x 32 queries), sweeping the
 // key tiles (32 rows of K and V) through double-buffered LDS.
-template <typename T, int DK, bool CAUSAL>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DK <= 64 ? 3 : 2)))
+template <typename T, int DK, bool CAUSAL, bool MASK>
+__global__ void __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(DK <= 64 ? (MASK ? 2 : 3) : (MASK ? 1 : 2))))
 attn_bwd_dq(const BwdParams p) {
   constexpr int BQ = 128, BK = 32;
   constexpr int RS = DK + 8;
@@ -367,7 +404,16 @@ attn_bwd_dq(const BwdParams p) {
     qf[s] = x ^ p.sign;
     dof[s] = y;
   }
-  const float l2 = qrow < Sq ? p.lse[(int64_t)bh * Sq + qrow] * kLog2e : INFINITY;  // past Sq: P = 0
+  // rows past Sq, and rows that saw no key in the forward (lse = -inf): P = 0
+  const float L = qrow < Sq ? p.lse[(int64_t)bh * Sq + qrow] : -INFINITY;
+  const float l2 = L > -INFINITY ? L * kLog2e : INFINITY;
+  // attention mask rows of this (batch, head); a lane reads its own query row
+  const int mkind = MASK ? p.mask_kind : MASK_NONE;
+  const int mes = MASK ? mask_bytes(mkind) : 1;
+  const __amdgpu_buffer_rsrc_t mrs =
+      uniform_rsrc(MASK ? (const void*)((const char*)p.mask + (b * p.m_b + h * p.m_h) * mes) : p.q,
+                   MASK ? ((int64_t)(Sq - 1) * p.m_q + (Sk + 7) / 8 * 8) * mes : 0);
+  const int mrow_off = MASK ? (int)((int64_t)min(qrow, Sq - 1) * p.m_q * mes) : 0;
   const float dl = qrow < Sq ? p.delta[(int64_t)bh * Sq + qrow] : 0.f;
 
   const int hk = h / p.group;
@@ -430,6 +476,36 @@ attn_bwd_dq(const BwdParams p) {
 #pragma unroll
       for (int st = 0; st < NKS; ++st) dp = Elt<T>::mma(*(const u32x4*)(vs + a_rd[st]), dof[st], dp);
       const bool edge = k0 + BK > Sk || (CAUSAL && k0 + BK - 1 > qblk * BQ + wave * 32);
+      // mask addends of the lane's 16 keys: two runs of 8 consecutive keys
+      // (acc_key), each one 8/16/32-byte read as in the forward
+      float madd[16];
+      if (MASK) {
+#pragma unroll
+        for (int run = 0; run < 2; ++run) {
+          const int kk = k0 + 16 * run + 8 * hh;
+          if (mkind == MASK_BOOL) {
+            const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(mrs, mrow_off + kk, 0, 0));
+#pragma unroll
+            for (int i = 0; i < 8; ++i) madd[8 * run + i] = ((w[i >> 2] >> (8 * (i & 3))) & 0xffu) ? 0.f : -INFINITY;
+          } else if (mkind == MASK_F32) {
+#pragma unroll
+            for (int hv = 0; hv < 2; ++hv) {
+              const f32x4 a = __builtin_bit_cast(
+                  f32x4, __builtin_amdgcn_raw_buffer_load_b128(mrs, mrow_off + 4 * (kk + 4 * hv), 0, 0));
+#pragma unroll
+              for (int i = 0; i < 4; ++i) madd[8 * run + 4 * hv + i] = a[i] * kLog2e;
+            }
+          } else {
+            const u32x4 w = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(mrs, mrow_off + 2 * kk, 0, 0));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const f32x2 a = mkind == MASK_F16 ? Elt<_Float16>::unpack(w[i]) : Elt<__bf16>::unpack(w[i]);
+              madd[8 * run + 2 * i] = a[0] * kLog2e;
+              madd[8 * run + 2 * i + 1] = a[1] * kLog2e;
+            }
+          }
+        }
+      }
       u32x4 ps[2];
 #pragma unroll
       for (int ks2 = 0; ks2 < 2; ++ks2)
@@ -440,6 +516,7 @@ attn_bwd_dq(const BwdParams p) {
           for (int u = 0; u < 2; ++u) {
             const int r = 8 * ks2 + 2 * e + u;
             float x = __builtin_fmaf(s[r], c, -l2);
+            if (MASK) x += madd[r];
             if (edge) {
               const int kk = k0 + acc_key(r, hh);
               if (kk >= Sk || (CAUSAL && kk > qrow)) x = -INFINITY;

@@ -8,25 +8,31 @@ namespace cmpext3 {
 
 namespace {
 
-template <typename T, int DK, bool CAUSAL>
+template <typename T, int DK, bool CAUSAL, bool MASK>
 hipError_t launch_bwd_t(const BwdParams& p0, hipStream_t s) {
   BwdParams p = p0;
   const int64_t rows = (int64_t)p.B * p.H * p.Sq;
   hipLaunchKernelGGL(attn_bwd_delta<T>, dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, s, p);
   p.n_blk = (p.Sk + 127) / 128;
   p.n_wg = p.B * p.Hkv * p.n_blk;
-  hipLaunchKernelGGL((attn_bwd_dkdv<T, DK, CAUSAL>), dim3(p.n_wg), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((attn_bwd_dkdv<T, DK, CAUSAL, MASK>), dim3(p.n_wg), dim3(256), 0, s, p);
   p.n_blk = (p.Sq + 127) / 128;
   p.n_wg = p.B * p.H * p.n_blk;
-  hipLaunchKernelGGL((attn_bwd_dq<T, DK, CAUSAL>), dim3(p.n_wg), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((attn_bwd_dq<T, DK, CAUSAL, MASK>), dim3(p.n_wg), dim3(256), 0, s, p);
   return hipGetLastError();
+}
+
+template <typename T, bool MASK>
+hipError_t launch_bwd_mask(const BwdParams& p, int dk, bool causal, hipStream_t s) {
+  if (dk == 64) return causal ? launch_bwd_t<T, 64, true, MASK>(p, s) : launch_bwd_t<T, 64, false, MASK>(p, s);
+  if (dk == 128) return causal ? launch_bwd_t<T, 128, true, MASK>(p, s) : launch_bwd_t<T, 128, false, MASK>(p, s);
+  return hipErrorNotSupported;
 }
 
 template <typename T>
 hipError_t launch_bwd_dtype(const BwdParams& p, int dk, bool causal, hipStream_t s) {
-  if (dk == 64) return causal ? launch_bwd_t<T, 64, true>(p, s) : launch_bwd_t<T, 64, false>(p, s);
-  if (dk == 128) return causal ? launch_bwd_t<T, 128, true>(p, s) : launch_bwd_t<T, 128, false>(p, s);
-  return hipErrorNotSupported;
+  return p.mask_kind != MASK_NONE ? launch_bwd_mask<T, true>(p, dk, causal, s)
+                                  : launch_bwd_mask<T, false>(p, dk, causal, s);
 }
 
 }  // namespace

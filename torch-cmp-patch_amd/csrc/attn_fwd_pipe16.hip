@@ -132,18 +132,27 @@ hipError_t launch_dk(const FwdParams& p, const SplitArgs& sa, hipStream_t s) {
   return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, occ, CAUSAL, PRESCALE, 1 | 8 | MOPT>(p, sa, s);
 }
 
-// Training forward (OPT 32: write the row log-sum-exp): buckets 64 and 128 only.
-template <typename T, bool CAUSAL, bool PRESCALE>
-hipError_t launch_lse(const FwdParams& p, const SplitArgs& sa, int dk, hipStream_t s) {
+// Training forward (OPT 32: write the row log-sum-exp; MOPT 16: with an
+// attention mask): buckets 64 and 128 only.
+template <typename T, bool CAUSAL, bool PRESCALE, int MOPT>
+hipError_t launch_lse_m(const FwdParams& p, const SplitArgs& sa, int dk, hipStream_t s) {
   if (dk == 64) {
-    if (p.D == 64) return launch_pipe16_cfg<T, 64, kPipeNw, kPipeBk, pipe_occ(64), CAUSAL, PRESCALE, 1 | 32>(p, sa, s);
-    return launch_pipe16_cfg<T, 64, kPipeNw, kPipeBk, pipe_occ(64), CAUSAL, PRESCALE, 1 | 8 | 32>(p, sa, s);
+    if (p.D == 64)
+      return launch_pipe16_cfg<T, 64, kPipeNw, kPipeBk, pipe_occ(64), CAUSAL, PRESCALE, 1 | 32 | MOPT>(p, sa, s);
+    return launch_pipe16_cfg<T, 64, kPipeNw, kPipeBk, pipe_occ(64), CAUSAL, PRESCALE, 1 | 8 | 32 | MOPT>(p, sa, s);
   }
   if (dk == 128) {
-    if (p.D == 128) return launch_pipe16_cfg<T, 128, kPipeNw, kPipeBk, pipe_occ(128), CAUSAL, PRESCALE, 1 | 32>(p, sa, s);
-    return launch_pipe16_cfg<T, 128, kPipeNw, kPipeBk, pipe_occ(128), CAUSAL, PRESCALE, 1 | 8 | 32>(p, sa, s);
+    if (p.D == 128)
+      return launch_pipe16_cfg<T, 128, kPipeNw, kPipeBk, pipe_occ(128), CAUSAL, PRESCALE, 1 | 32 | MOPT>(p, sa, s);
+    return launch_pipe16_cfg<T, 128, kPipeNw, kPipeBk, pipe_occ(128), CAUSAL, PRESCALE, 1 | 8 | 32 | MOPT>(p, sa, s);
   }
   return hipErrorNotSupported;
+}
+
+template <typename T, bool CAUSAL, bool PRESCALE>
+hipError_t launch_lse(const FwdParams& p, const SplitArgs& sa, int dk, hipStream_t s) {
+  return p.mask_kind != MASK_NONE ? launch_lse_m<T, CAUSAL, PRESCALE, 16>(p, sa, dk, s)
+                                  : launch_lse_m<T, CAUSAL, PRESCALE, 0>(p, sa, dk, s);
 }
 
 template <typename T, bool CAUSAL, bool PRESCALE, int MOPT = 0>
@@ -227,7 +236,7 @@ hipError_t launch_pipe16(const FwdParams& p0, int dk0, bool bf16, bool causal, b
       sa = SplitArgs{n_blocks(p.B, p.H, p.Sq), 1, nullptr, nullptr};
     }
   }
-  if (p.lse) {  // training forward: unmasked (checked by the caller)
+  if (p.lse) {  // training forward, masked or not
     if (bf16) return causal ? launch_lse<__bf16, true, false>(p, sa, dk, s) : launch_lse<__bf16, false, false>(p, sa, dk, s);
     if (prescale)
       return causal ? launch_lse<_Float16, true, true>(p, sa, dk, s) : launch_lse<_Float16, false, true>(p, sa, dk, s);

@@ -224,7 +224,8 @@ float resolve_scale(c10::optional<double> scale_arg, int64_t D) {
 // Training forward: (out, lse), lse = [B, H, Sq] fp32 natural-log row
 // log-sum-exp, the state attention_bwd needs.
 std::vector<torch::Tensor> attention_fwd_lse(torch::Tensor query, torch::Tensor key, torch::Tensor value,
-                                             c10::optional<double> scale_arg, bool causal) {
+                                             c10::optional<double> scale_arg, bool causal,
+                                             c10::optional<torch::Tensor> attn_mask) {
   const int dtype = training_dtype(query, key, value);
   const int64_t B = query.size(0), H = query.size(1), Sq = query.size(2), D = query.size(3);
   const int64_t Sk = key.size(2), Hkv = key.size(1), Dp = (D + 7) / 8 * 8;
@@ -235,12 +236,20 @@ std::vector<torch::Tensor> attention_fwd_lse(torch::Tensor query, torch::Tensor 
   torch::Tensor lse = torch::empty({B, H, Sq}, query.options().dtype(at::kFloat));
   torch::Tensor out = torch::empty({B, H, Sq, Dp}, query.options());
   if (out.numel() == 0) return {Dp == D ? out : out.narrow(3, 0, D), lse};
+  Mask mask;
+  int64_t ms[3] = {0, 0, 0};
+  if (attn_mask.has_value() && attn_mask->defined()) {
+    mask = prepare_mask(*attn_mask, query, B, H, Sq, Sk);
+    strides3(mask.t, ms);
+  }
   const torch::Tensor q = abi_layout(query, Dp), k = abi_layout(key, Dp), v = abi_layout(value, Dp);
   int64_t qs[3], ks[3], vs[3], os[3];
   strides3(q, qs); strides3(k, ks); strides3(v, vs); strides3(out, os);
   const int rc = cmpext3_attn_fwd_lse(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                                       lse.data_ptr<float>(), dtype, (int)B, (int)H, (int)Hkv, (int)Sq,
-                                      (int)Sk, (int)Dp, qs, ks, vs, os, scale, causal ? 1 : 0, stream);
+                                      (int)Sk, (int)Dp, qs, ks, vs, os,
+                                      mask.dtype >= 0 ? mask.t.data_ptr() : nullptr, mask.dtype, ms, scale,
+                                      causal ? 1 : 0, stream);
   TORCH_CHECK(rc == CMPEXT3_OK, "cmpext3 attention: ", cmpext3_attn_strerror(rc));
   return {Dp == D ? out : out.narrow(3, 0, D).contiguous(), lse};
 }
@@ -249,7 +258,8 @@ std::vector<torch::Tensor> attention_fwd_lse(torch::Tensor query, torch::Tensor 
 // attention_fwd_lse(query, key, value, scale, causal)[0].
 std::vector<torch::Tensor> attention_bwd(torch::Tensor query, torch::Tensor key, torch::Tensor value,
                                          torch::Tensor out, torch::Tensor grad_out, torch::Tensor lse,
-                                         c10::optional<double> scale_arg, bool causal) {
+                                         c10::optional<double> scale_arg, bool causal,
+                                         c10::optional<torch::Tensor> attn_mask) {
   const int dtype = training_dtype(query, key, value);
   const int64_t B = query.size(0), H = query.size(1), Sq = query.size(2), D = query.size(3);
   const int64_t Sk = key.size(2), Hkv = key.size(1), Dp = (D + 7) / 8 * 8;
@@ -277,13 +287,20 @@ std::vector<torch::Tensor> attention_bwd(torch::Tensor query, torch::Tensor key,
     const torch::Tensor o = abi_layout(out, Dp), g = abi_layout(grad_out, Dp);
     const torch::Tensor l = lse.contiguous();
     torch::Tensor delta = torch::empty({B, H, Sq}, query.options().dtype(at::kFloat));
+    Mask mask;
+    int64_t ms[3] = {0, 0, 0};
+    if (attn_mask.has_value() && attn_mask->defined()) {
+      mask = prepare_mask(*attn_mask, query, B, H, Sq, Sk);
+      strides3(mask.t, ms);
+    }
     int64_t qs[3], ks[3], vs[3], os[3], gs[3], dqs[3], dks[3], dvs[3];
     strides3(q, qs); strides3(k, ks); strides3(v, vs); strides3(o, os); strides3(g, gs);
     strides3(dq, dqs); strides3(dk, dks); strides3(dv, dvs);
     const int rc = cmpext3_attn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), g.data_ptr(),
                                     l.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                                     delta.data_ptr<float>(), dtype, (int)B, (int)H, (int)Hkv, (int)Sq,
-                                    (int)Sk, (int)Dp, qs, ks, vs, os, gs, dqs, dks, dvs, scale,
+                                    (int)Sk, (int)Dp, qs, ks, vs, os, gs, dqs, dks, dvs,
+                                    mask.dtype >= 0 ? mask.t.data_ptr() : nullptr, mask.dtype, ms, scale,
                                     causal ? 1 : 0, stream);
     TORCH_CHECK(rc == CMPEXT3_OK, "cmpext3 attention backward: ", cmpext3_attn_strerror(rc));
   }
@@ -315,10 +332,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "Training forward (fp16/bf16, D <= 128): returns (out, lse), lse = fp32 [B,H,Sq] row "
         "log-sum-exp (natural log)",
         py::arg("query"), py::arg("key"), py::arg("value"), py::arg("scale") = py::none(),
-        py::arg("causal") = false);
+        py::arg("causal") = false, py::arg("attn_mask") = py::none());
   m.def("attention_bwd", &attention_bwd,
         "Training backward: (dq, dk, dv) from q, k, v, out, grad_out and the forward's lse",
         py::arg("query"), py::arg("key"), py::arg("value"), py::arg("out"), py::arg("grad_out"),
-        py::arg("lse"), py::arg("scale") = py::none(), py::arg("causal") = false);
+        py::arg("lse"), py::arg("scale") = py::none(), py::arg("causal") = false,
+        py::arg("attn_mask") = py::none());
   m.def("abi_version", &cmpext3_attn_abi_version, "C ABI version of libcmpext3_attn.so");
 }
