@@ -10,8 +10,12 @@ oracle = float64 SDPA on the CPU over the same rounded inputs.
 Shapes: fewer blocks than CUs (every block split, up to 8 parts), one whole
 round plus a remainder, ragged key counts whose parts get odd tile counts
 (a masked padding tile inside a part), scores spread over tens of log2 units
-(parts settle on different offsets before the merge), and back-to-back
-launches of different plans (the per-wave counters must come back to zero).
+(parts settle on different offsets before the merge), back-to-back
+launches of different plans (the per-wave counters must come back to zero),
+and HIP graph capture (on a fresh stream the launch runs unsplit with no
+allocation or memset in the graph; on a stream that already owns an exchange
+buffer the split launch is captured and every replay, with eager work and
+synchronisations in between, equals the eager result bit for bit).
 """
 from __future__ import annotations
 
@@ -108,3 +112,50 @@ def test_causal_and_whole_rounds_do_not_split():
     if torch.cuda.get_device_properties(0).multi_processor_count == 256:
         assert "key-split" not in _split_text(q, 2, 4, 4096, 4096, 64)
         assert "key-split" in _split_text(q, 2, 10, 4096, 4096, 64)
+
+
+def _replays(g, out, reps=4):
+    """Replay a captured graph with eager work (and a sync) between replays."""
+    results = []
+    for _ in range(reps):
+        g.replay()
+        torch.randn(4096, device="cuda").mul_(2).sum().item()   # eager work in between
+        torch.cuda.synchronize()
+        results.append(out.clone())
+    return results
+
+
+def test_graph_capture_on_a_fresh_stream_runs_unsplit():
+    """Under capture the library allocates nothing (no exchange buffer, no
+    memset node): a split-eligible launch on a stream it has not seen runs
+    unsplit, and every replay matches the oracle and the first replay."""
+    q, k, v = _inputs("fp16", 1, 2, 256, 2048, 64, seed=21)
+    assert "key-split" in _split_text(q, 1, 2, 256, 2048, 64)
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), 0.125)
+    import cmpext3
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        out = cmpext3.ops.attention(q, k, v, 0.125, False)
+    res = _replays(g, out)
+    for r in res:
+        assert orc.max_abs_err(r.cpu(), ref) <= TOL["fp16"]
+        assert torch.equal(r, res[0])
+
+
+def test_graph_capture_after_eager_use_replays_the_split():
+    """A stream that already owns an exchange buffer records the split launch;
+    the merge puts its counters back itself, so every replay equals the eager
+    result bit for bit."""
+    q, k, v = _inputs("bf16", 1, 3, 256, 2048, 64, seed=22)
+    import cmpext3
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        eager = cmpext3.ops.attention(q, k, v, 0.125, False)
+    s.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        out = cmpext3.ops.attention(q, k, v, 0.125, False)
+    for r in _replays(g, out):
+        assert torch.equal(r, eager)
+    assert orc.max_abs_err(eager.cpu(), orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), 0.125)) <= TOL["bf16"]
