@@ -55,6 +55,8 @@ CASES = [
     ("fp16", 1, 2, 64, 1024, 64, False, -0.2),    # negative scale, key split in the forward
     ("bf16", 2, 1, 1, 33, 128, False, None),      # one query row
     ("fp16", 1, 1, 37, 1, 64, True, None),        # one key
+    ("fp16", 1, 2, 100, 200, 64, False, 0.0),     # scale 0: uniform P, no score gradient
+    ("bf16", 1, 1, 64, 96, 64, True, 1e-39),      # denormal scale (the kernel's c is floored)
 ]
 
 

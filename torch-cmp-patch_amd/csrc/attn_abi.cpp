@@ -292,9 +292,10 @@ int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
     p.m_b = mask_str[0]; p.m_h = mask_str[1]; p.m_q = mask_str[2];
     p.mask_kind = mask_kind_of(mask_dtype);
   }
-  // scale 0: the dK/dV kernel divides by c; c = 1e-30 puts every finite score
-  // within 1e-22 of the exp2 argument scale 0 gives, and keeps -lse2 / c finite
-  p.c = scale == 0.f ? 1e-30f : fabsf(scale) * cmpext3::kLog2e;
+  // The dK/dV kernel divides by c.  For |scale| * log2(e) below 1e-30 (scale 0
+  // and denormal scales) c = 1e-30 moves each exp2 argument by at most
+  // 1e-30 * |score|, and keeps -lse2 / c finite
+  p.c = fmaxf(fabsf(scale) * cmpext3::kLog2e, 1e-30f);
   p.scale = scale;
   p.sign = scale < 0.f ? 0x80008000u : 0u;
   const hipError_t err = cmpext3::launch_bwd16(p, dtype == CMPEXT3_DTYPE_BF16, causal != 0, stream);

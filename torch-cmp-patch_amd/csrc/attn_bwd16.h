@@ -190,9 +190,12 @@ attn_bwd_dkdv(const BwdParams p) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   // key blocks in order (causal: the first blocks see the most queries, so
   // they start first); XCD-contiguous ranges share Q/dO in L2
-  const int tile = xcd_remap(blockIdx.x, p.n_wg);
-  const int bhk = tile / p.n_blk, kb = tile - bhk * p.n_blk;  // (batch, K/V head), key block
-  const int b = bhk / p.Hkv, hk = bhk - b * p.Hkv;
+  // (the divisions run on the vector unit: readfirstlane keeps the indices,
+  // and the per-head address arithmetic of the sweep, in scalar registers)
+  const int tile = __builtin_amdgcn_readfirstlane(xcd_remap(blockIdx.x, p.n_wg));
+  const int bhk = __builtin_amdgcn_readfirstlane(tile / p.n_blk);  // (batch, K/V head)
+  const int kb = tile - bhk * p.n_blk;                             // key block
+  const int b = __builtin_amdgcn_readfirstlane(bhk / p.Hkv), hk = bhk - b * p.Hkv;
   const int Sq = p.Sq, Sk = p.Sk, D = p.D;
   const int kw0 = kb * BKV + wave * 32;  // first key of this wave
   const int key = kw0 + l32;             // this lane's key
@@ -237,38 +240,42 @@ attn_bwd_dkdv(const BwdParams p) {
   for (int db = 0; db < NDB; ++db) dva[db] = dka[db] = (f32x16){};
 
   // The sweep: query tiles t0 .. t1-1 of each query head of the group, as one
-  // sequence j = g * nt + (t - t0).
+  // sequence of nj tiles.  (fg, ft) is the head and tile of the next fetch,
+  // (cg, ct) those of the tile being computed: running counters, no divisions.
   const int t0 = CAUSAL ? kb * (BKV / BQ) : 0;  // query tiles before the block see none of its keys
   const int t1 = (Sq + BQ - 1) / BQ;
   const int nt = t1 > t0 ? t1 - t0 : 0;
   const int nj = nt * p.group;
   u32x4 xq[TileLoader<DK>::N], xd[TileLoader<DK>::N];
-  float xl = -INFINITY, xdl = 0.f;
-  const float inv_c = 1.f / p.c;  // c > 0 (the caller substitutes a tiny c for scale 0)
-  auto fetch = [&](int j) {
-    const int g = j / nt, t = t0 + (j - g * nt);
-    const int h = hk * p.group + g;
+  float xl = -INFINITY, xdl = 0.f;  // raw lse / Delta of the fetched rows
+  const float inv_c = 1.f / p.c;    // c > 0 (the caller floors it for tiny |scale|)
+  const int h0 = hk * p.group;      // first query head of the group
+  int fg = 0, ft = t0;
+  auto fetch = [&]() {
+    const int h = h0 + fg;
     const uint16_t* qg = (const uint16_t*)p.q + b * p.q_b + h * p.q_h;
     const uint16_t* dog = (const uint16_t*)p.dout + b * p.do_b + h * p.do_h;
     const __amdgpu_buffer_rsrc_t qrs = uniform_rsrc(qg, ((int64_t)(Sq - 1) * p.q_s + D) * 2);
     const __amdgpu_buffer_rsrc_t dors = uniform_rsrc(dog, ((int64_t)(Sq - 1) * p.do_s + D) * 2);
-    const int q0 = t * BQ;
+    const int q0 = ft * BQ;
     lq.load(qrs, (int)(q0 * p.q_s * 2), xq);
     ldo.load(dors, (int)(q0 * p.do_s * 2), xd);
-    // this head's lse / Delta rows: a wave-uniform base (kept in SGPRs) plus
-    // the 32-bit row index
+    // this head's lse / Delta rows; used only in put(), so the loads are not
+    // waited for before the current tile's products
     const int64_t hoff = ((int64_t)b * p.H + h) * Sq;
-    const int hlo = __builtin_amdgcn_readfirstlane((int)(uint32_t)hoff);
-    const int hhi = __builtin_amdgcn_readfirstlane((int)(uint32_t)(hoff >> 32));
-    const int64_t hoff_u = ((int64_t)(uint32_t)hhi << 32) | (uint32_t)hlo;
-    const float* lse_h = p.lse + hoff_u;
-    const float* dlt_h = p.delta + hoff_u;
     if (tid < BQ) {
       const int row = q0 + tid;
-      // rows past Sq, and rows that saw no key in the forward (lse = -inf): P = 0
-      const float L = row < Sq ? lse_h[row] : -INFINITY;
-      xl = L > -INFINITY ? -(L * kLog2e) * inv_c : -INFINITY;
-      xdl = row < Sq ? -dlt_h[row] : 0.f;
+      // rows past Sq: P = 0
+      xl = -INFINITY;
+      xdl = 0.f;
+      if (row < Sq) {
+        xl = p.lse[hoff + row];
+        xdl = p.delta[hoff + row];
+      }
+    }
+    if (++ft == t1) {
+      ft = t0;
+      ++fg;
     }
   };
   auto put = [&](int slot) {
@@ -276,21 +283,31 @@ attn_bwd_dkdv(const BwdParams p) {
     lq.store(base, xq);
     ldo.store(base + BQ * RS, xd);
     if (tid < BQ) {
-      lsd[slot][0][tid] = xl;
-      lsd[slot][1][tid] = xdl;
+      // rows that saw no key in the forward (lse = -inf): P = 0
+      lsd[slot][0][tid] = xl > -INFINITY ? -(xl * kLog2e) * inv_c : -INFINITY;
+      lsd[slot][1][tid] = -xdl;
     }
   };
 
   const float c = p.c;
-  if (nj > 0) {
-    fetch(0);
-    put(0);
+  // lane = key, registers = head-dim columns
+  uint16_t* dkg = (uint16_t*)p.dk + b * p.dk_b + hk * p.dk_h;
+  uint16_t* dvg = (uint16_t*)p.dv + b * p.dv_b + hk * p.dv_h;
+  if (nj == 0) {  // no query sees this block (causal): zero gradients
+    store_rows<T, NDB>(dvg, p.dv_s, key, Sk, D, hh, dva, 1.f);
+    store_rows<T, NDB>(dkg, p.dk_s, key, Sk, D, hh, dka, p.scale);
+    return;
   }
+  // (the loop is entered only past put(0), whose waits cover the operand
+  // loads above: no load of those is outstanding inside the loop)
+  fetch();
+  put(0);
   lds_barrier();
+  int cg = 0, ct = t0;
   for (int j = 0; j < nj; ++j) {
     const int slot = j & 1;
-    if (j + 1 < nj) fetch(j + 1);
-    const int q0 = (t0 + j % nt) * BQ;
+    if (j + 1 < nj) fetch();
+    const int q0 = ct * BQ;
     // causal: a tile whose last query precedes this wave's first key adds nothing
     if (!CAUSAL || q0 + BQ - 1 >= kw0) {
       const uint16_t* qs = lds + slot * 2 * BQ * RS;
@@ -301,7 +318,7 @@ attn_bwd_dkdv(const BwdParams p) {
       float madd[16];
       if (MASK) {
         const int kind = p.mask_kind, mes = mask_bytes(kind);
-        const int h = hk * p.group + j / nt;
+        const int h = h0 + cg;
         const __amdgpu_buffer_rsrc_t mrs = uniform_rsrc(
             (const char*)p.mask + (b * p.m_b + h * p.m_h) * mes, ((int64_t)(Sq - 1) * p.m_q + (Sk + 7) / 8 * 8) * mes);
 #pragma unroll
@@ -357,11 +374,12 @@ attn_bwd_dkdv(const BwdParams p) {
     }
     if (j + 1 < nj) put(slot ^ 1);
     lds_barrier();
+    if (++ct == t1) {
+      ct = t0;
+      ++cg;
+    }
   }
 
-  // lane = key, registers = head-dim columns
-  uint16_t* dkg = (uint16_t*)p.dk + b * p.dk_b + hk * p.dk_h;
-  uint16_t* dvg = (uint16_t*)p.dv + b * p.dv_b + hk * p.dv_h;
   store_rows<T, NDB>(dvg, p.dv_s, key, Sk, D, hh, dva, 1.f);
   store_rows<T, NDB>(dkg, p.dk_s, key, Sk, D, hh, dka, p.scale);
 }
