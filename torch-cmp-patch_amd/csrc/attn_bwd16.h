@@ -344,7 +344,15 @@ attn_bwd_dkdv(const BwdParams p) {
 #pragma unroll
       for (int st = 0; st < NKS; ++st) dp = Elt<T>::mma(*(const u32x4*)(dos + a_rd[st]), vf[st], dp);
       // s = S - lse2 / c, dp = dP - Delta
-      const bool diag = CAUSAL && q0 < kw0 + 31;
+      float x[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[r] = MASK ? __builtin_fmaf(s[r], c, madd[r]) : s[r] * c;
+      // causal diagonal tile: one wave-uniform branch around all 16 checks
+      if (CAUSAL && q0 < kw0 + 31) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (key > q0 + acc_key(r, hh)) x[r] = -INFINITY;
+      }
       u32x4 pp[2], ps[2];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
@@ -352,12 +360,7 @@ attn_bwd_dkdv(const BwdParams p) {
         for (int e = 0; e < 4; ++e) {
           float pv[2];
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const int r = 8 * ks + 2 * e + u;
-            float x = MASK ? __builtin_fmaf(s[r], c, madd[r]) : s[r] * c;
-            if (diag && key > q0 + acc_key(r, hh)) x = -INFINITY;
-            pv[u] = fast_exp2(x);
-          }
+          for (int u = 0; u < 2; ++u) pv[u] = fast_exp2(x[8 * ks + 2 * e + u]);
           pp[ks][e] = Elt<T>::pack(pv[0], pv[1]);
           ps[ks][e] = Elt<T>::pack(pv[0] * dp[8 * ks + 2 * e], pv[1] * dp[8 * ks + 2 * e + 1]);
         }
@@ -524,6 +527,20 @@ attn_bwd_dq(const BwdParams p) {
           }
         }
       }
+      float x[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        x[r] = __builtin_fmaf(s[r], c, -l2);
+        if (MASK) x[r] += madd[r];
+      }
+      // one wave-uniform branch around all 16 checks: per-element branches
+      // would be if-converted into selects that every tile pays for
+      if (edge) {
+        const int lim = CAUSAL ? min(Sk, qrow + 1) : Sk;  // keys below lim count
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (k0 + acc_key(r, hh) >= lim) x[r] = -INFINITY;
+      }
       u32x4 ps[2];
 #pragma unroll
       for (int ks2 = 0; ks2 < 2; ++ks2)
@@ -533,13 +550,7 @@ attn_bwd_dq(const BwdParams p) {
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
             const int r = 8 * ks2 + 2 * e + u;
-            float x = __builtin_fmaf(s[r], c, -l2);
-            if (MASK) x += madd[r];
-            if (edge) {
-              const int kk = k0 + acc_key(r, hh);
-              if (kk >= Sk || (CAUSAL && kk > qrow)) x = -INFINITY;
-            }
-            pv[u] = fast_exp2(x) * (dp[r] - dl);
+            pv[u] = fast_exp2(x[r]) * (dp[r] - dl);
           }
           ps[ks2][e] = Elt<T>::pack(pv[0], pv[1]);
         }
