@@ -296,6 +296,41 @@ def test_masked_training_pair(case, kind, causal):
         assert _rel_err(got, ref) <= TOL[dtype], name
 
 
+MASK_GQA_TRAIN = [
+    # dtype, B, H, Hkv, Sq, Sk, D, kind
+    ("fp16", 2, 6, 2, 150, 260, 64, "bool_full"),
+    ("bf16", 1, 4, 1, 100, 1100, 128, "add_heads"),   # multi-query, forward key split when non-causal
+    ("fp16", 1, 8, 2, 64, 500, 64, "add_2d_f32"),
+]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("case", MASK_GQA_TRAIN, ids=[f"{c[0]}-H{c[2]}of{c[3]}-q{c[4]}k{c[5]}d{c[6]}-{c[7]}"
+                                                      for c in MASK_GQA_TRAIN])
+def test_masked_grouped_query_training_pair(case, causal):
+    """Masks and grouped-query K/V together: the dK/dV sweep over a group's
+    query heads reads each query head's own mask rows."""
+    dtype, B, H, Hkv, Sq, Sk, D, kind = case
+    g = torch.Generator().manual_seed(H * Sq + Sk + D)
+    mk = lambda h, S: torch.randn(B, h, S, D, generator=g).to(TDT[dtype]).cuda()
+    q, k, v, do = mk(H, Sq), mk(Hkv, Sk), mk(Hkv, Sk), mk(H, Sq)
+    m = _train_mask(kind, B, H, Sq, Sk, dtype, seed=Sk)
+    s = D ** -0.5
+    out, lse = abi.attn_fwd_lse(q, k, v, s, causal, attn_mask=m)
+    dq, dk, dv = abi.attn_bwd(q, k, v, out, do, lse, s, causal, attn_mask=m)
+    torch.cuda.synchronize()
+    grp = H // Hkv
+    kr, vr = (t.cpu().repeat_interleave(grp, dim=1) for t in (k, v))
+    qc, dc, mc = q.cpu(), do.cpu(), m.cpu()
+    assert orc.max_abs_err(out.cpu(), orc.sdpa_np(qc, kr, vr, s, causal, attn_mask=mc)) <= TOL[dtype]
+    assert orc.max_abs_err(lse.cpu(), orc.sdpa_lse_np(qc, kr, s, causal, attn_mask=mc)) <= TOL[dtype]
+    dq_r, dk_r, dv_r = orc.sdpa_bwd_np(qc, kr, vr, dc, s, causal, attn_mask=mc)
+    dk_r = dk_r.reshape(B, Hkv, grp, Sk, D).sum(axis=2)
+    dv_r = dv_r.reshape(B, Hkv, grp, Sk, D).sum(axis=2)
+    for name, got, ref in zip(("dq", "dk", "dv"), (dq, dk, dv), (dq_r, dk_r, dv_r)):
+        assert _rel_err(got, ref) <= TOL[dtype], name
+
+
 def test_masked_training_dead_rows():
     """Rows whose keys are all dropped: output 0, lse -inf, no gradient."""
     q, k, v, do = _inputs("fp16", 1, 2, 96, 200, 64, seed=77)

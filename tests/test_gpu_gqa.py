@@ -141,3 +141,35 @@ def test_gqa_packed_strided_query_and_output():
     assert abi.attn_fwd_raw(q, k, v, o, 0.125, False) == abi.OK
     torch.cuda.synchronize()
     assert orc.max_abs_err(o.cpu(), _oracle(q, k, v, 0.125, False)) <= TOL["fp16"]
+
+
+MASKED = [
+    # dtype, B, H, Hkv, Sq, Sk, D, mask shape (None = full [B, H, Sq, Sk])
+    ("fp16", 2, 6, 2, 150, 260, 64, None),
+    ("bf16", 1, 8, 2, 40, 1500, 128, (1, 8, 40, 1500)),   # short query sweep: masks are never packed
+    ("fp16", 1, 4, 1, 96, 900, 64, (96, 900)),            # 2-D mask, multi-query, key split
+]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("case", MASKED, ids=[f"{c[0]}-H{c[2]}of{c[3]}-q{c[4]}k{c[5]}d{c[6]}" for c in MASKED])
+def test_gqa_with_attention_mask(case, causal):
+    """Grouped-query K/V together with an attention mask: the mask indexes
+    query heads, K/V head h / (H / H_kv) serves query head h."""
+    dtype, B, H, Hkv, Sq, Sk, D, mshape = case
+    q, k, v = _gqa_inputs(dtype, B, H, Hkv, Sq, Sk, D, seed=Sq * 3 + Sk)
+    g = torch.Generator().manual_seed(D + Sk)
+    if mshape is None:
+        m = torch.rand(B, H, Sq, Sk, generator=g) > 0.25
+        m[..., 0] = True
+    else:
+        m = (torch.randn(*mshape, generator=g) * 1.5).to(q.dtype)
+        m[..., 2::7] = -math.inf
+    m = m.cuda()
+    scale = 1.0 / math.sqrt(D)
+    out = abi.attn_fwd(q, k, v, scale, causal, attn_mask=m)
+    torch.cuda.synchronize()
+    grp = H // Hkv
+    kr, vr = (t.cpu().repeat_interleave(grp, dim=1) for t in (k, v))
+    want = orc.sdpa_np(q.cpu(), kr, vr, scale, causal, attn_mask=m.cpu())
+    assert orc.max_abs_err(out.cpu(), want) <= TOL[dtype]
