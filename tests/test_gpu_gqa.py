@@ -114,7 +114,7 @@ PACKED = [
     ("fp16", 2, 16, 2, 5, 700, 64),      # ragged rows per head, 8 heads per group
     ("fp16", 1, 8, 4, 64, 333, 64),      # the largest packed Sq
     ("bf16", 1, 12, 3, 7, 2048, 96),     # head dim below its bucket
-    ("bf16", 1, 32, 8, 1, 32768, 128),   # long-context decode: 32 key parts, 3 of 4 waves rowless
+    ("bf16", 1, 32, 8, 1, 32768, 128),   # long-context decode: 64 key parts, 3 of 4 waves rowless
 ]
 
 

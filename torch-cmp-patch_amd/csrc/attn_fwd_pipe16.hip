@@ -55,14 +55,19 @@ int device_cus() {
   return cus[dev];
 }
 
-// Exchange buffer sized for the largest plan on this device: at most one part
-// per CU (split blocks * parts <= CUs), kPipeNw waves, DP <= 128.
+// Exchange buffer sized for the largest plan on this device: at most
+// kMaxPartsPerCu parts per CU (split blocks * parts <= kMaxPartsPerCu * CUs),
+// kPipeNw waves, DP <= 128.
+constexpr int kMaxPartsPerCu = 2;
+
 struct Exchange {
   f32x4* ws;
   int* cnt;
 };
 
-size_t exchange_ws_bytes(int cus) { return (size_t)cus * kPipeNw * split_vectors(128) * 64 * sizeof(f32x4); }
+size_t exchange_ws_bytes(int cus) {
+  return (size_t)cus * kMaxPartsPerCu * kPipeNw * split_vectors(128) * 64 * sizeof(f32x4);
+}
 size_t exchange_cnt_bytes(int cus) { return (size_t)cus * kPipeNw * sizeof(int); }
 
 bool exchange_for(hipStream_t s, int cus, Exchange& out) {
@@ -115,7 +120,12 @@ SplitArgs split_plan(int n, int ntiles, int occ, int cus, bool causal) {
   if (causal || cus <= 0) return sa;
   const int full = n / cus, rem = n - full * cus;
   if (rem == 0 || full + 1 > occ) return sa;  // whole rounds, or more than fits at once
-  int parts = cus / rem;
+  // After whole rounds each CU takes one part of the round that remains.  With
+  // no whole round (fewer blocks than CUs: decode, short sweeps) each CU can
+  // hold several parts at once: more key ranges streamed side by side, more
+  // loads in flight (a decode step with one part per CU reaches ~5.2 TB/s).
+  const int per_cu = full == 0 ? (occ < kMaxPartsPerCu ? occ : kMaxPartsPerCu) : 1;
+  int parts = per_cu * cus / rem;
   if (parts > ntiles / kMinPartTiles) parts = ntiles / kMinPartTiles;
   if (parts < 2) return sa;
   sa.nfull = full * cus;
