@@ -69,7 +69,9 @@ def test_describe_key_split_plan():
     self-attention: 640 blocks of 128 queries = 2 whole rounds + 128 blocks
     cut in 2 key ranges (one part per CU); 2*4*32 = 256 blocks fill whole
     rounds; causal launches and short key sweeps never split; 4 blocks of
-    2048 keys (64 tiles) get 8 parts of 8 tiles."""
+    2048 keys (64 tiles) get 8 parts of 8 tiles.  With no whole round every
+    CU holds two parts: 128 blocks of 4096 keys (a packed decode step) get
+    4 parts each, 200 blocks get 2."""
     import torch
     if torch.cuda.is_available():
         pytest.skip("plan depends on the visible device's CU count")
@@ -79,6 +81,9 @@ def test_describe_key_split_plan():
     assert "key-split" not in abi.describe(f16, 2, 10, 4096, 4096, 64, True)[1]
     assert "key-split" not in abi.describe(f16, 1, 2, 256, 300, 64)[1]
     assert "key-split: 0 whole + 4 x 8 parts" in abi.describe(f16, 1, 2, 256, 2048, 64)[1]
+    bf16 = abi.DTYPE_BF16
+    assert "key-split: 0 whole + 128 x 4 parts" in abi.describe(bf16, 16, 8, 2, 4096, 128)[1]
+    assert "key-split: 0 whole + 200 x 2 parts" in abi.describe(f16, 1, 200, 100, 4096, 64)[1]
 
 
 def _call(q=16, k=16, v=16, o=16, dtype=abi.DTYPE_F16, B=1, H=1, Sq=8, Sk=8, D=64,
