@@ -102,9 +102,11 @@ def test_bwd_is_deterministic():
         assert torch.equal(a, b)
 
 
-def test_bwd_strided_views():
-    """[B,S,H,D] memory viewed as [B,H,S,D] for every operand and gradient."""
-    B, S, H, D = 1, 192, 4, 64
+@pytest.mark.parametrize("D", [64, 128])
+def test_bwd_strided_views(D):
+    """[B,S,H,D] memory viewed as [B,H,S,D] for every operand and gradient
+    (D = 128: the dK/dV kernel's V operands parked in LDS)."""
+    B, S, H = 1, 192, 4
     g = torch.Generator().manual_seed(3)
     mk = lambda: torch.randn(B, S, H, D, generator=g).half().cuda().transpose(1, 2)
     q, k, v, do = mk(), mk(), mk(), mk()
@@ -194,6 +196,7 @@ GQA_CASES = [
     ("fp16", 1, 8, 2, 256, 256, 64, False),
     ("bf16", 2, 6, 3, 300, 200, 128, True),
     ("fp16", 1, 4, 1, 130, 700, 64, True),    # multi-query, causal Sq < Sk
+    ("fp16", 1, 8, 2, 256, 384, 128, False),  # D = 128 non-causal: V operands parked in LDS
 ]
 
 
