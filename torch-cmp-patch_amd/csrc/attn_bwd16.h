@@ -176,27 +176,29 @@ __device__ __forceinline__ void store_rows(uint16_t* base, int64_t row_stride, i
 
 // ---- dK, dV for one block of 128 keys (4 waves x 32 keys), sweeping the
 // query tiles (32 rows of Q, dO, lse, Delta) through double-buffered LDS.
-// Waves per SIMD: D <= 64: 3 (2 causal or masked), the most the registers
-// allow without spilling; D <= 128: 2 with V parked in LDS (the causal and
-// the masked variants spill 8 registers and are still 12-20% faster than at
-// 1), 1 masked causal (its K/V operands and dK/dV accumulators alone take
-// 192 registers).
+// Waves per SIMD: D <= 64: 3 (masked with V parked in LDS; 4 spilled
+// registers), 2 causal; D <= 128: 2 with V parked in LDS (the causal and the
+// masked variants spill 8 registers and are still 12-20% faster than at 1),
+// 1 masked causal (its K/V operands and dK/dV accumulators alone take 192
+// registers).
 template <typename T, int DK, bool CAUSAL, bool MASK>
 __global__ void __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu(DK <= 64 ? (CAUSAL || MASK ? 2 : 3) : (MASK && CAUSAL ? 1 : 2))))
+__attribute__((amdgpu_waves_per_eu(DK <= 64 ? (CAUSAL ? 2 : 3) : (MASK && CAUSAL ? 1 : 2))))
 attn_bwd_dkdv(const BwdParams p) {
   constexpr int BQ = 32, BKV = 128;
   constexpr int RS = bwd_lds_stride(DK);  // LDS row stride (halves)
   constexpr int NKS = DK / 16, NDB = DK / 32;
   static_assert(DK % 32 == 0, "head-dim bucket");
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 2 * BQ * RS];  // [slot][Q, dO][row][col]
-  // D > 64: the V operands live in LDS instead of registers (32 fewer VGPRs:
-  // two waves per SIMD instead of one; dK/dV 349 -> 268 us on bf16
-  // [4,16,2048,128], 275 -> 241 us causal, masked backward 603 -> 481 us).
-  // Each lane reads back only what it wrote, so no barrier orders the
-  // parking stores.  Masked causal launches (which would spill 32 registers
-  // at two waves) keep their registers and one wave per SIMD.
-  constexpr bool VLDS = DK > 64 && !(MASK && CAUSAL);
+  // The V operands live in LDS instead of registers where that buys a wave
+  // per SIMD: D > 64 (32 fewer VGPRs, two waves instead of one; dK/dV
+  // 349 -> 268 us on bf16 [4,16,2048,128], 275 -> 241 us causal, masked
+  // backward 603 -> 481 us) and D <= 64 masked non-causal (three waves
+  // instead of two: masked SDXL-shape backward 913 -> 616 us).  Each lane
+  // reads back only what it wrote, so no barrier orders the parking stores.
+  // Not for masked causal D > 64 (32 spilled registers at two waves) or
+  // causal D <= 64 (three waves with V parked measured slower: 301 -> 327 us).
+  constexpr bool VLDS = DK > 64 ? !(MASK && CAUSAL) : (MASK && !CAUSAL);
   constexpr int RSV = DK + 8;
   __shared__ __attribute__((aligned(16))) uint16_t vpark[VLDS ? BKV * RSV : 8];
   // [slot][-lse2 / c, -Delta][row]: the starting values of the S and dP
