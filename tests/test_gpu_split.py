@@ -114,6 +114,17 @@ def test_causal_and_whole_rounds_do_not_split():
         assert "key-split" in _split_text(q, 2, 10, 4096, 4096, 64)
 
 
+def test_fewer_blocks_than_cus_take_two_parts_per_cu():
+    """With no whole round each CU holds two parts at once: a packed decode
+    step (128 blocks of 4096 keys) is cut in 4 key ranges per block, and the
+    result still matches the oracle."""
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("plan checked for a 256-CU MI355X")
+    q, k, v = _inputs("bf16", 16, 8, 2, 4096, 128, seed=5)
+    assert "key-split: 0 whole + 128 x 4 parts" in _split_text(q, 16, 8, 2, 4096, 128)
+    _check(q, k, v, 128 ** -0.5, False, "bf16")
+
+
 def _replays(g, out, reps=4):
     """Replay a captured graph with eager work (and a sync) between replays."""
     results = []
