@@ -2,8 +2,8 @@
 
 Mirrors the reference's mock-based suite for this path
 (tests/test_cmpext3_monkeypatch.py there: TestGradSafe/TestUsable,
-TestEnableDisable :91-180, TestAutoselect :476-643,
-TestScaledDotProductAttention :857-926), written against this package: the
+TestEnableDisable :91-180, TestScaledDotProductAttention :857-926),
+written against this package: the
 native module is a fake whose `attention` is a MagicMock (`native` fixture),
 and force_eligible() lets CPU tensors through the GPU/dtype gate.
 """
@@ -249,170 +249,6 @@ class TestScaledDotProductAttention:
         out = F.scaled_dot_product_attention(q, k, v, enable_gqa=True)
         _called_once_with_tensors(native.attention, q, k, v, None, False)
         assert torch.allclose(out, STOCK_SDPA(q, k, v, enable_gqa=True))
-
-
-class TestAutoselect:
-    @staticmethod
-    def _timed(monkeypatch, autoselect, timings):
-        monkeypatch.setattr(autoselect, "_time", lambda fn: (timings[fn], fn()))
-
-    def test_picks_the_faster_implementation(self, autoselecting, monkeypatch):
-        calls = {"native": 0, "stock": 0}
-
-        def native():
-            calls["native"] += 1
-            return torch.zeros(4)
-
-        def stock():
-            calls["stock"] += 1
-            return torch.zeros(4)
-
-        self._timed(monkeypatch, autoselecting, {native: 0.001, stock: 0.010})
-        autoselecting.choose("op", ("k",), native, stock)
-        d = autoselecting._decisions[("k",)]
-        assert d.use_native and d.speedup == pytest.approx(10.0)
-        before = calls["stock"]
-        for _ in range(3):
-            autoselecting.choose("op", ("k",), native, stock)
-        assert calls["stock"] == before
-
-    def test_picks_stock_when_the_kernel_is_slower(self, autoselecting, monkeypatch):
-        calls = {"native": 0}
-
-        def native():
-            calls["native"] += 1
-            return torch.zeros(4)
-
-        def stock():
-            return torch.zeros(4)
-
-        self._timed(monkeypatch, autoselecting, {native: 0.010, stock: 0.001})
-        autoselecting.choose("op", ("k",), native, stock)
-        assert not autoselecting._decisions[("k",)].use_native
-        before = calls["native"]
-        for _ in range(3):
-            autoselecting.choose("op", ("k",), native, stock)
-        assert calls["native"] == before
-
-    def test_rejects_a_kernel_whose_output_disagrees(self, autoselecting, monkeypatch):
-        native = lambda: torch.full((4,), 10.0)  # noqa: E731
-        stock = lambda: torch.zeros(4)  # noqa: E731
-        self._timed(monkeypatch, autoselecting, {native: 0.001, stock: 0.010})
-        got = autoselecting.choose("op", ("k",), native, stock)
-        d = autoselecting._decisions[("k",)]
-        assert not d.use_native and "mismatch" in d.note
-        assert torch.equal(got, torch.zeros(4))
-
-    def test_tolerates_rounding_differences(self, autoselecting, monkeypatch):
-        native = lambda: torch.ones(4) * (1.0 + 1e-6)  # noqa: E731
-        stock = lambda: torch.ones(4)  # noqa: E731
-        self._timed(monkeypatch, autoselecting, {native: 0.001, stock: 0.010})
-        autoselecting.choose("op", ("k",), native, stock)
-        assert autoselecting._decisions[("k",)].use_native
-
-    @pytest.mark.parametrize("dtype,rel,ok", [(torch.float16, 2e-2, True), (torch.float16, 4e-2, False),
-                                              (torch.bfloat16, 4e-2, True), (torch.float32, 2e-3, False)])
-    def test_per_dtype_tolerance(self, autoselecting, monkeypatch, dtype, rel, ok):
-        native = lambda: (torch.ones(8) * (1 + rel)).to(dtype)  # noqa: E731
-        stock = lambda: torch.ones(8).to(dtype)  # noqa: E731
-        self._timed(monkeypatch, autoselecting, {native: 0.001, stock: 0.010})
-        autoselecting.choose("op", ("k",), native, stock)
-        assert autoselecting._decisions[("k",)].use_native is ok
-
-    def test_rejects_non_finite_output(self, autoselecting, monkeypatch):
-        native = lambda: torch.full((4,), float("nan"))  # noqa: E731
-        stock = lambda: torch.zeros(4)  # noqa: E731
-        self._timed(monkeypatch, autoselecting, {native: 0.001, stock: 0.010})
-        autoselecting.choose("op", ("k",), native, stock)
-        assert not autoselecting._decisions[("k",)].use_native
-
-    def test_shape_mismatch_is_rejected(self, autoselecting, monkeypatch):
-        native = lambda: torch.zeros(5)  # noqa: E731
-        stock = lambda: torch.zeros(4)  # noqa: E731
-        self._timed(monkeypatch, autoselecting, {native: 0.001, stock: 0.010})
-        autoselecting.choose("op", ("k",), native, stock)
-        assert "shape" in autoselecting._decisions[("k",)].note
-
-    def test_kernel_that_raises_is_never_probed_again(self, autoselecting):
-        calls = {"native": 0}
-
-        def native():
-            calls["native"] += 1
-            raise RuntimeError("unsupported shape")
-
-        stock = lambda: torch.zeros(4)  # noqa: E731
-        for _ in range(3):
-            assert torch.equal(autoselecting.choose("op", ("k",), native, stock), torch.zeros(4))
-        assert calls["native"] == 1
-        assert "RuntimeError" in autoselecting._decisions[("k",)].note
-
-    def test_one_off_failure_does_not_overturn_a_good_decision(self, autoselecting, monkeypatch):
-        state = {"fail": False}
-        calls = {"stock": 0}
-
-        def native():
-            if state["fail"]:
-                raise RuntimeError("transient")
-            return torch.zeros(4)
-
-        def stock():
-            calls["stock"] += 1
-            return torch.zeros(4)
-
-        self._timed(monkeypatch, autoselecting, {native: 0.001, stock: 0.010})
-        autoselecting.choose("op", ("k",), native, stock)
-        settled = calls["stock"]
-        state["fail"] = True
-        autoselecting.choose("op", ("k",), native, stock)
-        assert calls["stock"] == settled + 1
-        assert autoselecting._decisions[("k",)].use_native
-        state["fail"] = False
-        autoselecting.choose("op", ("k",), native, stock)
-        assert calls["stock"] == settled + 1
-
-    def test_out_of_memory_during_probe_records_nothing(self, autoselecting):
-        def native():
-            raise torch.OutOfMemoryError("probe OOM")
-
-        stock = lambda: torch.zeros(4)  # noqa: E731
-        assert torch.equal(autoselecting.choose("op", ("k",), native, stock), torch.zeros(4))
-        assert ("k",) not in autoselecting._decisions
-        assert autoselecting._probe_counts.get("op", 0) == 0
-
-    def test_stops_probing_after_too_many_signatures(self, autoselecting, monkeypatch):
-        native = lambda: torch.zeros(4)  # noqa: E731
-        stock = lambda: torch.zeros(4)  # noqa: E731
-        self._timed(monkeypatch, autoselecting, {native: 0.001, stock: 0.010})
-        cap = autoselecting._MAX_SIGNATURES_PER_OP
-        for i in range(cap + 5):
-            autoselecting.choose("op", ("k", i), native, stock)
-        assert autoselecting._probe_counts["op"] == cap
-        beyond = autoselecting._decisions[("k", cap + 3)]
-        assert beyond.use_native and "not probed" in beyond.note
-
-    def test_disabled_autoselect_always_uses_the_kernel(self, monkeypatch):
-        from cmpext3 import autoselect
-        calls = {"stock": 0}
-
-        def stock():
-            calls["stock"] += 1
-            return torch.ones(4)
-
-        monkeypatch.setattr(autoselect, "_ENABLED", False)
-        got = cmpext3._dispatch("op", torch.zeros(4), ("k",), lambda: torch.zeros(4), stock)
-        assert torch.equal(got, torch.zeros(4)) and calls["stock"] == 0
-
-    def test_sdpa_signature_key_and_report(self, autoselecting, patched, native, monkeypatch):
-        force_eligible(monkeypatch)
-        q, k, v = _qkv(1, 2, 3, 4)
-        native.attention.side_effect = lambda *a: STOCK_SDPA(q, k, v)
-        F.scaled_dot_product_attention(q, k, v, scale=0.5)
-        keys = list(autoselecting._decisions)
-        assert keys == [(q.shape, q.dtype, k.shape, v.shape, 0.5, False)]
-        assert "attention fp32" in cmpext3.autoselect_report()
-
-    def test_report_when_empty(self, autoselecting):
-        assert "no kernel decisions" in cmpext3.autoselect_report()
 
 
 def test_missing_native_extension_fails_loudly(tmp_path):
