@@ -174,3 +174,51 @@ def test_training_entry_points_reject_before_launch():
     assert _call_bwd(mask=16, mask_dtype=7) == abi.E_DTYPE
     assert _call_bwd(mask=24, mask_dtype=abi.DTYPE_BOOL) == abi.E_ALIGN
     assert _call_bwd(mask=16, mask_dtype=abi.DTYPE_BOOL, mask_str=(0, 0, 6)) == abi.E_ALIGN
+
+
+def _call_masked(k_row=64, q_row=64, o_row=64, Sk=1 << 17, Sq=1, mask_str=(0, 0, 0), lse=0,
+                 mask_dtype=abi.DTYPE_BOOL):
+    """A masked (or training) call whose K/V rows sit k_row elements apart:
+    fake, aligned device addresses, so only the host checks may run."""
+    vp = ctypes.c_void_p
+    q_st = (ctypes.c_int64 * 3)(q_row * Sq, q_row * Sq, q_row)
+    kv_st = (ctypes.c_int64 * 3)(k_row * Sk, k_row * Sk, k_row)
+    o_st = (ctypes.c_int64 * 3)(o_row * Sq, o_row * Sq, o_row)
+    m_st = (ctypes.c_int64 * 3)(*mask_str)
+    if lse:
+        return abi.lib().cmpext3_attn_fwd_lse(vp(16), vp(16), vp(16), vp(16), vp(lse), abi.DTYPE_F16, 1,
+                                              1, 1, Sq, Sk, 64, q_st, kv_st, kv_st, o_st, vp(16),
+                                              mask_dtype, m_st, ctypes.c_float(0.125), 0, None)
+    return abi.lib().cmpext3_attn_fwd_masked(vp(16), vp(16), vp(16), vp(16), abi.DTYPE_F16, 1, 1, 1, Sq,
+                                             Sk, 64, q_st, kv_st, kv_st, o_st, vp(16), mask_dtype, m_st,
+                                             ctypes.c_float(0.125), 0, None)
+
+
+def test_mask_is_never_dropped_for_wide_kv_rows():
+    """Only the pipelined kernel applies masks, and it addresses the whole
+    key sweep with 32-bit offsets.  A long masked sweep over K/V rows of a
+    packed QKV buffer (row stride 3 * 16 heads * 64) exceeds that: the call
+    must be refused (so the binding falls back to stock), not run unmasked."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("fake device addresses: host-side checks only")
+    wide = 3 * 32 * 128  # 131072 keys of 24 KiB rows: 3.2 GB past the first row
+    assert _call_masked(k_row=wide, Sk=1 << 17) == abi.E_TOO_LARGE
+    assert _call_masked(k_row=wide, Sk=1 << 17, mask_dtype=abi.DTYPE_F32) == abi.E_TOO_LARGE
+    assert _call_masked(k_row=wide, Sk=1 << 17, lse=16, mask_dtype=-1) == abi.E_TOO_LARGE
+
+
+def test_training_forward_refuses_what_its_backward_would():
+    """The backward addresses Q and dO (laid out like O) with 32-bit tile
+    offsets; the training forward checks the same, so a step never passes
+    the forward and then fails in the backward (where autograd has no stock
+    fallback)."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("fake device addresses: host-side checks only")
+    wide, Sq = 3 * 32 * 128, 1 << 17
+    # the backward refuses Q or dO rows this wide (one stride for all operands here)
+    assert _call_bwd(strides=(wide * Sq, wide * Sq, wide), Sq=Sq, Sk=64) == abi.E_TOO_LARGE
+    for q_row, o_row in ((wide, 64), (64, wide)):
+        fwd = _call_masked(q_row=q_row, o_row=o_row, Sq=Sq, Sk=64, lse=16, mask_dtype=-1)
+        assert fwd == abi.E_TOO_LARGE

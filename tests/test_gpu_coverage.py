@@ -1,0 +1,101 @@
+"""GPU parity of routes the product serves beyond the BASELINE shapes.
+
+Same bar as tests/test_gpu_parity.py (max |kernel - oracle| <= 1e-2 fp16,
+2e-2 bf16, 1e-4 fp32; oracle = float64 SDPA on the CPU over the same rounded
+inputs):
+
+  * head dims that are not a whole number of 16-byte chunks, for every
+    dtype, through the torch binding (ops.attention), causal and not;
+    the reference's fp32 kernel takes any D <= 128
+    (src/cuda/fp32_attention.cu:200-204);
+  * head dims 160, 192 and 256 over long key sweeps (>= 1024 keys, many
+    tiles, scores wide enough to force offset rescales), causal and not; the
+    reference serves D = 160 at any key length
+    (src/cuda/fp16_flash_attention_hfma2.cu:278-285);
+  * the reference's production sequence length S = 17402
+    (cmpext3/__init__.py:16-20, tests_hardware/test_attention_bf16_routing.py:240-243),
+    bf16 [1, 4, 17402, 64], causal and not: ragged in every tiling here
+    (17402 = 135 * 128 + 122 = 543 * 32 + 26).  The kernel runs the whole
+    problem; the oracle checks a sample of query rows that includes the first
+    rows, the ragged last tile and rows spread over the sweep.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import cmpext3
+from cmpext3 import abi
+from cmpext3 import workloads as W
+from oracle import sdpa_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL = orc.TOLERANCE
+
+
+def _inputs(dtype, B, H, Sq, Sk, D, seed):
+    return W.Workload("cov", dtype, B, H, Sq, Sk, D, seed=seed).make_inputs("cuda")
+
+
+@pytest.mark.parametrize("dtype,D", [("fp32", 33), ("fp32", 36), ("fp32", 100), ("fp32", 3),
+                                     ("bf16", 36), ("bf16", 100), ("bf16", 2),
+                                     ("fp16", 33), ("fp16", 100)])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("Sq,Sk", [(70, 50), (129, 300)])
+def test_odd_head_dims_every_dtype(dtype, D, causal, Sq, Sk):
+    q, k, v = _inputs(dtype, 1, 2, Sq, Sk, D, seed=D * 31 + Sk)
+    print(f"odd D: {dtype} D={D} Sq={Sq} Sk={Sk} causal={causal}", flush=True)
+    out = cmpext3.ops.attention(q, k, v, None, causal)
+    torch.cuda.synchronize()
+    assert out.shape == q.shape and out.dtype == q.dtype
+    ref = orc.sdpa_c(q.cpu(), k.cpu(), v.cpu(), None, causal)
+    err = orc.max_abs_err(out.cpu(), ref)
+    assert err <= TOL[dtype], f"max abs err {err:.3e}"
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("D", [160, 192, 256])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("Sq,Sk,scale", [(160, 1100, None), (1024, 1024, None), (96, 2049, 1.0)])
+def test_large_head_dims_long_key_sweeps(dtype, D, causal, Sq, Sk, scale):
+    """Many key tiles per query block on the D > 128 kernel; scale 1 spreads
+    the scores over tens of log2 units, so the running offset rises on
+    later tiles (rescales of O and l)."""
+    q, k, v = _inputs(dtype, 1, 2, Sq, Sk, D, seed=D + Sk)
+    print(f"large D: {dtype} D={D} Sq={Sq} Sk={Sk} causal={causal} scale={scale}", flush=True)
+    eff = 1.0 / math.sqrt(D) if scale is None else scale
+    out = abi.attn_fwd(q, k, v, eff, causal)
+    torch.cuda.synchronize()
+    ref = orc.sdpa_c(q.cpu(), k.cpu(), v.cpu(), eff, causal)
+    err = orc.max_abs_err(out.cpu(), ref)
+    assert err <= TOL[dtype], f"max abs err {err:.3e}"
+
+
+def _sample_rows(S, n_spread=200, seed=0):
+    rng = np.random.default_rng(seed)
+    tail = range(S - 150, S)                       # the ragged last block and tile
+    head = range(0, 40)
+    spread = rng.choice(S, size=n_spread, replace=False)
+    return np.unique(np.concatenate([np.fromiter(head, int), spread, np.fromiter(tail, int)]))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_production_length_17402(causal):
+    S, D = 17402, 64
+    q, k, v = _inputs("bf16", 1, 4, S, S, D, seed=17402 + causal)
+    print(f"S=17402 bf16 causal={causal}", flush=True)
+    out = cmpext3.ops.attention(q, k, v, None, causal)
+    torch.cuda.synchronize()
+    rows = _sample_rows(S, seed=causal)
+    qs = q.cpu()[:, :, rows]
+    mask = None
+    if causal:  # row r of the sample is query position rows[r]: keys 0..rows[r]
+        mask = torch.from_numpy(np.arange(S)[None, :] <= rows[:, None]).view(1, 1, len(rows), S)
+    ref = orc.sdpa_np(qs, k.cpu(), v.cpu(), 1.0 / math.sqrt(D), False, attn_mask=mask)
+    err = orc.max_abs_err(out.cpu()[:, :, rows], ref)
+    assert err <= TOL["bf16"], f"max abs err {err:.3e}"
+    assert bool(torch.isfinite(out).all())

@@ -12,10 +12,10 @@ round plus a remainder, ragged key counts whose parts get odd tile counts
 (a masked padding tile inside a part), scores spread over tens of log2 units
 (parts settle on different offsets before the merge), back-to-back
 launches of different plans (the per-wave counters must come back to zero),
-and HIP graph capture (on a fresh stream the launch runs unsplit with no
-allocation or memset in the graph; on a stream that already owns an exchange
-buffer the split launch is captured and every replay, with eager work and
-synchronisations in between, equals the eager result bit for bit).
+and HIP graph capture (under capture every launch runs unsplit: nothing is
+allocated or cleared in the graph and it holds no exchange buffer, so
+replays on another stream beside eager split launches stay correct; replays
+equal each other bit for bit and match the oracle).
 """
 from __future__ import annotations
 
@@ -154,19 +154,35 @@ def test_graph_capture_on_a_fresh_stream_runs_unsplit():
         assert torch.equal(r, res[0])
 
 
-def test_graph_capture_after_eager_use_replays_the_split():
-    """A stream that already owns an exchange buffer records the split launch;
-    the merge puts its counters back itself, so every replay equals the eager
-    result bit for bit."""
+def test_graph_capture_never_carries_a_streams_exchange_buffer():
+    """A stream that already owns an exchange buffer still records its launch
+    unsplit under capture, so the graph holds no buffer address.  Replays on a
+    second stream, running beside eager split launches on the capturing
+    stream, equal each other bit for bit and match the oracle, and so do the
+    eager results."""
     q, k, v = _inputs("bf16", 1, 3, 256, 2048, 64, seed=22)
+    assert "key-split" in _split_text(q, 1, 3, 256, 2048, 64)
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), 0.125)
     import cmpext3
-    s = torch.cuda.Stream()
+    s, s2 = torch.cuda.Stream(), torch.cuda.Stream()
     with torch.cuda.stream(s):
-        eager = cmpext3.ops.attention(q, k, v, 0.125, False)
+        eager = cmpext3.ops.attention(q, k, v, 0.125, False)   # s now owns a buffer
     s.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
         out = cmpext3.ops.attention(q, k, v, 0.125, False)
-    for r in _replays(g, out):
-        assert torch.equal(r, eager)
-    assert orc.max_abs_err(eager.cpu(), orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), 0.125)) <= TOL["bf16"]
+    torch.cuda.synchronize()
+    replays, eagers = [], []
+    for _ in range(4):
+        with torch.cuda.stream(s2):
+            g.replay()
+            replays.append(out.clone())
+        with torch.cuda.stream(s):
+            eagers.append(cmpext3.ops.attention(q, k, v, 0.125, False))
+    torch.cuda.synchronize()
+    for r in replays:
+        assert torch.equal(r, replays[0])
+        assert orc.max_abs_err(r.cpu(), ref) <= TOL["bf16"]
+    for e in eagers:
+        assert torch.equal(e, eager)
+    assert orc.max_abs_err(eager.cpu(), ref) <= TOL["bf16"]

@@ -152,6 +152,13 @@ int cmpext3_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o, i
 
 namespace {
 
+// Byte offsets of every row of an S-row sweep, plus one 64-row tile past it,
+// stay below 2^31 (the pipelined and backward kernels' 32-bit buffer offsets).
+bool tile_offsets_fit(int S, int64_t s0, int64_t s1) {
+  const int64_t rs = s0 > s1 ? s0 : s1;
+  return (int64_t)(S + 64) * rs * 2 < INT32_MAX;
+}
+
 // Forward with every option; lse (may be null) receives the row log-sum-exp.
 int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, int dtype, int B, int H,
              int H_kv, int Sq, int Sk, int D, const int64_t q_str[3], const int64_t k_str[3],
@@ -175,6 +182,10 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
   if (dtype != CMPEXT3_DTYPE_F32 &&
       (k_str[2] * 64 + 256 > INT32_MAX || v_str[2] * 64 + 256 > INT32_MAX))
     return CMPEXT3_E_TOO_LARGE;
+  // masks and the log-sum-exp exist only in the pipelined kernel, which
+  // addresses every K/V tile of the sweep with 32-bit buffer offsets: a call
+  // beyond that must fail here rather than run a kernel without them
+  if ((masked || lse) && !tile_offsets_fit(Sk, k_str[2], v_str[2])) return CMPEXT3_E_TOO_LARGE;
 
   cmpext3::FwdParams p;
   memset(&p, 0, sizeof p);
@@ -204,12 +215,6 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
   return err == hipSuccess ? CMPEXT3_OK : CMPEXT3_E_LAUNCH;
 }
 
-// Row offsets of one 32-row tile past the last row stay below 2^31 bytes.
-bool tile_offsets_fit(int S, int64_t s0, int64_t s1) {
-  const int64_t rs = s0 > s1 ? s0 : s1;
-  return (int64_t)(S + 64) * rs * 2 < INT32_MAX;
-}
-
 }  // namespace
 
 extern "C" {
@@ -235,8 +240,13 @@ int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, f
   if (!lse || ((uintptr_t)lse & 3u) != 0) return CMPEXT3_E_INVALID;
   if (!k_str || !v_str) return CMPEXT3_E_INVALID;
   // the pipelined kernel (the one that writes the log-sum-exp) addresses K/V
-  // tiles with 32-bit buffer offsets
-  if (!tile_offsets_fit(Sk, k_str[2], v_str[2])) return CMPEXT3_E_TOO_LARGE;
+  // tiles with 32-bit buffer offsets, and the backward that consumes this
+  // forward's state does the same for Q and dO (dO takes O's layout): refuse
+  // here what cmpext3_attn_bwd would refuse, so no training step can pass the
+  // forward and then fail in its backward
+  if (!q_str || !o_str) return CMPEXT3_E_INVALID;
+  if (!tile_offsets_fit(Sk, k_str[2], v_str[2]) || !tile_offsets_fit(Sq, q_str[2], o_str[2]))
+    return CMPEXT3_E_TOO_LARGE;
   return fwd_impl(q, k, v, o, lse, dtype, B, H, H_kv, Sq, Sk, D, q_str, k_str, v_str, o_str, mask,
                   mask_dtype, mask_str, scale, causal, stream);
 }

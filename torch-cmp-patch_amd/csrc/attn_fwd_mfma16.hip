@@ -77,7 +77,9 @@ hipError_t launch_mfma16(const FwdParams& p, bool bf16, bool causal, hipStream_t
   if (dk < 0) return hipErrorInvalidValue;
   if (short16_applies(p, dk, causal)) return launch_short16(p, dk, bf16, s);
   if (pipe16_applies(p, dk)) return launch_pipe16(p, dk, bf16, causal, use_prescale(p, bf16), s);
-  if (p.lse) return hipErrorNotSupported;  // the v2 kernel writes no log-sum-exp
+  // the v2 kernel has neither a log-sum-exp output nor mask code: refuse
+  // rather than run without them (the ABI rejects such calls earlier)
+  if (p.lse || p.mask_kind != MASK_NONE) return hipErrorNotSupported;
   if (bf16)
     return causal ? launch_bucket<__bf16, true, false>(p, dk, s)
                   : launch_bucket<__bf16, false, false>(p, dk, s);

@@ -8,10 +8,11 @@
 // workgroups and 32-key tiles; the waves per SIMD are the most the registers
 // allow without spilling (D = 32: 4, D <= 64: 3, D <= 128: 2).
 //
-// The key split (no counterpart in the reference) needs a small exchange
-// buffer per (device, stream), allocated on first use and kept for the life
-// of the process.  Where it cannot be had (a stream under graph capture, an
-// allocation failure, too many streams) the launch simply runs unsplit.
+// The key split (no counterpart in the reference) needs an exchange buffer
+// per (device, stream): 35.7 MB on 256 CUs, allocated on first use and kept
+// for the life of the process, for at most 16 streams per device (571 MB).
+// Where it cannot be had (a stream under graph capture, an allocation
+// failure, a 17th stream) the launch simply runs unsplit.
 #include <stdio.h>
 
 #include <map>
@@ -70,12 +71,23 @@ size_t exchange_ws_bytes(int cus) {
 }
 size_t exchange_cnt_bytes(int cus) { return (size_t)cus * kPipeNw * sizeof(int); }
 
+// The exchange buffer of (current device, stream s), allocated on first use.
+// A stream under graph capture never gets one, not even the buffer it already
+// owns: a captured launch would carry that buffer's address into every
+// replay, and a replay on another stream while s runs an eager split launch
+// would share its counters and partials.  Captured launches therefore run
+// unsplit, and nothing is allocated or cleared while a graph is recorded.
 bool exchange_for(hipStream_t s, int cus, Exchange& out) {
   static std::mutex mu;
   static std::map<std::pair<int, hipStream_t>, Exchange> cache;
   static int per_dev[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return false;
+  }
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
     (void)hipGetLastError();
     return false;
   }
@@ -87,11 +99,6 @@ bool exchange_for(hipStream_t s, int cus, Exchange& out) {
     return true;
   }
   if (per_dev[dev] >= kMaxStreams) return false;
-  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
-    (void)hipGetLastError();
-    return false;
-  }
   const size_t wsb = exchange_ws_bytes(cus), cb = exchange_cnt_bytes(cus);
   void* mem = nullptr;
   if (hipMalloc(&mem, wsb + cb) != hipSuccess) {

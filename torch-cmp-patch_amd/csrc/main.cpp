@@ -284,7 +284,11 @@ std::vector<torch::Tensor> attention_bwd(torch::Tensor query, torch::Tensor key,
     dv.zero_();
   } else {
     const torch::Tensor q = abi_layout(query, Dp), k = abi_layout(key, Dp), v = abi_layout(value, Dp);
-    const torch::Tensor o = abi_layout(out, Dp), g = abi_layout(grad_out, Dp);
+    // dO gets O's row stride limits (32-bit tile offsets); a gradient in an
+    // exotic layout is packed rather than refused
+    const torch::Tensor o = abi_layout(out, Dp);
+    torch::Tensor g = abi_layout(grad_out, Dp);
+    if ((Sq + 64) * std::max<int64_t>(g.stride(2), 1) * 2 >= INT32_MAX) g = g.contiguous();
     const torch::Tensor l = lse.contiguous();
     torch::Tensor delta = torch::empty({B, H, Sq}, query.options().dtype(at::kFloat));
     Mask mask;
