@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define CMPEXT3_ATTN_ABI_VERSION 5
+#define CMPEXT3_ATTN_ABI_VERSION 6
 
 /* dtype codes (CMPEXT3_DTYPE_BOOL: attention masks only) */
 #define CMPEXT3_DTYPE_F16  0
@@ -129,6 +129,30 @@ int cmpext3_attn_fwd_masked(const void* q, const void* k, const void* v, void* o
                             const int64_t v_str[3], const int64_t o_str[3],
                             const void* mask, int mask_dtype, const int64_t mask_str[3],
                             float scale, int causal, hipStream_t stream);
+
+/*
+ * Allocation-free forward: the arguments, results and return codes of
+ * cmpext3_attn_fwd_masked (mask_dtype -1 = no mask, H_kv == H = no grouping),
+ * but nothing is ever allocated or freed: key-split launches exchange their
+ * partial results through a fixed 16 MiB (+ 16 KiB of counters) array per
+ * device inside the library's code object instead of the per-stream buffer
+ * the other entry points allocate.  A split that would need more is cut to
+ * fewer key ranges (down to none), so no problem is refused for lack of
+ * room.  Every call on one device shares that device's array: calls that
+ * overlap in time on one device (two streams, or a graph replay beside an
+ * eager call) race and may mix results; calls in stream order do not.
+ * Launches may be captured into a HIP graph (the array's address is fixed).
+ *
+ * Reference: none.  No counterpart in the reference; it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * with a fixed memory budget, harnesses that forbid hipMalloc).
+ */
+int cmpext3_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* o,
+                             int dtype, int B, int H, int H_kv, int Sq, int Sk, int D,
+                             const int64_t q_str[3], const int64_t k_str[3],
+                             const int64_t v_str[3], const int64_t o_str[3],
+                             const void* mask, int mask_dtype, const int64_t mask_str[3],
+                             float scale, int causal, hipStream_t stream);
 
 /*
  * Training forward: as cmpext3_attn_fwd_masked (mask_dtype -1 = no mask), and

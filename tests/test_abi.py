@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version_and_messages():
-    assert abi.lib().cmpext3_attn_abi_version() == 5
+    assert abi.lib().cmpext3_attn_abi_version() == 6
     for code in range(10):
         assert abi.strerror(code) and abi.strerror(code) != "unknown error code"
     assert abi.strerror(99) == "unknown error code"

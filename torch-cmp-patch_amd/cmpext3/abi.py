@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcmpext3_
 
 # Every function include/cmpext3_attn.h declares.
 SYMBOLS = ("cmpext3_attn_fwd", "cmpext3_attn_fwd_gqa", "cmpext3_attn_fwd_masked",
-           "cmpext3_attn_fwd_lse", "cmpext3_attn_bwd",
+           "cmpext3_attn_fwd_noalloc", "cmpext3_attn_fwd_lse", "cmpext3_attn_bwd",
            "cmpext3_attn_strerror", "cmpext3_attn_abi_version", "cmpext3_attn_describe")
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_BOOL = 0, 1, 2, 3
@@ -43,6 +43,8 @@ def lib() -> ctypes.CDLL:
                                               i64p, i64p, i64p, i64p, vp, ci, i64p,
                                               ctypes.c_float, ci, vp]
         L.cmpext3_attn_fwd_masked.restype = ci
+        L.cmpext3_attn_fwd_noalloc.argtypes = L.cmpext3_attn_fwd_masked.argtypes
+        L.cmpext3_attn_fwd_noalloc.restype = ci
         L.cmpext3_attn_fwd_lse.argtypes = [vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci, ci,
                                            i64p, i64p, i64p, i64p, vp, ci, i64p, ctypes.c_float, ci, vp]
         L.cmpext3_attn_fwd_lse.restype = ci
@@ -128,6 +130,20 @@ def attn_fwd_raw(q, k, v, o, scale: float, causal: bool = False, stream=None,
         return lib().cmpext3_attn_fwd_gqa(*ptrs, dtype_code(q.dtype), B, H, k.shape[1], Sq,
                                           k.shape[2], Dx, *tail)
     return lib().cmpext3_attn_fwd(*ptrs, dtype_code(q.dtype), B, H, Sq, k.shape[2], Dx, *tail)
+
+
+def attn_fwd_noalloc_raw(q, k, v, o, scale: float, causal: bool = False, stream=None,
+                         attn_mask=None) -> int:
+    """Call cmpext3_attn_fwd_noalloc (the allocation-free forward) on
+    caller-allocated tensors; k/v may hold fewer heads than q.  Returns the C
+    return code."""
+    B, H, Sq, D = q.shape
+    mp, mdt, mst, _keep = _mask_args(attn_mask, B, H, Sq, k.shape[2])
+    vp = ctypes.c_void_p
+    return lib().cmpext3_attn_fwd_noalloc(
+        *(vp(t.data_ptr()) for t in (q, k, v, o)), dtype_code(q.dtype), B, H, k.shape[1], Sq,
+        k.shape[2], D, _strides(q), _strides(k), _strides(v), _strides(o), mp, mdt, mst,
+        ctypes.c_float(scale), int(causal), vp(_handle(q, stream)))
 
 
 def attn_fwd(q, k, v, scale: Optional[float] = None, causal: bool = False, stream=None,

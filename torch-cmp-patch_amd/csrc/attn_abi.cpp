@@ -163,7 +163,8 @@ bool tile_offsets_fit(int S, int64_t s0, int64_t s1) {
 int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, int dtype, int B, int H,
              int H_kv, int Sq, int Sk, int D, const int64_t q_str[3], const int64_t k_str[3],
              const int64_t v_str[3], const int64_t o_str[3], const void* mask, int mask_dtype,
-             const int64_t mask_str[3], float scale, int causal, hipStream_t stream) {
+             const int64_t mask_str[3], float scale, int causal, hipStream_t stream,
+             bool fixed_exchange = false) {
   int rc = check_shape(dtype, B, H, Sq, Sk, D);
   if (rc != CMPEXT3_OK) return rc;
   if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;
@@ -206,6 +207,7 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
   // exp2-domain multiplier; a negative scale is folded into Q's sign bits
   p.c = fabsf(scale) * cmpext3::kLog2e;
   p.q_sign = (scale < 0.f) ? (dtype == CMPEXT3_DTYPE_F32 ? 0x80000000u : 0x80008000u) : 0u;
+  p.fixed_exchange = fixed_exchange ? 1 : 0;
 
   hipError_t err;
   if (dtype == CMPEXT3_DTYPE_F32)
@@ -226,6 +228,15 @@ int cmpext3_attn_fwd_masked(const void* q, const void* k, const void* v, void* o
                             int causal, hipStream_t stream) {
   return fwd_impl(q, k, v, o, nullptr, dtype, B, H, H_kv, Sq, Sk, D, q_str, k_str, v_str, o_str, mask,
                   mask_dtype, mask_str, scale, causal, stream);
+}
+
+int cmpext3_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* o, int dtype, int B,
+                             int H, int H_kv, int Sq, int Sk, int D, const int64_t q_str[3],
+                             const int64_t k_str[3], const int64_t v_str[3], const int64_t o_str[3],
+                             const void* mask, int mask_dtype, const int64_t mask_str[3], float scale,
+                             int causal, hipStream_t stream) {
+  return fwd_impl(q, k, v, o, nullptr, dtype, B, H, H_kv, Sq, Sk, D, q_str, k_str, v_str, o_str, mask,
+                  mask_dtype, mask_str, scale, causal, stream, /*fixed_exchange=*/true);
 }
 
 int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, float* lse, int dtype,

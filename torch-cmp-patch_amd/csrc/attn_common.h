@@ -45,6 +45,9 @@ struct FwdParams {
   // whole group of query heads and q_g / o_g over one query head
   int pack_sq;
   int64_t q_g, o_g;
+  // host side only: the key split exchanges through the library's fixed
+  // per-device scratch instead of a per-stream allocated buffer
+  int fixed_exchange;
 };
 
 // attention-mask element kinds (FwdParams::mask_kind)

@@ -55,8 +55,11 @@ namespace cmpext3 {
 // puts the counter back to zero.  nparts == 1: no split, ws/cnt unused.
 struct SplitArgs {
   int nfull, nparts;
-  f32x4* ws;  // split blocks * nparts * NW * (DP / 8 + 1) * 64 float4
-  int* cnt;   // split blocks * NW counters, zero between launches
+  f32x4* ws;  // split blocks * nparts * nwl * (DP / 8 + 1) * 64 float4
+  int* cnt;   // split blocks * nwl counters, zero between launches
+  // waves per block that hold query rows (and so exchange): NW, or fewer
+  // when a single query block is shorter than the workgroup (decode)
+  int nwl;
 };
 
 // float4 vectors each lane leaves per part: its O fragments, then (m, l)
@@ -561,8 +564,9 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
     constexpr int NV = split_vectors(DP);
     static_assert(NV == NDB * 4 + 1, "O fragments + (m, l)");
     const int sb = lb - sa.nfull;
-    const __amdgpu_buffer_rsrc_t wsr = uniform_rsrc(sa.ws, (int64_t)(sb + 1) * nparts * NW * NV * 64 * 16);
-    auto voff = [&](int q, int k) { return ((((sb * nparts + q) * NW + wave) * NV + k) * 64 + lane) * 16; };
+    const int nwl = sa.nwl;  // waves past it hold no rows and left above
+    const __amdgpu_buffer_rsrc_t wsr = uniform_rsrc(sa.ws, (int64_t)(sb + 1) * nparts * nwl * NV * 64 * 16);
+    auto voff = [&](int q, int k) { return ((((sb * nparts + q) * nwl + wave) * NV + k) * 64 + lane) * 16; };
     // device-scope (aux 16 = sc1) 16-byte accesses; the builtins move dwords, so the
     // fp32 values go through explicit bit casts
     auto st_ws = [&](f32x4 x, int off) {
@@ -579,10 +583,10 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
     st_ws((f32x4){lsum > 0.f ? mb : -INFINITY, lsum, 0.f, 0.f}, voff(part, NDB * 4));
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     int old = 0;
-    if (lane == 0) old = __hip_atomic_fetch_add(sa.cnt + sb * NW + wave, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) old = __hip_atomic_fetch_add(sa.cnt + sb * nwl + wave, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     old = __builtin_amdgcn_readfirstlane(old);
     if (old != nparts - 1) return;
-    if (lane == 0) __hip_atomic_store(sa.cnt + sb * NW + wave, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) __hip_atomic_store(sa.cnt + sb * nwl + wave, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // Merge every part, this one included, from the exchange buffer in part
     // order: the same instructions on the same values whichever part arrives
     // last, so a rerun is bit-identical.

@@ -8,11 +8,13 @@
 // workgroups and 32-key tiles; the waves per SIMD are the most the registers
 // allow without spilling (D = 32: 4, D <= 64: 3, D <= 128: 2).
 //
-// The key split (no counterpart in the reference) needs an exchange buffer
-// per (device, stream): 35.7 MB on 256 CUs, allocated on first use and kept
-// for the life of the process, for at most 16 streams per device (571 MB).
-// Where it cannot be had (a stream under graph capture, an allocation
-// failure, a 17th stream) the launch simply runs unsplit.
+// The key split (no counterpart in the reference) needs an exchange buffer.
+// The ordinary entry points use one per (device, stream): 35.7 MB on 256 CUs,
+// allocated on first use and kept for the life of the process, for at most
+// 16 streams per device (571 MB).  Where it cannot be had (a stream under
+// graph capture, an allocation failure, a 17th stream) the launch simply runs
+// unsplit.  The allocation-free entry point uses a fixed per-device array in
+// this file instead (`scratch` below) and never allocates.
 #include <stdio.h>
 
 #include <map>
@@ -118,12 +120,80 @@ bool exchange_for(hipStream_t s, int cus, Exchange& out) {
   return true;
 }
 
+// ---- Exchange storage of the allocation-free entry point
+//
+// One fixed array per device in the library's code object, zero-filled when
+// the code object is loaded on a device and never allocated or freed by the
+// library: 16 MiB of partial (O, m, l) vectors, then one counter per (split
+// block, wave).  Every allocation-free call on a device shares it, so such
+// calls that overlap in time on one device (two streams, or a graph replay
+// beside an eager call) race; calls in stream order are safe, because each
+// merge puts its counter back to zero.  Host code never passes `scratch`
+// itself to a kernel (in host code the name is only a stand-in for the
+// device symbol): the device address comes from hipGetSymbolAddress, once
+// per device.
+constexpr size_t kScratchWsBytes = size_t(16) << 20;
+constexpr int kScratchCounters = 4096;
+constexpr size_t kScratchBytes = kScratchWsBytes + kScratchCounters * sizeof(int);
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+__global__ void zero_ints(int* __restrict__ x, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = 0;
+}
+
+struct ScratchSlot {
+  std::once_flag once;
+  void* ptr = nullptr;  // device address of `scratch` on this device
+};
+
+// This device's scratch, resolved on the first call with the device current.
+// The counters are cleared then by a fill kernel on the caller's stream (a
+// kernel node, not a memset node, if that first call is being captured); the
+// code object's zero fill already covers every later case.
+bool scratch_for(hipStream_t s, Exchange& out) {
+  static ScratchSlot slots[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return false;
+  }
+  ScratchSlot& sl = slots[dev];
+  std::call_once(sl.once, [&] {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) {
+      (void)hipGetLastError();
+      return;
+    }
+    int* cnt = (int*)((char*)ptr + kScratchWsBytes);
+    hipLaunchKernelGGL(zero_ints, dim3((kScratchCounters + 255) / 256), dim3(256), 0, s, cnt, kScratchCounters);
+    if (hipGetLastError() != hipSuccess) return;
+    sl.ptr = ptr;
+  });
+  if (!sl.ptr) return false;
+  out.ws = (f32x4*)sl.ptr;
+  out.cnt = (int*)((char*)sl.ptr + kScratchWsBytes);
+  return true;
+}
+
+// Waves per block that hold query rows: all of them unless the launch is a
+// single block shorter than the workgroup (decode, packed grouped-query rows).
+int exchange_waves(int n_qblk, int Sq) {
+  return n_qblk > 1 ? kPipeNw : (Sq + 31) / 32 < kPipeNw ? (Sq + 31) / 32 : kPipeNw;
+}
+
+// Exchange bytes of a plan: one 1 KiB vector per lane-set, split_vectors per
+// (split block, part, exchanging wave).
+size_t plan_ws_bytes(const SplitArgs& sa, int n, int dp) {
+  return (size_t)(n - sa.nfull) * sa.nparts * sa.nwl * split_vectors(dp) * 64 * sizeof(f32x4);
+}
+
 // Which blocks run whole and how the rest are cut.  n blocks on `cus` CUs at
 // `occ` workgroups per CU; the dispatcher hands workgroup i to CU i mod cus
 // while all of them fit, so after the whole rounds each CU takes exactly one
 // part.  Causal launches keep their longest-first order and never split.
 SplitArgs split_plan(int n, int ntiles, int occ, int cus, bool causal) {
-  SplitArgs sa = {n, 1, nullptr, nullptr};
+  SplitArgs sa = {n, 1, nullptr, nullptr, kPipeNw};
   if (causal || cus <= 0) return sa;
   const int full = n / cus, rem = n - full * cus;
   if (rem == 0 || full + 1 > occ) return sa;  // whole rounds, or more than fits at once
@@ -243,14 +313,34 @@ hipError_t launch_pipe16(const FwdParams& p0, int dk0, bool bf16, bool causal, b
   if (!prescale && p.c == 0.f) p.c = 1e-30f;
   const int cus = device_cus();
   const int occ = p.mask_kind != MASK_NONE ? pipe_occ_masked(dk) : pipe_occ(dk);
-  SplitArgs sa = split_plan(n_blocks(p.B, p.H, p.Sq), n_key_tiles(p.Sk), occ, cus, causal);
-  if (sa.nparts > 1) {
+  const int n = n_blocks(p.B, p.H, p.Sq);
+  SplitArgs sa = split_plan(n, n_key_tiles(p.Sk), occ, cus, causal);
+  sa.nwl = exchange_waves((p.Sq + kPipeNw * 32 - 1) / (kPipeNw * 32), p.Sq);
+  const SplitArgs whole = {n, 1, nullptr, nullptr, sa.nwl};
+  if (sa.nparts > 1 && p.fixed_exchange) {
+    // Allocation-free call: cut the plan to what the fixed scratch holds (an
+    // unsplit launch needs none of it, so no problem is ever refused for it).
+    const int dp = (dk + 31) / 32 * 32;
+    const int nsplit = n - sa.nfull;
+    const size_t per_part = (size_t)nsplit * sa.nwl * split_vectors(dp) * 64 * sizeof(f32x4);
+    const int fit = (int64_t)nsplit * sa.nwl > kScratchCounters ? 0 : (int)(kScratchWsBytes / per_part);
+    if (sa.nparts > fit) sa.nparts = fit;
+    if (sa.nparts < 2) {
+      sa = whole;
+    } else {
+      Exchange e;
+      if (!scratch_for(s, e)) return hipErrorNotInitialized;
+      if (plan_ws_bytes(sa, n, dp) > kScratchWsBytes) return hipErrorInvalidValue;
+      sa.ws = e.ws;
+      sa.cnt = e.cnt;
+    }
+  } else if (sa.nparts > 1) {
     Exchange e;
     if (exchange_for(s, cus, e)) {
       sa.ws = e.ws;
       sa.cnt = e.cnt;
     } else {
-      sa = SplitArgs{n_blocks(p.B, p.H, p.Sq), 1, nullptr, nullptr};
+      sa = whole;
     }
   }
   if (p.lse) {  // training forward, masked or not
