@@ -15,8 +15,12 @@ line.
                from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
                (null if absent)
   cpu_baseline stock torch SDPA on the host CPU (what the reference runs for CPU
-               tensors), same workload and dtype, bounded to ~10 s
-  configs      the same kernel timing for every BASELINE config (informational)
+               tensors), same workload and dtype, bounded to ~10 s; with the
+               host's CPU model, torch version and thread counts
+  configs      every BASELINE config: the same kernel timing, stock torch SDPA
+               on the host CPU in the config's dtype (time, TFLOP/s, GPU
+               speedup), and the GPU output's max abs error against torch's CPU
+               math SDPA on fp32-upcast inputs, with the north-star tolerance
 
 --backward times a training step instead: the forward that keeps the row
 log-sum-exp plus the backward (Delta, dK/dV and dQ kernels), FLOPs counted as
@@ -87,6 +91,63 @@ def time_kernel(fn, steps: int, warmup: int):
     return wall, dev
 
 
+def host_info() -> dict:
+    """The host the CPU baseline ran on: CPU model (lscpu "Model name"), the
+    torch version, and the thread count torch uses."""
+    import subprocess
+    import torch
+    model = None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.split(":")[0].strip() == "Model name":
+                model = line.split(":", 1)[1].strip()
+                break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    if model is None:
+        try:
+            with open("/proc/cpuinfo") as f:
+                for line in f:
+                    if line.startswith("model name"):
+                        model = line.split(":", 1)[1].strip()
+                        break
+        except OSError:
+            pass
+    return {"cpu_model": model, "torch_version": torch.__version__,
+            "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads()}
+
+
+def config_cpu_and_error(wl, out_gpu, budget_s: float = 4.0) -> dict:
+    """Per-config CPU figures: stock torch SDPA on the
+    host CPU in the config's own dtype (1 warmup + timed calls, ~budget_s),
+    and the GPU output's max abs error against torch's CPU math SDPA on the
+    fp32-upcast inputs (BASELINE.md section 2's reference)."""
+    import torch
+    import torch.nn.functional as F
+    torch.set_num_threads(os.cpu_count() or 1)
+    q, k, v = wl.make_inputs("cpu")
+    gqa = wl.kv_heads != wl.H
+    call = lambda a, b, c: F.scaled_dot_product_attention(  # noqa: E731
+        a, b, c, is_causal=wl.causal, scale=wl.eff_scale, enable_gqa=gqa)
+    t0 = time.perf_counter()
+    call(q, k, v)
+    one = time.perf_counter() - t0
+    n = max(1, min(10, int(budget_s / max(one, 1e-3))))
+    t0 = time.perf_counter()
+    for _ in range(n):
+        call(q, k, v)
+    dt = (time.perf_counter() - t0) / n
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    with sdpa_kernel(SDPBackend.MATH):
+        ref = call(q.float(), k.float(), v.float())
+    err = float((out_gpu.float().cpu() - ref).abs().max())
+    tol = {"fp16": 1e-2, "bf16": 2e-2, "fp32": 1e-4}[wl.dtype]
+    return {"cpu_ms": round(dt * 1e3, 3), "cpu_tflops": round(wl.flops() / dt / 1e12, 5),
+            "cpu_calls": n, "max_abs_err_vs_cpu_fp32_math": err, "tolerance": tol,
+            "within_tolerance": err <= tol}
+
+
 def cpu_baseline(wl, budget_s: float = 10.0):
     import torch
     import torch.nn.functional as F
@@ -111,6 +172,7 @@ def cpu_baseline(wl, budget_s: float = 10.0):
                    f"(the reference's path for CPU inputs), full {wl.name} workload "
                    f"{list(wl.shapes()[0])} {wl.dtype}, 1 warmup + {n} timed calls, "
                    f"{dt * 1e3:.1f} ms/call, os.cpu_count()={os.cpu_count()}"),
+        **host_info(),
     }
 
 
@@ -272,13 +334,19 @@ def main() -> int:
             qo, ko, vo = other.make_inputs("cuda")
             f2 = lambda: cmpext3.ops.attention(qo, ko, vo, other.eff_scale, other.causal)  # noqa
             _, d2 = time_kernel(f2, 20, 5)
-            configs[other.name] = {
+            entry = {
                 "us_per_launch": round(d2 * 1e6, 2),
                 "tflops": round(other.flops() / d2 / 1e12, 2),
                 "pct_fp16_mfma_peak": round(100 * other.flops() / d2 / 1e12 / 2516.6, 2),
                 "pct_dtype_peak": round(100 * other.flops() / d2 / 1e12 / W.PEAK_TFLOPS[other.dtype], 2),
                 "hbm_gbs_algorithmic": round(other.bytes() / d2 / 1e9, 1),
             }
+            if not args.no_cpu_baseline:
+                out = f2()
+                torch.cuda.synchronize()
+                entry.update(config_cpu_and_error(other, out))
+                entry["gpu_speedup_vs_cpu"] = round(entry["cpu_ms"] / (d2 * 1e3), 1)
+            configs[other.name] = entry
             del qo, ko, vo
 
     line = {

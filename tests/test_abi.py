@@ -84,6 +84,13 @@ def test_describe_key_split_plan():
     bf16 = abi.DTYPE_BF16
     assert "key-split: 0 whole + 128 x 4 parts" in abi.describe(bf16, 16, 8, 2, 4096, 128)[1]
     assert "key-split: 0 whole + 200 x 2 parts" in abi.describe(f16, 1, 200, 100, 4096, 64)[1]
+    # fp32: 64-row blocks, split only with fewer blocks than CUs (about two
+    # parts per CU, at least 4 tiles of 32 keys each), never causal
+    f32 = abi.DTYPE_F32
+    assert "key-split: 128 x 4 parts" in abi.describe(f32, 1, 8, 1024, 1024, 64)[1]
+    assert "key-split" not in abi.describe(f32, 1, 8, 1024, 1024, 64, True)[1]
+    assert "key-split" not in abi.describe(f32, 2, 8, 4096, 4096, 40)[1]
+    assert "key-split: 4 x 5 parts" in abi.describe(f32, 1, 2, 100, 700, 40)[1]
 
 
 def _call(q=16, k=16, v=16, o=16, dtype=abi.DTYPE_F16, B=1, H=1, Sq=8, Sk=8, D=64,

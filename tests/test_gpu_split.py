@@ -125,6 +125,37 @@ def test_fewer_blocks_than_cus_take_two_parts_per_cu():
     _check(q, k, v, 128 ** -0.5, False, "bf16")
 
 
+# fp32 key split: fewer query blocks (64 rows) than CUs, non-causal
+SPLIT32 = [
+    # B, H, Sq, Sk, D
+    (1, 8, 1024, 1024, 64),   # 128 blocks, 4 parts of 8 tiles
+    (1, 2, 100, 700, 40),     # 4 ragged blocks, parts of 4-5 tiles (odd counts), D = 40
+    (1, 1, 20, 2000, 64),     # one short block: only 2 waves hold rows and exchange
+    (1, 3, 64, 777, 96),      # D below its bucket, ragged Sk
+]
+
+
+@pytest.mark.parametrize("case", SPLIT32, ids=[f"fp32-B{c[0]}H{c[1]}-q{c[2]}k{c[3]}d{c[4]}" for c in SPLIT32])
+def test_split_parity_fp32(case):
+    B, H, Sq, Sk, D = case
+    q, k, v = _inputs("fp32", B, H, Sq, Sk, D, seed=Sq + Sk + D)
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert "key-split" in _split_text(q, B, H, Sq, Sk, D), _split_text(q, B, H, Sq, Sk, D)
+    out = _check(q, k, v, 1.0 / math.sqrt(D), False, "fp32")
+    # every part merges in part order: a rerun is bit-identical
+    assert torch.equal(out, _check(q, k, v, 1.0 / math.sqrt(D), False, "fp32"))
+
+
+def test_split_fp32_wide_scores_and_causal_unsplit():
+    """Scores over tens of log2 units (each part settles on its own offset),
+    and causal fp32 launches, which never split."""
+    q, k, v = _inputs("fp32", 1, 2, 128, 1500, 64, seed=31)
+    q = q * 6
+    _check(q, k, v, 0.125, False, "fp32")
+    assert "key-split" not in _split_text(q, 1, 2, 128, 1500, 64, causal=True)
+    _check(q, k, v, 0.125, True, "fp32")
+
+
 def _replays(g, out, reps=4):
     """Replay a captured graph with eager work (and a sync) between replays."""
     results = []

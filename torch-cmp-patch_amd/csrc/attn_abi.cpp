@@ -23,7 +23,7 @@ hipError_t launch_mfma32(const FwdParams& p, bool causal, hipStream_t s);
 int mfma16_bucket(int D);
 int mfma32_bucket(int D);
 void describe_mfma16(int D, int B, int H, int Sq, int Sk, bool causal, char* buf, int len);
-void describe_mfma32(int D, int Sq, char* buf, int len);
+void describe_mfma32(int D, int B, int H, int Sq, int Sk, bool causal, char* buf, int len);
 }  // namespace cmpext3
 
 namespace {
@@ -123,7 +123,7 @@ int cmpext3_attn_describe(int dtype, int B, int H, int Sq, int Sk, int D, int ca
     } else {
       char kb[224];
       if (dtype == CMPEXT3_DTYPE_F32)
-        cmpext3::describe_mfma32(D, Sq, kb, sizeof kb);
+        cmpext3::describe_mfma32(D, B, H, Sq, Sk, causal != 0, kb, sizeof kb);
       else
         cmpext3::describe_mfma16(D, B, H, Sq, Sk, causal != 0, kb, sizeof kb);
       snprintf(buf, len, "%s%s", kb, causal ? " causal" : "");

@@ -50,6 +50,9 @@ struct FwdParams {
   int fixed_exchange;
 };
 
+// Compute units of the current device (host side; 256 on MI355X).
+int device_cus();
+
 // attention-mask element kinds (FwdParams::mask_kind)
 constexpr int MASK_NONE = -1;
 constexpr int MASK_F16 = 0;   // additive, fp16
@@ -120,6 +123,43 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // compiler from moving LDS accesses across it.
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Key split of the last query blocks: workgroups [0, nfull) take whole
+// blocks; the next (n_blocks - nfull) * nparts take one key range each of the
+// remaining blocks.  Per (split block, wave) the parts leave their partial O,
+// offset and row sum in ws; the last to arrive (counter in cnt) merges and
+// puts the counter back to zero.  nparts == 1: no split, ws/cnt unused.
+struct SplitArgs {
+  int nfull, nparts;
+  f32x4* ws;  // split blocks * nparts * nwl * (float4 vectors per lane) * 64 float4
+  int* cnt;   // split blocks * nwl counters, zero between launches
+  // waves per block that hold query rows (and so exchange): NW, or fewer
+  // when a single query block is shorter than the workgroup (decode)
+  int nwl;
+};
+
+// float4 vectors each lane of the fp16/bf16 kernels leaves per part: its O
+// fragments, then (m, l)
+constexpr int split_vectors(int dp) { return dp / 8 + 1; }
+
+// Exchange space for a key split (host side, attn_fwd_pipe16.hip): at least
+// ws_bytes of partials and ncnt zeroed counters, from the library's fixed
+// per-device scratch (fixed != 0: the allocation-free entry point) or from the
+// stream's allocated buffer.  False when none is available (a stream under
+// graph capture, a failed allocation, a plan larger than the space): the
+// caller then launches unsplit.
+bool split_exchange(hipStream_t s, bool fixed, size_t ws_bytes, int ncnt, f32x4** ws, int** cnt);
+
+// Raw buffer resource over [base, base + bytes) (gfx9 dword3: 32-bit raw
+// reads).  The fields go through readfirstlane so that the compiler keeps the
+// descriptor in SGPRs instead of wrapping every load in a waterfall loop.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base, int64_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  const int n = __builtin_amdgcn_readfirstlane((int)bytes);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, n, 0x00020000);
 }
 
 }  // namespace cmpext3

@@ -11,6 +11,13 @@
 // V stays row-major in LDS: a PV A-operand element is V[key][d] with d along
 // the 16 lanes of a group, which is a conflict-free LDS read.
 //
+// Key split (non-causal launches with fewer query blocks than CUs, such as
+// [1, 8, 1024, 64]): each block's key range is cut into parts run by separate
+// workgroups, which shortens every wave's dependency chain over the keys and
+// fills the idle CUs.  Every part leaves its fp32 (O, m, l) in the exchange
+// buffer; the last part of a (block, wave) to finish merges all of them in
+// part order and writes the output (the protocol of attn_fwd_pipe16.h).
+//
 // Reference: src/cuda/fp32_attention.cu:35-198 (one thread per query row,
 // serial D loops, non-causal only, Sq == Sk only, D <= 128, and 1/l taken
 // through an fp16 reciprocal at :179-180).  This kernel drops every one of
@@ -27,7 +34,7 @@ __device__ __forceinline__ f32x4 mma32(float a, float b, f32x4 c) {
 // blocks per wave.
 template <int DK, int NW, int NQB, int BK, bool CAUSAL>
 __global__ void __launch_bounds__(NW * 64)
-attn_fwd_mfma32(const FwdParams p) {
+attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
   constexpr int NT = NW * 64;
   constexpr int QPW = 16 * NQB;
   constexpr int BQ = NW * QPW;
@@ -53,8 +60,15 @@ attn_fwd_mfma32(const FwdParams p) {
   const int l16 = lane & 15;
   const int g = lane >> 4;
 
+  int lb = blockIdx.x, part = 0, nparts = 1;
+  if (lb >= sa.nfull) {
+    const int r = lb - sa.nfull;
+    nparts = sa.nparts;
+    lb = sa.nfull + r / nparts;
+    part = r - (lb - sa.nfull) * nparts;
+  }
   int bh, qblk;
-  wg_tile(blockIdx.x, p, CAUSAL, bh, qblk);
+  wg_tile(lb, p, CAUSAL, bh, qblk);
   const int b = bh / p.H;
   const int h = bh - b * p.H;
   const int q0 = qblk * BQ;
@@ -69,7 +83,10 @@ attn_fwd_mfma32(const FwdParams p) {
 
   int kend = Sk;
   if (CAUSAL) kend = min(Sk, q0 + BQ);
-  const int ntiles = (kend + BK - 1) / BK;
+  // this workgroup's key tiles [tbase, tbase + ntiles) (causal launches never split)
+  const int ntall = (kend + BK - 1) / BK;
+  const int tbase = part * ntall / nparts;
+  const int ntiles = (part + 1) * ntall / nparts - tbase;
 
   // Q^T as the B operand: lane (l16, g) holds Q[row][4s + g]
   float qf[NQB][NKS];
@@ -99,7 +116,7 @@ attn_fwd_mfma32(const FwdParams p) {
 
   u32x4 kreg[KLD], vreg[VLD];
   auto load_tile = [&](int t) {
-    const int k0 = t * BK;
+    const int k0 = (tbase + t) * BK;
 #pragma unroll
     for (int it = 0; it < KLD; ++it) {
       const int ci = it * NT + tid;
@@ -148,7 +165,7 @@ attn_fwd_mfma32(const FwdParams p) {
     __syncthreads();
     if (t + 1 < ntiles) load_tile(t + 1);
 
-    const int k0 = t * BK;
+    const int k0 = (tbase + t) * BK;
     const bool active = !CAUSAL || k0 <= qw0 + QPW - 1;
     if (active) {
       const float* ks = lds + buf * (KTILE + VTILE);
@@ -231,12 +248,71 @@ attn_fwd_mfma32(const FwdParams p) {
     }
   }
 
+  // full row sums (each lane summed its own keys)
+  float lrow[NQB];
 #pragma unroll
   for (int qb = 0; qb < NQB; ++qb) {
     float l = l_run[qb];
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
-    const float inv = 1.f / l;
+    lrow[qb] = l;
+  }
+  if (!CAUSAL && nparts > 1) {
+    // a wave whose rows all lie past Sq has nothing to exchange; every part
+    // of the block agrees on that
+    if (qw0 >= Sq) return;
+    // Leave this part's state, then let the last part of the block merge
+    // (device-scope (aux 16 = sc1) 16-byte accesses, coherent across the
+    // XCDs' L2s; fp32 goes through bit casts because the builtins move dwords)
+    constexpr int NV = NQB * (NDB + 1);
+    const int sb = lb - sa.nfull, nwl = sa.nwl;
+    const __amdgpu_buffer_rsrc_t wsr = uniform_rsrc(sa.ws, (int64_t)(sb + 1) * nparts * nwl * NV * 64 * 16);
+    auto voff = [&](int q, int k) { return ((((sb * nparts + q) * nwl + wave) * NV + k) * 64 + lane) * 16; };
+    auto st_ws = [&](f32x4 x, int off) {
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), wsr, off, 0, 16);
+    };
+    auto ld_ws = [&](int off) { return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wsr, off, 0, 16)); };
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) st_ws(oacc[qb][db], voff(part, qb * (NDB + 1) + db));
+      // a row whose keys of this part are all masked holds nothing: offset -inf
+      st_ws((f32x4){lrow[qb] > 0.f ? m_run[qb] : -INFINITY, lrow[qb], 0.f, 0.f}, voff(part, qb * (NDB + 1) + NDB));
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    int old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(sa.cnt + sb * nwl + wave, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old != nparts - 1) return;
+    if (lane == 0) __hip_atomic_store(sa.cnt + sb * nwl + wave, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // merge every part, this one included, in part order: the same
+    // instructions on the same values whichever part arrives last
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+      float mt = -INFINITY;
+      for (int q = 0; q < nparts; ++q) mt = fmaxf(mt, ld_ws(voff(q, qb * (NDB + 1) + NDB))[0]);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) oacc[qb][db] = (f32x4){};
+      float l = 0.f;
+      for (int q = 0; q < nparts; ++q) {
+        const f32x4 ml = ld_ws(voff(q, qb * (NDB + 1) + NDB));
+        const float a = ml[0] == -INFINITY ? 0.f : fast_exp2(ml[0] - mt);
+        l = __builtin_fmaf(ml[1], a, l);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const f32x4 x = ld_ws(voff(q, qb * (NDB + 1) + db));
+#pragma unroll
+          for (int i = 0; i < 4; ++i) oacc[qb][db][i] = __builtin_fmaf(x[i], a, oacc[qb][db][i]);
+        }
+      }
+      lrow[qb] = l;
+    }
+  }
+
+#pragma unroll
+  for (int qb = 0; qb < NQB; ++qb) {
+    // a row that saw no key at all gives zeros, as torch does
+    const float inv = lrow[qb] > 0.f ? 1.f / lrow[qb] : 0.f;
     const int qrow = qw0 + 16 * qb + l16;
     if (qrow < Sq) {
       float* orow = og + (int64_t)qrow * p.o_s;
@@ -249,6 +325,11 @@ attn_fwd_mfma32(const FwdParams p) {
   }
 }
 
+// Key split plan: only when the query blocks leave CUs idle (fewer blocks than
+// CUs), non-causal, into enough parts for about two workgroups per CU, each
+// part at least kMinTiles32 key tiles long.
+constexpr int kMinTiles32 = 4;
+
 template <int DK, bool CAUSAL>
 hipError_t launch_mfma32_inst(const FwdParams& p0, hipStream_t stream) {
   // One 16-row query block per wave: measured on MI355X, two per wave only
@@ -259,12 +340,30 @@ hipError_t launch_mfma32_inst(const FwdParams& p0, hipStream_t stream) {
   constexpr int NQB = 1;
   constexpr int BK = (DK <= 128) ? 32 : 16;
   constexpr int BQ = NW * 16 * NQB;
+  constexpr int NDB = (DK + 15) / 16;
   FwdParams p = p0;
   p.n_qblk = (p.Sq + BQ - 1) / BQ;
   p.n_wg = p.B * p.H * p.n_qblk;
   if (p.n_wg == 0) return hipSuccess;
-  hipLaunchKernelGGL((attn_fwd_mfma32<DK, NW, NQB, BK, CAUSAL>), dim3(p.n_wg), dim3(NW * 64), 0,
-                     stream, p);
+  const int n = p.n_wg;
+  // waves per block that hold query rows (a single block shorter than BQ has fewer)
+  const int nwl = p.n_qblk > 1 ? NW : (p.Sq + 15) / 16 < NW ? (p.Sq + 15) / 16 : NW;
+  SplitArgs sa = {n, 1, nullptr, nullptr, nwl};
+  const int cus = device_cus();
+  if (!CAUSAL && n < cus) {
+    int parts = 2 * cus / n;
+    const int ntiles = (p.Sk + BK - 1) / BK;
+    if (parts > ntiles / kMinTiles32) parts = ntiles / kMinTiles32;
+    if (parts >= 2) {
+      const size_t ws_bytes = (size_t)n * parts * nwl * NQB * (NDB + 1) * 64 * sizeof(f32x4);
+      f32x4* ws = nullptr;
+      int* cnt = nullptr;
+      if (split_exchange(stream, p.fixed_exchange != 0, ws_bytes, n * nwl, &ws, &cnt))
+        sa = SplitArgs{0, parts, ws, cnt, nwl};
+    }
+  }
+  const int nwg = sa.nfull + (n - sa.nfull) * sa.nparts;
+  hipLaunchKernelGGL((attn_fwd_mfma32<DK, NW, NQB, BK, CAUSAL>), dim3(nwg), dim3(NW * 64), 0, stream, p, sa);
   return hipGetLastError();
 }
 
@@ -300,11 +399,19 @@ hipError_t launch_mfma32(const FwdParams& p, bool causal, hipStream_t s) {
   return causal ? launch_mfma32_dk<true>(p, dk, s) : launch_mfma32_dk<false>(p, dk, s);
 }
 
-void describe_mfma32(int D, int Sq, char* buf, int len) {
+void describe_mfma32(int D, int B, int H, int Sq, int Sk, bool causal, char* buf, int len) {
   const int dk = mfma32_bucket(D);
-  const int bq = 64;
-  snprintf(buf, len, "mfma32 16x16x4f32 S^T-form: DK=%d DPV=%d waves=4 BQ=%d BK=%d qblocks=%d", dk,
-           (dk + 15) / 16 * 16, bq, dk <= 128 ? 32 : 16, (Sq + bq - 1) / bq);
+  const int bq = 64, bk = dk <= 128 ? 32 : 16;
+  const int n = B * H * ((Sq + bq - 1) / bq), cus = device_cus();
+  int parts = 1;
+  if (!causal && n > 0 && n < cus) {
+    parts = 2 * cus / n;
+    if (parts > (Sk + bk - 1) / bk / kMinTiles32) parts = (Sk + bk - 1) / bk / kMinTiles32;
+  }
+  char split[48] = "";
+  if (parts >= 2) snprintf(split, sizeof split, " key-split: %d x %d parts", n, parts);
+  snprintf(buf, len, "mfma32 16x16x4f32 S^T-form: DK=%d DPV=%d waves=4 BQ=%d BK=%d qblocks=%d%s", dk,
+           (dk + 15) / 16 * 16, bq, bk, (Sq + bq - 1) / bq, split);
 }
 
 }  // namespace cmpext3

@@ -48,34 +48,6 @@
 
 namespace cmpext3 {
 
-// Key split of the last query blocks: workgroups [0, nfull) take whole
-// blocks; the next (n_blocks - nfull) * nparts take one key range each of the
-// remaining blocks.  Per (split block, wave) the parts leave their partial O,
-// offset and row sum in ws; the last to arrive (counter in cnt) merges and
-// puts the counter back to zero.  nparts == 1: no split, ws/cnt unused.
-struct SplitArgs {
-  int nfull, nparts;
-  f32x4* ws;  // split blocks * nparts * nwl * (DP / 8 + 1) * 64 float4
-  int* cnt;   // split blocks * nwl counters, zero between launches
-  // waves per block that hold query rows (and so exchange): NW, or fewer
-  // when a single query block is shorter than the workgroup (decode)
-  int nwl;
-};
-
-// float4 vectors each lane leaves per part: its O fragments, then (m, l)
-constexpr int split_vectors(int dp) { return dp / 8 + 1; }
-
-// Raw buffer resource over [base, base + bytes) (gfx9 dword3: 32-bit raw
-// reads).  The fields go through readfirstlane so that the compiler keeps the
-// descriptor in SGPRs instead of wrapping every load in a waterfall loop.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base, int64_t bytes) {
-  const uint64_t a = (uint64_t)base;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
-  const int n = __builtin_amdgcn_readfirstlane((int)bytes);
-  return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, n, 0x00020000);
-}
-
 // OPT bit 0: s_setprio(1) around the MFMA-heavy block.  OPT bit 1: unpadded
 // XOR-swizzled LDS rows (DK == DP in {32, 64, 128}).  OPT bit 2: leave the
 // interleave to the compiler (no sched_barrier fences).  OPT bit 3: the head
@@ -300,13 +272,17 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
     const int k0 = (tbase + j) * BK;
     return (k0 + BK > kpe) || (CAUSAL && k0 + BK - 1 > qlo);
   };
+  // The lane's key base is laundered through an empty asm inside the (rarely
+  // taken) branch: written plainly, the compiler hoists the 16 per-element key
+  // computations out of the branch and every tile pays for them.
   auto mask = [&](int j, f32x16 (&sc)[NKB]) {
-    const int k0 = (tbase + j) * BK;
+    int k0 = (tbase + j) * BK + 8 * hh;
+    asm volatile("" : "+v"(k0));
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int key = k0 + 32 * kb + acc_key(r, hh);
+        const int key = k0 + 32 * kb + acc_key(r, 0);
         if (key >= kpe || (CAUSAL && key > qrow)) sc[kb][r] = -INFINITY;
       }
   };

@@ -40,24 +40,6 @@ constexpr int kMinPartTiles = 8;
 constexpr int kMaxStreams = 16;
 constexpr int kMi355xCus = 256;  // used by describe() when no device is visible
 
-int device_cus() {
-  static int cus[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
-    (void)hipGetLastError();
-    return kMi355xCus;
-  }
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
-      (void)hipGetLastError();
-      return kMi355xCus;
-    }
-    cus[dev] = n;
-  }
-  return cus[dev];
-}
-
 // Exchange buffer sized for the largest plan on this device: at most
 // kMaxPartsPerCu parts per CU (split blocks * parts <= kMaxPartsPerCu * CUs),
 // kPipeNw waves, DP <= 128.
@@ -259,6 +241,40 @@ int n_blocks(int B, int H, int Sq) { return B * H * ((Sq + kPipeNw * 32 - 1) / (
 int n_key_tiles(int Sk) { return (Sk + kPipeBk - 1) / kPipeBk; }
 
 }  // namespace
+
+// Compute units of the current device (256 on MI355X), cached per device.
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return kMi355xCus;
+  }
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+      (void)hipGetLastError();
+      return kMi355xCus;
+    }
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+bool split_exchange(hipStream_t s, bool fixed, size_t ws_bytes, int ncnt, f32x4** ws, int** cnt) {
+  Exchange e;
+  if (fixed) {
+    if (ws_bytes > kScratchWsBytes || ncnt > kScratchCounters || !scratch_for(s, e)) return false;
+  } else {
+    const int cus = device_cus();
+    if (ws_bytes > exchange_ws_bytes(cus) || (size_t)ncnt * sizeof(int) > exchange_cnt_bytes(cus) ||
+        !exchange_for(s, cus, e))
+      return false;
+  }
+  *ws = e.ws;
+  *cnt = e.cnt;
+  return true;
+}
 
 // True when the pipelined kernel takes this problem: head-dim bucket <= 128,
 // a key sweep long enough for its prologue (four tiles in flight) to pay off
