@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define CMPEXT3_ATTN_ABI_VERSION 6
+#define CMPEXT3_ATTN_ABI_VERSION 7
 
 /* dtype codes (CMPEXT3_DTYPE_BOOL: attention masks only) */
 #define CMPEXT3_DTYPE_F16  0
@@ -50,8 +50,8 @@ extern "C" {
 #define CMPEXT3_OK                 0
 #define CMPEXT3_E_INVALID          1  /* null pointer, negative size, bad stride */
 #define CMPEXT3_E_DTYPE            2  /* dtype code not one of the above */
-#define CMPEXT3_E_HEAD_DIM         3  /* D outside 1..256 or not a multiple of 8 (f16/bf16) / 4 (f32) */
-#define CMPEXT3_E_ALIGN            4  /* a base pointer or a row stride is not 16-byte aligned */
+#define CMPEXT3_E_HEAD_DIM         3  /* D outside 1..256; masked/training calls: D not a multiple of 8 (f16/bf16) / 4 (f32) */
+#define CMPEXT3_E_ALIGN            4  /* a pointer not element-aligned; masked/training calls: base pointer or row stride not 16-byte aligned */
 #define CMPEXT3_E_EMPTY_KEYS       5  /* Sk == 0 with Sq > 0: softmax over nothing */
 #define CMPEXT3_E_LAUNCH           6  /* the HIP launch itself failed */
 #define CMPEXT3_E_TOO_LARGE        7  /* a size does not fit the kernel's index arithmetic */
@@ -62,7 +62,15 @@ extern "C" {
  * Fused attention forward.
  *
  *   q : [B, H, Sq, D]   k, v : [B, H, Sk, D]   o : [B, H, Sq, D]  (all `dtype`)
- *   *_str[3] : element strides of dims {0, 1, 2}; dim 3 has stride 1.
+ *   *_str[3] : element strides of dims {0, 1, 2} (>= 0); dim 3 has stride 1.
+ *   D        : any head dim 1..256.  Pointers need only element alignment:
+ *              rows of whole 16-byte chunks with 16-byte aligned base
+ *              pointers and strides run the vector-load kernels; any other
+ *              layout (odd D, a 2-byte offset view, BSHD views of such
+ *              heads) runs element-granular variants of the same kernels in
+ *              place, with no copy (calls that pass a mask, and the
+ *              training entry points, still need whole 16-byte aligned
+ *              chunks: CMPEXT3_E_HEAD_DIM / CMPEXT3_E_ALIGN otherwise).
  *   scale    : multiplier of Q K^T (any finite value, 0 and negative allowed).
  *   causal   : non-zero -> key j is visible to query i iff j <= i
  *              (top-left aligned, the torch `is_causal` convention also for

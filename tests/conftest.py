@@ -117,6 +117,25 @@ def patched():
         cmpext3.disable()
 
 
+@pytest.fixture
+def run_without_copies():
+    """run(fn): call fn() (one attention call on the GPU) and check that the
+    only device memory it took from torch's allocator is its output, i.e. no
+    padded or contiguous copy of Q, K or V was made (the allocator rounds
+    every block up to 512 bytes)."""
+    def run(fn):
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        before = torch.cuda.memory_allocated()
+        out = fn()
+        torch.cuda.synchronize()
+        grew = torch.cuda.max_memory_allocated() - before
+        nbytes = out.untyped_storage().nbytes()
+        assert grew <= (nbytes + 511) // 512 * 512, f"{grew} bytes allocated for a {nbytes}-byte output"
+        return out
+    return run
+
+
 def force_eligible(monkeypatch):
     """Make the GPU/dtype and grad gates pass so CPU tensors reach the native branch."""
     monkeypatch.setattr(cmpext3, "_usable", lambda *a, **k: True)

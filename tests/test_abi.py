@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version_and_messages():
-    assert abi.lib().cmpext3_attn_abi_version() == 6
+    assert abi.lib().cmpext3_attn_abi_version() == 7
     for code in range(10):
         assert abi.strerror(code) and abi.strerror(code) != "unknown error code"
     assert abi.strerror(99) == "unknown error code"
@@ -46,14 +46,18 @@ def test_version_and_messages():
 
 @pytest.mark.parametrize("dtype,D,expect", [
     (abi.DTYPE_F16, 64, abi.OK), (abi.DTYPE_BF16, 128, abi.OK), (abi.DTYPE_F32, 40, abi.OK),
-    (abi.DTYPE_F16, 36, abi.E_HEAD_DIM), (abi.DTYPE_F32, 6, abi.E_HEAD_DIM),
-    (abi.DTYPE_F16, 264, abi.E_HEAD_DIM), (7, 64, abi.E_DTYPE),
+    (abi.DTYPE_F16, 36, abi.OK), (abi.DTYPE_F32, 6, abi.OK), (abi.DTYPE_BF16, 1, abi.OK),
+    (abi.DTYPE_F16, 264, abi.E_HEAD_DIM), (abi.DTYPE_F32, 0, abi.E_HEAD_DIM), (7, 64, abi.E_DTYPE),
 ])
 def test_describe_classifies(dtype, D, expect):
     rc, text = abi.describe(dtype, 2, 10, 4096, 4096, D)
     assert rc == expect
     if rc == abi.OK:
         assert "mfma" in text
+        # a head dim that is not whole 16-byte chunks runs in place on a
+        # narrow-row variant
+        es = 4 if dtype == abi.DTYPE_F32 else 2
+        assert ("narrow rows" in text) == (D * es % 16 != 0)
 
 
 def test_describe_baseline_configs():
@@ -102,17 +106,32 @@ def _call(q=16, k=16, v=16, o=16, dtype=abi.DTYPE_F16, B=1, H=1, Sq=8, Sk=8, D=6
 
 
 # Fake device addresses: every case below must be rejected before any launch.
+# (Odd head dims and 2-byte aligned rows are accepted by the unmasked entry
+# points, so they appear here only with a mask, which needs whole chunks.)
 def test_rejections_before_launch():
     assert _call(dtype=5) == abi.E_DTYPE
     assert _call(B=-1) == abi.E_INVALID
     assert _call(D=0) == abi.E_HEAD_DIM
-    assert _call(D=12) == abi.E_HEAD_DIM
+    assert _call(D=257) == abi.E_HEAD_DIM
     assert _call(Sk=0) == abi.E_EMPTY_KEYS
     assert _call(q=0) == abi.E_INVALID
-    assert _call(q=24) == abi.E_ALIGN
-    assert _call(strides=(512, 512, 60)) == abi.E_ALIGN
+    assert _call(q=25) == abi.E_ALIGN                      # not element-aligned
+    assert _call(dtype=abi.DTYPE_F32, o=18) == abi.E_ALIGN  # fp32 needs 4 bytes
+    assert _call(strides=(512, 512, -64)) == abi.E_INVALID
     assert _call(scale=float("inf")) == abi.E_INVALID
     assert _call(scale=float("nan")) == abi.E_INVALID
+    assert _call_masked_layout(D=12) == abi.E_HEAD_DIM
+    assert _call_masked_layout(q=24) == abi.E_ALIGN
+    assert _call_masked_layout(strides=(512, 512, 60)) == abi.E_ALIGN
+
+
+def _call_masked_layout(q=16, D=64, strides=(512, 512, 64)):
+    st = (ctypes.c_int64 * 3)(*strides)
+    ms = (ctypes.c_int64 * 3)(0, 0, 0)
+    return abi.lib().cmpext3_attn_fwd_masked(ctypes.c_void_p(q), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                             ctypes.c_void_p(16), abi.DTYPE_F16, 1, 1, 1, 8, 8, D, st, st,
+                                             st, st, ctypes.c_void_p(16), abi.DTYPE_BOOL, ms,
+                                             ctypes.c_float(0.125), 0, None)
 
 
 def test_empty_problem_is_a_noop_even_without_pointers():
@@ -163,10 +182,12 @@ def test_training_entry_points_reject_before_launch():
     assert _call_lse(lse=0) == abi.E_INVALID
     assert _call_lse(lse=18) == abi.E_INVALID
     assert _call_lse(q=24) == abi.E_ALIGN
+    assert _call_lse(D=36) == abi.E_HEAD_DIM               # training needs whole chunks
     assert _call_lse(Sk=0) == abi.E_EMPTY_KEYS
     assert _call_lse(lse=0, q=0, Sq=0) == abi.OK          # empty problem
     assert _call_bwd(dtype=abi.DTYPE_F32) == abi.E_TRAINING
     assert _call_bwd(D=136) == abi.E_TRAINING
+    assert _call_bwd(D=36) == abi.E_HEAD_DIM
     assert _call_bwd(delta=0) == abi.E_INVALID
     assert _call_bwd(lse=0) == abi.E_INVALID
     assert _call_bwd(delta=18) == abi.E_ALIGN

@@ -5,7 +5,8 @@ Same bar as tests/test_gpu_parity.py (max |kernel - oracle| <= 1e-2 fp16,
 inputs):
 
   * head dims that are not a whole number of 16-byte chunks, for every
-    dtype, through the torch binding (ops.attention), causal and not;
+    dtype, through the torch binding (ops.attention), causal and not, run
+    in place (the call allocates nothing but its output);
     the reference's fp32 kernel takes any D <= 128
     (src/cuda/fp32_attention.cu:200-204);
   * head dims 160, 192 and 256 over long key sweeps (>= 1024 keys, many
@@ -41,19 +42,73 @@ def _inputs(dtype, B, H, Sq, Sk, D, seed):
     return W.Workload("cov", dtype, B, H, Sq, Sk, D, seed=seed).make_inputs("cuda")
 
 
+
 @pytest.mark.parametrize("dtype,D", [("fp32", 33), ("fp32", 36), ("fp32", 100), ("fp32", 3),
                                      ("bf16", 36), ("bf16", 100), ("bf16", 2),
-                                     ("fp16", 33), ("fp16", 100)])
+                                     ("fp16", 33), ("fp16", 100), ("fp16", 50)])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("Sq,Sk", [(70, 50), (129, 300)])
-def test_odd_head_dims_every_dtype(dtype, D, causal, Sq, Sk):
+def test_odd_head_dims_every_dtype(dtype, D, causal, Sq, Sk, run_without_copies):
     q, k, v = _inputs(dtype, 1, 2, Sq, Sk, D, seed=D * 31 + Sk)
     print(f"odd D: {dtype} D={D} Sq={Sq} Sk={Sk} causal={causal}", flush=True)
-    out = cmpext3.ops.attention(q, k, v, None, causal)
-    torch.cuda.synchronize()
+    if dtype != "fp32" and D % 2:
+        # 16-bit rows of an odd element count: the binding pads them (faster
+        # than the in-place 2-byte path, which test_two_byte_rows_through_the_abi covers)
+        out = cmpext3.ops.attention(q, k, v, None, causal)
+    else:
+        out = run_without_copies(lambda: cmpext3.ops.attention(q, k, v, None, causal))
     assert out.shape == q.shape and out.dtype == q.dtype
     ref = orc.sdpa_c(q.cpu(), k.cpu(), v.cpu(), None, causal)
     err = orc.max_abs_err(out.cpu(), ref)
+    assert err <= TOL[dtype], f"max abs err {err:.3e}"
+
+
+@pytest.mark.parametrize("dtype,D,layout,scale,causal,shape", [
+    ("fp16", 36, "bhsd", None, False, (1, 2, 256, 2048)),  # key split, 8-byte pieces
+    ("bf16", 100, "bshd", None, True, (2, 3, 300, 300)),   # [B,S,H,D] view: row stride H*D
+    ("fp16", 60, "bhsd", 0.0, False, (1, 2, 130, 700)),    # scale 0, ragged tiles
+    ("fp16", 50, "bshd", None, False, (1, 4, 77, 77)),     # short keys, 4-byte pieces (v2 kernel)
+    ("bf16", 90, "bhsd", 1.0, False, (1, 2, 200, 1000)),   # 4-byte pieces, wide scores (rescales)
+])
+def test_narrow_rows_in_place(dtype, D, layout, scale, causal, shape, run_without_copies):
+    """Narrow-row variants (head dims that are not whole 16-byte chunks) on
+    the pipelined kernel (8- and 4-byte pieces, Sk >= 256) and the v2 kernel
+    (short sweeps), with the key split, BSHD views, scale 0 and scores wide
+    enough to move the running offset."""
+    B, H, Sq, Sk = shape
+    wl = W.Workload("narrow", dtype, B, H, Sq, Sk, D, seed=D + Sq)
+    q, k, v = wl.make_inputs("cuda", layout=layout)
+    print(f"narrow rows: {dtype} D={D} {layout} scale={scale} causal={causal} {shape}", flush=True)
+    out = run_without_copies(lambda: cmpext3.ops.attention(q, k, v, scale, causal))
+    ref = orc.sdpa_c(q.cpu(), k.cpu(), v.cpu(), scale, causal)
+    err = orc.max_abs_err(out.cpu(), ref)
+    assert err <= TOL[dtype], f"max abs err {err:.3e}"
+    assert out.stride() == q.stride() if layout == "bshd" else out.is_contiguous()
+
+
+@pytest.mark.parametrize("dtype,D,offset,causal,Sq,Sk", [
+    ("fp16", 33, 0, True, 200, 300),    # odd head dim: 66-byte rows
+    ("bf16", 64, 1, False, 130, 77),    # 2-byte offset views of aligned rows
+    ("fp16", 161, 0, False, 96, 1100),  # odd D above 128 (the v2 kernel's only path)
+])
+def test_two_byte_rows_through_the_abi(dtype, D, offset, causal, Sq, Sk):
+    """Rows the C ABI reads in 2-byte pieces (the v2 kernel's narrow variant):
+    in place, caller-allocated output, against the oracle."""
+    B, H = 1, 2
+    g = torch.Generator().manual_seed(D + Sk)
+    dt = W.DTYPES[dtype]
+
+    def make(S):
+        flat = torch.randn(B * H * S * D + offset, generator=g).to(dt).cuda()
+        return flat[offset:].view(B, H, S, D)
+    q, k, v = make(Sq), make(Sk), make(Sk)
+    o = make(Sq)
+    print(f"2-byte rows: {dtype} D={D} offset={offset} causal={causal} Sq={Sq} Sk={Sk}", flush=True)
+    scale = D ** -0.5
+    assert abi.attn_fwd_raw(q, k, v, o, scale, causal) == abi.OK
+    torch.cuda.synchronize()
+    ref = orc.sdpa_c(q.cpu(), k.cpu(), v.cpu(), scale, causal)
+    err = orc.max_abs_err(o.cpu(), ref)
     assert err <= TOL[dtype], f"max abs err {err:.3e}"
 
 

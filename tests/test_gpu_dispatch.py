@@ -54,22 +54,40 @@ def test_bshd_query_gets_bshd_output(patched):
 
 
 @pytest.mark.parametrize("D", [4, 12, 36, 100])
-def test_odd_head_dims_are_repacked(D):
+def test_odd_head_dims_run_in_place(D, run_without_copies):
     wl = W.Workload("odd", "fp16", 1, 2, 70, 50, D, seed=D)
     q, k, v = wl.make_inputs("cuda")
-    out = cmpext3.ops.attention(q, k, v, None, True)
+    out = run_without_copies(lambda: cmpext3.ops.attention(q, k, v, None, True))
     ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), None, True)
     assert out.shape == q.shape
     assert orc.max_abs_err(out.cpu(), ref) <= orc.TOLERANCE["fp16"]
 
 
-def test_misaligned_storage_is_repacked():
-    base = torch.randn(1 * 2 * 64 * 64 + 1, dtype=torch.float16, device="cuda")
-    q = base[1:].view(1, 2, 64, 64)                   # 2-byte offset: not 16-byte aligned
-    k = torch.randn(1, 2, 64, 64, dtype=torch.float16, device="cuda")
-    out = cmpext3.ops.attention(q, k, k, 0.2, False)
-    ref = orc.sdpa_np(q.cpu(), k.cpu(), k.cpu(), 0.2)
-    assert orc.max_abs_err(out.cpu(), ref) <= orc.TOLERANCE["fp16"]
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("Sk", [64, 300])
+def test_misaligned_storage(causal, Sk, run_without_copies):
+    """A 4-byte offset view runs in place (4-byte pieces); a 2-byte offset
+    view is repacked by the binding (faster than 2-byte pieces)."""
+    k = torch.randn(1, 2, Sk, 64, dtype=torch.float16, device="cuda")
+    for off in (2, 1):
+        base = torch.randn(1 * 2 * 64 * 64 + off, dtype=torch.float16, device="cuda")
+        q = base[off:].view(1, 2, 64, 64)
+        if off == 2:
+            out = run_without_copies(lambda: cmpext3.ops.attention(q, k, k, 0.2, causal))
+        else:
+            out = cmpext3.ops.attention(q, k, k, 0.2, causal)
+        ref = orc.sdpa_np(q.cpu(), k.cpu(), k.cpu(), 0.2, causal)
+        assert orc.max_abs_err(out.cpu(), ref) <= orc.TOLERANCE["fp16"]
+
+
+def test_odd_head_dim_with_a_mask_is_repacked():
+    """Masked calls need whole 16-byte chunks: the binding repacks those."""
+    wl = W.Workload("oddmask", "bf16", 1, 2, 70, 300, 36, seed=3)
+    q, k, v = wl.make_inputs("cuda")
+    keep = torch.rand(1, 1, 70, 300, device="cuda") > 0.3
+    out = cmpext3.ops.attention(q, k, v, None, False, keep)
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), None, False, attn_mask=keep.cpu())
+    assert orc.max_abs_err(out.cpu(), ref) <= orc.TOLERANCE["bf16"]
 
 
 def test_runs_on_the_callers_stream():

@@ -90,9 +90,11 @@ def test_noalloc_matches_the_allocating_entry_point_on_calls_in_a_row():
 def test_noalloc_passes_argument_checks_like_the_masked_entry_point():
     q, k, v = _inputs("fp16", 1, 2, 2, 64, 300, 64, 0)
     o = torch.empty_like(q)
-    # a head dim that is not whole 16-byte chunks, through both entry points
+    # a masked call whose head dim is not whole 16-byte chunks
     bad = q[..., :60]
-    assert abi.attn_fwd_noalloc_raw(bad, k[..., :60], v[..., :60], o[..., :60], 0.1) == abi.E_HEAD_DIM
+    keep = torch.ones(1, 1, 64, 300, dtype=torch.bool, device="cuda")
+    assert abi.attn_fwd_noalloc_raw(bad, k[..., :60], v[..., :60], o[..., :60], 0.1,
+                                    attn_mask=keep) == abi.E_HEAD_DIM
     # fp32 with a mask: refused before any launch
     m = torch.ones(1, 1, 64, 300, dtype=torch.bool, device="cuda")
     qf, kf, vf = (t.float() for t in (q, k, v))

@@ -106,6 +106,12 @@ EXTRA_WORKLOADS = [
     Workload("qwen3_decode_bf16", "bf16", 16, 16, 1, 4096, 128, scale=1 / math.sqrt(128), seed=6,
              Hkv=8, note="Qwen3-0.6B-style decode step: 16 query heads over 8 K/V heads "
                          "(native GQA), 4096-token KV cache, non-causal"),
+    # head dims that are not a whole number of 16-byte chunks: run in place on
+    # the element-granular kernel variants (one kernel per call, no copies)
+    Workload("odd_dim_fp16", "fp16", 1, 8, 2048, 2048, 100, seed=7,
+             note="head dim 100 (not a multiple of 8 halves), fp16, non-causal"),
+    Workload("odd_dim_fp32", "fp32", 1, 8, 1024, 1024, 33, seed=8,
+             note="head dim 33 (not a multiple of 4 floats), fp32, non-causal"),
 ]
 BY_NAME = {w.name: w for w in WORKLOADS + EXTRA_WORKLOADS}
 

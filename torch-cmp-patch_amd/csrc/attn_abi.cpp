@@ -45,7 +45,6 @@ int check_shape(int dtype, int B, int H, int Sq, int Sk, int D) {
   if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;  // nothing to compute
   if (Sk == 0) return CMPEXT3_E_EMPTY_KEYS;
   if (D == 0 || D > 256) return CMPEXT3_E_HEAD_DIM;
-  if (D % (16 / es) != 0) return CMPEXT3_E_HEAD_DIM;  // whole 16-byte chunks per row
   // workgroup count and in-kernel int arithmetic on (b*H + h) and row indices
   if ((int64_t)B * H * ((Sq + 63) / 64) > (int64_t)INT32_MAX / 2) return CMPEXT3_E_TOO_LARGE;
   if (Sq > INT32_MAX - 512 || Sk > INT32_MAX - 512) return CMPEXT3_E_TOO_LARGE;
@@ -53,6 +52,9 @@ int check_shape(int dtype, int B, int H, int Sq, int Sk, int D) {
 }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+bool aligned_to(const void* ptr, int es) { return ((uintptr_t)ptr % (uintptr_t)es) == 0; }
+// rows of whole 16-byte chunks (the pipelined, short-key and training kernels)
+bool whole_chunks(int dtype, int D) { return D % (16 / elem_size(dtype)) == 0; }
 
 // attention-mask arguments (mask_dtype -1 = none): CMPEXT3_OK or an error code
 int check_mask(const void* mask, int mask_dtype, const int64_t mask_str[3], int dtype, int D, int Sq, int Sk) {
@@ -76,7 +78,8 @@ int mask_kind_of(int mask_dtype) {
          : mask_dtype == CMPEXT3_DTYPE_BF16 ? cmpext3::MASK_BF16 : cmpext3::MASK_F16;
 }
 
-// A stride only matters if its dimension has more than one index.
+// A stride only matters if its dimension has more than one index: each must
+// be non-negative and a multiple of 16 bytes (es = element size).
 bool stride_ok(const int64_t s[3], int n0, int n1, int n2, int es) {
   const int64_t n[3] = {n0, n1, n2};
   for (int i = 0; i < 3; ++i) {
@@ -84,6 +87,30 @@ bool stride_ok(const int64_t s[3], int n0, int n1, int n2, int es) {
     if (s[i] < 0) return false;
     if ((s[i] * es) % 16 != 0) return false;
   }
+  return true;
+}
+// Largest of 2, 4, 8, 16 bytes dividing every base pointer, every row stride
+// (of a dimension with more than one index) and the row length D * es.
+int piece_bytes(const void* q, const void* k, const void* v, const void* o, int D, int es,
+                const int64_t q_str[3], const int64_t k_str[3], const int64_t v_str[3],
+                const int64_t o_str[3], int B, int H, int H_kv, int Sq, int Sk) {
+  uint64_t bits = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o | (uint64_t)D * es;
+  auto add = [&](const int64_t s[3], int n0, int n1, int n2) {
+    const int64_t n[3] = {n0, n1, n2};
+    for (int i = 0; i < 3; ++i)
+      if (n[i] > 1) bits |= (uint64_t)s[i] * es;
+  };
+  add(q_str, B, H, Sq);
+  add(k_str, B, H_kv, Sk);
+  add(v_str, B, H_kv, Sk);
+  add(o_str, B, H, Sq);
+  return (bits & 15) == 0 ? 16 : (bits & 7) == 0 ? 8 : (bits & 3) == 0 ? 4 : 2;
+}
+
+bool strides_nonneg(const int64_t s[3], int n0, int n1, int n2) {
+  const int64_t n[3] = {n0, n1, n2};
+  for (int i = 0; i < 3; ++i)
+    if (n[i] > 1 && s[i] < 0) return false;
   return true;
 }
 
@@ -99,8 +126,11 @@ const char* cmpext3_attn_strerror(int code) {
     case CMPEXT3_E_INVALID: return "invalid argument (null pointer, negative size or stride)";
     case CMPEXT3_E_DTYPE: return "unsupported dtype (expected f16, bf16 or f32)";
     case CMPEXT3_E_HEAD_DIM:
-      return "unsupported head dim (need 1..256 and a multiple of 8 for f16/bf16, 4 for f32)";
-    case CMPEXT3_E_ALIGN: return "misaligned tensor (base pointers and row strides must be 16-byte aligned)";
+      return "unsupported head dim (need 1..256; masked and training calls need a multiple of 8 for f16/bf16, "
+             "4 for f32)";
+    case CMPEXT3_E_ALIGN:
+      return "misaligned tensor (pointers must be element-aligned; masked and training calls need 16-byte "
+             "aligned base pointers and row strides)";
     case CMPEXT3_E_EMPTY_KEYS: return "key/value sequence is empty";
     case CMPEXT3_E_LAUNCH: return "HIP kernel launch failed";
     case CMPEXT3_E_TOO_LARGE: return "problem too large for 32-bit tile indexing";
@@ -175,10 +205,19 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
   if (!q || !k || !v || !o || !q_str || !k_str || !v_str || !o_str) return CMPEXT3_E_INVALID;
   if (!isfinite(scale)) return CMPEXT3_E_INVALID;
   const int es = elem_size(dtype);
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return CMPEXT3_E_ALIGN;
-  if (!stride_ok(q_str, B, H, Sq, es) || !stride_ok(k_str, B, H_kv, Sk, es) ||
-      !stride_ok(v_str, B, H_kv, Sk, es) || !stride_ok(o_str, B, H, Sq, es))
+  if (!aligned_to(q, es) || !aligned_to(k, es) || !aligned_to(v, es) || !aligned_to(o, es))
     return CMPEXT3_E_ALIGN;
+  if (!strides_nonneg(q_str, B, H, Sq) || !strides_nonneg(k_str, B, H_kv, Sk) ||
+      !strides_nonneg(v_str, B, H_kv, Sk) || !strides_nonneg(o_str, B, H, Sq))
+    return CMPEXT3_E_INVALID;
+  // Rows of whole, 16-byte aligned chunks run the vector-load kernels; any
+  // other layout (head dim not a multiple of 16 bytes, a base pointer or row
+  // stride off 16 bytes) runs the narrow variants in place, in pieces of the
+  // largest of 2, 4, 8 bytes that divides every address, row stride and the
+  // row length.  Those exist for unmasked inference only.
+  const int piece = piece_bytes(q, k, v, o, D, es, q_str, k_str, v_str, o_str, B, H, H_kv, Sq, Sk);
+  const bool chunks = piece == 16;
+  if (!chunks && (masked || lse)) return whole_chunks(dtype, D) ? CMPEXT3_E_ALIGN : CMPEXT3_E_HEAD_DIM;
   // the fp16/bf16 kernel addresses one K/V tile with 32-bit element offsets
   if (dtype != CMPEXT3_DTYPE_F32 &&
       (k_str[2] * 64 + 256 > INT32_MAX || v_str[2] * 64 + 256 > INT32_MAX))
@@ -208,6 +247,7 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
   p.c = fabsf(scale) * cmpext3::kLog2e;
   p.q_sign = (scale < 0.f) ? (dtype == CMPEXT3_DTYPE_F32 ? 0x80000000u : 0x80008000u) : 0u;
   p.fixed_exchange = fixed_exchange ? 1 : 0;
+  p.elem_rows = chunks ? 0 : piece;
 
   hipError_t err;
   if (dtype == CMPEXT3_DTYPE_F32)
@@ -273,6 +313,7 @@ int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
   if (rc != CMPEXT3_OK) return rc;
   if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;
   if (dtype == CMPEXT3_DTYPE_F32 || D > 128) return CMPEXT3_E_TRAINING;
+  if (!whole_chunks(dtype, D)) return CMPEXT3_E_HEAD_DIM;
   if (H_kv < 1 || H_kv > H || H % H_kv != 0) return CMPEXT3_E_INVALID;
   rc = check_mask(mask, mask_dtype, mask_str, dtype, D, Sq, Sk);
   if (rc != CMPEXT3_OK) return rc;

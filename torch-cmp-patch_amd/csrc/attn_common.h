@@ -48,6 +48,11 @@ struct FwdParams {
   // host side only: the key split exchanges through the library's fixed
   // per-device scratch instead of a per-stream allocated buffer
   int fixed_exchange;
+  // 0 when every row is whole 16-byte chunks at 16-byte aligned addresses;
+  // otherwise the piece size in bytes (2, 4 or 8) of the narrow variants
+  // (ld_cols16 / ld_cols32): the largest that divides every base pointer,
+  // row stride and D * element size
+  int elem_rows;
 };
 
 // Compute units of the current device (host side; 256 on MI355X).
@@ -123,6 +128,61 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // compiler from moving LDS accesses across it.
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Narrow row access (FwdParams::elem_rows = a, the largest of 2, 4, 8 bytes
+// that divides every base pointer, every row stride and the row length D *
+// element size): for head dims that are not a whole number of 16-byte chunks
+// and for rows or base pointers that are not 16-byte aligned.  A 16-byte
+// chunk is assembled from a-byte pieces, each naturally aligned; since the
+// row length is a multiple of a, a piece lies wholly inside or wholly past
+// the head dim, and pieces past it (n = elements of the chunk inside the
+// head dim) are neither read nor written.  No row is read past its head
+// dim and nothing is copied.
+__device__ __forceinline__ u32x4 ld_cols16(const uint16_t* p, int n, int a) {
+  u32x4 x = {0u, 0u, 0u, 0u};
+  if (a == 8) {
+    const u32x2* q = (const u32x2*)p;
+    const u32x2 lo = q[0];  // n >= 4: the chunk's first piece is in the head dim
+    x[0] = lo[0];
+    x[1] = lo[1];
+    if (n > 4) {
+      const u32x2 hi = q[1];
+      x[2] = hi[0];
+      x[3] = hi[1];
+    }
+  } else if (a == 4) {
+    const uint32_t* q = (const uint32_t*)p;
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      if (2 * w < n) x[w] = q[w];
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (e < n) x[e >> 1] |= (uint32_t)p[e] << (16 * (e & 1));
+  }
+  return x;
+}
+// the first n (<= 4) of 4 packed 16-bit values w to p, in a-byte pieces
+__device__ __forceinline__ void st_cols16x4(uint16_t* p, u32x2 w, int n, int a) {
+  if (a == 8) {
+    *(u32x2*)p = w;  // n == 4
+  } else if (a == 4) {
+    uint32_t* q = (uint32_t*)p;
+    q[0] = w[0];
+    if (n > 2) q[1] = w[1];
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (e < n) p[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+  }
+}
+__device__ __forceinline__ u32x4 ld_cols32(const float* p, int n) {
+  u32x4 x = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (e < n) x[e] = __float_as_uint(p[e]);
+  return x;
 }
 
 // Key split of the last query blocks: workgroups [0, nfull) take whole

@@ -123,7 +123,10 @@ __device__ __forceinline__ int lds_swz(int r) {
 // for DK == DP in {32, 64, 128}).  OPT bit 2: decide the rescale from the
 // tile's row sum after the exponentials instead of from the row max before
 // them (measured slower on MI355X: the PV MFMAs then wait for the whole sum).
-// The padded, max-first form is the default.
+// The padded, max-first form is the default.  OPT bit 6: narrow rows
+// (ld_cols16 / st_cols16x4, FwdParams::elem_rows): any head dim and any
+// 2-byte aligned rows, read and written in 2-, 4- or 8-byte pieces, columns
+// past D never touched.
 template <typename T, int DK, int DP, int NW, int QB, int BK, int OCC, bool CAUSAL, bool PRESCALE,
           int OPT = 0>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
@@ -134,6 +137,7 @@ attn_fwd_mfma16(const FwdParams p) {
   // LDS rows padded by 16 bytes (a 64-row K/V tile then reads without
   // measurable bank conflicts), or unpadded with XOR-swizzled 16-byte chunks.
   constexpr bool SWZ = (OPT & 2) && (DK == DP) && (DK == 32 || DK == 64 || DK == 128);
+  constexpr bool ELEM = (OPT & 64) != 0;
   constexpr int RSK = SWZ ? DK : DK + 8;  // K tile row stride (halves)
   constexpr int RSV = SWZ ? DP : DP + 8;  // V tile row stride (halves)
   constexpr int KTILE = BK * RSK;
@@ -185,7 +189,10 @@ attn_fwd_mfma16(const FwdParams p) {
     for (int s = 0; s < NKS; ++s) {
       const int d = 16 * s + 8 * hh;
       u32x4 x = {0u, 0u, 0u, 0u};
-      if (row < Sq && d < D) x = *(const u32x4*)(qg + (int64_t)row * p.q_s + d);
+      if (row < Sq && d < D) {
+        const uint16_t* src = qg + (int64_t)row * p.q_s + d;
+        x = ELEM ? ld_cols16(src, D - d, p.elem_rows) : *(const u32x4*)src;
+      }
       if (PRESCALE) {
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
@@ -216,24 +223,26 @@ attn_fwd_mfma16(const FwdParams p) {
   const float c = p.c;
 
   // ---- per-thread global/LDS offsets of its tile chunks (fixed across tiles)
-  int kgo[KLD], klo[KLD], krow[KLD];
+  int kgo[KLD], klo[KLD], krow[KLD], kn[KLD];
   bool kok[KLD];
 #pragma unroll
   for (int it = 0; it < KLD; ++it) {
     const int ci = it * NT + tid;
     const int r = ci / KCH, c8 = ci - r * KCH;
     krow[it] = r;
+    kn[it] = D - 8 * c8;  // columns of the chunk inside the head dim (ELEM)
     kok[it] = (BK * KCH % NT == 0 || ci < BK * KCH) && 8 * c8 < D;
     kgo[it] = r * (int)p.k_s + 8 * c8;
     klo[it] = r * RSK + 8 * (SWZ ? (c8 ^ lds_swz<DK>(r)) : c8);
   }
-  int vgo[VLD], vlo[VLD], vrow[VLD];
+  int vgo[VLD], vlo[VLD], vrow[VLD], vn[VLD];
   bool vok[VLD];
 #pragma unroll
   for (int it = 0; it < VLD; ++it) {
     const int ci = it * NT + tid;
     const int r = ci / VCH, c8 = ci - r * VCH;
     vrow[it] = r;
+    vn[it] = D - 8 * c8;
     vok[it] = (BK * VCH % NT == 0 || ci < BK * VCH) && 8 * c8 < D;
     vgo[it] = r * (int)p.v_s + 8 * c8;
     vlo[it] = r * RSV + 8 * (SWZ ? (c8 ^ lds_swz<DP>(r)) : c8);
@@ -241,7 +250,9 @@ attn_fwd_mfma16(const FwdParams p) {
   const int64_t kstep = (int64_t)BK * p.k_s, vstep = (int64_t)BK * p.v_s;
 
   u32x4 kreg[KLD], vreg[VLD];
-  const bool cols_full = (D == DK) && (D == DP);  // no zero-filled head-dim columns
+  // no zero-filled head-dim columns (element-granular rows always take the
+  // checked path below)
+  const bool cols_full = !ELEM && (D == DK) && (D == DP);
   auto load_tile = [&](int t) {
     const int k0 = t * BK;
     const uint16_t* kt = kg + t * kstep;
@@ -259,13 +270,15 @@ attn_fwd_mfma16(const FwdParams p) {
 #pragma unroll
     for (int it = 0; it < KLD; ++it) {
       u32x4 x = {0u, 0u, 0u, 0u};
-      if (kok[it] && k0 + krow[it] < Sk) x = *(const u32x4*)(kt + kgo[it]);
+      if (kok[it] && k0 + krow[it] < Sk)
+        x = ELEM ? ld_cols16(kt + kgo[it], kn[it], p.elem_rows) : *(const u32x4*)(kt + kgo[it]);
       kreg[it] = x;
     }
 #pragma unroll
     for (int it = 0; it < VLD; ++it) {
       u32x4 x = {0u, 0u, 0u, 0u};
-      if (vok[it] && k0 + vrow[it] < Sk) x = *(const u32x4*)(vt + vgo[it]);
+      if (vok[it] && k0 + vrow[it] < Sk)
+        x = ELEM ? ld_cols16(vt + vgo[it], vn[it], p.elem_rows) : *(const u32x4*)(vt + vgo[it]);
       vreg[it] = x;
     }
   };
@@ -466,7 +479,10 @@ attn_fwd_mfma16(const FwdParams p) {
             u32x2 w;
             w[0] = Elt<T>::pack(oacc[qb][db][4 * g + 0] * inv, oacc[qb][db][4 * g + 1] * inv);
             w[1] = Elt<T>::pack(oacc[qb][db][4 * g + 2] * inv, oacc[qb][db][4 * g + 3] * inv);
-            *(u32x2*)(orow + d) = w;
+            if (ELEM)
+              st_cols16x4(orow + d, w, D - d, p.elem_rows);
+            else
+              *(u32x2*)(orow + d) = w;
           }
         }
       }

@@ -9,6 +9,7 @@
 // autotune idea (setup.py:54-123): entries were chosen by an offline sweep on
 // an MI355X; nothing is measured at build or run time.
 #include <stdio.h>
+#include <string.h>
 
 #include "attn_fwd_mfma16.h"
 
@@ -30,25 +31,26 @@ constexpr Tile16 tile16(int dk) {
   return dk <= 96 ? Tile16{4, 1, 64, 3} : dk <= 128 ? Tile16{4, 1, 64, 2} : Tile16{4, 1, 32, 1};
 }
 
-template <typename T, int DK, bool CAUSAL, bool PRESCALE>
+// OPT 1: s_setprio(1) around the MFMA blocks (padded LDS rows, max-first
+// rescale); OPT 64: element-granular rows (FwdParams::elem_rows)
+template <typename T, int DK, bool CAUSAL, bool PRESCALE, int EOPT>
 hipError_t launch_dk(const FwdParams& p, hipStream_t s) {
   constexpr Tile16 tt = tile16(DK);
-  // OPT 1: s_setprio(1) around the MFMA blocks (padded LDS rows, max-first rescale)
-  return launch_mfma16_cfg<T, DK, tt.nw, tt.qb, tt.bk, tt.occ, CAUSAL, PRESCALE, 1>(p, s);
+  return launch_mfma16_cfg<T, DK, tt.nw, tt.qb, tt.bk, tt.occ, CAUSAL, PRESCALE, 1 | EOPT>(p, s);
 }
 
-template <typename T, bool CAUSAL, bool PRESCALE>
+template <typename T, bool CAUSAL, bool PRESCALE, int EOPT = 0>
 hipError_t launch_bucket(const FwdParams& p, int dk, hipStream_t s) {
   switch (dk) {
-    case 32: return launch_dk<T, 32, CAUSAL, PRESCALE>(p, s);
-    case 48: return launch_dk<T, 48, CAUSAL, PRESCALE>(p, s);
-    case 64: return launch_dk<T, 64, CAUSAL, PRESCALE>(p, s);
-    case 80: return launch_dk<T, 80, CAUSAL, PRESCALE>(p, s);
-    case 96: return launch_dk<T, 96, CAUSAL, PRESCALE>(p, s);
-    case 128: return launch_dk<T, 128, CAUSAL, PRESCALE>(p, s);
-    case 160: return launch_dk<T, 160, CAUSAL, PRESCALE>(p, s);
-    case 192: return launch_dk<T, 192, CAUSAL, PRESCALE>(p, s);
-    case 256: return launch_dk<T, 256, CAUSAL, PRESCALE>(p, s);
+    case 32: return launch_dk<T, 32, CAUSAL, PRESCALE, EOPT>(p, s);
+    case 48: return launch_dk<T, 48, CAUSAL, PRESCALE, EOPT>(p, s);
+    case 64: return launch_dk<T, 64, CAUSAL, PRESCALE, EOPT>(p, s);
+    case 80: return launch_dk<T, 80, CAUSAL, PRESCALE, EOPT>(p, s);
+    case 96: return launch_dk<T, 96, CAUSAL, PRESCALE, EOPT>(p, s);
+    case 128: return launch_dk<T, 128, CAUSAL, PRESCALE, EOPT>(p, s);
+    case 160: return launch_dk<T, 160, CAUSAL, PRESCALE, EOPT>(p, s);
+    case 192: return launch_dk<T, 192, CAUSAL, PRESCALE, EOPT>(p, s);
+    case 256: return launch_dk<T, 256, CAUSAL, PRESCALE, EOPT>(p, s);
   }
   return hipErrorInvalidValue;
 }
@@ -75,6 +77,19 @@ static bool use_prescale(const FwdParams& p, bool bf16) { return !bf16 && p.c <=
 hipError_t launch_mfma16(const FwdParams& p, bool bf16, bool causal, hipStream_t s) {
   const int dk = mfma16_bucket(p.D);
   if (dk < 0) return hipErrorInvalidValue;
+  if (p.elem_rows) {
+    // narrow rows (unmasked inference only; the ABI sends masked and training
+    // calls here only with whole aligned chunks): 4- or 8-byte pieces on the
+    // pipelined kernel where it applies, else this kernel in any piece size
+    if (p.lse || p.mask_kind != MASK_NONE) return hipErrorNotSupported;
+    if (p.elem_rows >= 4 && pipe16_applies(p, dk))
+      return launch_pipe16(p, dk, bf16, causal, use_prescale(p, bf16), s);
+    if (bf16)
+      return causal ? launch_bucket<__bf16, true, false, 64>(p, dk, s)
+                    : launch_bucket<__bf16, false, false, 64>(p, dk, s);
+    return causal ? launch_bucket<_Float16, true, false, 64>(p, dk, s)
+                  : launch_bucket<_Float16, false, false, 64>(p, dk, s);
+  }
   if (short16_applies(p, dk, causal)) return launch_short16(p, dk, bf16, s);
   if (pipe16_applies(p, dk)) return launch_pipe16(p, dk, bf16, causal, use_prescale(p, bf16), s);
   // the v2 kernel has neither a log-sum-exp output nor mask code: refuse
@@ -98,20 +113,25 @@ void describe_mfma16(int D, int B, int H, int Sq, int Sk, bool causal, char* buf
   p.Sk = Sk;
   p.k_s = p.v_s = D;
   p.mask_kind = MASK_NONE;
-  if (short16_applies(p, dk, causal)) {
+  // contiguous rows of a D that is not whole 16-byte chunks are narrow: in
+  // 4- or 8-byte pieces (D even) on the pipelined kernel where it applies
+  const bool elem = D % 8 != 0;
+  if (!elem && short16_applies(p, dk, causal)) {
     describe_short16(dk, Sq, Sk, buf, len);
     return;
   }
-  if (pipe16_applies(p, dk)) {
-    describe_pipe16(dk, B, H, Sq, Sk, causal, buf, len);
+  if ((!elem || D % 2 == 0) && pipe16_applies(p, dk)) {
+    describe_pipe16(elem ? (dk <= 64 ? 64 : 128) : dk, B, H, Sq, Sk, causal, buf, len);
+    if (elem) snprintf(buf + strlen(buf), len - strlen(buf), " narrow rows");
     return;
   }
   const Tile16 t = tile16(dk);
   const int bq = t.nw * t.qb * 32;
   snprintf(buf, len,
            "mfma16 32x32x16 S^T-form: DK=%d DP=%d waves=%d qblocks/wave=%d BQ=%d BK=%d "
-           "waves/SIMD=%d qtiles=%d",
-           dk, (dk + 31) / 32 * 32, t.nw, t.qb, bq, t.bk, t.occ, (Sq + bq - 1) / bq);
+           "waves/SIMD=%d qtiles=%d%s",
+           dk, (dk + 31) / 32 * 32, t.nw, t.qb, bq, t.bk, t.occ, (Sq + bq - 1) / bq,
+           elem ? " narrow rows" : "");
 }
 
 }  // namespace cmpext3

@@ -31,8 +31,9 @@ __device__ __forceinline__ f32x4 mma32(float a, float b, f32x4 c) {
 }
 
 // DK: head dim bucket (multiple of 4, zero-padded above D); NQB: 16-row query
-// blocks per wave.
-template <int DK, int NW, int NQB, int BK, bool CAUSAL>
+// blocks per wave.  ELEM: element-granular K/V/O rows (any head dim, any
+// 4-byte aligned rows; ld_cols32), columns past D never touched.
+template <int DK, int NW, int NQB, int BK, bool CAUSAL, bool ELEM>
 __global__ void __launch_bounds__(NW * 64)
 attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
   constexpr int NT = NW * 64;
@@ -122,8 +123,10 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
       const int ci = it * NT + tid;
       const int r = ci / KCH, c4 = ci - (ci / KCH) * KCH;
       u32x4 x = {0u, 0u, 0u, 0u};
-      if ((BK * KCH % NT == 0 || ci < BK * KCH) && k0 + r < Sk && 4 * c4 < D)
-        x = *(const u32x4*)(kg + (int64_t)(k0 + r) * p.k_s + 4 * c4);
+      if ((BK * KCH % NT == 0 || ci < BK * KCH) && k0 + r < Sk && 4 * c4 < D) {
+        const float* src = kg + (int64_t)(k0 + r) * p.k_s + 4 * c4;
+        x = ELEM ? ld_cols32(src, D - 4 * c4) : *(const u32x4*)src;
+      }
       kreg[it] = x;
     }
 #pragma unroll
@@ -131,8 +134,10 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
       const int ci = it * NT + tid;
       const int r = ci / VCH, c4 = ci - (ci / VCH) * VCH;
       u32x4 x = {0u, 0u, 0u, 0u};
-      if ((BK * VCH % NT == 0 || ci < BK * VCH) && k0 + r < Sk && 4 * c4 < D)
-        x = *(const u32x4*)(vg + (int64_t)(k0 + r) * p.v_s + 4 * c4);
+      if ((BK * VCH % NT == 0 || ci < BK * VCH) && k0 + r < Sk && 4 * c4 < D) {
+        const float* src = vg + (int64_t)(k0 + r) * p.v_s + 4 * c4;
+        x = ELEM ? ld_cols32(src, D - 4 * c4) : *(const u32x4*)src;
+      }
       vreg[it] = x;
     }
   };
@@ -319,7 +324,13 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
         const int d = 16 * db + 4 * g;
-        if (d < D) *(f32x4*)(orow + d) = oacc[qb][db] * inv;
+        if (ELEM) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (d + e < D) orow[d + e] = oacc[qb][db][e] * inv;
+        } else if (d < D) {
+          *(f32x4*)(orow + d) = oacc[qb][db] * inv;
+        }
       }
     }
   }
@@ -330,7 +341,7 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
 // part at least kMinTiles32 key tiles long.
 constexpr int kMinTiles32 = 4;
 
-template <int DK, bool CAUSAL>
+template <int DK, bool CAUSAL, bool ELEM>
 hipError_t launch_mfma32_inst(const FwdParams& p0, hipStream_t stream) {
   // One 16-row query block per wave: measured on MI355X, two per wave only
   // lengthen each wave's dependency chain (1.6x slower on [1,8,1024,1024,64],
@@ -363,7 +374,8 @@ hipError_t launch_mfma32_inst(const FwdParams& p0, hipStream_t stream) {
     }
   }
   const int nwg = sa.nfull + (n - sa.nfull) * sa.nparts;
-  hipLaunchKernelGGL((attn_fwd_mfma32<DK, NW, NQB, BK, CAUSAL>), dim3(nwg), dim3(NW * 64), 0, stream, p, sa);
+  hipLaunchKernelGGL((attn_fwd_mfma32<DK, NW, NQB, BK, CAUSAL, ELEM>), dim3(nwg), dim3(NW * 64), 0, stream, p,
+                     sa);
   return hipGetLastError();
 }
 
@@ -375,20 +387,20 @@ int mfma32_bucket(int D) {
   return -1;
 }
 
-template <bool CAUSAL>
+template <bool CAUSAL, bool ELEM>
 static hipError_t launch_mfma32_dk(const FwdParams& p, int dk, hipStream_t s) {
   switch (dk) {
-    case 16: return launch_mfma32_inst<16, CAUSAL>(p, s);
-    case 32: return launch_mfma32_inst<32, CAUSAL>(p, s);
-    case 40: return launch_mfma32_inst<40, CAUSAL>(p, s);
-    case 48: return launch_mfma32_inst<48, CAUSAL>(p, s);
-    case 64: return launch_mfma32_inst<64, CAUSAL>(p, s);
-    case 80: return launch_mfma32_inst<80, CAUSAL>(p, s);
-    case 96: return launch_mfma32_inst<96, CAUSAL>(p, s);
-    case 128: return launch_mfma32_inst<128, CAUSAL>(p, s);
-    case 160: return launch_mfma32_inst<160, CAUSAL>(p, s);
-    case 192: return launch_mfma32_inst<192, CAUSAL>(p, s);
-    case 256: return launch_mfma32_inst<256, CAUSAL>(p, s);
+    case 16: return launch_mfma32_inst<16, CAUSAL, ELEM>(p, s);
+    case 32: return launch_mfma32_inst<32, CAUSAL, ELEM>(p, s);
+    case 40: return launch_mfma32_inst<40, CAUSAL, ELEM>(p, s);
+    case 48: return launch_mfma32_inst<48, CAUSAL, ELEM>(p, s);
+    case 64: return launch_mfma32_inst<64, CAUSAL, ELEM>(p, s);
+    case 80: return launch_mfma32_inst<80, CAUSAL, ELEM>(p, s);
+    case 96: return launch_mfma32_inst<96, CAUSAL, ELEM>(p, s);
+    case 128: return launch_mfma32_inst<128, CAUSAL, ELEM>(p, s);
+    case 160: return launch_mfma32_inst<160, CAUSAL, ELEM>(p, s);
+    case 192: return launch_mfma32_inst<192, CAUSAL, ELEM>(p, s);
+    case 256: return launch_mfma32_inst<256, CAUSAL, ELEM>(p, s);
   }
   return hipErrorInvalidValue;
 }
@@ -396,7 +408,9 @@ static hipError_t launch_mfma32_dk(const FwdParams& p, int dk, hipStream_t s) {
 hipError_t launch_mfma32(const FwdParams& p, bool causal, hipStream_t s) {
   const int dk = mfma32_bucket(p.D);
   if (dk < 0) return hipErrorInvalidValue;
-  return causal ? launch_mfma32_dk<true>(p, dk, s) : launch_mfma32_dk<false>(p, dk, s);
+  if (p.elem_rows)
+    return causal ? launch_mfma32_dk<true, true>(p, dk, s) : launch_mfma32_dk<false, true>(p, dk, s);
+  return causal ? launch_mfma32_dk<true, false>(p, dk, s) : launch_mfma32_dk<false, false>(p, dk, s);
 }
 
 void describe_mfma32(int D, int B, int H, int Sq, int Sk, bool causal, char* buf, int len) {
@@ -410,8 +424,9 @@ void describe_mfma32(int D, int B, int H, int Sq, int Sk, bool causal, char* buf
   }
   char split[48] = "";
   if (parts >= 2) snprintf(split, sizeof split, " key-split: %d x %d parts", n, parts);
-  snprintf(buf, len, "mfma32 16x16x4f32 S^T-form: DK=%d DPV=%d waves=4 BQ=%d BK=%d qblocks=%d%s", dk,
-           (dk + 15) / 16 * 16, bq, bk, (Sq + bq - 1) / bq, split);
+  snprintf(buf, len, "mfma32 16x16x4f32 S^T-form: DK=%d DPV=%d waves=4 BQ=%d BK=%d qblocks=%d%s%s", dk,
+           (dk + 15) / 16 * 16, bq, bk, (Sq + bq - 1) / bq, split,
+           D % 4 != 0 ? " narrow rows" : "");
 }
 
 }  // namespace cmpext3

@@ -54,7 +54,11 @@ namespace cmpext3 {
 // dim is not a multiple of 16 (D < DK), so K columns past D are zeroed.
 // OPT bit 4: an attention mask (p.mask) is applied to every tile's scores
 // before the exponentials (with CAUSAL, a pair must pass both).  OPT bit 5: each row's
-// log-sum-exp goes to p.lse (the training forward).
+// log-sum-exp goes to p.lse (the training forward).  OPT bit 6: narrow rows
+// (FwdParams::elem_rows 4 or 8: head dims that are not whole 16-byte chunks,
+// rows or base pointers off 16 bytes): K/V tiles are read as 4-byte pieces,
+// K pieces past the head dim at an out-of-range offset (so they read as zero
+// with no per-tile work), Q and O through ld_cols16 / st_cols16x4.
 template <typename T, int DK, int DP, int NW, int BK, int OCC, bool CAUSAL, bool PRESCALE, int OPT = 0>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
 attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
@@ -62,6 +66,7 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   constexpr int BQ = NW * 32;
   constexpr bool SWZ = (OPT & 2) && (DK == DP) && (DK == 32 || DK == 64 || DK == 128);
   constexpr bool MASK = (OPT & 16) != 0;
+  constexpr bool NARROW = (OPT & 64) != 0;
   // K/V tile row strides (halves): rows padded by 16 bytes, by 48 at D = 128
   // (fewer LDS bank conflicts there: 2-3% faster on causal bf16 D = 128,
   // no change at D = 64)
@@ -140,7 +145,10 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   for (int s = 0; s < NKS; ++s) {
     const int d = 16 * s + 8 * hh;
     u32x4 x = {0u, 0u, 0u, 0u};
-    if (qrow < Sq && d < D) x = *(const u32x4*)(qg + row_off(qrow, p.q_g, p.q_s) + d);
+    if (qrow < Sq && d < D) {
+      const uint16_t* src = qg + row_off(qrow, p.q_g, p.q_s) + d;
+      x = NARROW ? ld_cols16(src, D - d, p.elem_rows) : *(const u32x4*)src;
+    }
     if (PRESCALE) {
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
@@ -176,6 +184,10 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   const __amdgpu_buffer_rsrc_t vrs = uniform_rsrc(vg, ((int64_t)(Sk - 1) * p.v_s + D) * 2);
   int kvo[KLD], klo[KLD];
   bool kz[KLD];  // chunk lies in the zero-filled head-dim columns
+  // NARROW: byte offset of each 4-byte K piece; a piece past the head dim
+  // gets an offset beyond every buffer range (the host keeps ranges below
+  // 2^31, and 2^31 plus a tile offset stays below 2^32), so it reads zero
+  int kvp[NARROW ? KLD : 1][4];
 #pragma unroll
   for (int it = 0; it < KLD; ++it) {
     const int ci = it * NT + tid;
@@ -183,6 +195,10 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
     kz[it] = 8 * c8 >= D;
     kvo[it] = r * ks_b + 16 * c8;
     klo[it] = r * RSK + 8 * (SWZ ? (c8 ^ lds_swz<DK>(r)) : c8);
+    if constexpr (NARROW) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) kvp[it][w] = 8 * c8 + 2 * w < D ? kvo[it] + 4 * w : (int)0x80000000u;
+    }
   }
   int vvo[VLD], vlo[VLD];
 #pragma unroll
@@ -196,14 +212,28 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   auto load_k = [&](int j, u32x4 (&kr)[KLD]) {
     const int so = (tbase + min(j, ntiles - 1)) * BK * ks_b;
 #pragma unroll
-    for (int it = 0; it < KLD; ++it)
-      kr[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, kvo[it], so, 0));
+    for (int it = 0; it < KLD; ++it) {
+      if constexpr (NARROW) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) kr[it][w] = __builtin_amdgcn_raw_buffer_load_b32(krs, kvp[it][w], so, 0);
+      } else {
+        kr[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, kvo[it], so, 0));
+      }
+    }
   };
+  // NARROW: V pieces past the head dim read whatever follows (other rows, or
+  // zero past the buffer range); they only feed output columns never stored
   auto load_v = [&](int j, u32x4 (&vr)[VLD]) {
     const int so = (tbase + min(j, ntiles - 1)) * BK * vs_b;
 #pragma unroll
-    for (int it = 0; it < VLD; ++it)
-      vr[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vvo[it], so, 0));
+    for (int it = 0; it < VLD; ++it) {
+      if constexpr (NARROW) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) vr[it][w] = __builtin_amdgcn_raw_buffer_load_b32(vrs, vvo[it] + 4 * w, so, 0);
+      } else {
+        vr[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vvo[it], so, 0));
+      }
+    }
   };
   // K columns past D are zeroed (Q is zero there, and 0 * finite = 0 keeps
   // the padded k-steps exact); V columns past D only feed discarded outputs.
@@ -605,7 +635,10 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
           u32x2 w;
           w[0] = Elt<T>::pack(oacc[db][4 * g + 0] * inv, oacc[db][4 * g + 1] * inv);
           w[1] = Elt<T>::pack(oacc[db][4 * g + 2] * inv, oacc[db][4 * g + 3] * inv);
-          *(u32x2*)(orow + d) = w;
+          if (NARROW)
+            st_cols16x4(orow + d, w, D - d, p.elem_rows);
+          else
+            *(u32x2*)(orow + d) = w;
         }
       }
   }

@@ -224,6 +224,17 @@ hipError_t launch_lse(const FwdParams& p, const SplitArgs& sa, int dk, hipStream
                                   : launch_lse_m<T, CAUSAL, PRESCALE, 0>(p, sa, dk, s);
 }
 
+// Narrow rows (OPT 64, FwdParams::elem_rows 4 or 8): unmasked inference,
+// buckets 64 and 128 only (other head dims are zero-padded up to them).
+template <typename T, bool CAUSAL>
+hipError_t launch_narrow(const FwdParams& p, const SplitArgs& sa, int dk, hipStream_t s) {
+  if (dk == 64)
+    return launch_pipe16_cfg<T, 64, kPipeNw, kPipeBk, pipe_occ(64), CAUSAL, false, 1 | 64>(p, sa, s);
+  if (dk == 128)
+    return launch_pipe16_cfg<T, 128, kPipeNw, kPipeBk, pipe_occ(128), CAUSAL, false, 1 | 64>(p, sa, s);
+  return hipErrorNotSupported;
+}
+
 template <typename T, bool CAUSAL, bool PRESCALE, int MOPT = 0>
 hipError_t launch_bucket(const FwdParams& p, const SplitArgs& sa, int dk, hipStream_t s) {
   switch (dk) {
@@ -320,13 +331,15 @@ void pack_query_heads(FwdParams& p) {
 hipError_t launch_pipe16(const FwdParams& p0, int dk0, bool bf16, bool causal, bool prescale, hipStream_t s) {
   FwdParams p = p0;
   if (packs_query_heads(p, causal)) pack_query_heads(p);
-  // the training forward has the 64 and 128 buckets only
-  const int dk = p.lse ? (dk0 <= 64 ? 64 : 128) : dk0;
+  // the training forward and the narrow-row variants have the 64 and 128
+  // buckets only
+  const int dk = (p.lse || p.elem_rows) ? (dk0 <= 64 ? 64 : 128) : dk0;
+  if (p.elem_rows && (p.elem_rows < 4 || p.lse || p.mask_kind != MASK_NONE)) return hipErrorNotSupported;
   // Without pre-scaling, masked keys enter as raw -inf and meet the multiplier
   // c in one FMA; scale 0 would make that 0 * -inf.  A multiplier of 1e-30
   // instead leaves every finite score's exp2 argument within 1e-22 of -m,
   // which rounds to the same probability as scale 0 gives, and keeps -inf.
-  if (!prescale && p.c == 0.f) p.c = 1e-30f;
+  if ((!prescale || p.elem_rows) && p.c == 0.f) p.c = 1e-30f;
   const int cus = device_cus();
   const int occ = p.mask_kind != MASK_NONE ? pipe_occ_masked(dk) : pipe_occ(dk);
   const int n = n_blocks(p.B, p.H, p.Sq);
@@ -364,6 +377,11 @@ hipError_t launch_pipe16(const FwdParams& p0, int dk0, bool bf16, bool causal, b
     if (prescale)
       return causal ? launch_lse<_Float16, true, true>(p, sa, dk, s) : launch_lse<_Float16, false, true>(p, sa, dk, s);
     return causal ? launch_lse<_Float16, true, false>(p, sa, dk, s) : launch_lse<_Float16, false, false>(p, sa, dk, s);
+  }
+  if (p.elem_rows) {  // never pre-scaled: the narrow fp16 kernels then spill
+    if (bf16)
+      return causal ? launch_narrow<__bf16, true>(p, sa, dk, s) : launch_narrow<__bf16, false>(p, sa, dk, s);
+    return causal ? launch_narrow<_Float16, true>(p, sa, dk, s) : launch_narrow<_Float16, false>(p, sa, dk, s);
   }
   if (p.mask_kind != MASK_NONE) {  // with causal, a pair must pass both rules
     if (bf16)

@@ -14,8 +14,10 @@
 //     gets its output in [B,S,H,D] memory too, returned as the same kind of
 //     view (the reference's HFMA2 path does this for fp16, :1652);
 //   * head dims that are not a whole number of 16-byte chunks, and tensors
-//     whose base pointer or row strides are not 16-byte aligned, are repacked
-//     into zero-padded contiguous copies instead of being rejected;
+//     whose base pointer or row strides are not 16-byte aligned, run in place
+//     (narrow-row kernel variants); calls with an attn_mask, and 16-bit rows
+//     with an odd element count or offset (2-byte pieces, slower in place
+//     than copied), repack such inputs into zero-padded contiguous copies;
 //   * K/V may hold fewer heads than Q (grouped-query attention);
 //   * attn_mask (bool or additive f16/bf16/f32, broadcast like torch's SDPA)
 //     runs natively for f16/bf16 with D <= 128, alone or combined with causal
@@ -102,6 +104,22 @@ Mask prepare_mask(const torch::Tensor& m0, const torch::Tensor& query, int64_t B
   return mk;
 }
 
+// Would the C ABI read these rows in 2-byte pieces?  True for 16-bit dtypes
+// when the row length, a base pointer or a row stride is an odd number of
+// 16-bit elements (the ABI's piece size is the largest of 2/4/8/16 bytes
+// dividing all of them).
+bool two_byte_rows(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v,
+                   const torch::Tensor& o, int64_t D) {
+  if (q.element_size() != 2) return false;
+  uint64_t bits = (uint64_t)D * 2;
+  for (const torch::Tensor* t : {&q, &k, &v, &o}) {
+    bits |= (uintptr_t)t->data_ptr();
+    for (int i = 0; i < 3; ++i)
+      if (t->size(i) > 1) bits |= (uint64_t)t->stride(i) * 2;
+  }
+  return (bits & 3) != 0;
+}
+
 bool is_bshd_view(const torch::Tensor& t) {
   // [B,H,S,D] view of [B,S,H,D] memory
   const int64_t H = t.size(1), S = t.size(2), D = t.size(3);
@@ -155,9 +173,17 @@ torch::Tensor attention(torch::Tensor query, torch::Tensor key, torch::Tensor va
                           : torch::empty({B, H, Sq, D}, query.options());
   if (out.numel() == 0) return out;
 
-  int rc = launch(query, key, value, out, dtype, (int)D, scale, causal, mask, stream);
+  // Rows the C ABI would read in 2-byte pieces (f16/bf16 with an odd head dim
+  // or an odd element offset) go through the padded copy below instead: on
+  // MI355X the copies plus the vector-load kernel take about a third of the
+  // time of the in-place 2-byte path (D = 33: 45 us against 123 us).
+  int rc = two_byte_rows(query, key, value, out, D)
+               ? CMPEXT3_E_ALIGN
+               : launch(query, key, value, out, dtype, (int)D, scale, causal, mask, stream);
   if (rc == CMPEXT3_E_ALIGN || rc == CMPEXT3_E_HEAD_DIM) {
-    // Repack into contiguous copies zero-padded to whole 16-byte chunks.
+    // Masked calls, and 2-byte rows (the ABI runs any other layout in
+    // place): repack into contiguous copies zero-padded to whole 16-byte
+    // chunks.
     // Zero columns add nothing to Q K^T, and the padded V columns only produce
     // output columns that are cut away again; `scale` already used the true D.
     const int64_t chunk = (dtype == CMPEXT3_DTYPE_F32) ? 4 : 8;
