@@ -187,13 +187,14 @@ __device__ __forceinline__ u32x4 ld_cols32(const float* p, int n) {
 
 // Key split of the last query blocks: workgroups [0, nfull) take whole
 // blocks; the next (n_blocks - nfull) * nparts take one key range each of the
-// remaining blocks.  Per (split block, wave) the parts leave their partial O,
-// offset and row sum in ws; the last to arrive (counter in cnt) merges and
-// puts the counter back to zero.  nparts == 1: no split, ws/cnt unused.
+// remaining blocks.  Per (split block, wave) the parts leave their partial
+// O, offset and row sum in ws; one part merges them all and puts the two
+// counters of the (block, wave) in cnt back to zero (the protocols are in
+// attn_fwd_pipe16.h).  nparts == 1: no split, ws/cnt unused.
 struct SplitArgs {
   int nfull, nparts;
   f32x4* ws;  // split blocks * nparts * nwl * (float4 vectors per lane) * 64 float4
-  int* cnt;   // split blocks * nwl counters, zero between launches
+  int* cnt;   // 2 * split blocks * nwl counters, zero between launches
   // waves per block that hold query rows (and so exchange): NW, or fewer
   // when a single query block is shorter than the workgroup (decode)
   int nwl;

@@ -16,7 +16,8 @@
 // workgroups, which shortens every wave's dependency chain over the keys and
 // fills the idle CUs.  Every part leaves its fp32 (O, m, l) in the exchange
 // buffer; the last part of a (block, wave) to finish merges all of them in
-// part order and writes the output (the protocol of attn_fwd_pipe16.h).
+// part order and writes the output (the many-part protocol of
+// attn_fwd_pipe16.h).
 //
 // Reference: src/cuda/fp32_attention.cu:35-198 (one thread per query row,
 // serial D loops, non-causal only, Sq == Sk only, D <= 128, and 1/l taken
@@ -266,9 +267,10 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
     // a wave whose rows all lie past Sq has nothing to exchange; every part
     // of the block agrees on that
     if (qw0 >= Sq) return;
-    // Leave this part's state, then let the last part of the block merge
-    // (device-scope (aux 16 = sc1) 16-byte accesses, coherent across the
-    // XCDs' L2s; fp32 goes through bit casts because the builtins move dwords)
+    // Every part leaves its state and counts itself in; the last one in
+    // merges (its own state straight from registers) and writes the output.
+    // Device-scope (aux 16 = sc1) 16-byte accesses, coherent across the
+    // XCDs' L2s; fp32 goes through bit casts because the builtins move dwords.
     constexpr int NV = NQB * (NDB + 1);
     const int sb = lb - sa.nfull, nwl = sa.nwl;
     const __amdgpu_buffer_rsrc_t wsr = uniform_rsrc(sa.ws, (int64_t)(sb + 1) * nparts * nwl * NV * 64 * 16);
@@ -277,29 +279,47 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), wsr, off, 0, 16);
     };
     auto ld_ws = [&](int off) { return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wsr, off, 0, 16)); };
+    int* const ctr = sa.cnt + 2 * (sb * nwl + wave);  // parts in (the second counter is unused here)
+    // a row whose keys of this part are all masked holds nothing: offset -inf
+    float m_own[NQB];
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
+      m_own[qb] = lrow[qb] > 0.f ? m_run[qb] : -INFINITY;
 #pragma unroll
       for (int db = 0; db < NDB; ++db) st_ws(oacc[qb][db], voff(part, qb * (NDB + 1) + db));
-      // a row whose keys of this part are all masked holds nothing: offset -inf
-      st_ws((f32x4){lrow[qb] > 0.f ? m_run[qb] : -INFINITY, lrow[qb], 0.f, 0.f}, voff(part, qb * (NDB + 1) + NDB));
+      st_ws((f32x4){m_own[qb], lrow[qb], 0.f, 0.f}, voff(part, qb * (NDB + 1) + NDB));
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     int old = 0;
-    if (lane == 0) old = __hip_atomic_fetch_add(sa.cnt + sb * nwl + wave, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     old = __builtin_amdgcn_readfirstlane(old);
     if (old != nparts - 1) return;
-    if (lane == 0) __hip_atomic_store(sa.cnt + sb * nwl + wave, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // merge every part, this one included, in part order: the same
+    if (lane == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("" ::: "memory");  // the exchange loads stay after the count
+    // merge in part order, this part from its registers: the same
     // instructions on the same values whichever part arrives last
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
-      float mt = -INFINITY;
-      for (int q = 0; q < nparts; ++q) mt = fmaxf(mt, ld_ws(voff(q, qb * (NDB + 1) + NDB))[0]);
+      float mt = m_own[qb];
+      for (int q = 0; q < nparts; ++q)
+        if (q != part) mt = fmaxf(mt, ld_ws(voff(q, qb * (NDB + 1) + NDB))[0]);
+      f32x4 own[NDB];
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) oacc[qb][db] = (f32x4){};
+      for (int db = 0; db < NDB; ++db) {
+        own[db] = oacc[qb][db];
+        oacc[qb][db] = (f32x4){};
+      }
       float l = 0.f;
       for (int q = 0; q < nparts; ++q) {
+        if (q == part) {
+          const float a = m_own[qb] == -INFINITY ? 0.f : fast_exp2(m_own[qb] - mt);
+          l = __builtin_fmaf(lrow[qb], a, l);
+#pragma unroll
+          for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) oacc[qb][db][i] = __builtin_fmaf(own[db][i], a, oacc[qb][db][i]);
+          continue;
+        }
         const f32x4 ml = ld_ws(voff(q, qb * (NDB + 1) + NDB));
         const float a = ml[0] == -INFINITY ? 0.f : fast_exp2(ml[0] - mt);
         l = __builtin_fmaf(ml[1], a, l);
@@ -369,7 +389,7 @@ hipError_t launch_mfma32_inst(const FwdParams& p0, hipStream_t stream) {
       const size_t ws_bytes = (size_t)n * parts * nwl * NQB * (NDB + 1) * 64 * sizeof(f32x4);
       f32x4* ws = nullptr;
       int* cnt = nullptr;
-      if (split_exchange(stream, p.fixed_exchange != 0, ws_bytes, n * nwl, &ws, &cnt))
+      if (split_exchange(stream, p.fixed_exchange != 0, ws_bytes, 2 * n * nwl, &ws, &cnt))
         sa = SplitArgs{0, parts, ws, cnt, nwl};
     }
   }

@@ -44,6 +44,8 @@
 // Reference algorithm: src/cuda/fp16_flash_attention_hfma2.cu:72-243.
 #pragma once
 
+#include <type_traits>
+
 #include "attn_fwd_mfma16.h"
 
 namespace cmpext3 {
@@ -564,57 +566,153 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   // nothing to exchange or store; every part of the block agrees on that
   if (qlo >= Sq) return;
   if (!CAUSAL && nparts > 1) {  // causal launches never split
-    // Leave this part's state, then let the last part of the block merge.
-    // Device-scope (sc1) stores and loads keep the exchange coherent across
-    // the XCDs' L2s without cache-wide write-back or invalidation.
+    // Leave this part's state, then let the last part of the block merge
+    // (its own state straight from its registers).  Two parts (the
+    // tail of a whole-round grid, where each part holds up to 36 KB per
+    // 128-row block): a ticket is taken first, so only the first part writes
+    // and the second waits for it (it holds a ticket, so it is resident with
+    // only its stores left).  More parts (short-query grids, whose parts end
+    // together): every part writes, then counts itself in, and the last one
+    // in merges with no wait.  Device-scope (sc1) stores and loads keep the
+    // exchange coherent across the XCDs' L2s without cache-wide write-back
+    // or invalidation.
     constexpr int NV = split_vectors(DP);
     static_assert(NV == NDB * 4 + 1, "O fragments + (m, l)");
     const int sb = lb - sa.nfull;
     const int nwl = sa.nwl;  // waves past it hold no rows and left above
     const __amdgpu_buffer_rsrc_t wsr = uniform_rsrc(sa.ws, (int64_t)(sb + 1) * nparts * nwl * NV * 64 * 16);
     auto voff = [&](int q, int k) { return ((((sb * nparts + q) * nwl + wave) * NV + k) * 64 + lane) * 16; };
+    // Every lane moves its vectors, also lanes of rows past Sq (a decode
+    // step's wave holds one or two live rows): whole 1 KB runs per
+    // instruction measured faster than the sparse 16-byte pieces of the live
+    // rows alone (decode step 49.1 vs 51.1 us), partial lines being costlier
+    // to write through to memory than full ones.
     // device-scope (aux 16 = sc1) 16-byte accesses; the builtins move dwords, so the
     // fp32 values go through explicit bit casts
     auto st_ws = [&](f32x4 x, int off) {
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), wsr, off, 0, 16);
     };
     auto ld_ws = [&](int off) { return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wsr, off, 0, 16)); };
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        st_ws((f32x4){oacc[db][4 * g], oacc[db][4 * g + 1], oacc[db][4 * g + 2], oacc[db][4 * g + 3]},
-              voff(part, db * 4 + g));
+    int* const ctr = sa.cnt + 2 * (sb * nwl + wave);  // {parts in, parts written}
     // a part whose keys are all masked for this row holds nothing: offset -inf
-    st_ws((f32x4){lsum > 0.f ? mb : -INFINITY, lsum, 0.f, 0.f}, voff(part, NDB * 4));
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    int old = 0;
-    if (lane == 0) old = __hip_atomic_fetch_add(sa.cnt + sb * nwl + wave, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    old = __builtin_amdgcn_readfirstlane(old);
-    if (old != nparts - 1) return;
-    if (lane == 0) __hip_atomic_store(sa.cnt + sb * nwl + wave, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // Merge every part, this one included, from the exchange buffer in part
-    // order: the same instructions on the same values whichever part arrives
-    // last, so a rerun is bit-identical.
-    float mt = -INFINITY;
-    for (int q = 0; q < nparts; ++q) mt = fmaxf(mt, ld_ws(voff(q, NDB * 4))[0]);
-    moff = mt;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) oacc[db] = (f32x16){};
-    lsum = 0.f;
-    for (int q = 0; q < nparts; ++q) {
-      const f32x4 ml = ld_ws(voff(q, NDB * 4));
-      const float a = ml[0] == -INFINITY ? 0.f : fast_exp2(ml[0] - mt);
-      lsum = __builtin_fmaf(ml[1], a, lsum);
+    const float m_own = lsum > 0.f ? mb : -INFINITY;
+    // Two fp16 parts exchange their O normalised by their own row sum, in
+    // fp16 (a quarter of the bytes): 2 * NDB vectors, then (m, l) as 8 bytes
+    // per lane.  Both parts round their own O this way, so the result does
+    // not depend on which one writes (reruns stay bit-identical); rounding O/l
+    // to fp16 before the merge adds at most one fp16 rounding to the output.
+    const bool half_x = std::is_same<T, _Float16>::value && nparts == 2;
+    auto ml_off = [&](int q) {
+      return ((((sb * nparts + q) * nwl + wave) * NV + 2 * NDB) * 64) * 16 + lane * 8;
+    };
+    u32x4 own_h[2 * NDB];  // half_x: this part's O / l in fp16
+    if (half_x) {
+      const float il = lsum > 0.f ? 1.f / lsum : 0.f;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4 x = ld_ws(voff(q, db * 4 + g));
-#pragma unroll
-          for (int i = 0; i < 4; ++i) oacc[db][4 * g + i] = __builtin_fmaf(x[i], a, oacc[db][4 * g + i]);
-        }
+        for (int w = 0; w < 8; ++w)
+          own_h[2 * db + w / 4][w % 4] = Elt<T>::pack(oacc[db][2 * w] * il, oacc[db][2 * w + 1] * il);
     }
+    auto leave_state = [&]() {
+      if (half_x) {
+#pragma unroll
+        for (int v = 0; v < 2 * NDB; ++v)
+          __builtin_amdgcn_raw_buffer_store_b128(own_h[v], wsr, voff(part, v), 0, 16);
+        __builtin_amdgcn_raw_buffer_store_b64((u32x2){__float_as_uint(m_own), __float_as_uint(lsum)}, wsr,
+                                              ml_off(part), 0, 16);
+      } else {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            st_ws((f32x4){oacc[db][4 * g], oacc[db][4 * g + 1], oacc[db][4 * g + 2], oacc[db][4 * g + 3]},
+                  voff(part, db * 4 + g));
+        st_ws((f32x4){m_own, lsum, 0.f, 0.f}, voff(part, NDB * 4));
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    };
+    if (nparts == 2) {
+      int ticket = 0;
+      if (lane == 0) ticket = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ticket = __builtin_amdgcn_readfirstlane(ticket);
+      if (ticket == 0) {
+        leave_state();
+        if (lane == 0) __hip_atomic_store(ctr + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+      }
+      if (lane == 0) {
+        while (__hip_atomic_load(ctr + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0)
+          __builtin_amdgcn_s_sleep(1);
+        __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(ctr + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    } else {
+      leave_state();
+      int old = 0;
+      if (lane == 0) old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      old = __builtin_amdgcn_readfirstlane(old);
+      if (old != nparts - 1) return;
+      if (lane == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("" ::: "memory");  // the exchange loads stay after the wait
+    // Merge every part in part order, this one from its registers: the same
+    // instructions on the same values whichever part arrives last, so a
+    // rerun is bit-identical.
+    auto ml_of = [&](int q) -> f32x2 {
+      if (q == part) return (f32x2){m_own, lsum};
+      if (half_x) {
+        const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wsr, ml_off(q), 0, 16));
+        return (f32x2){__uint_as_float(w[0]), __uint_as_float(w[1])};
+      }
+      const f32x4 x = ld_ws(voff(q, NDB * 4));
+      return (f32x2){x[0], x[1]};
+    };
+    float mt = -INFINITY;
+    for (int q = 0; q < nparts; ++q) mt = fmaxf(mt, ml_of(q)[0]);
+    moff = mt;
+    f32x16 own[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      own[db] = oacc[db];
+      oacc[db] = (f32x16){};
+    }
+    float lnew = 0.f;
+    for (int q = 0; q < nparts; ++q) {
+      const f32x2 ml = ml_of(q);
+      const float a = ml[0] == -INFINITY ? 0.f : fast_exp2(ml[0] - mt);
+      lnew = __builtin_fmaf(ml[1], a, lnew);
+      if (half_x) {  // O / l in fp16, weighted by a * l
+        const float wq = a * ml[1];
+#pragma unroll
+        for (int v = 0; v < 2 * NDB; ++v) {
+          const u32x4 x = q == part ? own_h[v]
+                                    : __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wsr, voff(q, v), 0, 16));
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const f32x2 f = Elt<T>::unpack(x[w]);
+            const int i = 8 * (v & 1) + 2 * w;
+            oacc[v / 2][i] = __builtin_fmaf(f[0], wq, oacc[v / 2][i]);
+            oacc[v / 2][i + 1] = __builtin_fmaf(f[1], wq, oacc[v / 2][i + 1]);
+          }
+        }
+      } else if (q == part) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) oacc[db][i] = __builtin_fmaf(own[db][i], a, oacc[db][i]);
+      } else {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const f32x4 x = ld_ws(voff(q, db * 4 + g));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) oacc[db][4 * g + i] = __builtin_fmaf(x[i], a, oacc[db][4 * g + i]);
+          }
+      }
+    }
+    lsum = lnew;
   }
   // a row that saw no key at all (every key masked) gives zeros, as torch does
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;

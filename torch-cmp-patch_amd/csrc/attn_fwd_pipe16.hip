@@ -53,7 +53,8 @@ struct Exchange {
 size_t exchange_ws_bytes(int cus) {
   return (size_t)cus * kMaxPartsPerCu * kPipeNw * split_vectors(128) * 64 * sizeof(f32x4);
 }
-size_t exchange_cnt_bytes(int cus) { return (size_t)cus * kPipeNw * sizeof(int); }
+// two counters (tickets taken, parts written) per (split block, wave)
+size_t exchange_cnt_bytes(int cus) { return (size_t)2 * cus * kPipeNw * sizeof(int); }
 
 // The exchange buffer of (current device, stream s), allocated on first use.
 // A stream under graph capture never gets one, not even the buffer it already
@@ -352,7 +353,7 @@ hipError_t launch_pipe16(const FwdParams& p0, int dk0, bool bf16, bool causal, b
     const int dp = (dk + 31) / 32 * 32;
     const int nsplit = n - sa.nfull;
     const size_t per_part = (size_t)nsplit * sa.nwl * split_vectors(dp) * 64 * sizeof(f32x4);
-    const int fit = (int64_t)nsplit * sa.nwl > kScratchCounters ? 0 : (int)(kScratchWsBytes / per_part);
+    const int fit = (int64_t)2 * nsplit * sa.nwl > kScratchCounters ? 0 : (int)(kScratchWsBytes / per_part);
     if (sa.nparts > fit) sa.nparts = fit;
     if (sa.nparts < 2) {
       sa = whole;
