@@ -130,6 +130,23 @@ def test_large_head_dims_long_key_sweeps(dtype, D, causal, Sq, Sk, scale):
     assert err <= TOL[dtype], f"max abs err {err:.3e}"
 
 
+@pytest.mark.parametrize("Sk", [1, 17, 48, 49, 64, 65, 77, 80, 81, 100, 112, 113, 128])
+@pytest.mark.parametrize("dtype,D", [("fp16", 64), ("bf16", 40)])
+def test_short_key_slices(Sk, dtype, D):
+    """The short-key kernel at every 16-key slice count (3..8 slices: the
+    exponentials and PV MFMAs of slices past Sk are skipped), keys ragged
+    inside a slice and at slice edges."""
+    rc, text = abi.describe(abi.dtype_code(W.DTYPES[dtype]), 1, 3, 200, Sk, D)
+    assert rc == abi.OK and "short16" in text and f"keys<={16 * max(3, (Sk + 15) // 16)}" in text, text
+    q, k, v = _inputs(dtype, 1, 3, 200, Sk, D, seed=Sk)
+    print(f"short keys: {dtype} D={D} Sk={Sk}", flush=True)
+    out = abi.attn_fwd(q, k, v, D ** -0.5, False)
+    torch.cuda.synchronize()
+    ref = orc.sdpa_c(q.cpu(), k.cpu(), v.cpu(), D ** -0.5, False)
+    err = orc.max_abs_err(out.cpu(), ref)
+    assert err <= TOL[dtype], f"max abs err {err:.3e}"
+
+
 def _sample_rows(S, n_spread=200, seed=0):
     rng = np.random.default_rng(seed)
     tail = range(S - 150, S)                       # the ragged last block and tile

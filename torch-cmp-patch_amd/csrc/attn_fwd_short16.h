@@ -21,9 +21,13 @@ namespace cmpext3 {
 
 // OPT bit 0: s_setprio(1) around the MFMAs.  OPT bit 3: D < DK, K columns past
 // D are zeroed (Q is zero there, and 0 * finite keeps the padded k-steps exact).
-template <typename T, int DK, int DP, int NKB, int OPT = 0>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NKB <= 2 ? 3 : 2)))
+// NKH: 16-key slices that can hold keys (Sk <= 16 * NKH); the scores come in
+// blocks of 32 keys (NKB = ceil(NKH / 2)), but exponentials and PV MFMAs of a
+// slice past NKH are skipped (Sk = 77: 5 of 6 slices).
+template <typename T, int DK, int DP, int NKH, int OPT = 0>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((NKH + 1) / 2 <= 2 ? 3 : 2)))
 attn_fwd_short16(const FwdParams p) {
+  constexpr int NKB = (NKH + 1) / 2;
   constexpr int NW = 4, NT = 256, BQ = 128;
   constexpr int SK = 32 * NKB;             // keys held (padded)
   constexpr int RSK = DK + 8, RSV = DP + 8;
@@ -32,10 +36,10 @@ attn_fwd_short16(const FwdParams p) {
   constexpr int VLD = (SK * VCH + NT - 1) / NT;
   constexpr bool KFULL = SK * KCH % NT == 0;
   constexpr bool VFULL = SK * VCH % NT == 0;
-  constexpr int NCH = SK / 16;             // 16-key PV slices
+  constexpr int NCH = NKH;                 // 16-key PV slices that hold keys
   constexpr int NDB = DP / 32;
   constexpr int NKS = DK / 16;
-  static_assert(NKB >= 1 && NKB <= 4 && DK % 16 == 0 && DP % 32 == 0 && DK <= DP, "tile shape");
+  static_assert(NKH >= 1 && NKH <= 8 && DK % 16 == 0 && DP % 32 == 0 && DK <= DP, "tile shape");
 
   constexpr int RSQ = DP + 8;              // Q / O staging row stride (halves)
   constexpr int QLD = 32 * KCH / 64;       // 16-byte Q chunks per lane (32 rows per wave)
@@ -133,6 +137,7 @@ attn_fwd_short16(const FwdParams p) {
   for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
+      if (2 * kb + (r >> 3) >= NKH) continue;  // a slice past every key
       const int key = 32 * kb + acc_key(r, hh);
       float x = sc[kb][r] * c;
       if (key >= Sk) x = -INFINITY;
@@ -196,8 +201,9 @@ attn_fwd_short16(const FwdParams p) {
   }
 }
 
-template <typename T, int DK, int NKB, int OPT = 0>
+template <typename T, int DK, int NKH, int OPT = 0>
 hipError_t launch_short16_cfg(const FwdParams& p0, hipStream_t stream) {
+  constexpr int NKB = (NKH + 1) / 2;
   constexpr int DP = (DK + 31) / 32 * 32;
   FwdParams p = p0;
   p.n_qblk = (p.Sq + 127) / 128;
@@ -205,7 +211,7 @@ hipError_t launch_short16_cfg(const FwdParams& p0, hipStream_t stream) {
   if (p.n_wg == 0) return hipSuccess;
   const int64_t rs = p.k_s > p.v_s ? p.k_s : p.v_s;
   if ((int64_t)(32 * NKB) * rs * 2 >= (int64_t(1) << 31)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((attn_fwd_short16<T, DK, DP, NKB, OPT>), dim3(p.n_wg), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((attn_fwd_short16<T, DK, DP, NKH, OPT>), dim3(p.n_wg), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
