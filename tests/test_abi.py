@@ -92,6 +92,10 @@ def test_describe_key_split_plan():
     # parts per CU, at least 4 tiles of 32 keys each), never causal
     f32 = abi.DTYPE_F32
     assert "key-split: 128 x 4 parts" in abi.describe(f32, 1, 8, 1024, 1024, 64)[1]
+    # split launches of D <= 64 take 64-key tiles where that keeps the part count
+    assert "BK=64" in abi.describe(f32, 1, 8, 1024, 1024, 64)[1]
+    assert "BK=32" in abi.describe(f32, 1, 2, 100, 700, 40)[1]
+    assert "BK=32" in abi.describe(f32, 2, 8, 4096, 4096, 64)[1]
     assert "key-split" not in abi.describe(f32, 1, 8, 1024, 1024, 64, True)[1]
     assert "key-split" not in abi.describe(f32, 2, 8, 4096, 4096, 40)[1]
     assert "key-split: 4 x 5 parts" in abi.describe(f32, 1, 2, 100, 700, 40)[1]

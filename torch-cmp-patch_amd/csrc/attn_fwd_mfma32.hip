@@ -297,12 +297,22 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
     if (lane == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     asm volatile("" ::: "memory");  // the exchange loads stay after the count
     // merge in part order, this part from its registers: the same
-    // instructions on the same values whichever part arrives last
+    // instructions on the same values whichever part arrives last.  The
+    // exchange loads of CH parts are issued together (one memory round trip
+    // per CH parts instead of one per part); part indices past the last are
+    // clamped to it and their values dropped.
+    constexpr int CH = 4;
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
       float mt = m_own[qb];
-      for (int q = 0; q < nparts; ++q)
-        if (q != part) mt = fmaxf(mt, ld_ws(voff(q, qb * (NDB + 1) + NDB))[0]);
+      for (int q0 = 0; q0 < nparts; q0 += CH) {
+        float mq[CH];
+#pragma unroll
+        for (int j = 0; j < CH; ++j) mq[j] = ld_ws(voff(min(q0 + j, nparts - 1), qb * (NDB + 1) + NDB))[0];
+#pragma unroll
+        for (int j = 0; j < CH; ++j)
+          if (q0 + j < nparts && q0 + j != part) mt = fmaxf(mt, mq[j]);
+      }
       f32x4 own[NDB];
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
@@ -310,24 +320,28 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
         oacc[qb][db] = (f32x4){};
       }
       float l = 0.f;
-      for (int q = 0; q < nparts; ++q) {
-        if (q == part) {
-          const float a = m_own[qb] == -INFINITY ? 0.f : fast_exp2(m_own[qb] - mt);
-          l = __builtin_fmaf(lrow[qb], a, l);
+      for (int q0 = 0; q0 < nparts; q0 += CH) {
+        f32x4 ml[CH], x[CH][NDB];
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+          const int qq = min(q0 + j, nparts - 1);
+          ml[j] = ld_ws(voff(qq, qb * (NDB + 1) + NDB));
+#pragma unroll
+          for (int db = 0; db < NDB; ++db) x[j][db] = ld_ws(voff(qq, qb * (NDB + 1) + db));
+        }
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+          const int q = q0 + j;
+          if (q >= nparts) break;
+          const bool mine = q == part;
+          const float mq = mine ? m_own[qb] : ml[j][0];
+          const float a = mq == -INFINITY ? 0.f : fast_exp2(mq - mt);
+          l = __builtin_fmaf(mine ? lrow[qb] : ml[j][1], a, l);
 #pragma unroll
           for (int db = 0; db < NDB; ++db)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) oacc[qb][db][i] = __builtin_fmaf(own[db][i], a, oacc[qb][db][i]);
-          continue;
-        }
-        const f32x4 ml = ld_ws(voff(q, qb * (NDB + 1) + NDB));
-        const float a = ml[0] == -INFINITY ? 0.f : fast_exp2(ml[0] - mt);
-        l = __builtin_fmaf(ml[1], a, l);
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const f32x4 x = ld_ws(voff(q, qb * (NDB + 1) + db));
-#pragma unroll
-          for (int i = 0; i < 4; ++i) oacc[qb][db][i] = __builtin_fmaf(x[i], a, oacc[qb][db][i]);
+            for (int i = 0; i < 4; ++i)
+              oacc[qb][db][i] = __builtin_fmaf(mine ? own[db][i] : x[j][db][i], a, oacc[qb][db][i]);
         }
       }
       lrow[qb] = l;
@@ -358,18 +372,37 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
 
 // Key split plan: only when the query blocks leave CUs idle (fewer blocks than
 // CUs), non-causal, into enough parts for about two workgroups per CU, each
-// part at least kMinTiles32 key tiles long.
+// part at least kMinTiles32 key tiles long.  Returns the part count (1: no
+// split) for n query blocks and bk-key tiles.
 constexpr int kMinTiles32 = 4;
+int split_parts32(int n, int Sk, int bk, int cus, bool causal) {
+  if (causal || n <= 0 || n >= cus) return 1;
+  int parts = 2 * cus / n;
+  const int ntiles = (Sk + bk - 1) / bk;
+  if (parts > ntiles / kMinTiles32) parts = ntiles / kMinTiles32;
+  return parts >= 2 ? parts : 1;
+}
 
-template <int DK, bool CAUSAL, bool ELEM>
-hipError_t launch_mfma32_inst(const FwdParams& p0, hipStream_t stream) {
+// Keys per tile: 32 (16 above D = 128); split launches of head dims up to 64
+// take 64-key tiles, half the barriers per key, where that keeps the part
+// count (measured on MI355X: [1,8,1024,1024,64], 128 blocks x 4 parts,
+// 34.1 -> 33.0 us; an unsplit [2,8,4096,4096,64] is faster with 32, 601 vs
+// 635 us).
+int tile_keys32(int dk, int n, int Sk, int cus, bool causal) {
+  const int def = dk <= 128 ? 32 : 16;
+  if (dk > 64) return def;
+  const int p64 = split_parts32(n, Sk, 64, cus, causal);
+  return p64 >= 2 && p64 == split_parts32(n, Sk, def, cus, causal) ? 64 : def;
+}
+
+template <int DK, bool CAUSAL, bool ELEM, int BK>
+hipError_t launch_mfma32_bk(const FwdParams& p0, hipStream_t stream) {
   // One 16-row query block per wave: measured on MI355X, two per wave only
   // lengthen each wave's dependency chain (1.6x slower on [1,8,1024,1024,64],
   // 19% slower causal, equal on [2,8,4096,4096,40]), and 64-row workgroups
   // fill more CUs on small grids.
   constexpr int NW = 4;
   constexpr int NQB = 1;
-  constexpr int BK = (DK <= 128) ? 32 : 16;
   constexpr int BQ = NW * 16 * NQB;
   constexpr int NDB = (DK + 15) / 16;
   FwdParams p = p0;
@@ -380,23 +413,29 @@ hipError_t launch_mfma32_inst(const FwdParams& p0, hipStream_t stream) {
   // waves per block that hold query rows (a single block shorter than BQ has fewer)
   const int nwl = p.n_qblk > 1 ? NW : (p.Sq + 15) / 16 < NW ? (p.Sq + 15) / 16 : NW;
   SplitArgs sa = {n, 1, nullptr, nullptr, nwl};
-  const int cus = device_cus();
-  if (!CAUSAL && n < cus) {
-    int parts = 2 * cus / n;
-    const int ntiles = (p.Sk + BK - 1) / BK;
-    if (parts > ntiles / kMinTiles32) parts = ntiles / kMinTiles32;
-    if (parts >= 2) {
-      const size_t ws_bytes = (size_t)n * parts * nwl * NQB * (NDB + 1) * 64 * sizeof(f32x4);
-      f32x4* ws = nullptr;
-      int* cnt = nullptr;
-      if (split_exchange(stream, p.fixed_exchange != 0, ws_bytes, 2 * n * nwl, &ws, &cnt))
-        sa = SplitArgs{0, parts, ws, cnt, nwl};
-    }
+  const int parts = split_parts32(n, p.Sk, BK, device_cus(), CAUSAL);
+  if (parts >= 2) {
+    const size_t ws_bytes = (size_t)n * parts * nwl * NQB * (NDB + 1) * 64 * sizeof(f32x4);
+    f32x4* ws = nullptr;
+    int* cnt = nullptr;
+    if (split_exchange(stream, p.fixed_exchange != 0, ws_bytes, 2 * n * nwl, &ws, &cnt))
+      sa = SplitArgs{0, parts, ws, cnt, nwl};
   }
   const int nwg = sa.nfull + (n - sa.nfull) * sa.nparts;
   hipLaunchKernelGGL((attn_fwd_mfma32<DK, NW, NQB, BK, CAUSAL, ELEM>), dim3(nwg), dim3(NW * 64), 0, stream, p,
                      sa);
   return hipGetLastError();
+}
+
+template <int DK, bool CAUSAL, bool ELEM>
+hipError_t launch_mfma32_inst(const FwdParams& p, hipStream_t stream) {
+  constexpr int BK = (DK <= 128) ? 32 : 16;
+  if constexpr (!CAUSAL && DK <= 64) {
+    const int n = p.B * p.H * ((p.Sq + 63) / 64);
+    if (tile_keys32(DK, n, p.Sk, device_cus(), CAUSAL) == 64)
+      return launch_mfma32_bk<DK, CAUSAL, ELEM, 64>(p, stream);
+  }
+  return launch_mfma32_bk<DK, CAUSAL, ELEM, BK>(p, stream);
 }
 
 static const int kMfma32Dk[] = {16, 32, 40, 48, 64, 80, 96, 128, 160, 192, 256};
@@ -435,13 +474,10 @@ hipError_t launch_mfma32(const FwdParams& p, bool causal, hipStream_t s) {
 
 void describe_mfma32(int D, int B, int H, int Sq, int Sk, bool causal, char* buf, int len) {
   const int dk = mfma32_bucket(D);
-  const int bq = 64, bk = dk <= 128 ? 32 : 16;
+  const int bq = 64;
   const int n = B * H * ((Sq + bq - 1) / bq), cus = device_cus();
-  int parts = 1;
-  if (!causal && n > 0 && n < cus) {
-    parts = 2 * cus / n;
-    if (parts > (Sk + bk - 1) / bk / kMinTiles32) parts = (Sk + bk - 1) / bk / kMinTiles32;
-  }
+  const int bk = tile_keys32(dk, n, Sk, cus, causal);
+  const int parts = split_parts32(n, Sk, bk, cus, causal);
   char split[48] = "";
   if (parts >= 2) snprintf(split, sizeof split, " key-split: %d x %d parts", n, parts);
   snprintf(buf, len, "mfma32 16x16x4f32 S^T-form: DK=%d DPV=%d waves=4 BQ=%d BK=%d qblocks=%d%s%s", dk,

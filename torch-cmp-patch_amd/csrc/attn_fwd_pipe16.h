@@ -668,8 +668,25 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
       const f32x4 x = ld_ws(voff(q, NDB * 4));
       return (f32x2){x[0], x[1]};
     };
-    float mt = -INFINITY;
-    for (int q = 0; q < nparts; ++q) mt = fmaxf(mt, ml_of(q)[0]);
+    // fp32 exchange: the loads of CH parts are issued together (one memory
+    // round trip per CH parts, not per part); part indices past the last are
+    // clamped to it and dropped, the own part's loads (of whatever its slot
+    // holds) are replaced by its registers.
+    constexpr int CH = 4;                   // parts per batch of offset loads
+    constexpr int CH2 = NDB <= 2 ? 2 : 1;   // parts per batch of O loads (registers)
+    float mt = m_own;
+    if (half_x) {
+      mt = fmaxf(mt, ml_of(1 - part)[0]);
+    } else {
+      for (int q0 = 0; q0 < nparts; q0 += CH) {
+        float mq[CH];
+#pragma unroll
+        for (int j = 0; j < CH; ++j) mq[j] = ld_ws(voff(min(q0 + j, nparts - 1), NDB * 4))[0];
+#pragma unroll
+        for (int j = 0; j < CH; ++j)
+          if (q0 + j < nparts && q0 + j != part) mt = fmaxf(mt, mq[j]);
+      }
+    }
     moff = mt;
     f32x16 own[NDB];
 #pragma unroll
@@ -678,11 +695,11 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
       oacc[db] = (f32x16){};
     }
     float lnew = 0.f;
-    for (int q = 0; q < nparts; ++q) {
-      const f32x2 ml = ml_of(q);
-      const float a = ml[0] == -INFINITY ? 0.f : fast_exp2(ml[0] - mt);
-      lnew = __builtin_fmaf(ml[1], a, lnew);
-      if (half_x) {  // O / l in fp16, weighted by a * l
+    if (half_x) {
+      for (int q = 0; q < nparts; ++q) {  // O / l in fp16, weighted by a * l
+        const f32x2 ml = ml_of(q);
+        const float a = ml[0] == -INFINITY ? 0.f : fast_exp2(ml[0] - mt);
+        lnew = __builtin_fmaf(ml[1], a, lnew);
         const float wq = a * ml[1];
 #pragma unroll
         for (int v = 0; v < 2 * NDB; ++v) {
@@ -696,20 +713,34 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
             oacc[v / 2][i + 1] = __builtin_fmaf(f[1], wq, oacc[v / 2][i + 1]);
           }
         }
-      } else if (q == part) {
+      }
+    } else {
+      for (int q0 = 0; q0 < nparts; q0 += CH2) {
+        f32x4 ml[CH2], x[CH2][NDB * 4];
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
+        for (int j = 0; j < CH2; ++j) {
+          const int qq = min(q0 + j, nparts - 1);
+          ml[j] = ld_ws(voff(qq, NDB * 4));
 #pragma unroll
-          for (int i = 0; i < 16; ++i) oacc[db][i] = __builtin_fmaf(own[db][i], a, oacc[db][i]);
-      } else {
+          for (int v = 0; v < NDB * 4; ++v) x[j][v] = ld_ws(voff(qq, v));
+        }
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
+        for (int j = 0; j < CH2; ++j) {
+          const int q = q0 + j;
+          if (q >= nparts) break;
+          const bool mine = q == part;
+          const float mq = mine ? m_own : ml[j][0];
+          const float a = mq == -INFINITY ? 0.f : fast_exp2(mq - mt);
+          lnew = __builtin_fmaf(mine ? lsum : ml[j][1], a, lnew);
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const f32x4 x = ld_ws(voff(q, db * 4 + g));
+          for (int db = 0; db < NDB; ++db)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) oacc[db][4 * g + i] = __builtin_fmaf(x[i], a, oacc[db][4 * g + i]);
-          }
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                oacc[db][4 * g + i] =
+                    __builtin_fmaf(mine ? own[db][4 * g + i] : x[j][db * 4 + g][i], a, oacc[db][4 * g + i]);
+        }
       }
     }
     lsum = lnew;
