@@ -5,12 +5,18 @@
  * [B, H, S, D] tensors that already live in device memory.  The caller owns
  * every input and output buffer.  The library itself keeps one exchange
  * buffer per (device, stream) for launches that split key ranges across
- * workgroups (fp16/bf16, non-causal, D <= 128, when the query blocks do not
- * fill whole rounds of the GPU): allocated with hipMalloc on the first such
- * launch on that stream (about 70 KB per CU), kept until the process ends.
- * On a stream under graph capture, after a failed allocation, or past 16
- * streams per device those launches run without the split, with the same
- * results.  All launches go on the stream the caller passes.
+ * workgroups (non-causal, when the query blocks do not fill whole rounds of
+ * the GPU; fp16/bf16 with D <= 128, and fp32 with fewer query blocks than
+ * CUs): allocated with hipMalloc on the first such launch on that stream
+ * (about 140 KB per CU), kept until the process ends, so at most 16 of them
+ * per device.  On a stream under graph capture, after a failed allocation,
+ * or past 16 streams per device those launches run without the split: the
+ * same result within rounding (a split adds the parts' partial sums in
+ * another order, and two-part fp16 splits round each part's O/l to fp16),
+ * bit-identical from one call to the next either way.  Launches on one
+ * stream are ordered, so a stream's buffer is never used by two launches at
+ * once; graph replays are unsplit and share nothing.  All launches go on the
+ * stream the caller passes.
  *
  * Reference interfaces this replaces (WifiLast/torch-cmp-patch):
  *   - launch_flash_attention_hfma2(q, k, v, o, B, H, Sq, Sk, D, qs, ks, vs, os,
