@@ -147,6 +147,30 @@ def test_short_key_slices(Sk, dtype, D):
     assert err <= TOL[dtype], f"max abs err {err:.3e}"
 
 
+@pytest.mark.parametrize("dtype,D,layout,scale,shape", [
+    ("fp16", 40, "bshd", None, (2, 3, 130, 77)),    # [B,S,H,D] view, D below its bucket
+    ("bf16", 64, "bshd", -0.125, (1, 4, 257, 50)),  # negative scale
+    ("fp16", 64, "bhsd", 0.0, (1, 2, 100, 33)),     # scale 0: uniform weights
+    ("fp16", 96, "bshd", 0.5, (1, 2, 31, 128)),     # fewer rows than one wave holds
+    ("bf16", 128, "bhsd", None, (1, 3, 4096, 120)),  # a long sweep of query blocks
+])
+def test_short_keys_layouts_and_scales(dtype, D, layout, scale, shape, run_without_copies):
+    """The short-key kernel's buffer loads and stores of Q and O: row strides
+    of [B,S,H,D] views (the chunks past a head dim below its bucket hold the
+    next head's values, which must be neither used nor overwritten), rows past
+    Sq, negative and zero scales."""
+    B, H, Sq, Sk = shape
+    rc, text = abi.describe(abi.dtype_code(W.DTYPES[dtype]), B, H, Sq, Sk, D)
+    assert rc == abi.OK and "short16" in text, text
+    wl = W.Workload("short", dtype, B, H, Sq, Sk, D, seed=D + Sk)
+    q, k, v = wl.make_inputs("cuda", layout=layout)
+    print(f"short keys: {dtype} D={D} {layout} scale={scale} {shape}", flush=True)
+    out = run_without_copies(lambda: cmpext3.ops.attention(q, k, v, scale, False))
+    ref = orc.sdpa_c(q.cpu(), k.cpu(), v.cpu(), scale, False)
+    err = orc.max_abs_err(out.cpu(), ref)
+    assert err <= TOL[dtype], f"max abs err {err:.3e}"
+
+
 def _sample_rows(S, n_spread=200, seed=0):
     rng = np.random.default_rng(seed)
     tail = range(S - 150, S)                       # the ragged last block and tile

@@ -88,8 +88,8 @@ __device__ __forceinline__ float mask_elem(__amdgpu_buffer_rsrc_t rs, int off, i
 // ---- Delta_i = sum_d dO_id * O_id (fp32), 8 lanes per row
 template <typename T>
 __global__ void __launch_bounds__(256) attn_bwd_delta(const BwdParams p) {
-  const int sub = threadIdx.x & 7;
-  const int64_t g = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);  // row over B*H*Sq
+  const int sub = thread_x() & 7;
+  const int64_t g = (int64_t)block_x() * 32 + (thread_x() >> 3);  // row over B*H*Sq
   const bool live = g < (int64_t)p.B * p.H * p.Sq;
   float acc = 0.f;
   if (live) {
@@ -205,12 +205,12 @@ attn_bwd_dkdv(const BwdParams p) {
   // accumulators, so that the MFMAs leave S - lse2 / c and dP - Delta
   __shared__ __attribute__((aligned(16))) float lsd[2][2][BQ];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int tid = thread_x(), wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   // key blocks in order (causal: the first blocks see the most queries, so
   // they start first); XCD-contiguous ranges share Q/dO in L2
   // (the divisions run on the vector unit: readfirstlane keeps the indices,
   // and the per-head address arithmetic of the sweep, in scalar registers)
-  const int tile = __builtin_amdgcn_readfirstlane(xcd_remap(blockIdx.x, p.n_wg));
+  const int tile = __builtin_amdgcn_readfirstlane(xcd_remap(block_x(), p.n_wg));
   const int bhk = __builtin_amdgcn_readfirstlane(tile / p.n_blk);  // (batch, K/V head)
   const int kb = tile - bhk * p.n_blk;                             // key block
   const int b = __builtin_amdgcn_readfirstlane(bhk / p.Hkv), hk = bhk - b * p.Hkv;
@@ -436,12 +436,12 @@ attn_bwd_dq(const BwdParams p) {
   constexpr int RSD = DK + 8;
   __shared__ __attribute__((aligned(16))) uint16_t dpark[DLDS ? BQ * RSD : 8];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int tid = thread_x(), wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   int bh, qblk;
   {
     FwdParams fp;
     fp.B = p.B; fp.H = p.H; fp.n_qblk = p.n_blk; fp.n_wg = p.n_wg;
-    wg_tile(blockIdx.x, fp, CAUSAL, bh, qblk);  // causal: longest key sweeps first
+    wg_tile(block_x(), fp, CAUSAL, bh, qblk);  // causal: longest key sweeps first
   }
   const int b = bh / p.H, h = bh - b * p.H;
   const int Sq = p.Sq, Sk = p.Sk, D = p.D;

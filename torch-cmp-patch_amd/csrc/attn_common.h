@@ -55,6 +55,14 @@ struct FwdParams {
   int elem_rows;
 };
 
+// Work-item and workgroup index through the AMDGPU builtins.  Kernel files
+// built with -mno-amdgpu-ieee cannot inline the device library's helpers
+// behind threadIdx / blockIdx (their IEEE-mode attribute differs): those
+// become real calls whose results land in VGPRs, so every tile index after
+// them is computed with vector (often quarter-rate) integer instructions.
+__device__ __forceinline__ int thread_x() { return (int)__builtin_amdgcn_workitem_id_x(); }
+__device__ __forceinline__ int block_x() { return (int)__builtin_amdgcn_workgroup_id_x(); }
+
 // Compute units of the current device (host side; 256 on MI355X).
 int device_cus();
 

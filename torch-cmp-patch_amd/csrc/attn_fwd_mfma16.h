@@ -154,7 +154,7 @@ attn_fwd_mfma16(const FwdParams p) {
 
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * (KTILE + VTILE)];
 
-  const int tid = threadIdx.x;
+  const int tid = thread_x();
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int l32 = lane & 31;
@@ -162,7 +162,7 @@ attn_fwd_mfma16(const FwdParams p) {
 
   // ---- which (batch, head, query block) this workgroup owns
   int bh, qblk;
-  wg_tile(blockIdx.x, p, CAUSAL, bh, qblk);
+  wg_tile(block_x(), p, CAUSAL, bh, qblk);
   const int b = bh / p.H;
   const int h = bh - b * p.H;
   const int q0 = qblk * BQ;

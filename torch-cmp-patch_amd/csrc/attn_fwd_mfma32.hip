@@ -56,13 +56,13 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
 
   __shared__ __attribute__((aligned(16))) float lds[2 * (KTILE + VTILE)];
 
-  const int tid = threadIdx.x;
+  const int tid = thread_x();
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int l16 = lane & 15;
   const int g = lane >> 4;
 
-  int lb = blockIdx.x, part = 0, nparts = 1;
+  int lb = block_x(), part = 0, nparts = 1;
   if (lb >= sa.nfull) {
     const int r = lb - sa.nfull;
     nparts = sa.nparts;

@@ -93,13 +93,13 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   uint16_t* const kbase = lds;               // K(j) at kbase + (j & 1) * KTILE
   uint16_t* const vbase = lds + 2 * KTILE;   // V(j) at vbase + (j & 1) * VTILE
 
-  const int tid = threadIdx.x;
+  const int tid = thread_x();
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int l32 = lane & 31;
   const int hh = lane >> 5;
 
-  int lb = blockIdx.x, part = 0, nparts = 1;
+  int lb = block_x(), part = 0, nparts = 1;
   if (lb >= sa.nfull) {
     const int r = lb - sa.nfull;
     nparts = sa.nparts;

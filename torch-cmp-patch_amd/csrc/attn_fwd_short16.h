@@ -48,9 +48,9 @@ attn_fwd_short16(const FwdParams p) {
   uint16_t* const ks = lds;
   uint16_t* const vs = lds + SK * RSK;
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int tid = thread_x(), wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   int bh, qblk;
-  wg_tile(blockIdx.x, p, false, bh, qblk);
+  wg_tile(block_x(), p, false, bh, qblk);
   const int b = bh / p.H, h = bh - b * p.H;
   const int Sq = p.Sq, Sk = p.Sk, D = p.D;
   const int qlo = qblk * BQ + wave * 32;   // first query row of this wave
@@ -64,29 +64,52 @@ attn_fwd_short16(const FwdParams p) {
   uint16_t* __restrict__ og = (uint16_t*)p.o + b * p.o_b + h * p.o_h;
 
   // ---- every global load first: this wave's 32 Q rows in row order (chunk
-  // i of the 32 x KCH chunks to lane i mod 64), then all of K/V through
-  // buffer loads (rows at or past Sk read as zero)
+  // i of the 32 x KCH chunks to lane i mod 64), then all of K/V.  All of them
+  // are buffer accesses over this (batch, head)'s rows with 32-bit offsets
+  // (the host checks the extent): rows at or past Sq / Sk read as zero and O
+  // stores past Sq are dropped, so no row needs a condition.  When the chunks
+  // of a row divide the lanes, a load's row step is a scalar offset.
+  const int qs_b = (int)p.q_s * 2, os_b = (int)p.o_s * 2;
+  const int ks_b = (int)p.k_s * 2, vs_b = (int)p.v_s * 2;
+  const __amdgpu_buffer_rsrc_t qrs = uniform_rsrc(qg, ((int64_t)(Sq - 1) * p.q_s + D) * 2);
+  const __amdgpu_buffer_rsrc_t ors = uniform_rsrc(og, ((int64_t)(Sq - 1) * p.o_s + D) * 2);
+  const __amdgpu_buffer_rsrc_t krs = uniform_rsrc(kg, ((int64_t)(Sk - 1) * p.k_s + D) * 2);
+  const __amdgpu_buffer_rsrc_t vrs = uniform_rsrc(vg, ((int64_t)(Sk - 1) * p.v_s + D) * 2);
+  // byte offset of 16-byte chunk i (of NCHK per row) within rows of rb bytes:
+  // lane part in the vector offset, row step of iteration it in the scalar one
+  auto chunk_off = [](int i, int it, int per_it, int nchk, int rb, int& vo, int& so) {
+    if (per_it % nchk == 0) {
+      const int r = i / nchk;
+      vo = r * rb + 16 * (i - r * nchk);
+      so = it * (per_it / nchk) * rb;
+    } else {
+      const int ci = it * per_it + i, r = ci / nchk;
+      vo = r * rb + 16 * (ci - r * nchk);
+      so = 0;
+    }
+  };
   u32x4 qr[QLD];
 #pragma unroll
   for (int it = 0; it < QLD; ++it) {
-    const int ci = it * 64 + lane, r = ci / KCH, c8 = ci - r * KCH;
-    u32x4 x = {0u, 0u, 0u, 0u};
-    if (qlo + r < Sq && 8 * c8 < D) x = *(const u32x4*)(qg + (int64_t)(qlo + r) * p.q_s + 8 * c8);
+    int vo, so;
+    chunk_off(lane, it, 64, KCH, qs_b, vo, so);
+    u32x4 x = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qrs, qlo * qs_b + vo, so, 0));
+    const int c8 = (it * 64 + lane) % KCH;
+    if ((OPT & 8) && 8 * c8 >= D) x = (u32x4){0u, 0u, 0u, 0u};  // the next row's head dims
     qr[it] = x;
   }
-  const int ks_b = (int)p.k_s * 2, vs_b = (int)p.v_s * 2;
-  const __amdgpu_buffer_rsrc_t krs = uniform_rsrc(kg, ((int64_t)(Sk - 1) * p.k_s + D) * 2);
-  const __amdgpu_buffer_rsrc_t vrs = uniform_rsrc(vg, ((int64_t)(Sk - 1) * p.v_s + D) * 2);
   u32x4 kr[KLD], vr[VLD];
 #pragma unroll
   for (int it = 0; it < KLD; ++it) {
-    const int ci = it * NT + tid, r = ci / KCH, c8 = ci - r * KCH;
-    kr[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, r * ks_b + 16 * c8, 0, 0));
+    int vo, so;
+    chunk_off(tid, it, NT, KCH, ks_b, vo, so);
+    kr[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, vo, so, 0));
   }
 #pragma unroll
   for (int it = 0; it < VLD; ++it) {
-    const int ci = it * NT + tid, r = ci / VCH, c8 = ci - r * VCH;
-    vr[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, r * vs_b + 16 * c8, 0, 0));
+    int vo, so;
+    chunk_off(tid, it, NT, VCH, vs_b, vo, so);
+    vr[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vo, so, 0));
   }
 #pragma unroll
   for (int it = 0; it < KLD; ++it) {
@@ -111,7 +134,11 @@ attn_fwd_short16(const FwdParams p) {
   }
   u32x4 qf[NKS];
 #pragma unroll
-  for (int s = 0; s < NKS; ++s) qf[s] = *(const u32x4*)(qs + l32 * RSQ + 16 * s + 8 * hh) ^ p.q_sign;
+  for (int s = 0; s < NKS; ++s) qf[s] = *(const u32x4*)(qs + l32 * RSQ + 16 * s + 8 * hh);
+  if (p.q_sign) {  // negative scale (uniform)
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) qf[s] ^= p.q_sign;
+  }
   lds_barrier();
 
   // ---- all scores of the row: S^T = K Q^T over NKB blocks of 32 keys
@@ -130,21 +157,29 @@ attn_fwd_short16(const FwdParams p) {
   }
   if (OPT & 1) __builtin_amdgcn_s_setprio(0);
 
-  // ---- exact softmax over the row (keys past Sk masked)
+  // ---- exact softmax over the row.  Keys past Sk are masked only in the
+  // blocks that reach past it (a uniform branch: the key capacity keeps every
+  // block but the last whole when Sk > 48).  The max is taken over the raw
+  // scores and the exp2 argument is one FMA, s * c - m * c (c > 0; the host
+  // turns scale 0 into a tiny c, so masked keys stay -inf instead of 0 * inf).
   const float c = p.c;
   float mq = -INFINITY;
 #pragma unroll
-  for (int kb = 0; kb < NKB; ++kb)
+  for (int kb = 0; kb < NKB; ++kb) {
+    if (32 * (kb + 1) > Sk) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        if (2 * kb + (r >> 3) >= NKH) continue;  // a slice past every key
+        if (32 * kb + acc_key(r, hh) >= Sk) sc[kb][r] = -INFINITY;
+      }
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      if (2 * kb + (r >> 3) >= NKH) continue;  // a slice past every key
-      const int key = 32 * kb + acc_key(r, hh);
-      float x = sc[kb][r] * c;
-      if (key >= Sk) x = -INFINITY;
-      sc[kb][r] = x;
-      mq = fmaxf(mq, x);
+      if (2 * kb + (r >> 3) >= NKH) continue;
+      mq = fmaxf(mq, sc[kb][r]);
     }
-  const float m = xhalf_max(mq);  // finite: Sk >= 1 keeps key 0 in every row
+  }
+  const float m = xhalf_max(mq) * c;  // finite: Sk >= 1 keeps key 0 in every row
   u32x4 pf[NCH];
   float ls0 = 0.f, ls1 = 0.f;
 #pragma unroll
@@ -152,7 +187,8 @@ attn_fwd_short16(const FwdParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int kb = ch >> 1, cc = ch & 1;
-      const uint32_t w = Elt<T>::pack(fast_exp2(sc[kb][8 * cc + 2 * e] - m), fast_exp2(sc[kb][8 * cc + 2 * e + 1] - m));
+      const uint32_t w = Elt<T>::pack(fast_exp2(__builtin_fmaf(sc[kb][8 * cc + 2 * e], c, -m)),
+                                      fast_exp2(__builtin_fmaf(sc[kb][8 * cc + 2 * e + 1], c, -m)));
       pf[ch][e] = w;
       if (e & 1) ls1 = Elt<T>::sum2(w, ls1);
       else ls0 = Elt<T>::sum2(w, ls0);
@@ -197,7 +233,12 @@ attn_fwd_short16(const FwdParams p) {
   for (int it = 0; it < OLD; ++it) {
     const int ci = it * 64 + lane, r = ci / VCH, c8 = ci - r * VCH;
     const u32x4 x = *(const u32x4*)(qs + r * RSQ + 8 * c8);
-    if (qlo + r < Sq && 8 * c8 < D) *(u32x4*)(og + (int64_t)(qlo + r) * p.o_s + 8 * c8) = x;
+    int vo, so;
+    chunk_off(lane, it, 64, VCH, os_b, vo, so);
+    // chunks past D (a head dim below its bucket, or DP > DK) would land on
+    // the next row's head dims
+    if (!((OPT & 8) || DP != DK) || 8 * c8 < D)
+      __builtin_amdgcn_raw_buffer_store_b128(x, ors, qlo * os_b + vo, so, 0);
   }
 }
 
@@ -206,6 +247,7 @@ hipError_t launch_short16_cfg(const FwdParams& p0, hipStream_t stream) {
   constexpr int NKB = (NKH + 1) / 2;
   constexpr int DP = (DK + 31) / 32 * 32;
   FwdParams p = p0;
+  if (p.c == 0.f) p.c = 1e-30f;  // scale 0: every finite exp2 argument rounds to 0
   p.n_qblk = (p.Sq + 127) / 128;
   p.n_wg = p.B * p.H * p.n_qblk;
   if (p.n_wg == 0) return hipSuccess;

@@ -39,8 +39,11 @@ int key_slices(int Sk) { return Sk <= 48 ? 3 : (Sk + 15) / 16; }
 
 bool short16_applies(const FwdParams& p, int dk, bool causal) {
   if (causal || p.mask_kind != MASK_NONE || p.lse || dk > 128 || p.Sk > 128) return false;
+  // 32-bit buffer offsets: K/V rows up to the key capacity, Q/O rows up to
+  // the last query block's end
   const int64_t rs = p.k_s > p.v_s ? p.k_s : p.v_s;
-  return (int64_t)128 * rs * 2 < (int64_t(1) << 31);
+  const int64_t qs = p.q_s > p.o_s ? p.q_s : p.o_s;
+  return (int64_t)128 * rs * 2 < (int64_t(1) << 31) && ((int64_t)p.Sq + 128) * qs * 2 < (int64_t(1) << 31);
 }
 
 hipError_t launch_short16(const FwdParams& p, int dk, bool bf16, hipStream_t s) {
