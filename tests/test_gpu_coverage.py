@@ -171,6 +171,27 @@ def test_short_keys_layouts_and_scales(dtype, D, layout, scale, shape, run_witho
     assert err <= TOL[dtype], f"max abs err {err:.3e}"
 
 
+@pytest.mark.parametrize("dtype,B,H,Sq,Sk,D,scale", [
+    ("fp16", 2, 4, 1, 4096, 64, None),     # decode step: three waves hold no rows
+    ("bf16", 1, 3, 33, 1000, 128, None),   # two rowless waves, ragged Sk
+    ("fp16", 1, 2, 64, 777, 96, 1.0),      # exactly two rowless waves, D below its bucket, wide scores
+    ("bf16", 2, 2, 80, 600, 64, None),     # one rowless wave: the ordinary variant
+])
+def test_short_query_blocks_with_rowless_waves(dtype, B, H, Sq, Sk, D, scale):
+    """A single query block whose last waves hold no rows: those waves only
+    stage K/V tiles for the others (and leave before the key-split exchange)."""
+    rc, text = abi.describe(abi.dtype_code(W.DTYPES[dtype]), B, H, Sq, Sk, D)
+    assert rc == abi.OK and "pipe16" in text, text
+    q, k, v = _inputs(dtype, B, H, Sq, Sk, D, seed=Sq + Sk)
+    eff = 1.0 / math.sqrt(D) if scale is None else scale
+    print(f"rowless waves: {dtype} B={B} H={H} Sq={Sq} Sk={Sk} D={D} scale={eff}", flush=True)
+    out = abi.attn_fwd(q, k, v, eff, False)
+    torch.cuda.synchronize()
+    ref = orc.sdpa_c(q.cpu(), k.cpu(), v.cpu(), eff, False)
+    err = orc.max_abs_err(out.cpu(), ref)
+    assert err <= TOL[dtype], f"max abs err {err:.3e}"
+
+
 def _sample_rows(S, n_spread=200, seed=0):
     rng = np.random.default_rng(seed)
     tail = range(S - 150, S)                       # the ragged last block and tile

@@ -60,7 +60,10 @@ namespace cmpext3 {
 // (FwdParams::elem_rows 4 or 8: head dims that are not whole 16-byte chunks,
 // rows or base pointers off 16 bytes): K/V tiles are read as 4-byte pieces,
 // K pieces past the head dim at an out-of-range offset (so they read as zero
-// with no per-tile work), Q and O through ld_cols16 / st_cols16x4.
+// with no per-tile work), Q and O through ld_cols16 / st_cols16x4.  OPT bit
+// 7: waves whose rows all lie past Sq (a single short query block: decode,
+// packed query groups) only stage K/V tiles for the others, with no score,
+// exponential or PV work.
 template <typename T, int DK, int DP, int NW, int BK, int OCC, bool CAUSAL, bool PRESCALE, int OPT = 0>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
 attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
@@ -120,6 +123,7 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   const int Sq = p.Sq, Sk = p.Sk, D = p.D;
   const int qlo = q0 + wave * 32;          // first query row of this wave
   const int qrow = qlo + l32;
+  const bool live = !(OPT & 128) || qlo < Sq;  // wave-uniform
   // element offset of row r: packed grouped-query rows interleave the group's
   // query heads (query head r / pack_sq, position r % pack_sq)
   auto row_off = [&](int r, int64_t s_head, int64_t s_row) -> int64_t {
@@ -457,7 +461,7 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
     // every wave is done reading K(t) and V(t-1); K(t+1), V(t) are visible
     lds_barrier();
     u32x4 kf[NKB][NKS];
-    read_kf((t + 1) & 1, kf);  // stale data on the last tile; those scores are dropped
+    if (live) read_kf((t + 1) & 1, kf);  // stale data on the last tile; those scores are dropped
     // this iteration's register set holds K(t+2), V(t+1) (loaded two
     // iterations ago) and is refilled with K(t+4), V(t+3).  Past the last
     // tile the set holds a clamped copy that lands in a buffer no later
@@ -466,6 +470,7 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
     store_v(t + 1, vr);
     load_k(t + 4, kr);
     load_v(t + 3, vr);
+    if (!live) return;  // a wave with no rows only stages tiles
 
     u32x4 vfr[NPV];
     const uint16_t* vs = vbase + (t & 1) * VTILE;
