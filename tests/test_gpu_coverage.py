@@ -176,10 +176,14 @@ def test_short_keys_layouts_and_scales(dtype, D, layout, scale, shape, run_witho
     ("bf16", 1, 3, 33, 1000, 128, None),   # two rowless waves, ragged Sk
     ("fp16", 1, 2, 64, 777, 96, 1.0),      # exactly two rowless waves, D below its bucket, wide scores
     ("bf16", 2, 2, 80, 600, 64, None),     # one rowless wave: the ordinary variant
+    ("fp16", 1, 3, 5, 3000, 40, None),     # D below its bucket (K columns zeroed by the loaders)
+    ("bf16", 1, 2, 50, 513, 32, None),     # 128 chunks per K tile over 128 loader threads
+    ("fp16", 2, 2, 1, 900, 72, 1.0),       # DP above DK, odd tile count
 ])
 def test_short_query_blocks_with_rowless_waves(dtype, B, H, Sq, Sk, D, scale):
-    """A single query block whose last waves hold no rows: those waves only
-    stage K/V tiles for the others (and leave before the key-split exchange)."""
+    """A single query block whose last waves hold no rows: those waves are
+    the only K/V loaders (a register ring two or four tiles ahead) and leave
+    before the key-split exchange; the waves with rows only compute."""
     rc, text = abi.describe(abi.dtype_code(W.DTYPES[dtype]), B, H, Sq, Sk, D)
     assert rc == abi.OK and "pipe16" in text, text
     q, k, v = _inputs(dtype, B, H, Sq, Sk, D, seed=Sq + Sk)

@@ -61,9 +61,11 @@ namespace cmpext3 {
 // rows or base pointers off 16 bytes): K/V tiles are read as 4-byte pieces,
 // K pieces past the head dim at an out-of-range offset (so they read as zero
 // with no per-tile work), Q and O through ld_cols16 / st_cols16x4.  OPT bit
-// 7: waves whose rows all lie past Sq (a single short query block: decode,
-// packed query groups) only stage K/V tiles for the others, with no score,
-// exponential or PV work.
+// 7: a single short query block (decode, packed query groups; the host sends
+// it with at least two of the NW waves holding no rows): those rowless waves
+// are the only ones that load and store K/V tiles, LDEPTH tiles ahead in
+// registers the waves with rows need for their scores, and the waves with
+// rows only compute.
 template <typename T, int DK, int DP, int NW, int BK, int OCC, bool CAUSAL, bool PRESCALE, int OPT = 0>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
 attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
@@ -260,6 +262,67 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
       if (VFULL || it * NT + tid < BK * VCH) *(u32x4*)(dst + vlo[it]) = vr[it];
   };
 
+  // OPT 128: the rowless waves (ltid = their thread index, nlt = their
+  // thread count, at least 128) move every chunk of a tile.  Chunks past the
+  // tile get an offset beyond every buffer range: they read zero, fetch
+  // nothing and are not stored.
+  constexpr bool LOADERS = (OPT & 128) != 0;
+  static_assert(!(LOADERS && (NARROW || MASK || CAUSAL)), "loader waves: plain non-causal launches only");
+  // tiles in flight per loader wave (its register ring): 4 at D <= 64, where
+  // a tile is small (decode fp16 D = 64: 50 -> 43 us against the compute
+  // waves loading two tiles ahead), 2 above (at D = 128 a deeper ring was
+  // slower: 32k-key decode 108 us at 2, 110 at 3, 112 at 4, 118 at 6)
+  constexpr int LDEPTH = DK <= 64 ? 4 : 2;
+  constexpr int LKLD = LOADERS ? (BK * KCH + 127) / 128 : 1;
+  constexpr int LVLD = LOADERS ? (BK * VCH + 127) / 128 : 1;
+  const int nlive = LOADERS ? min(NW, (Sq - q0 + 31) / 32) : NW;
+  const int ltid = tid - nlive * 64, nlt = (NW - nlive) * 64;
+  int lkvo[LKLD], lklo[LKLD], lvvo[LVLD], lvlo[LVLD];
+  bool lkz[LKLD];
+  if constexpr (LOADERS) {
+#pragma unroll
+    for (int it = 0; it < LKLD; ++it) {
+      const int ci = it * nlt + ltid, r = ci / KCH, c8 = ci - r * KCH;
+      lkz[it] = 8 * c8 >= D;
+      lkvo[it] = ci < BK * KCH ? r * ks_b + 16 * c8 : (int)0x80000000u;
+      lklo[it] = ci < BK * KCH ? r * RSK + 8 * (SWZ ? (c8 ^ lds_swz<DK>(r)) : c8) : -1;
+    }
+#pragma unroll
+    for (int it = 0; it < LVLD; ++it) {
+      const int ci = it * nlt + ltid, r = ci / VCH, c8 = ci - r * VCH;
+      lvvo[it] = ci < BK * VCH ? r * vs_b + 16 * c8 : (int)0x80000000u;
+      lvlo[it] = ci < BK * VCH ? r * RSV + 8 * (SWZ ? (c8 ^ lds_swz<DP>(r)) : c8) : -1;
+    }
+  }
+  auto lload_k = [&](int j, u32x4 (&kr)[LKLD]) {
+    const int so = (tbase + min(j, ntiles - 1)) * BK * ks_b;
+#pragma unroll
+    for (int it = 0; it < LKLD; ++it)
+      kr[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, lkvo[it], so, 0));
+  };
+  auto lload_v = [&](int j, u32x4 (&vr)[LVLD]) {
+    const int so = (tbase + min(j, ntiles - 1)) * BK * vs_b;
+#pragma unroll
+    for (int it = 0; it < LVLD; ++it)
+      vr[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, lvvo[it], so, 0));
+  };
+  auto lstore_k = [&](int slot, const u32x4 (&kr)[LKLD]) {
+    uint16_t* dst = kbase + slot * KTILE;
+#pragma unroll
+    for (int it = 0; it < LKLD; ++it)
+      if (lklo[it] >= 0) {
+        u32x4 x = kr[it];
+        if ((OPT & 8) && lkz[it]) x = (u32x4){0u, 0u, 0u, 0u};
+        *(u32x4*)(dst + lklo[it]) = x;
+      }
+  };
+  auto lstore_v = [&](int j, const u32x4 (&vr)[LVLD]) {
+    uint16_t* dst = vbase + (j & 1) * VTILE;
+#pragma unroll
+    for (int it = 0; it < LVLD; ++it)
+      if (lvlo[it] >= 0) *(u32x4*)(dst + lvlo[it]) = vr[it];
+  };
+
   // lane-constant parts of the fragment read addresses
   int k_rd[NKS];
   {
@@ -380,19 +443,53 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   // ---- prologue: K(0), V(0), K(1) in LDS; register set A holds K(2), V(1)
   // for iteration 0 and set B holds K(3), V(2) for iteration 1
   u32x4 kA[KLD], vA[VLD], kB[KLD], vB[VLD];
-  load_k(0, kA);
-  load_v(0, vA);
-  load_k(1, kB);
-  store_k(0, kA);
-  store_v(0, vA);
-  store_k(1, kB);
-  load_k(2, kA);
-  load_v(1, vA);
-  // set A must stay the older group: the loop waits for it with set B's loads
-  // still counted as in flight
-  __builtin_amdgcn_sched_barrier(0);
-  load_k(3, kB);
-  load_v(2, vB);
+  if constexpr (LOADERS) {
+    if (!live) {
+      // Loader waves: the same barrier sequence as the waves with rows (the
+      // prologue's, then one per iteration), with ring set i % LDEPTH holding
+      // K(i+2), V(i+1) for iteration i
+      u32x4 lk[LDEPTH][LKLD], lv[LDEPTH][LVLD];
+      lload_k(0, lk[0]);
+      lload_v(0, lv[0]);
+      lload_k(1, lk[1]);
+      lstore_k(0, lk[0]);
+      lstore_v(0, lv[0]);
+      lstore_k(1, lk[1]);
+#pragma unroll
+      for (int j = 0; j < LDEPTH; ++j) {
+        lload_k(j + 2, lk[j]);
+        lload_v(j + 1, lv[j]);
+      }
+      lds_barrier();
+      for (int t = 0; t < nt2; t += LDEPTH) {
+#pragma unroll
+        for (int j = 0; j < LDEPTH; ++j) {
+          if (t + j < nt2) {
+            lds_barrier();
+            lstore_k((t + j) & 1, lk[j]);
+            lstore_v(t + j + 1, lv[j]);
+            lload_k(t + j + 2 + LDEPTH, lk[j]);
+            lload_v(t + j + 1 + LDEPTH, lv[j]);
+          }
+        }
+      }
+      return;  // no rows: nothing to exchange or store
+    }
+  } else {
+    load_k(0, kA);
+    load_v(0, vA);
+    load_k(1, kB);
+    store_k(0, kA);
+    store_v(0, vA);
+    store_k(1, kB);
+    load_k(2, kA);
+    load_v(1, vA);
+    // set A must stay the older group: the loop waits for it with set B's loads
+    // still counted as in flight
+    __builtin_amdgcn_sched_barrier(0);
+    load_k(3, kB);
+    load_v(2, vB);
+  }
   lds_barrier();
   constexpr int NQK = NKB * NKS;  // score MFMAs per tile
   constexpr int NPV = NCH * NDB;  // PV MFMAs per tile
@@ -461,16 +558,18 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
     // every wave is done reading K(t) and V(t-1); K(t+1), V(t) are visible
     lds_barrier();
     u32x4 kf[NKB][NKS];
-    if (live) read_kf((t + 1) & 1, kf);  // stale data on the last tile; those scores are dropped
+    read_kf((t + 1) & 1, kf);  // stale data on the last tile; those scores are dropped
     // this iteration's register set holds K(t+2), V(t+1) (loaded two
     // iterations ago) and is refilled with K(t+4), V(t+3).  Past the last
     // tile the set holds a clamped copy that lands in a buffer no later
-    // iteration reads, so the stores need no condition.
-    store_k(t & 1, kr);
-    store_v(t + 1, vr);
-    load_k(t + 4, kr);
-    load_v(t + 3, vr);
-    if (!live) return;  // a wave with no rows only stages tiles
+    // iteration reads, so the stores need no condition.  (OPT 128: the
+    // loader waves do this instead.)
+    if constexpr (!LOADERS) {
+      store_k(t & 1, kr);
+      store_v(t + 1, vr);
+      load_k(t + 4, kr);
+      load_v(t + 3, vr);
+    }
 
     u32x4 vfr[NPV];
     const uint16_t* vs = vbase + (t & 1) * VTILE;
