@@ -138,6 +138,37 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Wait until at most N vector-memory operations of this wave are in flight
+// (they complete in issue order).  Needed for loads that write LDS directly,
+// which the compiler does not order against later LDS reads.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Raw buffer descriptor words (gfx9: base, stride 0, num_records, 32-bit raw
+// reads), wave-uniform, for loads issued through inline assembly.
+__device__ __forceinline__ u32x4 uniform_rsrc_words(const void* base, int64_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)) & 0xffffu;
+  const uint32_t n = (uint32_t)__builtin_amdgcn_readfirstlane((int)bytes);
+  return (u32x4){lo, hi, n, 0x00020000u};
+}
+
+// 16 bytes per lane from the buffer (voffset + soffset) straight into LDS:
+// lane i writes [lds_byte + 16 i, lds_byte + 16 i + 16); an offset outside
+// the buffer writes zeros; lanes off in EXEC write nothing.  Issued as inline
+// assembly so that the compiler neither waits for these loads before its own
+// LDS reads (it cannot tell the ring slots apart) nor counts them: the caller
+// orders them with wait_vmcnt and a barrier.  M0 carries the LDS address
+// (the compiler writes it; one wait state before the load reads it).
+__device__ __forceinline__ void lds_dma16(const u32x4& rs, uint32_t lds_byte, int voff, int soff) {
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               ::"v"(voff), "s"(rs), "s"(soff), "{m0}"(lds_byte)
+               : "memory");
+}
+
 // Narrow row access (FwdParams::elem_rows = a, the largest of 2, 4, 8 bytes
 // that divides every base pointer, every row stride and the row length D *
 // element size): for head dims that are not a whole number of 16-byte chunks

@@ -65,7 +65,13 @@ namespace cmpext3 {
 // it with at least two of the NW waves holding no rows): those rowless waves
 // are the only ones that load and store K/V tiles, LDEPTH tiles ahead in
 // registers the waves with rows need for their scores, and the waves with
-// rows only compute.
+// rows only compute.  OPT bit 8: K/V tiles go from memory straight into LDS
+// (buffer_load_dwordx4 ... lds: lane i of an instruction writes the 16 bytes
+// at M0 + 16 i), DMA_AHEAD tiles ahead into a ring of four K and four V tiles,
+// with no staging registers and no LDS store instructions; every wave issues
+// the same number of these loads per tile and waits for its own with an
+// explicit vmcnt before the barrier that publishes them (the compiler does not
+// track LDS written this way).
 template <typename T, int DK, int DP, int NW, int BK, int OCC, bool CAUSAL, bool PRESCALE, int OPT = 0>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
 attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
@@ -93,10 +99,15 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   constexpr int NDB = DP / 32;            // 32-row output blocks
   constexpr int NKS = DK / 16;            // score k-steps
   static_assert(BK % 32 == 0 && DK % 16 == 0 && DP % 32 == 0 && DK <= DP, "tile shape");
+  constexpr bool DMA = (OPT & 256) != 0;
+  static_assert(!(DMA && (NARROW || MASK || (OPT & 128))), "LDS DMA: plain unmasked launches only");
+  constexpr int NR = DMA ? 4 : 2;  // K (and V) tiles held in LDS
+  constexpr int DMA_AHEAD = 3;     // DMA: tiles in flight ahead of the one read
+  static_assert(!DMA || DMA_AHEAD + 1 == NR, "ring of DMA_AHEAD + 1 tiles");
 
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * KTILE + 2 * VTILE];
-  uint16_t* const kbase = lds;               // K(j) at kbase + (j & 1) * KTILE
-  uint16_t* const vbase = lds + 2 * KTILE;   // V(j) at vbase + (j & 1) * VTILE
+  __shared__ __attribute__((aligned(16))) uint16_t lds[NR * KTILE + NR * VTILE];
+  uint16_t* const kbase = lds;                // K(j) at kbase + (j % NR) * KTILE
+  uint16_t* const vbase = lds + NR * KTILE;   // V(j) at vbase + (j % NR) * VTILE
 
   const int tid = thread_x();
   const int wave = tid >> 6;
@@ -260,6 +271,59 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
 #pragma unroll
     for (int it = 0; it < VLD; ++it)
       if (VFULL || it * NT + tid < BK * VCH) *(u32x4*)(dst + vlo[it]) = vr[it];
+  };
+
+  // OPT 256: a tile in LDS is BK rows of RSK (RSV) halves, i.e. NSK (NSV)
+  // 16-byte slots counted row by row (padding included).  Wave w fills slots
+  // [w * SPWK, (w + 1) * SPWK) with DIK instructions of 64 lanes (the last
+  // one partial when SPWK is not a multiple of 64); since a tile has 32 rows,
+  // every wave gets the same slot count and issues the same DG loads per tile
+  // group.  Each lane's source chunk is fixed for the whole sweep (the tile
+  // offset is the scalar soffset): padding slots, and K columns past D when
+  // they must be zero, get an offset beyond every buffer range, which writes
+  // zeros.
+  constexpr int RCK = RSK / 8, RCV = RSV / 8;
+  constexpr int NSK = BK * RCK, NSV = BK * RCV;
+  constexpr int SPWK = NSK / NW, SPWV = NSV / NW;
+  static_assert(!DMA || (NSK % NW == 0 && NSV % NW == 0 && RSK % 8 == 0 && RSV % 8 == 0), "DMA slot split");
+  constexpr int DIK = DMA ? (SPWK + 63) / 64 : 1;
+  constexpr int DIV = DMA ? (SPWV + 63) / 64 : 1;
+  constexpr int DG = DIK + DIV;  // loads per lane per tile group
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  int dko[DIK], dvo[DIV];
+  if constexpr (DMA) {
+#pragma unroll
+    for (int i = 0; i < DIK; ++i) {
+      const int j = 64 * i + lane, sl = wv * SPWK + j;
+      const int r = sl / RCK, cp = sl - r * RCK;
+      const int c = SWZ ? (cp ^ lds_swz<DK>(r)) : cp;
+      dko[i] = (j < SPWK && cp < KCH && !((OPT & 8) && 8 * c >= D)) ? r * ks_b + 16 * c : (int)0x80000000u;
+    }
+#pragma unroll
+    for (int i = 0; i < DIV; ++i) {
+      const int j = 64 * i + lane, sl = wv * SPWV + j;
+      const int r = sl / RCV, cp = sl - r * RCV;
+      const int c = SWZ ? (cp ^ lds_swz<DP>(r)) : cp;
+      dvo[i] = (j < SPWV && cp < VCH) ? r * vs_b + 16 * c : (int)0x80000000u;
+    }
+  }
+  typedef __attribute__((address_space(3))) uint16_t lds_u16;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u16*)lds;  // LDS byte address of the tiles
+  const u32x4 krw = uniform_rsrc_words(kg, ((int64_t)(Sk - 1) * p.k_s + D) * 2);
+  const u32x4 vrw = uniform_rsrc_words(vg, ((int64_t)(Sk - 1) * p.v_s + D) * 2);
+  // tile j (clamped to the last one) into ring slot `slot`
+  auto dma_k = [&](int j, int slot) {
+    const int so = (tbase + min(j, ntiles - 1)) * BK * ks_b;
+#pragma unroll
+    for (int i = 0; i < DIK; ++i)
+      if (64 * i + lane < SPWK) lds_dma16(krw, lds0 + 2 * (slot * KTILE + (wv * SPWK + 64 * i) * 8), dko[i], so);
+  };
+  auto dma_v = [&](int j, int slot) {
+    const int so = (tbase + min(j, ntiles - 1)) * BK * vs_b;
+#pragma unroll
+    for (int i = 0; i < DIV; ++i)
+      if (64 * i + lane < SPWV)
+        lds_dma16(vrw, lds0 + 2 * (NR * KTILE + slot * VTILE + (wv * SPWV + 64 * i) * 8), dvo[i], so);
   };
 
   // OPT 128: the rowless waves (ltid = their thread index, nlt = their
@@ -475,6 +539,17 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
       }
       return;  // no rows: nothing to exchange or store
     }
+  } else if constexpr (DMA) {
+    // K(0), then the groups the first DMA_AHEAD iterations would have issued
+    // (group u: K(u + 1), V(u)); the first group must be in LDS before the
+    // barrier, the later ones stay in flight
+    dma_k(0, 0);
+#pragma unroll
+    for (int u = 0; u < DMA_AHEAD; ++u) {
+      dma_k(u + 1, (u + 1) & (NR - 1));
+      dma_v(u, u & (NR - 1));
+    }
+    wait_vmcnt<(DMA_AHEAD - 1) * DG>();
   } else {
     load_k(0, kA);
     load_v(0, vA);
@@ -556,15 +631,24 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   auto step = [&](int t, f32x16 (&sc)[NKB], f32x16 (&sn)[NKB], u32x4 (&pc)[NCH], u32x4 (&pn)[NCH],
                   float& tc0, float& tc1, float& tn0, float& tn1, u32x4 (&kr)[KLD], u32x4 (&vr)[VLD]) {
     // every wave is done reading K(t) and V(t-1); K(t+1), V(t) are visible
+    // (OPT 256: this wave's loads of them, issued DMA_AHEAD iterations ago,
+    // are complete before the barrier publishes them)
+    if constexpr (DMA) wait_vmcnt<(DMA_AHEAD - 1) * DG>();
     lds_barrier();
     u32x4 kf[NKB][NKS];
-    read_kf((t + 1) & 1, kf);  // stale data on the last tile; those scores are dropped
-    // this iteration's register set holds K(t+2), V(t+1) (loaded two
-    // iterations ago) and is refilled with K(t+4), V(t+3).  Past the last
-    // tile the set holds a clamped copy that lands in a buffer no later
-    // iteration reads, so the stores need no condition.  (OPT 128: the
-    // loader waves do this instead.)
-    if constexpr (!LOADERS) {
+    read_kf((t + 1) & (NR - 1), kf);  // stale data on the last tile; those scores are dropped
+    if constexpr (DMA) {
+      // K(t + 1 + DMA_AHEAD) into the slot K(t) left, V(t + DMA_AHEAD) into
+      // the one V(t - 1) left; past the last tile a clamped copy lands in a
+      // slot no later iteration reads
+      dma_k(t + 1 + DMA_AHEAD, (t + 1 + DMA_AHEAD) & (NR - 1));
+      dma_v(t + DMA_AHEAD, (t + DMA_AHEAD) & (NR - 1));
+    } else if constexpr (!LOADERS) {
+      // this iteration's register set holds K(t+2), V(t+1) (loaded two
+      // iterations ago) and is refilled with K(t+4), V(t+3).  Past the last
+      // tile the set holds a clamped copy that lands in a buffer no later
+      // iteration reads, so the stores need no condition.  (OPT 128: the
+      // loader waves do this instead.)
       store_k(t & 1, kr);
       store_v(t + 1, vr);
       load_k(t + 4, kr);
@@ -572,7 +656,7 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
     }
 
     u32x4 vfr[NPV];
-    const uint16_t* vs = vbase + (t & 1) * VTILE;
+    const uint16_t* vs = vbase + (t & (NR - 1)) * VTILE;
     auto read_vfr = [&](int i) {
       const int ch = i / NDB, db = i - ch * NDB;
       const uint16_t* vp = vs + 16 * ch * RSV;
@@ -658,9 +742,25 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   // With an odd tile count the extra tile is a clamped copy of the last one
   // whose keys all lie past kpe: fully masked, it adds exactly zero.  The
   // last iteration's early units work on stale scores nobody reads.
-  for (int t = 0; t < nt2; t += 2) {
-    step(t, sA, sB, pA, pB, tA0, tA1, tB0, tB1, kA, vA);
-    step(t + 1, sB, sA, pB, pA, tB0, tB1, tA0, tA1, kB, vB);
+  if constexpr (DMA) {
+    // unrolled by the ring size so that every slot index is a constant; an
+    // exit after an even number of iterations waits for nothing (the loads
+    // write no registers)
+    for (int t = 0; t < nt2; t += 4) {
+      step(t, sA, sB, pA, pB, tA0, tA1, tB0, tB1, kA, vA);
+      step(t + 1, sB, sA, pB, pA, tB0, tB1, tA0, tA1, kB, vB);
+      if (t + 2 >= nt2) break;
+      step(t + 2, sA, sB, pA, pB, tA0, tA1, tB0, tB1, kA, vA);
+      step(t + 3, sB, sA, pB, pA, tB0, tB1, tA0, tA1, kB, vB);
+    }
+    // the clamped loads past the last tile are still writing this
+    // workgroup's LDS: they must land before the wave can leave
+    wait_vmcnt<0>();
+  } else {
+    for (int t = 0; t < nt2; t += 2) {
+      step(t, sA, sB, pA, pB, tA0, tA1, tB0, tB1, kA, vA);
+      step(t + 1, sB, sA, pB, pA, tB0, tB1, tA0, tA1, kB, vB);
+    }
   }
 
   // ---- epilogue
