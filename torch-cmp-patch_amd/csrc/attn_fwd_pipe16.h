@@ -22,7 +22,9 @@
 // between MFMA-sized steps).  LDS holds two K and two V tiles; K(t+2) goes
 // into the buffer K(t) left, V(t+1) into the one V(t-1) left, and the single
 // barrier per iteration orders those writes after the previous iteration's
-// reads.
+// reads.  With OPT bit 8 (below) the tiles instead load from memory straight
+// into a four-tile LDS ring: iteration t issues K(t+4), V(t+3) and stores
+// nothing.
 //
 // Softmax without a per-tile max.  Tile 0 sets the row offset m from its max;
 // later tiles are exponentiated as exp2(s*c - m) straight away.  The row sum
