@@ -191,9 +191,10 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   for (int db = 0; db < NDB; ++db) oacc[db] = (f32x16){};
   f32x16 bias = (f32x16){};
   float mb = 0.f;
-  // row sum of P over this lane's half of the keys, as two interleaved v_dot2
-  // chains carried across iterations (no per-iteration reduction to wait on)
-  float ls0 = 0.f, ls1 = 0.f;
+  // row sum of P over this lane's half of the keys: each tile's two
+  // interleaved v_dot2 chains (tc0, tc1) are added once, after the rescale
+  // check that needs their sum anyway
+  float ls = 0.f;
   // rescale threshold on the tile's row max over the offset: -inf until the
   // row has seen a live key (the first live tile sets the offset), then 8
   float thr = -INFINITY;
@@ -582,8 +583,7 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
     if (mx == -INFINITY) delta = 0.f;
     const float alpha = fast_exp2(-delta);
     mb += delta;
-    ls0 *= alpha;
-    ls1 *= alpha;
+    ls *= alpha;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) oacc[db] *= alpha;
     if (PRESCALE) bias -= delta;  // stays exactly -mb
@@ -699,7 +699,11 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
     // own max.  A lane row sum above 2^8 (always true if some probability
     // exceeds 2^8) sends the wave to the exact path: the tile max decides a
     // rescale as in the max-first scheme, and the tile is redone.
-    if (__builtin_amdgcn_ballot_w64(thr == -INFINITY || tc0 + tc1 > 256.f)) {
+    // Without an attention mask every row sees a key in the first tile of its
+    // sweep (key 0 under causal; rows past Sq score 0), so that tile already
+    // set the offset and thr is 8; only a mask can leave it at -inf.
+    float tsum = tc0 + tc1;
+    if (__builtin_amdgcn_ballot_w64((MASK && thr == -INFINITY) || tsum > 256.f)) {
       const float mx = xhalf_max(row_max(sc));
       if (__builtin_amdgcn_ballot_w64(mx > thr)) {
         const float delta = rescale(mx);
@@ -713,10 +717,10 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
         tc1 = 0.f;
 #pragma unroll
         for (int u = 0; u < NU; ++u) unit(u, sc, pc, tc0, tc1);
+        tsum = tc0 + tc1;
       }
     }
-    ls0 += tc0;
-    ls1 += tc1;
+    ls += tsum;
     if (MASK) {
       // the mask is added in the exp2 domain, so masked bf16 tiles are
       // converted here rather than unit by unit in stage B
@@ -777,7 +781,7 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   }
 
   // ---- epilogue
-  float lsum = xhalf_sum(ls0 + ls1);
+  float lsum = xhalf_sum(ls);
   float moff = mb;  // exp2-domain offset of lsum
   // a wave whose rows all lie past Sq (short or packed query sweeps) has
   // nothing to exchange or store; every part of the block agrees on that
