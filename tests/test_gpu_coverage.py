@@ -220,3 +220,32 @@ def test_production_length_17402(causal):
     err = orc.max_abs_err(out.cpu()[:, :, rows], ref)
     assert err <= TOL["bf16"], f"max abs err {err:.3e}"
     assert bool(torch.isfinite(out).all())
+
+
+@pytest.mark.parametrize("dtype,D,bucket", [("fp16", 120, 128), ("bf16", 120, 128), ("bf16", 56, 64),
+                                            ("fp16", 24, 32)])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("B,H,Sq,Sk", [(1, 2, 300, 300), (1, 2, 256, 2048)])
+def test_head_dim_below_bucket_with_nan_past_d(dtype, D, bucket, causal, B, H, Sq, Sk):
+    """Q/K/V as views of rows `bucket` elements wide whose columns past D
+    hold NaN: the pipelined kernel loads whole 16-byte chunks of its bucket
+    straight into LDS, and the K chunks past D must arrive as zeros (an
+    out-of-range load offset), never as the NaN behind them, or 0 * NaN
+    would reach every score of the row.  V chunks past D only feed output
+    columns that are never stored.  The (1, 2, 256, 2048) shape also takes
+    the key split when not causal."""
+    q, k, v = _inputs(dtype, B, H, Sq, Sk, D, seed=D + Sk + causal)
+    print(f"D below bucket: {dtype} D={D} bucket={bucket} {B}x{H}x{Sq}x{Sk} causal={causal}", flush=True)
+
+    def wide(t):
+        w = torch.full(t.shape[:-1] + (bucket,), float("nan"), dtype=t.dtype, device=t.device)
+        w[..., :D] = t
+        return w[..., :D]
+
+    scale = 1.0 / math.sqrt(D)
+    out = abi.attn_fwd(wide(q), wide(k), wide(v), scale, causal)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), scale, causal)
+    err = orc.max_abs_err(out.cpu(), ref)
+    assert err <= TOL[dtype], f"max abs err {err:.3e}"
