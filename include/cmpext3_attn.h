@@ -6,8 +6,8 @@
  * every input and output buffer.  The library itself keeps one exchange
  * buffer per (device, stream) for launches that split key ranges across
  * workgroups (non-causal, when the query blocks do not fill whole rounds of
- * the GPU; fp16/bf16 with D <= 128, and fp32 with fewer query blocks than
- * CUs): allocated with hipMalloc on the first such launch on that stream
+ * the GPU; fp16/bf16 with D <= 128, and fp32 with at most as many query
+ * blocks as CUs): allocated with hipMalloc on the first such launch on that stream
  * (about 140 KB per CU), kept until the process ends, so at most 16 of them
  * per device.  On a stream under graph capture, after a failed allocation,
  * or past 16 streams per device those launches run without the split: the

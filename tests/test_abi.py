@@ -88,12 +88,22 @@ def test_describe_key_split_plan():
     bf16 = abi.DTYPE_BF16
     assert "key-split: 0 whole + 128 x 4 parts" in abi.describe(bf16, 16, 8, 2, 4096, 128)[1]
     assert "key-split: 0 whole + 200 x 2 parts" in abi.describe(f16, 1, 200, 100, 4096, 64)[1]
-    # fp32: 64-row blocks, split only with fewer blocks than CUs (about two
-    # parts per CU, at least 4 tiles of 32 keys each), never causal
+    # fp32: 64-row blocks, split only with at most one block per CU (about
+    # two parts per CU, at least 4 tiles of 32 keys each), never causal
     f32 = abi.DTYPE_F32
     assert "key-split: 128 x 4 parts" in abi.describe(f32, 1, 8, 1024, 1024, 64)[1]
-    # split launches of D <= 64 take 64-key tiles where that keeps the part count
+    assert "key-split: 256 x 2 parts" in abi.describe(f32, 2, 8, 1024, 1024, 64)[1]
+    assert "key-split: 256 x 2 parts" in abi.describe(f32, 2, 8, 1024, 1024, 128)[1]
+    assert "key-split" not in abi.describe(f32, 2, 10, 1024, 1024, 64)[1]
+    # split launches of D <= 64 take 64-key tiles where that keeps the part
+    # count, and so do unsplit non-causal ones of one to two blocks per CU
     assert "BK=64" in abi.describe(f32, 1, 8, 1024, 1024, 64)[1]
+    assert "BK=64" in abi.describe(f32, 2, 8, 1024, 1024, 64)[1]
+    assert "BK=32" in abi.describe(f32, 2, 8, 1024, 1024, 128)[1]
+    assert "BK=64" in abi.describe(f32, 2, 10, 1024, 1024, 64)[1]
+    assert "BK=64" in abi.describe(f32, 2, 16, 1024, 1024, 64)[1]
+    assert "BK=32" in abi.describe(f32, 2, 17, 1024, 1024, 64)[1]
+    assert "BK=32" in abi.describe(f32, 2, 10, 1024, 1024, 64, True)[1]
     assert "BK=32" in abi.describe(f32, 1, 2, 100, 700, 40)[1]
     assert "BK=32" in abi.describe(f32, 2, 8, 4096, 4096, 64)[1]
     assert "key-split" not in abi.describe(f32, 1, 8, 1024, 1024, 64, True)[1]

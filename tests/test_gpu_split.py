@@ -1,4 +1,5 @@
-"""GPU parity of the key-split launches of the pipelined fp16/bf16 kernel.
+"""GPU parity of the key-split launches of the pipelined fp16/bf16 kernel
+(and of the fp32 kernel's plans at one to two query blocks per CU).
 
 When the query blocks do not fill whole rounds of the chip, the blocks past the
 last whole round run as several workgroups over disjoint key ranges, and the
@@ -217,3 +218,35 @@ def test_graph_capture_never_carries_a_streams_exchange_buffer():
     for e in eagers:
         assert torch.equal(e, eager)
     assert orc.max_abs_err(eager.cpu(), ref) <= TOL["bf16"]
+
+
+FP32_PLANS = [
+    # B, H, Sq, Sk, D, causal, plan that describe() names on a 256-CU device
+    (2, 8, 1024, 1024, 64, False, ("key-split: 256 x 2 parts", "BK=64")),   # one block per CU
+    (2, 8, 1000, 1500, 128, False, ("key-split: 256 x 2 parts", "BK=32")),  # ragged, D = 128
+    (1, 8, 2048, 2048, 40, False, ("key-split: 256 x 2 parts", "BK=64")),   # the D = 40 bucket
+    (2, 10, 1024, 1000, 64, False, ("BK=64",)),                             # 320 blocks: unsplit
+    (2, 8, 1024, 1024, 64, True, ("BK=32",)),                               # causal: never split
+]
+
+
+@pytest.mark.parametrize("case", FP32_PLANS,
+                         ids=[f"B{c[0]}H{c[1]}-q{c[2]}k{c[3]}d{c[4]}{'c' if c[5] else ''}" for c in FP32_PLANS])
+def test_fp32_plans_at_one_to_two_blocks_per_cu(case):
+    """fp32 launches of at most one block per CU split their keys in two; up
+    to two blocks per CU they run unsplit on 64-key tiles (D <= 64).  Each
+    plan against the oracle at 1e-4, and a rerun bit-identical."""
+    B, H, Sq, Sk, D, causal, plan = case
+    q, k, v = _inputs("fp32", B, H, Sq, Sk, D, seed=Sq + Sk + D)
+    text = _split_text(q, B, H, Sq, Sk, D, causal)
+    print(f"fp32 plan: {text}", flush=True)
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        for part in plan:
+            assert part in text, text
+        if len(plan) == 1:
+            assert "key-split" not in text, text
+    scale = D ** -0.5
+    out = _check(q, k, v, scale, causal, "fp32")
+    again = abi.attn_fwd(q, k, v, scale, causal)
+    torch.cuda.synchronize()
+    assert torch.equal(out, again)

@@ -11,10 +11,10 @@
 // V stays row-major in LDS: a PV A-operand element is V[key][d] with d along
 // the 16 lanes of a group, which is a conflict-free LDS read.
 //
-// Key split (non-causal launches with fewer query blocks than CUs, such as
-// [1, 8, 1024, 64]): each block's key range is cut into parts run by separate
-// workgroups, which shortens every wave's dependency chain over the keys and
-// fills the idle CUs.  Every part leaves its fp32 (O, m, l) in the exchange
+// Key split (non-causal launches with at most as many query blocks as CUs,
+// such as [1, 8, 1024, 64]): each block's key range is cut into parts run by
+// separate workgroups, which shortens every wave's dependency chain over the
+// keys and fills the idle CUs.  Every part leaves its fp32 (O, m, l) in the exchange
 // buffer; the last part of a (block, wave) to finish merges all of them in
 // part order and writes the output (the many-part protocol of
 // attn_fwd_pipe16.h).
@@ -370,27 +370,37 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
   }
 }
 
-// Key split plan: only when the query blocks leave CUs idle (fewer blocks than
-// CUs), non-causal, into enough parts for about two workgroups per CU, each
-// part at least kMinTiles32 key tiles long.  Returns the part count (1: no
-// split) for n query blocks and bk-key tiles.
+// Key split plan: only when the query blocks leave CUs idle or alone (at most
+// one block per CU), non-causal, into enough parts for about two workgroups
+// per CU, each part at least kMinTiles32 key tiles long.  Returns the part
+// count (1: no split) for n query blocks and bk-key tiles.  Measured on
+// MI355X at one block per CU (n = 256, 2 parts, 64-key tiles against the
+// unsplit launch): [2,8,1024,1024,64] 60.8 -> 54.1 us, [2,8,1024,4096,64]
+// 215 -> 172 us, [1,8,2048,2048,40] 95.5 -> 69.2 us, [2,8,1024,1024,128]
+// (32-key tiles) 107 -> 101 us; between one and two blocks per CU a split
+// changes nothing.
 constexpr int kMinTiles32 = 4;
 int split_parts32(int n, int Sk, int bk, int cus, bool causal) {
-  if (causal || n <= 0 || n >= cus) return 1;
+  if (causal || n <= 0 || n > cus) return 1;
   int parts = 2 * cus / n;
   const int ntiles = (Sk + bk - 1) / bk;
   if (parts > ntiles / kMinTiles32) parts = ntiles / kMinTiles32;
   return parts >= 2 ? parts : 1;
 }
 
-// Keys per tile: 32 (16 above D = 128); split launches of head dims up to 64
-// take 64-key tiles, half the barriers per key, where that keeps the part
-// count (measured on MI355X: [1,8,1024,1024,64], 128 blocks x 4 parts,
-// 34.1 -> 33.0 us; an unsplit [2,8,4096,4096,64] is faster with 32, 601 vs
-// 635 us).
+// Keys per tile: 32 (16 above D = 128).  Head dims up to 64 take 64-key
+// tiles, half the barriers per key, in split launches where that keeps the
+// part count and in unsplit non-causal launches of one to two blocks per CU,
+// all of them resident at the two workgroups per CU that 64-key tiles leave
+// room for in LDS (measured on MI355X: [1,8,1024,1024,64], 128 blocks x 4
+// parts, 34.1 -> 33.0 us; 320 to 448 unsplit blocks of [B,H,1024,1024,64]
+// 93.5-94.9 -> 89.0-91.0 us).  Beyond two blocks per CU 32-key tiles keep
+// more workgroups resident: an unsplit [2,8,4096,4096,64] (1024 blocks) takes
+// 601 us with 32, 635 with 64.
 int tile_keys32(int dk, int n, int Sk, int cus, bool causal) {
   const int def = dk <= 128 ? 32 : 16;
   if (dk > 64) return def;
+  if (!causal && n > cus) return n <= 2 * cus ? 64 : def;
   const int p64 = split_parts32(n, Sk, 64, cus, causal);
   return p64 >= 2 && p64 == split_parts32(n, Sk, def, cus, causal) ? 64 : def;
 }
