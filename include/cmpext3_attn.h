@@ -6,8 +6,9 @@
  * every input and output buffer.  The library itself keeps one exchange
  * buffer per (device, stream) for launches that split key ranges across
  * workgroups (non-causal, when the query blocks do not fill whole rounds of
- * the GPU; fp16/bf16 with D <= 128, and fp32 with at most as many query
- * blocks as CUs): allocated with hipMalloc on the first such launch on that stream
+ * the GPU; fp16/bf16 with D <= 128, fp16/bf16 with D > 128 and fewer query
+ * blocks than CUs, and fp32 with at most as many query blocks as CUs):
+ * allocated with hipMalloc on the first such launch on that stream
  * (about 140 KB per CU), kept until the process ends, so at most 16 of them
  * per device.  On a stream under graph capture, after a failed allocation,
  * or past 16 streams per device those launches run without the split: the
@@ -151,8 +152,8 @@ int cmpext3_attn_fwd_masked(const void* q, const void* k, const void* v, void* o
  * partial results through a fixed 16 MiB (+ 16 KiB of counters) array per
  * device inside the library's code object instead of the per-stream buffer
  * the other entry points allocate.  A split that would need more is cut to
- * fewer key ranges (down to none), so no problem is refused for lack of
- * room.  Every call on one device shares that device's array: calls that
+ * fewer key ranges (down to none; the fp32 and head-dim > 128 kernels go
+ * straight to none), so no problem is refused for lack of room.  Every call on one device shares that device's array: calls that
  * overlap in time on one device (two streams, or a graph replay beside an
  * eager call) race and may mix results; calls in stream order do not.
  * Launches may be captured into a HIP graph (the array's address is fixed).

@@ -109,6 +109,16 @@ def test_describe_key_split_plan():
     assert "key-split" not in abi.describe(f32, 1, 8, 1024, 1024, 64, True)[1]
     assert "key-split" not in abi.describe(f32, 2, 8, 4096, 4096, 40)[1]
     assert "key-split: 4 x 5 parts" in abi.describe(f32, 1, 2, 100, 700, 40)[1]
+    # head dims above 128 (one workgroup per CU): fewer blocks than CUs split
+    # into up to CUs / n parts of at least 4 tiles of 32 keys (at most 32, 8
+    # from the 192 bucket up), never causal
+    assert "key-split: 16 x 8 parts" in abi.describe(f16, 1, 16, 1, 16384, 256)[1]
+    assert "key-split: 64 x 4 parts" in abi.describe(f16, 1, 8, 1024, 4096, 160)[1]
+    assert "key-split: 8 x 32 parts" in abi.describe(f16, 1, 8, 1, 32768, 160)[1]
+    assert "key-split: 4 x 8 parts" in abi.describe(bf16, 1, 4, 100, 3000, 192)[1]
+    assert "key-split: 2 x 23 parts" in abi.describe(bf16, 1, 2, 70, 3000, 160)[1]
+    assert "key-split" not in abi.describe(f16, 1, 8, 1024, 4096, 160, True)[1]
+    assert "key-split" not in abi.describe(f16, 2, 10, 1024, 1024, 160)[1]
 
 
 def _call(q=16, k=16, v=16, o=16, dtype=abi.DTYPE_F16, B=1, H=1, Sq=8, Sk=8, D=64,

@@ -1,5 +1,6 @@
 """GPU parity of the key-split launches of the pipelined fp16/bf16 kernel
-(and of the fp32 kernel's plans at one to two query blocks per CU).
+(and of the fp32 kernel's plans at one to two query blocks per CU, and of the
+split and grouped-query row packing of the head-dim > 128 kernel).
 
 When the query blocks do not fill whole rounds of the chip, the blocks past the
 last whole round run as several workgroups over disjoint key ranges, and the
@@ -250,3 +251,54 @@ def test_fp32_plans_at_one_to_two_blocks_per_cu(case):
     again = abi.attn_fwd(q, k, v, scale, causal)
     torch.cuda.synchronize()
     assert torch.equal(out, again)
+
+
+BIG_D = [
+    # dtype, B, H, Hkv, Sq, Sk, D, scale (None = 1/sqrt(D)): head dims above
+    # 128 run the mfma16 kernel, one workgroup per CU; fewer blocks than CUs split
+    ("fp16", 1, 16, 8, 1, 16384, 256, None),    # long-context decode: packed rows, 8 blocks x 8 parts
+    ("bf16", 16, 16, 8, 1, 4096, 256, None),    # batched decode: 128 blocks x 2 parts
+    ("bf16", 2, 16, 4, 5, 3000, 160, None),     # 5 query rows x 4 heads packed per K/V head, ragged Sk, 23 parts
+    ("fp16", 1, 4, 4, 512, 4096, 160, None),    # prefill-like, 16 blocks x 16 parts
+    ("bf16", 1, 4, 4, 100, 3000, 192, -0.07),   # ragged rows and keys, negative scale, 8 parts
+    ("fp16", 1, 2, 2, 70, 2000, 199, None),     # odd head dim: element-granular rows, 15 parts
+]
+
+
+def _gqa_inputs(dtype, B, H, Hkv, Sq, Sk, D, seed):
+    return W.Workload("bigd", dtype, B, H, Sq, Sk, D, seed=seed, Hkv=Hkv).make_inputs("cuda")
+
+
+@pytest.mark.parametrize("case", BIG_D, ids=[f"{c[0]}-B{c[1]}H{c[2]}kv{c[3]}-q{c[4]}k{c[5]}d{c[6]}" for c in BIG_D])
+def test_large_head_dim_split_and_packed_rows(case):
+    """Head dims above 128 with fewer query blocks than CUs: each block's keys
+    are cut into parts and merged by the last part; grouped-query launches with
+    few query rows pack a K/V head's query heads into one problem.  Against the
+    oracle on K/V repeated per query head, and a rerun bit-identical."""
+    dtype, B, H, Hkv, Sq, Sk, D, scale = case
+    q, k, v = _gqa_inputs(dtype, B, H, Hkv, Sq, Sk, D, seed=Sq + Sk + D)
+    print(f"large-D split: {case}", flush=True)
+    if Hkv == H and torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert "key-split" in _split_text(q, B, H, Sq, Sk, D), _split_text(q, B, H, Sq, Sk, D)
+    s = D ** -0.5 if scale is None else scale
+    out = abi.attn_fwd(q, k, v, s)
+    again = abi.attn_fwd(q, k, v, s)
+    torch.cuda.synchronize()
+    g = H // Hkv
+    kx, vx = (t.cpu().repeat_interleave(g, dim=1) for t in (k, v))
+    err = orc.max_abs_err(out.cpu(), orc.sdpa_np(q.cpu(), kx, vx, s))
+    assert err <= TOL[dtype], f"max abs err {err:.3e}"
+    assert torch.equal(out, again)
+
+
+def test_large_head_dim_split_without_allocation():
+    """The allocation-free entry point runs the same split through the
+    library's fixed scratch (this plan's 2.1 MB fits it): bit for bit the
+    allocating entry point's output."""
+    q, k, v = _gqa_inputs("bf16", 1, 16, 8, 1, 16384, 256, seed=21)
+    s = 256 ** -0.5
+    want = abi.attn_fwd(q, k, v, s)
+    got = torch.empty_like(q)
+    assert abi.attn_fwd_noalloc_raw(q, k, v, got, s) == abi.OK
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)

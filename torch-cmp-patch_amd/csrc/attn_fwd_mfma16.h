@@ -33,6 +33,16 @@
 //    fp32 row sum, so the normaliser uses exactly the rounded P that the PV
 //    MFMA consumes.
 //
+// Key split (non-causal launches with fewer query blocks than CUs: decode
+// steps and short query sweeps, above all at head dims over 128 where one
+// workgroup fills a CU): each block's key range is cut into parts run by
+// separate workgroups; every part leaves its fp32 (O, m, l) in the exchange
+// buffer and the last part of a (block, wave) to finish merges all of them in
+// part order (its own from registers) and writes the output, as in
+// attn_fwd_mfma32.hip.  Grouped-query launches with few query rows arrive
+// with the query heads of a K/V head packed into the rows of one problem
+// (FwdParams::pack_sq), so that K/V is streamed once per K/V head.
+//
 // Reference algorithm: src/cuda/fp16_flash_attention_hfma2.cu:72-243 (Q
 // pre-scaled by scale*log2e, exp2 online softmax with fp32 running max/sum and
 // fp32 output accumulator, one final 1/l).  The reference's bf16 path casts to
@@ -130,7 +140,7 @@ __device__ __forceinline__ int lds_swz(int r) {
 template <typename T, int DK, int DP, int NW, int QB, int BK, int OCC, bool CAUSAL, bool PRESCALE,
           int OPT = 0>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
-attn_fwd_mfma16(const FwdParams p) {
+attn_fwd_mfma16(const FwdParams p, const SplitArgs sa) {
   constexpr int NT = NW * 64;
   constexpr int QPW = 32 * QB;          // query rows per wave
   constexpr int BQ = NW * QPW;
@@ -160,9 +170,17 @@ attn_fwd_mfma16(const FwdParams p) {
   const int l32 = lane & 31;
   const int hh = lane >> 5;
 
-  // ---- which (batch, head, query block) this workgroup owns
+  // ---- which (batch, head, query block) and which part of its keys this
+  // workgroup owns (causal launches never split)
+  int lb = block_x(), part = 0, nparts = 1;
+  if (!CAUSAL && lb >= sa.nfull) {
+    const int r = lb - sa.nfull;
+    nparts = sa.nparts;
+    lb = sa.nfull + r / nparts;
+    part = r - (lb - sa.nfull) * nparts;
+  }
   int bh, qblk;
-  wg_tile(block_x(), p, CAUSAL, bh, qblk);
+  wg_tile(lb, p, CAUSAL, bh, qblk);
   const int b = bh / p.H;
   const int h = bh - b * p.H;
   const int q0 = qblk * BQ;
@@ -174,10 +192,22 @@ attn_fwd_mfma16(const FwdParams p) {
 
   const int Sq = p.Sq, Sk = p.Sk, D = p.D;
   const int qw0 = q0 + wave * QPW;      // first query row of this wave
+  // element offset of row r: packed grouped-query rows interleave the group's
+  // query heads (query head r / pack_sq, position r % pack_sq)
+  auto row_off = [&](int r, int64_t s_head, int64_t s_row) -> int64_t {
+    if (p.pack_sq > 0) {
+      const int g = r / p.pack_sq;
+      return g * s_head + (int64_t)(r - g * p.pack_sq) * s_row;
+    }
+    return (int64_t)r * s_row;
+  };
 
   int kend = Sk;
   if (CAUSAL) kend = min(Sk, q0 + BQ);
-  const int ntiles = (kend + BK - 1) / BK;
+  // this workgroup's key tiles [tbase, tbase + ntiles)
+  const int ntall = (kend + BK - 1) / BK;
+  const int tbase = part * ntall / nparts;
+  const int ntiles = (part + 1) * ntall / nparts - tbase;
 
   // ---- Q as the B operand of S^T = K Q^T: lane holds Q[row][16s + 8hh .. +8]
   const float cq = p.q_sign ? -p.c : p.c;  // signed scale*log2(e) for PRESCALE
@@ -190,7 +220,7 @@ attn_fwd_mfma16(const FwdParams p) {
       const int d = 16 * s + 8 * hh;
       u32x4 x = {0u, 0u, 0u, 0u};
       if (row < Sq && d < D) {
-        const uint16_t* src = qg + (int64_t)row * p.q_s + d;
+        const uint16_t* src = qg + row_off(row, p.q_g, p.q_s) + d;
         x = ELEM ? ld_cols16(src, D - d, p.elem_rows) : *(const u32x4*)src;
       }
       if (PRESCALE) {
@@ -254,9 +284,9 @@ attn_fwd_mfma16(const FwdParams p) {
   // checked path below)
   const bool cols_full = !ELEM && (D == DK) && (D == DP);
   auto load_tile = [&](int t) {
-    const int k0 = t * BK;
-    const uint16_t* kt = kg + t * kstep;
-    const uint16_t* vt = vg + t * vstep;
+    const int k0 = (tbase + t) * BK;
+    const uint16_t* kt = kg + (tbase + t) * kstep;
+    const uint16_t* vt = vg + (tbase + t) * vstep;
     if (cols_full && k0 + BK <= Sk) {
       // interior tile: every chunk this thread owns is in bounds
 #pragma unroll
@@ -320,7 +350,7 @@ attn_fwd_mfma16(const FwdParams p) {
     __syncthreads();
     if (t + 1 < ntiles) load_tile(t + 1);
 
-    const int k0 = t * BK;
+    const int k0 = (tbase + t) * BK;
     const uint16_t* ks = lds + buf * (KTILE + VTILE);
     const uint16_t* vs = ks + KTILE;
 
@@ -463,13 +493,104 @@ attn_fwd_mfma16(const FwdParams p) {
     }
   }
 
-  // ---- epilogue: combine the two halves' partial sums, normalise, store
+  // ---- epilogue: combine the two halves' partial sums
+  float lrow[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) lrow[qb] = xhalf_sum(lsum[qb]);
+  if (!CAUSAL && nparts > 1) {
+    // a wave whose rows all lie past Sq (decode, packed query groups) has
+    // nothing to exchange; every part of the block agrees on that
+    if (qw0 >= Sq) return;
+    // Every part leaves its state and counts itself in; the last one in
+    // merges and writes the output.  Device-scope (aux 16 = sc1) 16-byte
+    // accesses, coherent across the XCDs' L2s.
+    constexpr int NVB = 4 * NDB + 1;  // float4 vectors per query block: O, then (m, l)
+    constexpr int NV = QB * NVB;
+    const int sb = lb - sa.nfull, nwl = sa.nwl;
+    const __amdgpu_buffer_rsrc_t wsr = uniform_rsrc(sa.ws, (int64_t)(sb + 1) * nparts * nwl * NV * 64 * 16);
+    auto voff = [&](int q, int k) { return ((((sb * nparts + q) * nwl + wave) * NV + k) * 64 + lane) * 16; };
+    auto st_ws = [&](f32x4 x, int off) {
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), wsr, off, 0, 16);
+    };
+    auto ld_ws = [&](int off) { return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wsr, off, 0, 16)); };
+    auto frag = [](const f32x16& a, int i) { return (f32x4){a[4 * i], a[4 * i + 1], a[4 * i + 2], a[4 * i + 3]}; };
+    int* const ctr = sa.cnt + 2 * (sb * nwl + wave);  // parts in (the second counter is unused here)
+    // a row that holds nothing from this part's keys: offset -inf
+    float m_own[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      m_own[qb] = lrow[qb] > 0.f ? mb[qb] : -INFINITY;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st_ws(frag(oacc[qb][db], i), voff(part, qb * NVB + 4 * db + i));
+      st_ws((f32x4){m_own[qb], lrow[qb], 0.f, 0.f}, voff(part, qb * NVB + 4 * NDB));
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    int old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old != nparts - 1) return;
+    if (lane == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("" ::: "memory");  // the exchange loads stay after the count
+    // merge in part order, this part from its registers: the same
+    // instructions on the same values whichever part arrives last.  CH parts'
+    // loads are issued together (fewer memory round trips) where the
+    // registers allow; part indices past the last are clamped and dropped.
+    constexpr int CH = NDB <= 2 ? 2 : 1;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      float mt = m_own[qb];
+      for (int q0 = 0; q0 < nparts; q0 += 4) {
+        float mq[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mq[j] = ld_ws(voff(min(q0 + j, nparts - 1), qb * NVB + 4 * NDB))[0];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (q0 + j < nparts && q0 + j != part) mt = fmaxf(mt, mq[j]);
+      }
+      f32x16 own[NDB];
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        own[db] = oacc[qb][db];
+        oacc[qb][db] = (f32x16){};
+      }
+      float l = 0.f;
+      for (int q0 = 0; q0 < nparts; q0 += CH) {
+        f32x4 ml[CH], x[CH][4 * NDB];
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+          const int qq = min(q0 + j, nparts - 1);
+          ml[j] = ld_ws(voff(qq, qb * NVB + 4 * NDB));
+#pragma unroll
+          for (int v = 0; v < 4 * NDB; ++v) x[j][v] = ld_ws(voff(qq, qb * NVB + v));
+        }
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+          const int q = q0 + j;
+          if (q >= nparts) break;
+          const bool mine = q == part;
+          const float mq = mine ? m_own[qb] : ml[j][0];
+          const float a = mq == -INFINITY ? 0.f : fast_exp2(mq - mt);
+          l = __builtin_fmaf(mine ? lrow[qb] : ml[j][1], a, l);
+#pragma unroll
+          for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+              oacc[qb][db][i] = __builtin_fmaf(mine ? own[db][i] : x[j][4 * db + i / 4][i % 4], a, oacc[qb][db][i]);
+        }
+      }
+      lrow[qb] = l;
+    }
+  }
+
+  // ---- normalise, store
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
-    const float inv = 1.f / xhalf_sum(lsum[qb]);
+    const float inv = lrow[qb] > 0.f ? 1.f / lrow[qb] : 0.f;
     const int qrow = qw0 + 32 * qb + l32;
     if (qrow < Sq) {
-      uint16_t* orow = og + (int64_t)qrow * p.o_s;
+      uint16_t* orow = og + row_off(qrow, p.o_g, p.o_s);
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
 #pragma unroll
@@ -491,6 +612,27 @@ attn_fwd_mfma16(const FwdParams p) {
 }
 
 // Launch one instance: grid = B*H*ceil(Sq/BQ) workgroups of NW waves.
+// Key split plan: only when the query blocks leave CUs idle (fewer blocks
+// than CUs), non-causal, into enough parts for up to two workgroups per CU
+// (as many as fit: one at head dims above 128), each part at least
+// kMinTiles16 key tiles long, and at most 32 parts (8 from a 192-wide output
+// up: the last part reads every other part's O back, one part per memory
+// round trip at those widths).  Measured on MI355X, bf16 grouped-query decode
+// over 8 K/V heads (8 packed blocks): D = 256, 16384 keys, 2 / 8 / 32 / 64
+// parts 428 / 178 / 306 / 592 us; D = 160, 32768 keys, 8 / 32 / 64 parts
+// 140 / 66 / 90 us.  Returns the part count (1: no split).
+constexpr int kMinTiles16 = 4;
+inline int split_parts16(int n, int ntiles, int wg_per_cu, int cus, bool causal, int dp) {
+  if (causal || n <= 0 || n >= cus) return 1;
+  int parts = (wg_per_cu < 2 ? wg_per_cu : 2) * cus / n;
+  if (parts > ntiles / kMinTiles16) parts = ntiles / kMinTiles16;
+  const int cap = dp >= 192 ? 8 : 32;
+  if (parts > cap) parts = cap;
+  return parts >= 2 ? parts : 1;
+}
+
+// Launch one instance: grid = B*H*ceil(Sq/BQ) workgroups of NW waves, times
+// the part count of split blocks.
 template <typename T, int DK, int NW, int QB, int BK, int OCC, bool CAUSAL, bool PRESCALE,
           int OPT = 0>
 hipError_t launch_mfma16_cfg(const FwdParams& p0, hipStream_t stream) {
@@ -500,8 +642,21 @@ hipError_t launch_mfma16_cfg(const FwdParams& p0, hipStream_t stream) {
   p.n_qblk = (p.Sq + BQ - 1) / BQ;
   p.n_wg = p.B * p.H * p.n_qblk;
   if (p.n_wg == 0) return hipSuccess;
-  hipLaunchKernelGGL((attn_fwd_mfma16<T, DK, DP, NW, QB, BK, OCC, CAUSAL, PRESCALE, OPT>), dim3(p.n_wg),
-                     dim3(NW * 64), 0, stream, p);
+  const int n = p.n_wg;
+  // waves per block that hold query rows (a single block shorter than BQ has fewer)
+  const int nwl = p.n_qblk > 1 ? NW : (p.Sq + QB * 32 - 1) / (QB * 32) < NW ? (p.Sq + QB * 32 - 1) / (QB * 32) : NW;
+  SplitArgs sa = {n, 1, nullptr, nullptr, nwl};
+  const int parts = split_parts16(n, (p.Sk + BK - 1) / BK, OCC, device_cus(), CAUSAL, DP);
+  if (parts >= 2) {
+    const size_t ws_bytes = (size_t)n * parts * nwl * QB * split_vectors(DP) * 64 * sizeof(f32x4);
+    f32x4* ws = nullptr;
+    int* cnt = nullptr;
+    if (split_exchange(stream, p.fixed_exchange != 0, ws_bytes, 2 * n * nwl, &ws, &cnt))
+      sa = SplitArgs{0, parts, ws, cnt, nwl};
+  }
+  const int nwg = sa.nfull + (n - sa.nfull) * sa.nparts;
+  hipLaunchKernelGGL((attn_fwd_mfma16<T, DK, DP, NW, QB, BK, OCC, CAUSAL, PRESCALE, OPT>), dim3(nwg),
+                     dim3(NW * 64), 0, stream, p, sa);
   return hipGetLastError();
 }
 

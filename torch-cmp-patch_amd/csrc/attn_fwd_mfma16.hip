@@ -63,6 +63,8 @@ hipError_t launch_short16(const FwdParams& p, int dk, bool bf16, hipStream_t s);
 void describe_short16(int dk, int Sq, int Sk, char* buf, int len);
 hipError_t launch_pipe16(const FwdParams& p, int dk, bool bf16, bool causal, bool prescale, hipStream_t s);
 void describe_pipe16(int dk, int B, int H, int Sq, int Sk, bool causal, char* buf, int len);
+bool packs_query_heads(const FwdParams& p, bool causal);
+void pack_query_heads(FwdParams& p);
 
 int mfma16_bucket(int D) {
   for (int dk : kMfma16Dk)
@@ -74,9 +76,16 @@ int mfma16_bucket(int D) {
 // path is taken for fp16 (for bf16 the scaled Q would keep only 8 mantissa bits).
 static bool use_prescale(const FwdParams& p, bool bf16) { return !bf16 && p.c <= 1.0f; }
 
-hipError_t launch_mfma16(const FwdParams& p, bool bf16, bool causal, hipStream_t s) {
-  const int dk = mfma16_bucket(p.D);
+hipError_t launch_mfma16(const FwdParams& p0, bool bf16, bool causal, hipStream_t s) {
+  const int dk = mfma16_bucket(p0.D);
   if (dk < 0) return hipErrorInvalidValue;
+  // grouped-query launches with few query rows that stay on this kernel run
+  // over K/V heads with the group's query rows packed into one problem (the
+  // pipelined kernel packs for itself)
+  FwdParams p = p0;
+  const bool pack = packs_query_heads(p0, causal) && !short16_applies(p0, dk, causal) &&
+                    !((!p0.elem_rows || p0.elem_rows >= 4) && pipe16_applies(p0, dk));
+  if (pack) pack_query_heads(p);
   if (p.elem_rows) {
     // narrow rows (unmasked inference only; the ABI sends masked and training
     // calls here only with whole aligned chunks): 4- or 8-byte pieces on the
@@ -127,10 +136,14 @@ void describe_mfma16(int D, int B, int H, int Sq, int Sk, bool causal, char* buf
   }
   const Tile16 t = tile16(dk);
   const int bq = t.nw * t.qb * 32;
+  const int n = B * H * ((Sq + bq - 1) / bq);
+  const int parts = split_parts16(n, (Sk + t.bk - 1) / t.bk, t.occ, device_cus(), causal, (dk + 31) / 32 * 32);
+  char split[48] = "";
+  if (parts >= 2) snprintf(split, sizeof split, " key-split: %d x %d parts", n, parts);
   snprintf(buf, len,
            "mfma16 32x32x16 S^T-form: DK=%d DP=%d waves=%d qblocks/wave=%d BQ=%d BK=%d "
-           "waves/SIMD=%d qtiles=%d%s",
-           dk, (dk + 31) / 32 * 32, t.nw, t.qb, bq, t.bk, t.occ, (Sq + bq - 1) / bq,
+           "waves/SIMD=%d qtiles=%d%s%s",
+           dk, (dk + 31) / 32 * 32, t.nw, t.qb, bq, t.bk, t.occ, (Sq + bq - 1) / bq, split,
            elem ? " narrow rows" : "");
 }
 
