@@ -302,3 +302,53 @@ def test_large_head_dim_split_without_allocation():
     assert abi.attn_fwd_noalloc_raw(q, k, v, got, s) == abi.OK
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+
+
+def test_large_head_dim_split_under_graph_capture():
+    """Head dims above 128 follow the same graph rules: through the allocating
+    entry point a launch captured on a stream that already owns an exchange
+    buffer records unsplit (replays on a second stream beside eager split
+    launches on the first stay bit-identical and match the oracle), and the
+    allocation-free entry point records its split through the fixed scratch,
+    whose replays equal its eager result bit for bit."""
+    import cmpext3
+    q, k, v = _gqa_inputs("fp16", 1, 4, 4, 1, 8192, 256, seed=23)
+    assert "key-split: 4 x 8 parts" in _split_text(q, 1, 4, 1, 8192, 256) or \
+        torch.cuda.get_device_properties(0).multi_processor_count != 256
+    s_ = 256 ** -0.5
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), s_)
+    s, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        eager = cmpext3.ops.attention(q, k, v, s_, False)   # s now owns a buffer
+    s.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        out = cmpext3.ops.attention(q, k, v, s_, False)
+    torch.cuda.synchronize()
+    replays, eagers = [], []
+    for _ in range(4):
+        with torch.cuda.stream(s2):
+            g.replay()
+            replays.append(out.clone())
+        with torch.cuda.stream(s):
+            eagers.append(cmpext3.ops.attention(q, k, v, s_, False))
+    torch.cuda.synchronize()
+    for r in replays:
+        assert torch.equal(r, replays[0])
+        assert orc.max_abs_err(r.cpu(), ref) <= TOL["fp16"]
+    for e in eagers:
+        assert torch.equal(e, eager)
+    assert orc.max_abs_err(eager.cpu(), ref) <= TOL["fp16"]
+
+    # allocation-free: eager first (the scratch's address is set up outside
+    # capture), then the captured split, replayed with eager work between
+    want = torch.empty_like(q)
+    assert abi.attn_fwd_noalloc_raw(q, k, v, want, s_) == abi.OK
+    torch.cuda.synchronize()
+    got = torch.empty_like(q)
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2, stream=s):
+        rc = abi.attn_fwd_noalloc_raw(q, k, v, got, s_, stream=s)
+    assert rc == abi.OK
+    for r in _replays(g2, got):
+        assert torch.equal(r, want)
