@@ -112,6 +112,14 @@ EXTRA_WORKLOADS = [
              note="head dim 100 (not a multiple of 8 halves), fp16, non-causal"),
     Workload("odd_dim_fp32", "fp32", 1, 8, 1024, 1024, 33, seed=8,
              note="head dim 33 (not a multiple of 4 floats), fp32, non-causal"),
+    # head dims above 128 (one workgroup per CU): grouped-query decode steps
+    # whose few blocks are key-split and whose query heads are packed per K/V head
+    Workload("gqa_decode_d160_bf16", "bf16", 16, 16, 1, 4096, 160, seed=9, Hkv=8,
+             note="decode step at the reference's largest tabled head dim (160): "
+                  "16 query heads over 8 K/V heads, 4096-token KV cache"),
+    Workload("long_decode_d256_bf16", "bf16", 1, 16, 1, 16384, 256, seed=10, Hkv=8,
+             note="single-sequence decode, head dim 256, 16 query heads over 8 K/V "
+                  "heads, 16384-token KV cache"),
 ]
 BY_NAME = {w.name: w for w in WORKLOADS + EXTRA_WORKLOADS}
 
