@@ -364,7 +364,7 @@ def main() -> int:
         "data": "synthetic (seeded N(0,1) Q/K/V, CPU generator -> device)",
         "config": {"workload": wl.name, "B": wl.B, "H": wl.H, "Hkv": wl.kv_heads, "Sq": wl.Sq,
                    "Sk": wl.Sk, "D": wl.D, "causal": wl.causal, "scale": wl.eff_scale,
-                   "entry": "cmpext3.ops.attention -> cmpext3_attn_fwd"},
+                   "entry": "cmpext3.ops.attention -> cmpext3_attn_fwd_ws"},
         "roofline": roofline,
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(wl),
         "configs": configs,

@@ -3,21 +3,21 @@
  *
  * One entry point computes O = softmax(scale * Q K^T [+ causal mask]) V for
  * [B, H, S, D] tensors that already live in device memory.  The caller owns
- * every input and output buffer.  The library itself keeps one exchange
- * buffer per (device, stream) for launches that split key ranges across
- * workgroups (non-causal, when the query blocks do not fill whole rounds of
- * the GPU; fp16/bf16 with D <= 128, fp16/bf16 with D > 128 and fewer query
- * blocks than CUs, and fp32 with at most as many query blocks as CUs):
- * allocated with hipMalloc on the first such launch on that stream
- * (about 140 KB per CU), kept until the process ends, so at most 16 of them
- * per device.  On a stream under graph capture, after a failed allocation,
- * or past 16 streams per device those launches run without the split: the
- * same result within rounding (a split adds the parts' partial sums in
- * another order, and two-part fp16 splits round each part's O/l to fp16),
- * bit-identical from one call to the next either way.  Launches on one
- * stream are ordered, so a stream's buffer is never used by two launches at
- * once; graph replays are unsplit and share nothing.  All launches go on the
- * stream the caller passes.
+ * every input and output buffer, and the library allocates no device memory
+ * of its own.  Launches that split key ranges across workgroups (non-causal,
+ * when the query blocks do not fill whole rounds of the GPU; fp16/bf16 with
+ * D <= 128, fp16/bf16 with D > 128 and fewer query blocks than CUs, and fp32
+ * with at most as many query blocks as CUs) exchange partial results through
+ * a caller-owned workspace (cmpext3_attn_fwd_ws, sized by
+ * cmpext3_attn_fwd_workspace_size) or, in the allocation-free entry point,
+ * through a fixed per-device array inside the library.  Every other call, and
+ * any call whose workspace is null or too small, runs without the split (or
+ * with fewer key ranges): the same result within rounding (a split adds the
+ * parts' partial sums in another order, and two-part fp16 splits round each
+ * part's O/l to fp16), bit-identical from one call to the next for a given
+ * plan.  No launch ever waits for another workgroup, so no interleaving of
+ * launches can hang the GPU.  All launches go on the stream the caller
+ * passes.
  *
  * Reference interfaces this replaces (WifiLast/torch-cmp-patch):
  *   - launch_flash_attention_hfma2(q, k, v, o, B, H, Sq, Sk, D, qs, ks, vs, os,
@@ -38,6 +38,7 @@
 #ifndef CMPEXT3_ATTN_H
 #define CMPEXT3_ATTN_H
 
+#include <stddef.h>
 #include <stdint.h>
 #include <hip/hip_runtime_api.h>
 
@@ -45,7 +46,7 @@
 extern "C" {
 #endif
 
-#define CMPEXT3_ATTN_ABI_VERSION 7
+#define CMPEXT3_ATTN_ABI_VERSION 8
 
 /* dtype codes (CMPEXT3_DTYPE_BOOL: attention masks only) */
 #define CMPEXT3_DTYPE_F16  0
@@ -86,8 +87,8 @@ extern "C" {
  *
  * Returns CMPEXT3_OK, or one of the CMPEXT3_E_* codes above, in which case
  * nothing was launched except for CMPEXT3_E_LAUNCH.  B*H*Sq == 0 is a no-op.
- * Thread-safe; no host synchronisation (the first split launch on a stream
- * allocates its exchange buffer and queues a clear of its counters on it).
+ * Thread-safe; no host synchronisation; nothing is allocated: this entry
+ * point never splits key ranges (cmpext3_attn_fwd_ws with a workspace does).
  */
 int cmpext3_attn_fwd(const void* q, const void* k, const void* v, void* o,
                      int dtype, int B, int H, int Sq, int Sk, int D,
@@ -146,17 +147,72 @@ int cmpext3_attn_fwd_masked(const void* q, const void* k, const void* v, void* o
                             float scale, int causal, hipStream_t stream);
 
 /*
+ * Workspace forward: the arguments, results and return codes of
+ * cmpext3_attn_fwd_masked (mask_dtype -1 = no mask, H_kv == H = no
+ * grouping), plus a caller-owned device workspace for the key split.
+ *
+ *   workspace       : device memory, 16-byte aligned (else CMPEXT3_E_ALIGN),
+ *                     or null (no split).
+ *   workspace_bytes : its size.  cmpext3_attn_fwd_workspace_size gives the
+ *                     bytes the full split plan of a problem takes; with
+ *                     less, the launch cuts its blocks into fewer key ranges,
+ *                     or runs unsplit.  Nothing is ever refused for it.
+ * The workspace's first 16 KiB are counters: they must be zero before the
+ * workspace is first used, and every launch leaves them zero when it
+ * completes, so one workspace can serve any sequence of calls, of any
+ * shapes, that run one after another (for example every call on one
+ * stream).  The rest needs no initialisation.  Two launches that may run at
+ * the same time must not share a workspace: they would not hang, but they
+ * could mix each other's partial results (wrong output, counters left
+ * non-zero for later calls).  The workspace is only read and written by the
+ * launch's kernels on `stream`.
+ *
+ * Reference: launch_flash_attention_hfma2 (src/cuda/fp16_flash_attention_hfma2.cu:269-272)
+ * takes no workspace; it never splits a block's keys.
+ */
+int cmpext3_attn_fwd_ws(const void* q, const void* k, const void* v, void* o,
+                        int dtype, int B, int H, int H_kv, int Sq, int Sk, int D,
+                        const int64_t q_str[3], const int64_t k_str[3],
+                        const int64_t v_str[3], const int64_t o_str[3],
+                        const void* mask, int mask_dtype, const int64_t mask_str[3],
+                        float scale, int causal, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream);
+
+/*
+ * Workspace bytes cmpext3_attn_fwd_ws (with_lse 0) or cmpext3_attn_fwd_lse
+ * (with_lse 1) needs to run the full key-split plan of this problem, for any
+ * row layout of its tensors; 0 when the problem never splits or the
+ * arguments are invalid.  Depends on the device's CU count (the current
+ * device; 256, MI355X's, when none is visible).  Host-only.
+ */
+size_t cmpext3_attn_fwd_workspace_size(int dtype, int B, int H, int H_kv, int Sq, int Sk, int D,
+                                       int mask_dtype, int causal, int with_lse);
+
+/*
+ * The key split a launch of this problem (contiguous [B,H,S,D] tensors) takes
+ * with workspace_bytes of workspace: *key_parts receives the key ranges each
+ * split query block is cut into (1 = unsplit; 0 on error).  Returns the code
+ * the launch would return before launching.  Host-only: runs the launch's
+ * own dispatch up to the point of launching.
+ */
+int cmpext3_attn_fwd_plan(int dtype, int B, int H, int H_kv, int Sq, int Sk, int D, int mask_dtype,
+                          int causal, int with_lse, size_t workspace_bytes, int* key_parts);
+
+/*
  * Allocation-free forward: the arguments, results and return codes of
  * cmpext3_attn_fwd_masked (mask_dtype -1 = no mask, H_kv == H = no grouping),
  * but nothing is ever allocated or freed: key-split launches exchange their
  * partial results through a fixed 16 MiB (+ 16 KiB of counters) array per
- * device inside the library's code object instead of the per-stream buffer
- * the other entry points allocate.  A split that would need more is cut to
- * fewer key ranges (down to none; the fp32 and head-dim > 128 kernels go
- * straight to none), so no problem is refused for lack of room.  Every call on one device shares that device's array: calls that
- * overlap in time on one device (two streams, or a graph replay beside an
- * eager call) race and may mix results; calls in stream order do not.
- * Launches may be captured into a HIP graph (the array's address is fixed).
+ * device inside the library's code object, in the layout of a
+ * cmpext3_attn_fwd_ws workspace.  A split that would need more is cut to
+ * fewer key ranges (down to none), so no problem is refused for lack of
+ * room.  Every call on one device shares that device's array: calls in
+ * stream order are safe; calls that overlap in time on one device (two
+ * streams, or a graph replay beside an eager call) must not be made -- they
+ * cannot hang (no launch waits for another workgroup), but they can give
+ * wrong results and leave counters non-zero, which can make later split
+ * calls on that device wrong too.  Launches may be captured into a HIP graph
+ * (the array's address is fixed).
  *
  * Reference: none.  No counterpart in the reference; it is for callers that
  * cannot allocate device memory (code under HIP graph capture, serving loops
@@ -180,6 +236,8 @@ int cmpext3_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* 
  *
  * Supported for f16/bf16 with D <= 128 (else CMPEXT3_E_TRAINING, nothing
  * launched).  Every such call runs the pipelined kernel, whatever Sk.
+ * workspace / workspace_bytes: as in cmpext3_attn_fwd_ws (null: no split;
+ * size from cmpext3_attn_fwd_workspace_size with with_lse = 1).
  *
  * Reference: none.  The reference is forward-only: its patch hands every
  * call with live autograd to stock torch (cmpext3/__init__.py:115-125).
@@ -189,7 +247,8 @@ int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, f
                          const int64_t q_str[3], const int64_t k_str[3],
                          const int64_t v_str[3], const int64_t o_str[3],
                          const void* mask, int mask_dtype, const int64_t mask_str[3],
-                         float scale, int causal, hipStream_t stream);
+                         float scale, int causal, void* workspace, size_t workspace_bytes,
+                         hipStream_t stream);
 
 /*
  * Backward of the attention above: given q, k, v, the forward output o, its

@@ -18,7 +18,7 @@ def _declared_functions():
     names = set()
     for h in (REPO / "include").glob("*.h"):
         text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
-        names |= set(re.findall(r"^\s*(?:int|const char\*|void)\s+(cmpext3_\w+)\s*\(", text, re.M))
+        names |= set(re.findall(r"^\s*(?:int|size_t|const char\*|void)\s+(cmpext3_\w+)\s*\(", text, re.M))
     return names
 
 
@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version_and_messages():
-    assert abi.lib().cmpext3_attn_abi_version() == 7
+    assert abi.lib().cmpext3_attn_abi_version() == 8
     for code in range(10):
         assert abi.strerror(code) and abi.strerror(code) != "unknown error code"
     assert abi.strerror(99) == "unknown error code"
@@ -186,7 +186,8 @@ def _call_lse(lse=16, dtype=abi.DTYPE_F16, D=64, q=16, Sq=8, Sk=8, scale=0.125):
     st = (ctypes.c_int64 * 3)(512, 512, 64)
     vp = ctypes.c_void_p
     return abi.lib().cmpext3_attn_fwd_lse(vp(q), vp(16), vp(16), vp(16), vp(lse), dtype, 1, 1, 1, Sq, Sk,
-                                          D, st, st, st, st, vp(0), -1, st, ctypes.c_float(scale), 0, None)
+                                          D, st, st, st, st, vp(0), -1, st, ctypes.c_float(scale), 0,
+                                          vp(0), 0, None)
 
 
 def _call_bwd(delta=16, lse=16, dtype=abi.DTYPE_F16, D=64, dq=16, Sq=8, Sk=8, scale=0.125,
@@ -240,7 +241,7 @@ def _call_masked(k_row=64, q_row=64, o_row=64, Sk=1 << 17, Sq=1, mask_str=(0, 0,
     if lse:
         return abi.lib().cmpext3_attn_fwd_lse(vp(16), vp(16), vp(16), vp(16), vp(lse), abi.DTYPE_F16, 1,
                                               1, 1, Sq, Sk, 64, q_st, kv_st, kv_st, o_st, vp(16),
-                                              mask_dtype, m_st, ctypes.c_float(0.125), 0, None)
+                                              mask_dtype, m_st, ctypes.c_float(0.125), 0, vp(0), 0, None)
     return abi.lib().cmpext3_attn_fwd_masked(vp(16), vp(16), vp(16), vp(16), abi.DTYPE_F16, 1, 1, 1, Sq,
                                              Sk, 64, q_st, kv_st, kv_st, o_st, vp(16), mask_dtype, m_st,
                                              ctypes.c_float(0.125), 0, None)
@@ -274,3 +275,60 @@ def test_training_forward_refuses_what_its_backward_would():
     for q_row, o_row in ((wide, 64), (64, wide)):
         fwd = _call_masked(q_row=q_row, o_row=o_row, Sq=Sq, Sk=64, lse=16, mask_dtype=-1)
         assert fwd == abi.E_TOO_LARGE
+
+
+def test_workspace_size_and_plan():
+    """The workspace a problem's full key-split plan takes (16 KiB of counters,
+    then one 1 KiB vector per lane set for every (split block, part, wave)),
+    and the plan a launch takes with a given workspace: none -> unsplit, too
+    little -> fewer key ranges or none, enough -> the full plan.  Host-only
+    dry runs of the launch's own dispatch (256 CUs without a device)."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("plan depends on the visible device's CU count")
+    f16, bf16, f32 = abi.DTYPE_F16, abi.DTYPE_BF16, abi.DTYPE_F32
+    ctr, vec = 16384, 64 * 16
+    # SDXL self-attention: 128 split blocks x 2 parts x 4 waves x (64/8 + 1) vectors
+    need = abi.workspace_size(f16, 2, 10, 10, 4096, 4096, 64)
+    assert need == ctr + 128 * 2 * 4 * 9 * vec
+    assert abi.plan(f16, 2, 10, 10, 4096, 4096, 64, 0) == (abi.OK, 1)          # null workspace: unsplit
+    assert abi.plan(f16, 2, 10, 10, 4096, 4096, 64, need) == (abi.OK, 2)
+    assert abi.plan(f16, 2, 10, 10, 4096, 4096, 64, need - 1) == (abi.OK, 1)   # less than 2 parts fit
+    assert abi.plan(f16, 2, 10, 10, 4096, 4096, 64, 1 << 40) == (abi.OK, 2)
+    # 4 blocks of 2048 keys, 8 parts; a workspace for 5 of them gets 5
+    need = abi.workspace_size(f16, 1, 2, 2, 256, 2048, 64)
+    assert need == ctr + 4 * 8 * 4 * 9 * vec
+    assert abi.plan(f16, 1, 2, 2, 256, 2048, 64, ctr + 4 * 5 * 4 * 9 * vec) == (abi.OK, 5)
+    # masked, and the training forward: the same plan and size
+    assert abi.workspace_size(f16, 1, 2, 2, 256, 2048, 64, mask_dtype=abi.DTYPE_BOOL) == need
+    assert abi.workspace_size(f16, 1, 2, 2, 256, 2048, 64, with_lse=True) == need
+    assert abi.plan(f16, 1, 2, 2, 256, 2048, 64, need, with_lse=True) == (abi.OK, 8)
+    # grouped-query decode (packed rows: one exchanging wave per block), D = 128
+    need = abi.workspace_size(bf16, 16, 16, 8, 1, 4096, 128)
+    assert need == ctr + 128 * 4 * 1 * 17 * vec
+    assert abi.plan(bf16, 16, 16, 8, 1, 4096, 128, need) == (abi.OK, 4)
+    # fp32 config 1: 128 blocks x 4 parts x 4 waves x (4 + 1) vectors
+    need = abi.workspace_size(f32, 1, 8, 8, 1024, 1024, 64)
+    assert need == ctr + 128 * 4 * 4 * 5 * vec
+    assert abi.plan(f32, 1, 8, 8, 1024, 1024, 64, need) == (abi.OK, 4)
+    assert abi.plan(f32, 1, 8, 8, 1024, 1024, 64, 0) == (abi.OK, 1)
+    # head dim 256 decode: 16 blocks x 8 parts
+    assert abi.plan(f16, 1, 16, 16, 1, 16384, 256, 1 << 30) == (abi.OK, 8)
+    # never split: causal, whole rounds, short keys
+    for args in ((f16, 2, 10, 10, 4096, 4096, 64, -1, True), (f16, 2, 4, 4, 4096, 4096, 64),
+                 (f16, 2, 10, 10, 4096, 77, 64)):
+        assert abi.workspace_size(*args) == 0
+    # errors: the size is 0 and the plan reports the code
+    assert abi.workspace_size(f16, 1, 1, 1, 8, 8, 300) == 0
+    assert abi.plan(f16, 1, 1, 1, 8, 8, 300, 0) == (abi.E_HEAD_DIM, 0)
+    assert abi.plan(f32, 1, 1, 1, 8, 8, 64, 0, mask_dtype=abi.DTYPE_BOOL) == (abi.E_MASK, 0)
+    assert abi.plan(f16, 1, 4, 3, 8, 8, 64, 0) == (abi.E_INVALID, 0)
+
+
+def test_workspace_alignment_is_checked_before_launch():
+    st = (ctypes.c_int64 * 3)(512, 512, 64)
+    vp = ctypes.c_void_p
+    rc = abi.lib().cmpext3_attn_fwd_ws(vp(16), vp(16), vp(16), vp(16), abi.DTYPE_F16, 1, 1, 1, 8, 8, 64,
+                                       st, st, st, st, vp(0), -1, st, ctypes.c_float(0.125), 0,
+                                       vp(24), 1 << 20, None)
+    assert rc == abi.E_ALIGN

@@ -15,7 +15,7 @@ round plus a remainder, ragged key counts whose parts get odd tile counts
 (parts settle on different offsets before the merge), back-to-back
 launches of different plans (the per-wave counters must come back to zero),
 and HIP graph capture (under capture every launch runs unsplit: nothing is
-allocated or cleared in the graph and it holds no exchange buffer, so
+allocated or cleared in the graph and it holds no workspace, so
 replays on another stream beside eager split launches stay correct; replays
 equal each other bit for bit and match the oracle).
 """
@@ -86,7 +86,7 @@ def test_split_wide_scores(dtype):
 
 
 def test_split_back_to_back_plans():
-    """Different split plans in a row on one stream share the exchange buffer;
+    """Different split plans in a row on one stream share the workspace;
     a rerun of the first must reproduce it bit for bit."""
     a = _inputs("fp16", 1, 2, 256, 2048, 64, seed=1)
     b = _inputs("fp16", 1, 17, 2048, 512, 64, seed=2)
@@ -170,7 +170,7 @@ def _replays(g, out, reps=4):
 
 
 def test_graph_capture_on_a_fresh_stream_runs_unsplit():
-    """Under capture the library allocates nothing (no exchange buffer, no
+    """Under capture the binding takes no workspace (nothing allocated, no
     memset node): a split-eligible launch on a stream it has not seen runs
     unsplit, and every replay matches the oracle and the first replay."""
     q, k, v = _inputs("fp16", 1, 2, 256, 2048, 64, seed=21)
@@ -188,7 +188,7 @@ def test_graph_capture_on_a_fresh_stream_runs_unsplit():
 
 
 def test_graph_capture_never_carries_a_streams_exchange_buffer():
-    """A stream that already owns an exchange buffer still records its launch
+    """A stream that already owns a workspace still records its launch
     unsplit under capture, so the graph holds no buffer address.  Replays on a
     second stream, running beside eager split launches on the capturing
     stream, equal each other bit for bit and match the oracle, and so do the
@@ -199,7 +199,7 @@ def test_graph_capture_never_carries_a_streams_exchange_buffer():
     import cmpext3
     s, s2 = torch.cuda.Stream(), torch.cuda.Stream()
     with torch.cuda.stream(s):
-        eager = cmpext3.ops.attention(q, k, v, 0.125, False)   # s now owns a buffer
+        eager = cmpext3.ops.attention(q, k, v, 0.125, False)   # s now owns a workspace
     s.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
@@ -294,7 +294,7 @@ def test_large_head_dim_split_and_packed_rows(case):
 def test_large_head_dim_split_without_allocation():
     """The allocation-free entry point runs the same split through the
     library's fixed scratch (this plan's 2.1 MB fits it): bit for bit the
-    allocating entry point's output."""
+    workspace entry point's output."""
     q, k, v = _gqa_inputs("bf16", 1, 16, 8, 1, 16384, 256, seed=21)
     s = 256 ** -0.5
     want = abi.attn_fwd(q, k, v, s)
@@ -305,9 +305,9 @@ def test_large_head_dim_split_without_allocation():
 
 
 def test_large_head_dim_split_under_graph_capture():
-    """Head dims above 128 follow the same graph rules: through the allocating
-    entry point a launch captured on a stream that already owns an exchange
-    buffer records unsplit (replays on a second stream beside eager split
+    """Head dims above 128 follow the same graph rules: through the binding
+    a launch captured on a stream that already owns a workspace records
+    unsplit (replays on a second stream beside eager split
     launches on the first stay bit-identical and match the oracle), and the
     allocation-free entry point records its split through the fixed scratch,
     whose replays equal its eager result bit for bit."""
@@ -319,7 +319,7 @@ def test_large_head_dim_split_under_graph_capture():
     ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), s_)
     s, s2 = torch.cuda.Stream(), torch.cuda.Stream()
     with torch.cuda.stream(s):
-        eager = cmpext3.ops.attention(q, k, v, s_, False)   # s now owns a buffer
+        eager = cmpext3.ops.attention(q, k, v, s_, False)   # s now owns a workspace
     s.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
@@ -352,3 +352,64 @@ def test_large_head_dim_split_under_graph_capture():
     assert rc == abi.OK
     for r in _replays(g2, got):
         assert torch.equal(r, want)
+
+
+def test_binding_takes_its_workspace_from_torch():
+    """The torch binding runs the key split through a workspace from torch's
+    caching allocator (one per stream, counted by memory_allocated), and its
+    output equals the C ABI's workspace entry point bit for bit; the plain
+    entry point (no workspace) runs unsplit and stays within tolerance."""
+    import cmpext3
+    q, k, v = _inputs("fp16", 2, 10, 4096, 4096, 64, seed=31)
+    need = abi.workspace_size(abi.DTYPE_F16, 2, 10, 10, 4096, 4096, 64)
+    assert need > 0
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        before = torch.cuda.memory_allocated()
+        out = cmpext3.ops.attention(q, k, v, 0.125, False)
+        grown = torch.cuda.memory_allocated() - before
+        held = cmpext3.ops.workspace_bytes(0)
+    s.synchronize()
+    print(f"workspace need {need} B, held {held} B, memory_allocated grew {grown} B", flush=True)
+    assert held >= need
+    assert grown >= need  # the output tensor plus the workspace
+    via_abi = torch.empty_like(q)
+    with torch.cuda.stream(s):
+        assert abi.attn_fwd_raw(q, k, v, via_abi, 0.125) == abi.OK
+        again = cmpext3.ops.attention(q, k, v, 0.125, False)
+    s.synchronize()
+    assert torch.equal(out, via_abi)
+    assert torch.equal(out, again)
+    plain = torch.empty_like(q)
+    assert abi.attn_fwd_raw(q, k, v, plain, 0.125, workspace=False) == abi.OK
+    torch.cuda.synchronize()
+    ref = orc.sdpa_np(q[:, :2].cpu(), k[:, :2].cpu(), v[:, :2].cpu(), 0.125)
+    assert orc.max_abs_err(plain[:, :2].cpu(), ref) <= TOL["fp16"]
+    assert orc.max_abs_err(out[:, :2].cpu(), ref) <= TOL["fp16"]
+
+
+def test_short_workspace_cuts_the_plan():
+    """A workspace with room for fewer key ranges than the plan asks runs
+    that many (here 5 of 8), within tolerance and bit-identical on rerun."""
+    q, k, v = _inputs("fp16", 1, 2, 256, 2048, 64, seed=32)
+    need = abi.workspace_size(abi.DTYPE_F16, 1, 2, 2, 256, 2048, 64)
+    part = (need - 16384) // 8
+    rc, parts = abi.plan(abi.DTYPE_F16, 1, 2, 2, 256, 2048, 64, 16384 + 5 * part)
+    assert (rc, parts) == (abi.OK, 5) or torch.cuda.get_device_properties(0).multi_processor_count != 256
+    import ctypes
+    ws = torch.zeros(16384 + 5 * part, dtype=torch.uint8, device="cuda")
+    outs = []
+    for _ in range(2):
+        o = torch.empty_like(q)
+        st = [(ctypes.c_int64 * 3)(t.stride(0), t.stride(1), t.stride(2)) for t in (q, k, v, o)]
+        rc = abi.lib().cmpext3_attn_fwd_ws(
+            *(ctypes.c_void_p(t.data_ptr()) for t in (q, k, v, o)), abi.DTYPE_F16, 1, 2, 2, 256, 2048, 64,
+            *st, ctypes.c_void_p(0), -1, st[0], ctypes.c_float(0.125), 0, ctypes.c_void_p(ws.data_ptr()),
+            ws.numel(), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert rc == abi.OK
+        outs.append(o)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    assert int(ws[:16384].count_nonzero()) == 0   # counters back at zero
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), 0.125)
+    assert orc.max_abs_err(outs[0].cpu(), ref) <= TOL["fp16"]

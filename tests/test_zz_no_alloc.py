@@ -1,9 +1,9 @@
 """GPU test of the allocation-free forward, cmpext3_attn_fwd_noalloc.
 
-The entry point runs the same kernels as cmpext3_attn_fwd_masked; only the key
-split's exchange differs (a fixed per-device array in the library instead of a
-per-stream allocated buffer).  Every call below takes a key-split plan that
-fits that array, so the allocation-free result must equal the allocating
+The entry point runs the same kernels as cmpext3_attn_fwd_ws; only the key
+split's exchange differs (a fixed per-device array in the library instead of
+the caller's workspace).  Every call in the first test takes a key-split plan
+that fits that array, so the allocation-free result must equal the workspace
 entry point's bit for bit (same kernels, same plan, same merge order), and
 both must lie within the north-star tolerance of the float64 oracle.  Calls
 run back to back, each one smaller than the one before, and the first is
@@ -65,7 +65,7 @@ def _oracle_check(name, dtype, q, k, v, out, scale, mask, heads=2):
     assert err <= TOL[dtype], f"{name}: max abs err {err:.3e} > {TOL[dtype]}"
 
 
-def test_noalloc_matches_the_allocating_entry_point_on_calls_in_a_row():
+def test_noalloc_matches_the_workspace_entry_point_on_calls_in_a_row():
     results = {}
     for seed, (name, dtype, B, H, Hkv, Sq, Sk, D, masked) in enumerate(CALLS):
         print(f"noalloc call {name}: {dtype} B={B} H={H}/{Hkv} Sq={Sq} Sk={Sk} D={D} mask={masked}",
@@ -77,7 +77,7 @@ def test_noalloc_matches_the_allocating_entry_point_on_calls_in_a_row():
         want = _call(lambda *a, **kw: abi.attn_fwd_raw(*a[:6], attn_mask=kw["attn_mask"]),
                      q, k, v, scale, mask)
         torch.cuda.synchronize()
-        assert torch.equal(got, want), f"{name}: differs from cmpext3_attn_fwd_masked"
+        assert torch.equal(got, want), f"{name}: differs from cmpext3_attn_fwd_ws"
         _oracle_check(name, dtype, q, k, v, got, scale, mask)
         results[name] = (q, k, v, scale, mask, got)
     # the first (largest) call again, after the smaller ones: bit for bit
@@ -99,3 +99,28 @@ def test_noalloc_passes_argument_checks_like_the_masked_entry_point():
     m = torch.ones(1, 1, 64, 300, dtype=torch.bool, device="cuda")
     qf, kf, vf = (t.float() for t in (q, k, v))
     assert abi.attn_fwd_noalloc_raw(qf, kf, vf, torch.empty_like(qf), 0.1, attn_mask=m) == abi.E_MASK
+
+
+# Plans larger than the fixed scratch: cut to fewer key ranges inside the
+# allocation-free entry point (the allocating plan differs, so these are
+# checked against the float64 oracle and against a rerun, not against the
+# workspace entry point).
+OVERSIZED = [
+    # 128 blocks x 4 parts of 4.7 MB partials: 18.9 MB, cut to 3 parts
+    ("fp16_128x4_cut", "fp16", 1, 16, 16, 1024, 8192, 64),
+    # fp32, D = 128: 128 blocks x 4 parts of 4.7 MB, cut to 3 parts
+    ("fp32_128x4_cut", "fp32", 1, 8, 8, 1024, 2048, 128),
+]
+
+
+@pytest.mark.parametrize("case", OVERSIZED, ids=[c[0] for c in OVERSIZED])
+def test_noalloc_cuts_plans_larger_than_its_scratch(case):
+    name, dtype, B, H, Hkv, Sq, Sk, D = case
+    print(f"noalloc oversized {name}: {dtype} B={B} H={H} Sq={Sq} Sk={Sk} D={D}", flush=True)
+    q, k, v = _inputs(dtype, B, H, Hkv, Sq, Sk, D, seed=7)
+    scale = D ** -0.5
+    got = _call(abi.attn_fwd_noalloc_raw, q, k, v, scale, None)
+    again = _call(abi.attn_fwd_noalloc_raw, q, k, v, scale, None)
+    torch.cuda.synchronize()
+    assert torch.equal(got, again), f"{name}: rerun differs"
+    _oracle_check(name, dtype, q, k, v, got, scale, None)

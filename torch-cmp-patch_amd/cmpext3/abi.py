@@ -14,6 +14,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcmpext3_
 
 # Every function include/cmpext3_attn.h declares.
 SYMBOLS = ("cmpext3_attn_fwd", "cmpext3_attn_fwd_gqa", "cmpext3_attn_fwd_masked",
+           "cmpext3_attn_fwd_ws", "cmpext3_attn_fwd_workspace_size", "cmpext3_attn_fwd_plan",
            "cmpext3_attn_fwd_noalloc", "cmpext3_attn_fwd_lse", "cmpext3_attn_bwd",
            "cmpext3_attn_strerror", "cmpext3_attn_abi_version", "cmpext3_attn_describe")
 
@@ -45,8 +46,18 @@ def lib() -> ctypes.CDLL:
         L.cmpext3_attn_fwd_masked.restype = ci
         L.cmpext3_attn_fwd_noalloc.argtypes = L.cmpext3_attn_fwd_masked.argtypes
         L.cmpext3_attn_fwd_noalloc.restype = ci
+        sz = ctypes.c_size_t
+        L.cmpext3_attn_fwd_ws.argtypes = [vp, vp, vp, vp, ci, ci, ci, ci, ci, ci, ci,
+                                          i64p, i64p, i64p, i64p, vp, ci, i64p,
+                                          ctypes.c_float, ci, vp, sz, vp]
+        L.cmpext3_attn_fwd_ws.restype = ci
+        L.cmpext3_attn_fwd_workspace_size.argtypes = [ci] * 10
+        L.cmpext3_attn_fwd_workspace_size.restype = sz
+        L.cmpext3_attn_fwd_plan.argtypes = [ci] * 10 + [sz, ctypes.POINTER(ci)]
+        L.cmpext3_attn_fwd_plan.restype = ci
         L.cmpext3_attn_fwd_lse.argtypes = [vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci, ci,
-                                           i64p, i64p, i64p, i64p, vp, ci, i64p, ctypes.c_float, ci, vp]
+                                           i64p, i64p, i64p, i64p, vp, ci, i64p, ctypes.c_float, ci,
+                                           vp, sz, vp]
         L.cmpext3_attn_fwd_lse.restype = ci
         L.cmpext3_attn_bwd.argtypes = ([vp] * 10 + [ci] * 7 + [i64p] * 8 + [vp, ci, i64p]
                                        + [ctypes.c_float, ci, vp])
@@ -69,6 +80,43 @@ def describe(dtype: int, B: int, H: int, Sq: int, Sk: int, D: int, causal: bool 
     buf = ctypes.create_string_buffer(256)
     rc = lib().cmpext3_attn_describe(dtype, B, H, Sq, Sk, D, int(causal), buf, 256)
     return rc, buf.value.decode()
+
+
+def workspace_size(dtype: int, B: int, H: int, Hkv: int, Sq: int, Sk: int, D: int,
+                   mask_dtype: int = -1, causal: bool = False, with_lse: bool = False) -> int:
+    """Bytes of workspace the full key-split plan of this problem takes (host only)."""
+    return lib().cmpext3_attn_fwd_workspace_size(dtype, B, H, Hkv, Sq, Sk, D, mask_dtype,
+                                                 int(causal), int(with_lse))
+
+
+def plan(dtype: int, B: int, H: int, Hkv: int, Sq: int, Sk: int, D: int, workspace_bytes: int,
+         mask_dtype: int = -1, causal: bool = False, with_lse: bool = False):
+    """(return code, key ranges per split block) a launch takes with this much
+    workspace (host only; 1 = unsplit)."""
+    parts = ctypes.c_int(-1)
+    rc = lib().cmpext3_attn_fwd_plan(dtype, B, H, Hkv, Sq, Sk, D, mask_dtype, int(causal),
+                                     int(with_lse), workspace_bytes, ctypes.byref(parts))
+    return rc, parts.value
+
+
+# Key-split workspaces of (device, stream), as the torch binding keeps them:
+# zero-filled byte tensors (the counters must start at zero; every launch
+# leaves them so), grown on demand, reused by the calls on that stream.
+_workspaces: dict = {}
+
+
+def workspace_for(t, handle: int, need: int):
+    """(pointer, bytes) of the workspace for stream `handle` on t's device, at
+    least `need` bytes; (None, 0) under graph capture or when need is 0."""
+    import torch
+    if need == 0 or torch.cuda.is_current_stream_capturing():
+        return None, 0
+    key = (t.device.index, handle)
+    w = _workspaces.get(key)
+    if w is None or w.numel() < need:
+        w = torch.zeros(need, dtype=torch.uint8, device=t.device)
+        _workspaces[key] = w
+    return w.data_ptr(), w.numel()
 
 
 def dtype_code(dtype) -> int:
@@ -101,9 +149,11 @@ def _strides(t):
 
 
 def attn_fwd_raw(q, k, v, o, scale: float, causal: bool = False, stream=None,
-                 D: Optional[int] = None, attn_mask=None) -> int:
-    """Call cmpext3_attn_fwd on [B,H,S,D] tensors (any strides with unit last stride),
-    or cmpext3_attn_fwd_gqa when k/v hold fewer heads than q (grouped-query).
+                 D: Optional[int] = None, attn_mask=None, workspace: bool = True) -> int:
+    """Call cmpext3_attn_fwd_ws on [B,H,S,D] tensors (any strides with unit last
+    stride; k/v may hold fewer heads than q: grouped-query) with this module's
+    workspace for the stream (workspace=False: no workspace, so no key split;
+    with no mask the plain cmpext3_attn_fwd / _gqa entry points are called).
     Returns the C return code; launches on `stream` (a torch.cuda.Stream, a raw
     handle, or None for the current stream)."""
     import torch
@@ -114,22 +164,24 @@ def attn_fwd_raw(q, k, v, o, scale: float, causal: bool = False, stream=None,
     else:
         handle = stream.cuda_stream
     B, H, Sq, Dq = q.shape
+    Dx = Dq if D is None else D
     ptrs = (ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()),
             ctypes.c_void_p(v.data_ptr()), ctypes.c_void_p(o.data_ptr()))
-    tail = (_strides(q), _strides(k), _strides(v), _strides(o),
-            ctypes.c_float(scale), int(causal), ctypes.c_void_p(handle))
-    Dx = Dq if D is None else D
-    if attn_mask is not None:
-        m = prepare_mask(attn_mask, B, H, Sq, k.shape[2])
-        mstr = (ctypes.c_int64 * 3)(m.stride(0), m.stride(1), m.stride(2))
-        rc = lib().cmpext3_attn_fwd_masked(*ptrs, dtype_code(q.dtype), B, H, k.shape[1], Sq,
-                                           k.shape[2], Dx, *tail[:4], ctypes.c_void_p(m.data_ptr()),
-                                           dtype_code(m.dtype), mstr, *tail[4:])
-        return rc
-    if k.shape[1] != H:
-        return lib().cmpext3_attn_fwd_gqa(*ptrs, dtype_code(q.dtype), B, H, k.shape[1], Sq,
-                                          k.shape[2], Dx, *tail)
-    return lib().cmpext3_attn_fwd(*ptrs, dtype_code(q.dtype), B, H, Sq, k.shape[2], Dx, *tail)
+    strides = (_strides(q), _strides(k), _strides(v), _strides(o))
+    dt = dtype_code(q.dtype)
+    if not workspace and attn_mask is None:
+        tail = (*strides, ctypes.c_float(scale), int(causal), ctypes.c_void_p(handle))
+        if k.shape[1] != H:
+            return lib().cmpext3_attn_fwd_gqa(*ptrs, dt, B, H, k.shape[1], Sq, k.shape[2], Dx, *tail)
+        return lib().cmpext3_attn_fwd(*ptrs, dt, B, H, Sq, k.shape[2], Dx, *tail)
+    mp, mdt, mst, _keep = _mask_args(attn_mask, B, H, Sq, k.shape[2])
+    wp, wb = None, 0
+    if workspace and q.is_cuda:
+        wp, wb = workspace_for(q, handle, workspace_size(dt, B, H, k.shape[1], Sq, k.shape[2], Dx,
+                                                         mdt, causal))
+    return lib().cmpext3_attn_fwd_ws(*ptrs, dt, B, H, k.shape[1], Sq, k.shape[2], Dx, *strides,
+                                     mp, mdt, mst, ctypes.c_float(scale), int(causal),
+                                     ctypes.c_void_p(wp), wb, ctypes.c_void_p(handle))
 
 
 def attn_fwd_noalloc_raw(q, k, v, o, scale: float, causal: bool = False, stream=None,
@@ -188,11 +240,15 @@ def attn_fwd_lse(q, k, v, scale: Optional[float] = None, causal: bool = False, s
     if scale is None:
         scale = D ** -0.5
     mp, mdt, mst, _keep = _mask_args(attn_mask, B, H, Sq, k.shape[2])
+    handle = _handle(q, stream)
+    wp, wb = workspace_for(q, handle, workspace_size(dtype_code(q.dtype), B, H, k.shape[1], Sq,
+                                                     k.shape[2], D, mdt, causal, with_lse=True))
     rc = lib().cmpext3_attn_fwd_lse(
         ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()),
         ctypes.c_void_p(o.data_ptr()), ctypes.c_void_p(lse.data_ptr()), dtype_code(q.dtype),
         B, H, k.shape[1], Sq, k.shape[2], D, _strides(q), _strides(k), _strides(v), _strides(o),
-        mp, mdt, mst, ctypes.c_float(scale), int(causal), ctypes.c_void_p(_handle(q, stream)))
+        mp, mdt, mst, ctypes.c_float(scale), int(causal), ctypes.c_void_p(wp), wb,
+        ctypes.c_void_p(handle))
     if rc != OK:
         raise RuntimeError(f"cmpext3_attn_fwd_lse: {strerror(rc)} (code {rc})")
     return o, lse

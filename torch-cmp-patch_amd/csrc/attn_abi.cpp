@@ -8,6 +8,7 @@
 // back; the reference's void launchers instead skipped the launch and left the
 // output unwritten (src/main.cpp:1741-1765).
 #include <math.h>
+#include <stdint.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -194,7 +195,7 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
              int H_kv, int Sq, int Sk, int D, const int64_t q_str[3], const int64_t k_str[3],
              const int64_t v_str[3], const int64_t o_str[3], const void* mask, int mask_dtype,
              const int64_t mask_str[3], float scale, int causal, hipStream_t stream,
-             bool fixed_exchange = false) {
+             void* workspace, size_t workspace_bytes, bool fixed_exchange = false) {
   int rc = check_shape(dtype, B, H, Sq, Sk, D);
   if (rc != CMPEXT3_OK) return rc;
   if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;
@@ -204,6 +205,7 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
   if (rc != CMPEXT3_OK) return rc;
   if (!q || !k || !v || !o || !q_str || !k_str || !v_str || !o_str) return CMPEXT3_E_INVALID;
   if (!isfinite(scale)) return CMPEXT3_E_INVALID;
+  if (workspace && !aligned16(workspace)) return CMPEXT3_E_ALIGN;
   const int es = elem_size(dtype);
   if (!aligned_to(q, es) || !aligned_to(k, es) || !aligned_to(v, es) || !aligned_to(o, es))
     return CMPEXT3_E_ALIGN;
@@ -247,6 +249,8 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
   p.c = fabsf(scale) * cmpext3::kLog2e;
   p.q_sign = (scale < 0.f) ? (dtype == CMPEXT3_DTYPE_F32 ? 0x80000000u : 0x80008000u) : 0u;
   p.fixed_exchange = fixed_exchange ? 1 : 0;
+  p.workspace = workspace;
+  p.workspace_bytes = workspace ? workspace_bytes : 0;
   p.elem_rows = chunks ? 0 : piece;
 
   hipError_t err;
@@ -257,9 +261,87 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
   return err == hipSuccess ? CMPEXT3_OK : CMPEXT3_E_LAUNCH;
 }
 
+// Dry run of the forward dispatch for a problem in contiguous [B,H,S,D]
+// layout whose rows are read in `elem`-byte pieces (0: whole 16-byte
+// chunks): the same launchers as fwd_impl with FwdParams::dry set, so the
+// plan recorded is the one a launch would take with workspace_bytes of
+// workspace.  Touches no device (the CU count falls back to MI355X's 256
+// when none is visible).
+int plan_impl(int dtype, int B, int H, int H_kv, int Sq, int Sk, int D, int mask_dtype, int causal,
+              int with_lse, int elem, size_t workspace_bytes, cmpext3::SplitInfo& info) {
+  info.need = 0;
+  info.parts = 1;
+  int rc = check_shape(dtype, B, H, Sq, Sk, D);
+  if (rc != CMPEXT3_OK || (int64_t)B * H * Sq == 0) return rc;
+  if (H_kv < 1 || H_kv > H || H % H_kv != 0) return CMPEXT3_E_INVALID;
+  if (with_lse && (dtype == CMPEXT3_DTYPE_F32 || D > 128)) return CMPEXT3_E_TRAINING;
+  if (mask_dtype != -1) {
+    if (mask_dtype < CMPEXT3_DTYPE_F16 || mask_dtype > CMPEXT3_DTYPE_BOOL) return CMPEXT3_E_DTYPE;
+    if (dtype == CMPEXT3_DTYPE_F32 || D > 128) return CMPEXT3_E_MASK;
+  }
+  if ((mask_dtype != -1 || with_lse) && elem != 0) return CMPEXT3_E_ALIGN;
+  cmpext3::FwdParams p;
+  memset(&p, 0, sizeof p);
+  const int64_t rs = elem ? D : (D + 7) / 8 * 8;  // element row stride of the dry run's layout
+  p.q_s = p.o_s = p.k_s = p.v_s = rs;
+  p.q_h = p.o_h = (int64_t)Sq * rs;
+  p.k_h = p.v_h = (int64_t)Sk * rs;
+  p.q_b = p.o_b = (int64_t)H * Sq * rs;
+  p.k_b = p.v_b = (int64_t)H_kv * Sk * rs;
+  p.B = B; p.H = H; p.Sq = Sq; p.Sk = Sk; p.D = D;
+  p.kv_group = H / H_kv;
+  p.mask_kind = mask_dtype == -1 ? cmpext3::MASK_NONE : mask_kind_of(mask_dtype);
+  p.lse = with_lse ? (float*)&info : nullptr;  // never dereferenced: marks the training forward
+  p.c = 0.125f;
+  p.workspace_bytes = workspace_bytes;
+  p.elem_rows = elem;
+  p.dry = &info;
+  hipError_t err;
+  if (dtype == CMPEXT3_DTYPE_F32)
+    err = cmpext3::launch_mfma32(p, causal != 0, nullptr);
+  else
+    err = cmpext3::launch_mfma16(p, dtype == CMPEXT3_DTYPE_BF16, causal != 0, nullptr);
+  return err == hipSuccess ? CMPEXT3_OK : CMPEXT3_E_INVALID;
+}
+
 }  // namespace
 
 extern "C" {
+
+size_t cmpext3_attn_fwd_workspace_size(int dtype, int B, int H, int H_kv, int Sq, int Sk, int D,
+                                       int mask_dtype, int causal, int with_lse) {
+  // the largest need over every row layout a call may arrive in: whole
+  // aligned chunks, and the 4- and 2-byte piece variants (narrow rows)
+  size_t need = 0;
+  for (int elem : {0, 4, 2}) {
+    cmpext3::SplitInfo info;
+    if (plan_impl(dtype, B, H, H_kv, Sq, Sk, D, mask_dtype, causal, with_lse, elem, SIZE_MAX, info) ==
+            CMPEXT3_OK &&
+        info.need > need)
+      need = info.need;
+  }
+  return need;
+}
+
+int cmpext3_attn_fwd_plan(int dtype, int B, int H, int H_kv, int Sq, int Sk, int D, int mask_dtype,
+                          int causal, int with_lse, size_t workspace_bytes, int* key_parts) {
+  cmpext3::SplitInfo info;
+  const int es = elem_size(dtype);
+  const int elem = es && D * es % 16 != 0 ? (D * es % 4 == 0 ? 4 : 2) : 0;
+  const int rc = plan_impl(dtype, B, H, H_kv, Sq, Sk, D, mask_dtype, causal, with_lse, elem,
+                           workspace_bytes, info);
+  if (key_parts) *key_parts = rc == CMPEXT3_OK ? info.parts : 0;
+  return rc;
+}
+
+int cmpext3_attn_fwd_ws(const void* q, const void* k, const void* v, void* o, int dtype, int B, int H,
+                        int H_kv, int Sq, int Sk, int D, const int64_t q_str[3], const int64_t k_str[3],
+                        const int64_t v_str[3], const int64_t o_str[3], const void* mask, int mask_dtype,
+                        const int64_t mask_str[3], float scale, int causal, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream) {
+  return fwd_impl(q, k, v, o, nullptr, dtype, B, H, H_kv, Sq, Sk, D, q_str, k_str, v_str, o_str, mask,
+                  mask_dtype, mask_str, scale, causal, stream, workspace, workspace_bytes);
+}
 
 int cmpext3_attn_fwd_masked(const void* q, const void* k, const void* v, void* o, int dtype, int B,
                             int H, int H_kv, int Sq, int Sk, int D, const int64_t q_str[3],
@@ -267,7 +349,7 @@ int cmpext3_attn_fwd_masked(const void* q, const void* k, const void* v, void* o
                             const void* mask, int mask_dtype, const int64_t mask_str[3], float scale,
                             int causal, hipStream_t stream) {
   return fwd_impl(q, k, v, o, nullptr, dtype, B, H, H_kv, Sq, Sk, D, q_str, k_str, v_str, o_str, mask,
-                  mask_dtype, mask_str, scale, causal, stream);
+                  mask_dtype, mask_str, scale, causal, stream, nullptr, 0);
 }
 
 int cmpext3_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* o, int dtype, int B,
@@ -276,14 +358,14 @@ int cmpext3_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* 
                              const void* mask, int mask_dtype, const int64_t mask_str[3], float scale,
                              int causal, hipStream_t stream) {
   return fwd_impl(q, k, v, o, nullptr, dtype, B, H, H_kv, Sq, Sk, D, q_str, k_str, v_str, o_str, mask,
-                  mask_dtype, mask_str, scale, causal, stream, /*fixed_exchange=*/true);
+                  mask_dtype, mask_str, scale, causal, stream, nullptr, 0, /*fixed_exchange=*/true);
 }
 
 int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, float* lse, int dtype,
                          int B, int H, int H_kv, int Sq, int Sk, int D, const int64_t q_str[3],
                          const int64_t k_str[3], const int64_t v_str[3], const int64_t o_str[3],
                          const void* mask, int mask_dtype, const int64_t mask_str[3], float scale,
-                         int causal, hipStream_t stream) {
+                         int causal, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   const int rc = check_shape(dtype, B, H, Sq, Sk, D);
   if (rc != CMPEXT3_OK) return rc;
   if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;
@@ -299,7 +381,7 @@ int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, f
   if (!tile_offsets_fit(Sk, k_str[2], v_str[2]) || !tile_offsets_fit(Sq, q_str[2], o_str[2]))
     return CMPEXT3_E_TOO_LARGE;
   return fwd_impl(q, k, v, o, lse, dtype, B, H, H_kv, Sq, Sk, D, q_str, k_str, v_str, o_str, mask,
-                  mask_dtype, mask_str, scale, causal, stream);
+                  mask_dtype, mask_str, scale, causal, stream, workspace, workspace_bytes);
 }
 
 int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,

@@ -14,6 +14,8 @@
 
 namespace cmpext3 {
 
+struct SplitInfo;
+
 struct FwdParams {
   const void* q;
   const void* k;
@@ -45,9 +47,17 @@ struct FwdParams {
   // whole group of query heads and q_g / o_g over one query head
   int pack_sq;
   int64_t q_g, o_g;
-  // host side only: the key split exchanges through the library's fixed
-  // per-device scratch instead of a per-stream allocated buffer
+  // host side only: where a key split exchanges its partial results.
+  // fixed_exchange != 0: the library's fixed per-device scratch (the
+  // allocation-free entry point); otherwise the caller's workspace
+  // (workspace_bytes of it; null / too small: fewer key ranges, or none).
   int fixed_exchange;
+  void* workspace;
+  size_t workspace_bytes;
+  // host side only: a dry run (workspace size query, plan description).
+  // When set, the launchers record the plan they would launch here and
+  // launch nothing.
+  SplitInfo* dry;
   // 0 when every row is whole 16-byte chunks at 16-byte aligned addresses;
   // otherwise the piece size in bytes (2, 4 or 8) of the narrow variants
   // (ld_cols16 / ld_cols32): the largest that divides every base pointer,
@@ -243,13 +253,31 @@ struct SplitArgs {
 // fragments, then (m, l)
 constexpr int split_vectors(int dp) { return dp / 8 + 1; }
 
-// Exchange space for a key split (host side, attn_fwd_pipe16.hip): at least
-// ws_bytes of partials and ncnt zeroed counters, from the library's fixed
-// per-device scratch (fixed != 0: the allocation-free entry point) or from the
-// stream's allocated buffer.  False when none is available (a stream under
-// graph capture, a failed allocation, a plan larger than the space): the
-// caller then launches unsplit.
-bool split_exchange(hipStream_t s, bool fixed, size_t ws_bytes, int ncnt, f32x4** ws, int** cnt);
+// Layout of every exchange space (the caller's workspace and the library's
+// fixed scratch alike): kExchangeCounters 32-bit counters first, then the
+// partial results.  The counters must be zero before a space's first use;
+// every split launch puts the ones it used back to zero, so a space reused
+// in stream order, for any problem shape, stays ready.
+constexpr int kExchangeCounters = 4096;
+constexpr size_t kExchangeCounterBytes = kExchangeCounters * sizeof(int);
+
+// What a launch would do (FwdParams::dry): the workspace bytes that let its
+// full key-split plan run (0: it never splits) and the key ranges per split
+// block it takes with the workspace it was given (1: unsplit).
+struct SplitInfo {
+  size_t need;
+  int parts;
+};
+
+// Bind a key-split plan to exchange space (host side, attn_fwd_pipe16.hip).
+// The plan cuts each of its split blocks into `parts` key ranges; one range
+// of all of them takes part_bytes of partials and the plan uses ncnt
+// counters.  Returns the key ranges that fit the space FwdParams names (the
+// fixed scratch, or the caller's workspace), at most `parts` and 1 when no
+// split fits (then the launch runs unsplit), and sets ws / cnt.  A dry run
+// records the full plan's need and the part count in p.dry and binds
+// nothing.
+int bind_exchange(const FwdParams& p, int parts, size_t part_bytes, int ncnt, f32x4** ws, int** cnt);
 
 // Raw buffer resource over [base, base + bytes) (gfx9 dword3: 32-bit raw
 // reads).  The fields go through readfirstlane so that the compiler keeps the

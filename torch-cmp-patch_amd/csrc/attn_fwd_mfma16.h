@@ -648,12 +648,14 @@ hipError_t launch_mfma16_cfg(const FwdParams& p0, hipStream_t stream) {
   SplitArgs sa = {n, 1, nullptr, nullptr, nwl};
   const int parts = split_parts16(n, (p.Sk + BK - 1) / BK, OCC, device_cus(), CAUSAL, DP);
   if (parts >= 2) {
-    const size_t ws_bytes = (size_t)n * parts * nwl * QB * split_vectors(DP) * 64 * sizeof(f32x4);
+    // every block is split; one key range of all of them takes part_bytes
+    const size_t part_bytes = (size_t)n * nwl * QB * split_vectors(DP) * 64 * sizeof(f32x4);
     f32x4* ws = nullptr;
     int* cnt = nullptr;
-    if (split_exchange(stream, p.fixed_exchange != 0, ws_bytes, 2 * n * nwl, &ws, &cnt))
-      sa = SplitArgs{0, parts, ws, cnt, nwl};
+    const int fit = bind_exchange(p, parts, part_bytes, 2 * n * nwl, &ws, &cnt);
+    if (fit >= 2) sa = SplitArgs{0, fit, ws, cnt, nwl};
   }
+  if (p.dry) return hipSuccess;
   const int nwg = sa.nfull + (n - sa.nfull) * sa.nparts;
   hipLaunchKernelGGL((attn_fwd_mfma16<T, DK, DP, NW, QB, BK, OCC, CAUSAL, PRESCALE, OPT>), dim3(nwg),
                      dim3(NW * 64), 0, stream, p, sa);

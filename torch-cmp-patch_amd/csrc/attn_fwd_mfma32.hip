@@ -425,12 +425,14 @@ hipError_t launch_mfma32_bk(const FwdParams& p0, hipStream_t stream) {
   SplitArgs sa = {n, 1, nullptr, nullptr, nwl};
   const int parts = split_parts32(n, p.Sk, BK, device_cus(), CAUSAL);
   if (parts >= 2) {
-    const size_t ws_bytes = (size_t)n * parts * nwl * NQB * (NDB + 1) * 64 * sizeof(f32x4);
+    // every block is split; one key range of all of them takes part_bytes
+    const size_t part_bytes = (size_t)n * nwl * NQB * (NDB + 1) * 64 * sizeof(f32x4);
     f32x4* ws = nullptr;
     int* cnt = nullptr;
-    if (split_exchange(stream, p.fixed_exchange != 0, ws_bytes, 2 * n * nwl, &ws, &cnt))
-      sa = SplitArgs{0, parts, ws, cnt, nwl};
+    const int fit = bind_exchange(p, parts, part_bytes, 2 * n * nwl, &ws, &cnt);
+    if (fit >= 2) sa = SplitArgs{0, fit, ws, cnt, nwl};
   }
+  if (p.dry) return hipSuccess;
   const int nwg = sa.nfull + (n - sa.nfull) * sa.nparts;
   hipLaunchKernelGGL((attn_fwd_mfma32<DK, NW, NQB, BK, CAUSAL, ELEM>), dim3(nwg), dim3(NW * 64), 0, stream, p,
                      sa);

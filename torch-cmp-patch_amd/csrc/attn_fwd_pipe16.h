@@ -788,15 +788,15 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   if (qlo >= Sq) return;
   if (!CAUSAL && nparts > 1) {  // causal launches never split
     // Leave this part's state, then let the last part of the block merge
-    // (its own state straight from its registers).  Two parts (the
-    // tail of a whole-round grid, where each part holds up to 36 KB per
-    // 128-row block): a ticket is taken first, so only the first part writes
-    // and the second waits for it (it holds a ticket, so it is resident with
-    // only its stores left).  More parts (short-query grids, whose parts end
-    // together): every part writes, then counts itself in, and the last one
-    // in merges with no wait.  Device-scope (sc1) stores and loads keep the
-    // exchange coherent across the XCDs' L2s without cache-wide write-back
-    // or invalidation.
+    // (its own state straight from its registers); no part ever waits for
+    // another workgroup.  Two parts (the tail of a whole-round grid, where
+    // each part holds up to 36 KB per 128-row block): the parts count their
+    // arrivals first, so usually only the first writes and the second merges
+    // (both write only when the second arrives while the first is still
+    // writing).  More parts (short-query grids, whose parts end together):
+    // every part writes, then counts itself in, and the last one in merges.
+    // Device-scope (sc1) stores and loads keep the exchange coherent across
+    // the XCDs' L2s without cache-wide write-back or invalidation.
     constexpr int NV = split_vectors(DP);
     static_assert(NV == NDB * 4 + 1, "O fragments + (m, l)");
     const int sb = lb - sa.nfull;
@@ -814,7 +814,7 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), wsr, off, 0, 16);
     };
     auto ld_ws = [&](int off) { return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wsr, off, 0, 16)); };
-    int* const ctr = sa.cnt + 2 * (sb * nwl + wave);  // {parts in, parts written}
+    int* const ctr = sa.cnt + 2 * (sb * nwl + wave);  // {parts arrived, states written}
     // a part whose keys are all masked for this row holds nothing: offset -inf
     const float m_own = lsum > 0.f ? mb : -INFINITY;
     // Two fp16 parts exchange their O normalised by their own row sum, in
@@ -854,17 +854,27 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     };
     if (nparts == 2) {
-      int ticket = 0;
-      if (lane == 0) ticket = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      ticket = __builtin_amdgcn_readfirstlane(ticket);
-      if (ticket == 0) {
+      // Arrival order decides who writes; nobody waits.  The first to arrive
+      // always leaves its state.  The second leaves it only if the first has
+      // not finished writing yet (the written counter still 0).  Whoever
+      // then completes the pair (finds the other's state written) merges.
+      auto add = [&](int* c) {
+        int old = 0;
+        if (lane == 0) old = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return __builtin_amdgcn_readfirstlane(old);
+      };
+      if (add(ctr) == 0) {
         leave_state();
-        if (lane == 0) __hip_atomic_store(ctr + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return;
+        if (add(ctr + 1) == 0) return;  // the second part merges
+      } else {
+        int w = 0;
+        if (lane == 0) w = __hip_atomic_load(ctr + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__builtin_amdgcn_readfirstlane(w) == 0) {
+          leave_state();
+          if (add(ctr + 1) == 0) return;  // the first part merges
+        }
       }
       if (lane == 0) {
-        while (__hip_atomic_load(ctr + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0)
-          __builtin_amdgcn_s_sleep(1);
         __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(ctr + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
@@ -876,7 +886,7 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
       if (old != nparts - 1) return;
       if (lane == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    asm volatile("" ::: "memory");  // the exchange loads stay after the wait
+    asm volatile("" ::: "memory");  // the exchange loads stay after the counters
     // Merge every part in part order, this one from its registers: the same
     // instructions on the same values whichever part arrives last, so a
     // rerun is bit-identical.
@@ -1005,6 +1015,7 @@ hipError_t launch_pipe16_cfg(const FwdParams& p0, const SplitArgs& sa, hipStream
   // buffer offsets of the K/V tiles are 32-bit
   const int64_t rs = p.k_s > p.v_s ? p.k_s : p.v_s;
   if ((int64_t)(p.Sk + BK) * rs * 2 >= (int64_t(1) << 31)) return hipErrorInvalidValue;
+  if (p.dry) return hipSuccess;
   const int nwg = sa.nfull + (p.n_wg - sa.nfull) * sa.nparts;
   hipLaunchKernelGGL((attn_fwd_pipe16<T, DK, DP, NW, BK, OCC, CAUSAL, PRESCALE, OPT>), dim3(nwg),
                      dim3(NW * 64), 0, stream, p, sa);

@@ -8,18 +8,15 @@
 // workgroups and 32-key tiles; the waves per SIMD are the most the registers
 // allow without spilling (D = 32: 4, D <= 64: 3, D <= 128: 2).
 //
-// The key split (no counterpart in the reference) needs an exchange buffer.
-// The ordinary entry points use one per (device, stream): 35.7 MB on 256 CUs,
-// allocated on first use and kept for the life of the process, for at most
-// 16 streams per device (571 MB).  Where it cannot be had (a stream under
-// graph capture, an allocation failure, a 17th stream) the launch simply runs
-// unsplit.  The allocation-free entry point uses a fixed per-device array in
-// this file instead (`scratch` below) and never allocates.
+// The key split (no counterpart in the reference) needs exchange space, and
+// the library allocates none: the workspace entry points take it from the
+// caller (cmpext3_attn_fwd_workspace_size says how much), the
+// allocation-free entry point uses a fixed per-device array in this file
+// (`scratch` below), and every other call runs unsplit.  bind_exchange, the
+// one place a plan meets its space, serves all the split kernels.
 #include <stdio.h>
 
-#include <map>
 #include <mutex>
-#include <utility>
 
 #include "attn_fwd_pipe16.h"
 
@@ -34,141 +31,53 @@ constexpr int pipe_occ(int dk) { return dk <= 32 ? 4 : dk <= 64 ? 3 : 2; }
 constexpr int pipe_occ_masked(int dk) { return dk <= 64 ? 3 : 2; }
 
 // Split plan limits: a part scans at least kMinPartTiles key tiles (shorter
-// parts spend more on their prologue and merge than they save), and at most
-// kMaxStreams streams per device get an exchange buffer.
+// parts spend more on their prologue and merge than they save); with no
+// whole round a CU holds at most kMaxPartsPerCu parts at once.
 constexpr int kMinPartTiles = 8;
-constexpr int kMaxStreams = 16;
-constexpr int kMi355xCus = 256;  // used by describe() when no device is visible
-
-// Exchange buffer sized for the largest plan on this device: at most
-// kMaxPartsPerCu parts per CU (split blocks * parts <= kMaxPartsPerCu * CUs),
-// kPipeNw waves, DP <= 128.
 constexpr int kMaxPartsPerCu = 2;
-
-struct Exchange {
-  f32x4* ws;
-  int* cnt;
-};
-
-size_t exchange_ws_bytes(int cus) {
-  return (size_t)cus * kMaxPartsPerCu * kPipeNw * split_vectors(128) * 64 * sizeof(f32x4);
-}
-// two counters (tickets taken, parts written) per (split block, wave)
-size_t exchange_cnt_bytes(int cus) { return (size_t)2 * cus * kPipeNw * sizeof(int); }
-
-// The exchange buffer of (current device, stream s), allocated on first use.
-// A stream under graph capture never gets one, not even the buffer it already
-// owns: a captured launch would carry that buffer's address into every
-// replay, and a replay on another stream while s runs an eager split launch
-// would share its counters and partials.  Captured launches therefore run
-// unsplit, and nothing is allocated or cleared while a graph is recorded.
-bool exchange_for(hipStream_t s, int cus, Exchange& out) {
-  static std::mutex mu;
-  static std::map<std::pair<int, hipStream_t>, Exchange> cache;
-  static int per_dev[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
-    (void)hipGetLastError();
-    return false;
-  }
-  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
-    (void)hipGetLastError();
-    return false;
-  }
-  std::lock_guard<std::mutex> lock(mu);
-  const auto key = std::make_pair(dev, s);
-  auto it = cache.find(key);
-  if (it != cache.end()) {
-    out = it->second;
-    return true;
-  }
-  if (per_dev[dev] >= kMaxStreams) return false;
-  const size_t wsb = exchange_ws_bytes(cus), cb = exchange_cnt_bytes(cus);
-  void* mem = nullptr;
-  if (hipMalloc(&mem, wsb + cb) != hipSuccess) {
-    (void)hipGetLastError();
-    return false;
-  }
-  Exchange e{(f32x4*)mem, (int*)((char*)mem + wsb)};
-  // the counters start at zero; every merge puts its counter back
-  if (hipMemsetAsync(e.cnt, 0, cb, s) != hipSuccess) {
-    (void)hipGetLastError();
-    (void)hipFree(mem);
-    return false;
-  }
-  cache[key] = e;
-  ++per_dev[dev];
-  out = e;
-  return true;
-}
+constexpr int kMi355xCus = 256;  // used when no device is visible (host-only calls)
 
 // ---- Exchange storage of the allocation-free entry point
 //
 // One fixed array per device in the library's code object, zero-filled when
 // the code object is loaded on a device and never allocated or freed by the
-// library: 16 MiB of partial (O, m, l) vectors, then one counter per (split
-// block, wave).  Every allocation-free call on a device shares it, so such
-// calls that overlap in time on one device (two streams, or a graph replay
-// beside an eager call) race; calls in stream order are safe, because each
-// merge puts its counter back to zero.  Host code never passes `scratch`
-// itself to a kernel (in host code the name is only a stand-in for the
-// device symbol): the device address comes from hipGetSymbolAddress, once
-// per device.
+// library: the counters, then 16 MiB of partial (O, m, l) vectors (the
+// layout of every exchange space, attn_common.h).  Every allocation-free
+// call on a device shares it.  Host code never passes `scratch` itself to a
+// kernel (in host code the name is only a stand-in for the device symbol):
+// the device address comes from hipGetSymbolAddress, once per device.
 constexpr size_t kScratchWsBytes = size_t(16) << 20;
-constexpr int kScratchCounters = 4096;
-constexpr size_t kScratchBytes = kScratchWsBytes + kScratchCounters * sizeof(int);
+constexpr size_t kScratchBytes = kExchangeCounterBytes + kScratchWsBytes;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
-__global__ void zero_ints(int* __restrict__ x, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) x[i] = 0;
-}
-
-struct ScratchSlot {
-  std::once_flag once;
-  void* ptr = nullptr;  // device address of `scratch` on this device
-};
-
-// This device's scratch, resolved on the first call with the device current.
-// The counters are cleared then by a fill kernel on the caller's stream (a
-// kernel node, not a memset node, if that first call is being captured); the
-// code object's zero fill already covers every later case.
-bool scratch_for(hipStream_t s, Exchange& out) {
-  static ScratchSlot slots[64];
+// This device's scratch address, looked up on the first call with the device
+// current (a failed lookup is retried on the next call; until one succeeds
+// the allocation-free calls run unsplit).  Nothing is launched: the code
+// object's zero fill is the counters' initial state.
+void* scratch_ptr() {
+  static std::mutex mu;
+  static void* ptrs[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
     (void)hipGetLastError();
-    return false;
+    return nullptr;
   }
-  ScratchSlot& sl = slots[dev];
-  std::call_once(sl.once, [&] {
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
     void* ptr = nullptr;
-    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) {
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess) {
       (void)hipGetLastError();
-      return;
+      return nullptr;
     }
-    int* cnt = (int*)((char*)ptr + kScratchWsBytes);
-    hipLaunchKernelGGL(zero_ints, dim3((kScratchCounters + 255) / 256), dim3(256), 0, s, cnt, kScratchCounters);
-    if (hipGetLastError() != hipSuccess) return;
-    sl.ptr = ptr;
-  });
-  if (!sl.ptr) return false;
-  out.ws = (f32x4*)sl.ptr;
-  out.cnt = (int*)((char*)sl.ptr + kScratchWsBytes);
-  return true;
+    ptrs[dev] = ptr;
+  }
+  return ptrs[dev];
 }
 
 // Waves per block that hold query rows: all of them unless the launch is a
 // single block shorter than the workgroup (decode, packed grouped-query rows).
 int exchange_waves(int n_qblk, int Sq) {
   return n_qblk > 1 ? kPipeNw : (Sq + 31) / 32 < kPipeNw ? (Sq + 31) / 32 : kPipeNw;
-}
-
-// Exchange bytes of a plan: one 1 KiB vector per lane-set, split_vectors per
-// (split block, part, exchanging wave).
-size_t plan_ws_bytes(const SplitArgs& sa, int n, int dp) {
-  return (size_t)(n - sa.nfull) * sa.nparts * sa.nwl * split_vectors(dp) * 64 * sizeof(f32x4);
 }
 
 // Which blocks run whole and how the rest are cut.  n blocks on `cus` CUs at
@@ -294,19 +203,39 @@ int device_cus() {
   return cus[dev];
 }
 
-bool split_exchange(hipStream_t s, bool fixed, size_t ws_bytes, int ncnt, f32x4** ws, int** cnt) {
-  Exchange e;
-  if (fixed) {
-    if (ws_bytes > kScratchWsBytes || ncnt > kScratchCounters || !scratch_for(s, e)) return false;
-  } else {
-    const int cus = device_cus();
-    if (ws_bytes > exchange_ws_bytes(cus) || (size_t)ncnt * sizeof(int) > exchange_cnt_bytes(cus) ||
-        !exchange_for(s, cus, e))
-      return false;
+int bind_exchange(const FwdParams& p, int parts, size_t part_bytes, int ncnt, f32x4** ws, int** cnt) {
+  *ws = nullptr;
+  *cnt = nullptr;
+  if (parts < 2) return 1;
+  // the space this call may use: the fixed scratch, or the caller's workspace
+  void* base = nullptr;
+  size_t bytes = 0;
+  if (p.dry) {
+    p.dry->need = kExchangeCounterBytes + (size_t)parts * part_bytes;
+    bytes = p.fixed_exchange ? kScratchBytes : p.workspace_bytes;
+  } else if (p.fixed_exchange) {
+    base = scratch_ptr();
+    bytes = base ? kScratchBytes : 0;
+  } else if (p.workspace) {
+    base = p.workspace;
+    bytes = p.workspace_bytes;
   }
-  *ws = e.ws;
-  *cnt = e.cnt;
-  return true;
+  // as many key ranges as the partials room holds, if the counters fit
+  int fit = 0;
+  if (bytes > kExchangeCounterBytes && ncnt <= kExchangeCounters && part_bytes > 0) {
+    const size_t room = (bytes - kExchangeCounterBytes) / part_bytes;
+    fit = room < (size_t)parts ? (int)room : parts;
+  }
+  if (fit < 2) fit = 1;
+  if (p.dry) {
+    p.dry->parts = fit;
+    return fit;
+  }
+  if (fit >= 2) {
+    *cnt = (int*)base;
+    *ws = (f32x4*)((char*)base + kExchangeCounterBytes);
+  }
+  return fit;
 }
 
 // True when the pipelined kernel takes this problem: head-dim bucket <= 128,
@@ -367,33 +296,18 @@ hipError_t launch_pipe16(const FwdParams& p0, int dk0, bool bf16, bool causal, b
   const int n = n_blocks(p.B, p.H, p.Sq);
   SplitArgs sa = split_plan(n, n_key_tiles(p.Sk), occ, cus, causal);
   sa.nwl = exchange_waves((p.Sq + kPipeNw * 32 - 1) / (kPipeNw * 32), p.Sq);
-  const SplitArgs whole = {n, 1, nullptr, nullptr, sa.nwl};
-  if (sa.nparts > 1 && p.fixed_exchange) {
-    // Allocation-free call: cut the plan to what the fixed scratch holds (an
-    // unsplit launch needs none of it, so no problem is ever refused for it).
+  if (sa.nparts > 1) {
+    // Exchange space: the fixed scratch or the caller's workspace, cut to
+    // fewer key ranges when the plan does not fit it (an unsplit launch needs
+    // none, so no problem is ever refused for want of space).  The plan keeps
+    // its whole blocks; only the split blocks' part count changes.
     const int dp = (dk + 31) / 32 * 32;
     const int nsplit = n - sa.nfull;
-    const size_t per_part = (size_t)nsplit * sa.nwl * split_vectors(dp) * 64 * sizeof(f32x4);
-    const int fit = (int64_t)2 * nsplit * sa.nwl > kScratchCounters ? 0 : (int)(kScratchWsBytes / per_part);
-    if (sa.nparts > fit) sa.nparts = fit;
-    if (sa.nparts < 2) {
-      sa = whole;
-    } else {
-      Exchange e;
-      if (!scratch_for(s, e)) return hipErrorNotInitialized;
-      if (plan_ws_bytes(sa, n, dp) > kScratchWsBytes) return hipErrorInvalidValue;
-      sa.ws = e.ws;
-      sa.cnt = e.cnt;
-    }
-  } else if (sa.nparts > 1) {
-    Exchange e;
-    if (exchange_for(s, cus, e)) {
-      sa.ws = e.ws;
-      sa.cnt = e.cnt;
-    } else {
-      sa = whole;
-    }
+    const size_t part_bytes = (size_t)nsplit * sa.nwl * split_vectors(dp) * 64 * sizeof(f32x4);
+    sa.nparts = bind_exchange(p, sa.nparts, part_bytes, 2 * nsplit * sa.nwl, &sa.ws, &sa.cnt);
+    if (sa.nparts < 2) sa = SplitArgs{n, 1, nullptr, nullptr, sa.nwl};
   }
+  if (p.dry) return hipSuccess;
   if (p.lse) {  // training forward, masked or not
     if (bf16) return causal ? launch_lse<__bf16, true, false>(p, sa, dk, s) : launch_lse<__bf16, false, false>(p, sa, dk, s);
     if (prescale)

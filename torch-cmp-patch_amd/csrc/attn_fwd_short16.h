@@ -253,6 +253,7 @@ hipError_t launch_short16_cfg(const FwdParams& p0, hipStream_t stream) {
   if (p.n_wg == 0) return hipSuccess;
   const int64_t rs = p.k_s > p.v_s ? p.k_s : p.v_s;
   if ((int64_t)(32 * NKB) * rs * 2 >= (int64_t(1) << 31)) return hipErrorInvalidValue;
+  if (p.dry) return hipSuccess;  // never splits
   hipLaunchKernelGGL((attn_fwd_short16<T, DK, DP, NKH, OPT>), dim3(p.n_wg), dim3(256), 0, stream, p);
   return hipGetLastError();
 }

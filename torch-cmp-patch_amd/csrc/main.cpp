@@ -27,6 +27,9 @@
 // counterpart: the reference is forward-only, cmpext3/__init__.py:115-125),
 // used by cmpext3's autograd Function.
 #include <cmath>
+#include <map>
+#include <mutex>
+#include <utility>
 #include <vector>
 
 #include <torch/extension.h>
@@ -53,6 +56,46 @@ struct Mask {
   int dtype = -1;
 };
 
+// Key-split workspace of one (device, stream): a byte tensor from torch's
+// caching allocator (so torch.cuda.memory_allocated counts it), zero-filled
+// when made -- its first 16 KiB are the counters every launch leaves at zero
+// -- and kept for later calls on the stream, replaced by a larger one when a
+// bigger plan arrives.  Calls on one stream run in order, so they can share
+// it.  A stream under graph capture gets none and its launch runs unsplit: a
+// captured launch would carry the buffer into replays that can run beside
+// eager calls on the stream.
+struct Workspace {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+
+std::mutex ws_mu;
+std::map<std::pair<int, hipStream_t>, torch::Tensor> ws_cache;  // guarded by ws_mu
+
+Workspace workspace_for(const torch::Tensor& like, hipStream_t stream, size_t need) {
+  Workspace w;
+  if (need == 0) return w;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cap) != hipSuccess) {
+    (void)hipGetLastError();
+    return w;
+  }
+  if (cap != hipStreamCaptureStatusNone) return w;
+  std::lock_guard<std::mutex> lock(ws_mu);
+  torch::Tensor& t = ws_cache[std::make_pair((int)like.get_device(), stream)];
+  if (!t.defined() || (size_t)t.numel() < need)
+    t = torch::zeros({(int64_t)need}, like.options().dtype(at::kByte));
+  w.ptr = t.data_ptr();
+  w.bytes = (size_t)t.numel();
+  return w;
+}
+
+size_t workspace_size_of(int device, hipStream_t stream) {
+  std::lock_guard<std::mutex> lock(ws_mu);
+  const auto it = ws_cache.find(std::make_pair(device, stream));
+  return it == ws_cache.end() ? 0 : (size_t)it->second.numel();
+}
+
 int launch(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v,
            torch::Tensor& o, int dtype, int D, float scale, bool causal, const Mask& mask,
            hipStream_t stream) {
@@ -66,11 +109,13 @@ int launch(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& 
   if (mask.dtype >= 0) {
     ms[0] = mask.t.stride(0); ms[1] = mask.t.stride(1); ms[2] = mask.t.stride(2);
   }
-  return cmpext3_attn_fwd_masked(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dtype,
-                                 (int)q.size(0), (int)q.size(1), (int)k.size(1), (int)q.size(2),
-                                 (int)k.size(2), D, qs, ks, vs, os,
-                                 mask.dtype >= 0 ? mask.t.data_ptr() : nullptr, mask.dtype, ms,
-                                 scale, causal ? 1 : 0, stream);
+  const int B = (int)q.size(0), H = (int)q.size(1), Hkv = (int)k.size(1), Sq = (int)q.size(2),
+            Sk = (int)k.size(2);
+  const Workspace ws = workspace_for(
+      q, stream, cmpext3_attn_fwd_workspace_size(dtype, B, H, Hkv, Sq, Sk, D, mask.dtype, causal ? 1 : 0, 0));
+  return cmpext3_attn_fwd_ws(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dtype, B, H, Hkv, Sq,
+                             Sk, D, qs, ks, vs, os, mask.dtype >= 0 ? mask.t.data_ptr() : nullptr,
+                             mask.dtype, ms, scale, causal ? 1 : 0, ws.ptr, ws.bytes, stream);
 }
 
 // torch's attn_mask broadcast to [B,H,Sq,Sk]; copied into a compact buffer
@@ -271,11 +316,15 @@ std::vector<torch::Tensor> attention_fwd_lse(torch::Tensor query, torch::Tensor 
   const torch::Tensor q = abi_layout(query, Dp), k = abi_layout(key, Dp), v = abi_layout(value, Dp);
   int64_t qs[3], ks[3], vs[3], os[3];
   strides3(q, qs); strides3(k, ks); strides3(v, vs); strides3(out, os);
+  const Workspace ws = workspace_for(
+      query, stream,
+      cmpext3_attn_fwd_workspace_size(dtype, (int)B, (int)H, (int)Hkv, (int)Sq, (int)Sk, (int)Dp, mask.dtype,
+                                      causal ? 1 : 0, 1));
   const int rc = cmpext3_attn_fwd_lse(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                                       lse.data_ptr<float>(), dtype, (int)B, (int)H, (int)Hkv, (int)Sq,
                                       (int)Sk, (int)Dp, qs, ks, vs, os,
                                       mask.dtype >= 0 ? mask.t.data_ptr() : nullptr, mask.dtype, ms, scale,
-                                      causal ? 1 : 0, stream);
+                                      causal ? 1 : 0, ws.ptr, ws.bytes, stream);
   TORCH_CHECK(rc == CMPEXT3_OK, "cmpext3 attention: ", cmpext3_attn_strerror(rc));
   return {Dp == D ? out : out.narrow(3, 0, D).contiguous(), lse};
 }
@@ -342,6 +391,11 @@ std::vector<torch::Tensor> attention_bwd(torch::Tensor query, torch::Tensor key,
   return {dq, dk, dv};
 }
 
+int64_t workspace_bytes(int64_t device) {
+  const hipStream_t stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA((c10::DeviceIndex)device).stream();
+  return (int64_t)workspace_size_of((int)device, stream);
+}
+
 std::string describe(int64_t dtype, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
                      bool causal) {
   char buf[256];
@@ -369,4 +423,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("lse"), py::arg("scale") = py::none(), py::arg("causal") = false,
         py::arg("attn_mask") = py::none());
   m.def("abi_version", &cmpext3_attn_abi_version, "C ABI version of libcmpext3_attn.so");
+  m.def("workspace_bytes", &workspace_bytes,
+        "Bytes of key-split workspace the binding keeps for the current stream of `device` (0: none yet)",
+        py::arg("device") = 0);
 }
