@@ -54,6 +54,11 @@ extern "C" {
 #define CMPEXT3_DTYPE_F32  2
 #define CMPEXT3_DTYPE_BOOL 3
 
+/* workspace layout: counters first (cmpext3_attn_fwd_ws), and the size of
+   the allocation-free entry point's fixed per-device array */
+#define CMPEXT3_WORKSPACE_COUNTER_BYTES 65536
+#define CMPEXT3_NOALLOC_SCRATCH_BYTES (65536 + 16777216)
+
 /* return codes */
 #define CMPEXT3_OK                 0
 #define CMPEXT3_E_INVALID          1  /* null pointer, negative size, bad stride */
@@ -157,7 +162,8 @@ int cmpext3_attn_fwd_masked(const void* q, const void* k, const void* v, void* o
  *                     bytes the full split plan of a problem takes; with
  *                     less, the launch cuts its blocks into fewer key ranges,
  *                     or runs unsplit.  Nothing is ever refused for it.
- * The workspace's first 16 KiB are counters: they must be zero before the
+ * The workspace's first CMPEXT3_WORKSPACE_COUNTER_BYTES (64 KiB) are
+ * counters: they must be zero before the
  * workspace is first used, and every launch leaves them zero when it
  * completes, so one workspace can serve any sequence of calls, of any
  * shapes, that run one after another (for example every call on one
@@ -202,9 +208,10 @@ int cmpext3_attn_fwd_plan(int dtype, int B, int H, int H_kv, int Sq, int Sk, int
  * Allocation-free forward: the arguments, results and return codes of
  * cmpext3_attn_fwd_masked (mask_dtype -1 = no mask, H_kv == H = no grouping),
  * but nothing is ever allocated or freed: key-split launches exchange their
- * partial results through a fixed 16 MiB (+ 16 KiB of counters) array per
- * device inside the library's code object, in the layout of a
- * cmpext3_attn_fwd_ws workspace.  A split that would need more is cut to
+ * partial results through a fixed array of CMPEXT3_NOALLOC_SCRATCH_BYTES
+ * (64 KiB of counters + 16 MiB) per device inside the library's code
+ * object: every call behaves as cmpext3_attn_fwd_ws with a workspace of
+ * that size (same plan, same result bit for bit).  A split that would need more is cut to
  * fewer key ranges (down to none), so no problem is refused for lack of
  * room.  Every call on one device shares that device's array: calls in
  * stream order are safe; calls that overlap in time on one device (two

@@ -79,9 +79,19 @@ def test_describe_key_split_plan():
     import torch
     if torch.cuda.is_available():
         pytest.skip("plan depends on the visible device's CU count")
-    f16 = abi.DTYPE_F16
+    f16, bf16 = abi.DTYPE_F16, abi.DTYPE_BF16
     assert "key-split: 512 whole + 128 x 2 parts" in abi.describe(f16, 2, 10, 4096, 4096, 64)[1]
-    assert "key-split" not in abi.describe(f16, 2, 4, 4096, 4096, 64)[1]
+    # whole CUs but a partial round of the 3 x 256 slots (one or two blocks per
+    # CU, nothing left to split): stream-K, equal shares of the block-tile
+    # sequence; also a last round at most half full at two workgroups per CU
+    assert "stream-K: 768 workgroups x 42 tiles of 256 blocks" in abi.describe(f16, 2, 4, 4096, 4096, 64)[1]
+    assert "stream-K: 768 workgroups x 85 tiles of 512 blocks" in abi.describe(f16, 2, 8, 4096, 4096, 64)[1]
+    assert "stream-K: 1024 workgroups x 80 tiles of 640 blocks" in abi.describe(bf16, 2, 10, 4096, 4096, 128)[1]
+    for H in (12, 16):  # one whole round; 1024 blocks past one round at three per CU
+        assert "stream-K" not in abi.describe(f16, 2, H, 4096, 4096, 64)[1]
+        assert "key-split" not in abi.describe(f16, 2, H, 4096, 4096, 64)[1]
+    # shares under 8 tiles: the classic plan (16 blocks past one round in 2 parts)
+    assert "key-split: 256 whole + 16 x 2 parts" in abi.describe(f16, 1, 17, 2048, 512, 64)[1]
     assert "key-split" not in abi.describe(f16, 2, 10, 4096, 4096, 64, True)[1]
     assert "key-split" not in abi.describe(f16, 1, 2, 256, 300, 64)[1]
     assert "key-split: 0 whole + 4 x 8 parts" in abi.describe(f16, 1, 2, 256, 2048, 64)[1]
@@ -110,9 +120,10 @@ def test_describe_key_split_plan():
     assert "key-split" not in abi.describe(f32, 2, 8, 4096, 4096, 40)[1]
     assert "key-split: 4 x 5 parts" in abi.describe(f32, 1, 2, 100, 700, 40)[1]
     # head dims above 128 (one workgroup per CU): fewer blocks than CUs split
-    # into up to CUs / n parts of at least 4 tiles of 32 keys (at most 32, 8
-    # from the 192 bucket up), never causal
-    assert "key-split: 16 x 8 parts" in abi.describe(f16, 1, 16, 1, 16384, 256)[1]
+    # into up to CUs / n parts of at least 4 tiles of 32 keys (at most 32; 8
+    # from the 192 bucket up when every wave of a block holds rows, as the
+    # waves then merge their own rows alone), never causal
+    assert "key-split: 16 x 16 parts" in abi.describe(f16, 1, 16, 1, 16384, 256)[1]
     assert "key-split: 64 x 4 parts" in abi.describe(f16, 1, 8, 1024, 4096, 160)[1]
     assert "key-split: 8 x 32 parts" in abi.describe(f16, 1, 8, 1, 32768, 160)[1]
     assert "key-split: 4 x 8 parts" in abi.describe(bf16, 1, 4, 100, 3000, 192)[1]
@@ -278,7 +289,7 @@ def test_training_forward_refuses_what_its_backward_would():
 
 
 def test_workspace_size_and_plan():
-    """The workspace a problem's full key-split plan takes (16 KiB of counters,
+    """The workspace a problem's full key-split plan takes (64 KiB of counters,
     then one 1 KiB vector per lane set for every (split block, part, wave)),
     and the plan a launch takes with a given workspace: none -> unsplit, too
     little -> fewer key ranges or none, enough -> the full plan.  Host-only
@@ -287,7 +298,7 @@ def test_workspace_size_and_plan():
     if torch.cuda.is_available():
         pytest.skip("plan depends on the visible device's CU count")
     f16, bf16, f32 = abi.DTYPE_F16, abi.DTYPE_BF16, abi.DTYPE_F32
-    ctr, vec = 16384, 64 * 16
+    ctr, vec = 65536, 64 * 16
     # SDXL self-attention: 128 split blocks x 2 parts x 4 waves x (64/8 + 1) vectors
     need = abi.workspace_size(f16, 2, 10, 10, 4096, 4096, 64)
     assert need == ctr + 128 * 2 * 4 * 9 * vec
@@ -295,6 +306,12 @@ def test_workspace_size_and_plan():
     assert abi.plan(f16, 2, 10, 10, 4096, 4096, 64, need) == (abi.OK, 2)
     assert abi.plan(f16, 2, 10, 10, 4096, 4096, 64, need - 1) == (abi.OK, 1)   # less than 2 parts fit
     assert abi.plan(f16, 2, 10, 10, 4096, 4096, 64, 1 << 40) == (abi.OK, 2)
+    # one block per CU, stream-K: 256 blocks x (128 / 42 + 2 = 5) part slots;
+    # without room for it the classic plan, which leaves such a grid unsplit
+    need = abi.workspace_size(f16, 2, 4, 4, 4096, 4096, 64)
+    assert need == ctr + 256 * 5 * 4 * 9 * vec
+    assert abi.plan(f16, 2, 4, 4, 4096, 4096, 64, need) == (abi.OK, 5)
+    assert abi.plan(f16, 2, 4, 4, 4096, 4096, 64, need - 1) == (abi.OK, 1)
     # 4 blocks of 2048 keys, 8 parts; a workspace for 5 of them gets 5
     need = abi.workspace_size(f16, 1, 2, 2, 256, 2048, 64)
     assert need == ctr + 4 * 8 * 4 * 9 * vec
@@ -312,10 +329,10 @@ def test_workspace_size_and_plan():
     assert need == ctr + 128 * 4 * 4 * 5 * vec
     assert abi.plan(f32, 1, 8, 8, 1024, 1024, 64, need) == (abi.OK, 4)
     assert abi.plan(f32, 1, 8, 8, 1024, 1024, 64, 0) == (abi.OK, 1)
-    # head dim 256 decode: 16 blocks x 8 parts
-    assert abi.plan(f16, 1, 16, 16, 1, 16384, 256, 1 << 30) == (abi.OK, 8)
+    # head dim 256 decode: 16 blocks x 16 parts (merged by the whole workgroup)
+    assert abi.plan(f16, 1, 16, 16, 1, 16384, 256, 1 << 30) == (abi.OK, 16)
     # never split: causal, whole rounds, short keys
-    for args in ((f16, 2, 10, 10, 4096, 4096, 64, -1, True), (f16, 2, 4, 4, 4096, 4096, 64),
+    for args in ((f16, 2, 10, 10, 4096, 4096, 64, -1, True), (f16, 2, 12, 12, 4096, 4096, 64),
                  (f16, 2, 10, 10, 4096, 77, 64)):
         assert abi.workspace_size(*args) == 0
     # errors: the size is 0 and the plan reports the code

@@ -43,6 +43,12 @@ def _split_text(q, B, H, Sq, Sk, D, causal=False):
     return abi.describe(abi.dtype_code(q.dtype), B, H, Sq, Sk, D, causal)[1]
 
 
+def _splits(text):
+    """Does the plan cut query blocks' keys over workgroups (a key split of the
+    last blocks, or a stream-K plan of equal shares)?"""
+    return "key-split" in text or "stream-K" in text
+
+
 def _check(q, k, v, scale, causal, dtype):
     out = abi.attn_fwd(q, k, v, scale, causal)
     torch.cuda.synchronize()
@@ -69,7 +75,7 @@ def test_split_parity(case):
     dtype, B, H, Sq, Sk, D = case
     q, k, v = _inputs(dtype, B, H, Sq, Sk, D, seed=Sq + Sk + D)
     text = _split_text(q, B, H, Sq, Sk, D)
-    assert "key-split" in text, text
+    assert _splits(text), text
     _check(q, k, v, 1.0 / math.sqrt(D), False, dtype)
 
 
@@ -81,7 +87,7 @@ def test_split_wide_scores(dtype):
     B, H, Sq, Sk, D = 1, 2, 200, 1500, 64
     q, k, v = _inputs(dtype, B, H, Sq, Sk, D, seed=77)
     q = (q.float() * 6).to(q.dtype)
-    assert "key-split" in _split_text(q, B, H, Sq, Sk, D)
+    assert _splits(_split_text(q, B, H, Sq, Sk, D))
     _check(q, k, v, 0.125, False, dtype)
 
 
@@ -103,17 +109,20 @@ def test_split_bshd_views():
     wl = W.Workload("v", "fp16", 1, 3, 200, 1200, 64, seed=8)
     q, k, v = wl.make_inputs("cuda", layout="bshd")
     assert not q.is_contiguous()
-    assert "key-split" in _split_text(q, 1, 3, 200, 1200, 64)
+    assert _splits(_split_text(q, 1, 3, 200, 1200, 64))
     _check(q, k, v, 0.125, False, "fp16")
 
 
 def test_causal_and_whole_rounds_do_not_split():
     q = torch.empty(1, dtype=torch.float16)
-    assert "key-split" not in _split_text(q, 1, 2, 256, 2048, 64, causal=True)
-    # 2 x 4 x 32 blocks = exactly one block per CU on a 256-CU MI355X
+    assert not _splits(_split_text(q, 1, 2, 256, 2048, 64, causal=True))
     if torch.cuda.get_device_properties(0).multi_processor_count == 256:
-        assert "key-split" not in _split_text(q, 2, 4, 4096, 4096, 64)
-        assert "key-split" in _split_text(q, 2, 10, 4096, 4096, 64)
+        # 2 x 12 x 32 blocks = one whole round at three workgroups per CU
+        assert not _splits(_split_text(q, 2, 12, 4096, 4096, 64))
+        # 640 blocks (SDXL): the last 128 split; 256 blocks (one per CU):
+        # equal shares of the block-tile sequence for all 768 slots
+        assert "key-split: 512 whole + 128 x 2 parts" in _split_text(q, 2, 10, 4096, 4096, 64)
+        assert "stream-K: 768 workgroups x 42 tiles of 256 blocks" in _split_text(q, 2, 4, 4096, 4096, 64)
 
 
 def test_fewer_blocks_than_cus_take_two_parts_per_cu():
@@ -142,7 +151,7 @@ def test_split_parity_fp32(case):
     B, H, Sq, Sk, D = case
     q, k, v = _inputs("fp32", B, H, Sq, Sk, D, seed=Sq + Sk + D)
     if torch.cuda.get_device_properties(0).multi_processor_count == 256:
-        assert "key-split" in _split_text(q, B, H, Sq, Sk, D), _split_text(q, B, H, Sq, Sk, D)
+        assert _splits(_split_text(q, B, H, Sq, Sk, D)), _split_text(q, B, H, Sq, Sk, D)
     out = _check(q, k, v, 1.0 / math.sqrt(D), False, "fp32")
     # every part merges in part order: a rerun is bit-identical
     assert torch.equal(out, _check(q, k, v, 1.0 / math.sqrt(D), False, "fp32"))
@@ -154,7 +163,7 @@ def test_split_fp32_wide_scores_and_causal_unsplit():
     q, k, v = _inputs("fp32", 1, 2, 128, 1500, 64, seed=31)
     q = q * 6
     _check(q, k, v, 0.125, False, "fp32")
-    assert "key-split" not in _split_text(q, 1, 2, 128, 1500, 64, causal=True)
+    assert not _splits(_split_text(q, 1, 2, 128, 1500, 64, causal=True))
     _check(q, k, v, 0.125, True, "fp32")
 
 
@@ -174,7 +183,7 @@ def test_graph_capture_on_a_fresh_stream_runs_unsplit():
     memset node): a split-eligible launch on a stream it has not seen runs
     unsplit, and every replay matches the oracle and the first replay."""
     q, k, v = _inputs("fp16", 1, 2, 256, 2048, 64, seed=21)
-    assert "key-split" in _split_text(q, 1, 2, 256, 2048, 64)
+    assert _splits(_split_text(q, 1, 2, 256, 2048, 64))
     ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), 0.125)
     import cmpext3
     s = torch.cuda.Stream()
@@ -194,7 +203,7 @@ def test_graph_capture_never_carries_a_streams_exchange_buffer():
     stream, equal each other bit for bit and match the oracle, and so do the
     eager results."""
     q, k, v = _inputs("bf16", 1, 3, 256, 2048, 64, seed=22)
-    assert "key-split" in _split_text(q, 1, 3, 256, 2048, 64)
+    assert _splits(_split_text(q, 1, 3, 256, 2048, 64))
     ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), 0.125)
     import cmpext3
     s, s2 = torch.cuda.Stream(), torch.cuda.Stream()
@@ -256,7 +265,7 @@ def test_fp32_plans_at_one_to_two_blocks_per_cu(case):
 BIG_D = [
     # dtype, B, H, Hkv, Sq, Sk, D, scale (None = 1/sqrt(D)): head dims above
     # 128 run the mfma16 kernel, one workgroup per CU; fewer blocks than CUs split
-    ("fp16", 1, 16, 8, 1, 16384, 256, None),    # long-context decode: packed rows, 8 blocks x 8 parts
+    ("fp16", 1, 16, 8, 1, 16384, 256, None),    # long-context decode: packed rows, 8 blocks x 32 parts
     ("bf16", 16, 16, 8, 1, 4096, 256, None),    # batched decode: 128 blocks x 2 parts
     ("bf16", 2, 16, 4, 5, 3000, 160, None),     # 5 query rows x 4 heads packed per K/V head, ragged Sk, 23 parts
     ("fp16", 1, 4, 4, 512, 4096, 160, None),    # prefill-like, 16 blocks x 16 parts
@@ -279,7 +288,7 @@ def test_large_head_dim_split_and_packed_rows(case):
     q, k, v = _gqa_inputs(dtype, B, H, Hkv, Sq, Sk, D, seed=Sq + Sk + D)
     print(f"large-D split: {case}", flush=True)
     if Hkv == H and torch.cuda.get_device_properties(0).multi_processor_count == 256:
-        assert "key-split" in _split_text(q, B, H, Sq, Sk, D), _split_text(q, B, H, Sq, Sk, D)
+        assert _splits(_split_text(q, B, H, Sq, Sk, D)), _split_text(q, B, H, Sq, Sk, D)
     s = D ** -0.5 if scale is None else scale
     out = abi.attn_fwd(q, k, v, s)
     again = abi.attn_fwd(q, k, v, s)
@@ -313,7 +322,7 @@ def test_large_head_dim_split_under_graph_capture():
     whose replays equal its eager result bit for bit."""
     import cmpext3
     q, k, v = _gqa_inputs("fp16", 1, 4, 4, 1, 8192, 256, seed=23)
-    assert "key-split: 4 x 8 parts" in _split_text(q, 1, 4, 1, 8192, 256) or \
+    assert "key-split: 4 x 32 parts" in _split_text(q, 1, 4, 1, 8192, 256) or \
         torch.cuda.get_device_properties(0).multi_processor_count != 256
     s_ = 256 ** -0.5
     ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), s_)
@@ -393,11 +402,12 @@ def test_short_workspace_cuts_the_plan():
     that many (here 5 of 8), within tolerance and bit-identical on rerun."""
     q, k, v = _inputs("fp16", 1, 2, 256, 2048, 64, seed=32)
     need = abi.workspace_size(abi.DTYPE_F16, 1, 2, 2, 256, 2048, 64)
-    part = (need - 16384) // 8
-    rc, parts = abi.plan(abi.DTYPE_F16, 1, 2, 2, 256, 2048, 64, 16384 + 5 * part)
+    ctr = 65536
+    part = (need - ctr) // 8
+    rc, parts = abi.plan(abi.DTYPE_F16, 1, 2, 2, 256, 2048, 64, ctr + 5 * part)
     assert (rc, parts) == (abi.OK, 5) or torch.cuda.get_device_properties(0).multi_processor_count != 256
     import ctypes
-    ws = torch.zeros(16384 + 5 * part, dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(ctr + 5 * part, dtype=torch.uint8, device="cuda")
     outs = []
     for _ in range(2):
         o = torch.empty_like(q)
@@ -410,6 +420,46 @@ def test_short_workspace_cuts_the_plan():
         outs.append(o)
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1])
-    assert int(ws[:16384].count_nonzero()) == 0   # counters back at zero
+    assert int(ws[:ctr].count_nonzero()) == 0   # counters back at zero
     ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), 0.125)
     assert orc.max_abs_err(outs[0].cpu(), ref) <= TOL["fp16"]
+
+
+STREAMK = [
+    # dtype, B, H, Sq, Sk, D: one block per CU (256), two per CU (512),
+    # bf16 D = 128 with a last round a quarter full (640 on 512 slots), and a
+    # ragged key count whose shares end inside tiles of different blocks
+    ("fp16", 2, 4, 4096, 4096, 64),
+    ("fp16", 2, 8, 2048, 3000, 64),
+    ("bf16", 2, 10, 4096, 4096, 128),
+    ("bf16", 2, 4, 4000, 2500, 64),
+]
+
+
+@pytest.mark.parametrize("case", STREAMK, ids=[f"{c[0]}-B{c[1]}H{c[2]}-q{c[3]}k{c[4]}d{c[5]}" for c in STREAMK])
+def test_streamk_parity(case):
+    """Stream-K launches (equal shares of the block-tile sequence; a block cut
+    between two or three workgroups merges in part order): the oracle on the
+    first and last heads, every head within tolerance of the unsplit launch,
+    a rerun bit-identical, and the workspace's counters back at zero."""
+    dtype, B, H, Sq, Sk, D = case
+    q, k, v = _inputs(dtype, B, H, Sq, Sk, D, seed=Sq + Sk + H)
+    text = _split_text(q, B, H, Sq, Sk, D)
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert "stream-K" in text, text
+    s = D ** -0.5
+    need = abi.workspace_size(abi.dtype_code(q.dtype), B, H, H, Sq, Sk, D)
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    outs = []
+    for w in (ws, ws, False):
+        o = torch.empty_like(q)
+        assert abi.attn_fwd_raw(q, k, v, o, s, workspace=w) == abi.OK
+        outs.append(o)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    assert int(ws[:abi.WORKSPACE_COUNTER_BYTES].count_nonzero()) == 0
+    assert (outs[0].float() - outs[2].float()).abs().max().item() <= TOL[dtype]
+    for h in (0, H - 1):
+        ref = orc.sdpa_np(q[:, h:h + 1].cpu(), k[:, h:h + 1].cpu(), v[:, h:h + 1].cpu(), s)
+        err = orc.max_abs_err(outs[0][:, h:h + 1].cpu(), ref)
+        assert err <= TOL[dtype], f"head {h}: max abs err {err:.3e}"

@@ -2,13 +2,13 @@
 
 The entry point runs the same kernels as cmpext3_attn_fwd_ws; only the key
 split's exchange differs (a fixed per-device array in the library instead of
-the caller's workspace).  Every call in the first test takes a key-split plan
-that fits that array, so the allocation-free result must equal the workspace
-entry point's bit for bit (same kernels, same plan, same merge order), and
-both must lie within the north-star tolerance of the float64 oracle.  Calls
-run back to back, each one smaller than the one before, and the first is
-repeated at the end: the shared counters must be back at zero after every
-merge, or the repeat would differ.
+the caller's workspace).  It must behave exactly like cmpext3_attn_fwd_ws
+given a workspace of the array's size (CMPEXT3_NOALLOC_SCRATCH_BYTES): same
+plan, so the results are equal bit for bit, and both must lie within the
+north-star tolerance of the float64 oracle.  Calls run back to back, each
+one smaller than the one before, and the first is repeated at the end: the
+shared counters must be back at zero after every merge, or the repeat would
+differ.
 """
 from __future__ import annotations
 
@@ -25,7 +25,8 @@ TOL = orc.TOLERANCE
 
 # name, dtype, B, H, H_kv, Sq, Sk, D, mask; in call order, largest first
 CALLS = [
-    # the headline: 640 blocks, the last 128 cut in 2 key ranges (9.4 MB of exchange)
+    # the headline: its stream-K plan needs more than the array holds, so the
+    # last 128 of its 640 blocks are cut in 2 key ranges (9.4 MB of exchange)
     ("headline_fp16", "fp16", 2, 10, 10, 4096, 4096, 64, False),
     # grouped-query decode step: packed rows, one exchanging wave per block, 4 parts
     ("decode_bf16_gqa", "bf16", 16, 16, 8, 1, 4096, 128, False),
@@ -67,6 +68,7 @@ def _oracle_check(name, dtype, q, k, v, out, scale, mask, heads=2):
 
 def test_noalloc_matches_the_workspace_entry_point_on_calls_in_a_row():
     results = {}
+    ws = torch.zeros(abi.NOALLOC_SCRATCH_BYTES, dtype=torch.uint8, device="cuda")
     for seed, (name, dtype, B, H, Hkv, Sq, Sk, D, masked) in enumerate(CALLS):
         print(f"noalloc call {name}: {dtype} B={B} H={H}/{Hkv} Sq={Sq} Sk={Sk} D={D} mask={masked}",
               flush=True)
@@ -74,7 +76,7 @@ def test_noalloc_matches_the_workspace_entry_point_on_calls_in_a_row():
         mask = _mask(B, Sk, seed) if masked else None
         scale = D ** -0.5
         got = _call(abi.attn_fwd_noalloc_raw, q, k, v, scale, mask)
-        want = _call(lambda *a, **kw: abi.attn_fwd_raw(*a[:6], attn_mask=kw["attn_mask"]),
+        want = _call(lambda *a, **kw: abi.attn_fwd_raw(*a[:6], attn_mask=kw["attn_mask"], workspace=ws),
                      q, k, v, scale, mask)
         torch.cuda.synchronize()
         assert torch.equal(got, want), f"{name}: differs from cmpext3_attn_fwd_ws"

@@ -19,6 +19,8 @@ SYMBOLS = ("cmpext3_attn_fwd", "cmpext3_attn_fwd_gqa", "cmpext3_attn_fwd_masked"
            "cmpext3_attn_strerror", "cmpext3_attn_abi_version", "cmpext3_attn_describe")
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_BOOL = 0, 1, 2, 3
+WORKSPACE_COUNTER_BYTES = 65536                     # CMPEXT3_WORKSPACE_COUNTER_BYTES
+NOALLOC_SCRATCH_BYTES = 65536 + 16 * 1024 * 1024    # CMPEXT3_NOALLOC_SCRATCH_BYTES
 (OK, E_INVALID, E_DTYPE, E_HEAD_DIM, E_ALIGN, E_EMPTY_KEYS, E_LAUNCH, E_TOO_LARGE, E_MASK,
  E_TRAINING) = range(10)
 
@@ -77,8 +79,8 @@ def strerror(code: int) -> str:
 
 
 def describe(dtype: int, B: int, H: int, Sq: int, Sk: int, D: int, causal: bool = False):
-    buf = ctypes.create_string_buffer(256)
-    rc = lib().cmpext3_attn_describe(dtype, B, H, Sq, Sk, D, int(causal), buf, 256)
+    buf = ctypes.create_string_buffer(384)
+    rc = lib().cmpext3_attn_describe(dtype, B, H, Sq, Sk, D, int(causal), buf, 384)
     return rc, buf.value.decode()
 
 
@@ -149,10 +151,11 @@ def _strides(t):
 
 
 def attn_fwd_raw(q, k, v, o, scale: float, causal: bool = False, stream=None,
-                 D: Optional[int] = None, attn_mask=None, workspace: bool = True) -> int:
+                 D: Optional[int] = None, attn_mask=None, workspace=True) -> int:
     """Call cmpext3_attn_fwd_ws on [B,H,S,D] tensors (any strides with unit last
     stride; k/v may hold fewer heads than q: grouped-query) with this module's
-    workspace for the stream (workspace=False: no workspace, so no key split;
+    workspace for the stream (workspace=True), a given uint8 device tensor
+    (zeroed before its first use), or none (workspace=False: no key split;
     with no mask the plain cmpext3_attn_fwd / _gqa entry points are called).
     Returns the C return code; launches on `stream` (a torch.cuda.Stream, a raw
     handle, or None for the current stream)."""
@@ -169,16 +172,18 @@ def attn_fwd_raw(q, k, v, o, scale: float, causal: bool = False, stream=None,
             ctypes.c_void_p(v.data_ptr()), ctypes.c_void_p(o.data_ptr()))
     strides = (_strides(q), _strides(k), _strides(v), _strides(o))
     dt = dtype_code(q.dtype)
-    if not workspace and attn_mask is None:
+    if workspace is False and attn_mask is None:
         tail = (*strides, ctypes.c_float(scale), int(causal), ctypes.c_void_p(handle))
         if k.shape[1] != H:
             return lib().cmpext3_attn_fwd_gqa(*ptrs, dt, B, H, k.shape[1], Sq, k.shape[2], Dx, *tail)
         return lib().cmpext3_attn_fwd(*ptrs, dt, B, H, Sq, k.shape[2], Dx, *tail)
     mp, mdt, mst, _keep = _mask_args(attn_mask, B, H, Sq, k.shape[2])
     wp, wb = None, 0
-    if workspace and q.is_cuda:
+    if workspace is True and q.is_cuda:
         wp, wb = workspace_for(q, handle, workspace_size(dt, B, H, k.shape[1], Sq, k.shape[2], Dx,
                                                          mdt, causal))
+    elif workspace is not False and workspace is not None:
+        wp, wb = workspace.data_ptr(), workspace.numel()
     return lib().cmpext3_attn_fwd_ws(*ptrs, dt, B, H, k.shape[1], Sq, k.shape[2], Dx, *strides,
                                      mp, mdt, mst, ctypes.c_float(scale), int(causal),
                                      ctypes.c_void_p(wp), wb, ctypes.c_void_p(handle))

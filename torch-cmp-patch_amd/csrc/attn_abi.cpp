@@ -152,7 +152,7 @@ int cmpext3_attn_describe(int dtype, int B, int H, int Sq, int Sk, int D, int ca
     } else if ((int64_t)B * H * Sq == 0) {
       snprintf(buf, len, "empty problem: no launch");
     } else {
-      char kb[224];
+      char kb[320];
       if (dtype == CMPEXT3_DTYPE_F32)
         cmpext3::describe_mfma32(D, B, H, Sq, Sk, causal != 0, kb, sizeof kb);
       else

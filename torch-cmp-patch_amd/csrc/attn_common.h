@@ -247,6 +247,10 @@ struct SplitArgs {
   // waves per block that hold query rows (and so exchange): NW, or fewer
   // when a single query block is shorter than the workgroup (decode)
   int nwl;
+  // stream-K launches of the pipelined kernel: the workgroup count (every
+  // block is a possible split block, nparts the part slots per block);
+  // 0 otherwise
+  int sk_wgs;
 };
 
 // float4 vectors each lane of the fp16/bf16 kernels leaves per part: its O
@@ -258,7 +262,7 @@ constexpr int split_vectors(int dp) { return dp / 8 + 1; }
 // partial results.  The counters must be zero before a space's first use;
 // every split launch puts the ones it used back to zero, so a space reused
 // in stream order, for any problem shape, stays ready.
-constexpr int kExchangeCounters = 4096;
+constexpr int kExchangeCounters = 16384;  // CMPEXT3_WORKSPACE_COUNTER_BYTES / 4
 constexpr size_t kExchangeCounterBytes = kExchangeCounters * sizeof(int);
 
 // What a launch would do (FwdParams::dry): the workspace bytes that let its

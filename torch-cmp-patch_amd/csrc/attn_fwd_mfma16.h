@@ -498,9 +498,6 @@ attn_fwd_mfma16(const FwdParams p, const SplitArgs sa) {
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) lrow[qb] = xhalf_sum(lsum[qb]);
   if (!CAUSAL && nparts > 1) {
-    // a wave whose rows all lie past Sq (decode, packed query groups) has
-    // nothing to exchange; every part of the block agrees on that
-    if (qw0 >= Sq) return;
     // Every part leaves its state and counts itself in; the last one in
     // merges and writes the output.  Device-scope (aux 16 = sc1) 16-byte
     // accesses, coherent across the XCDs' L2s.
@@ -508,12 +505,100 @@ attn_fwd_mfma16(const FwdParams p, const SplitArgs sa) {
     constexpr int NV = QB * NVB;
     const int sb = lb - sa.nfull, nwl = sa.nwl;
     const __amdgpu_buffer_rsrc_t wsr = uniform_rsrc(sa.ws, (int64_t)(sb + 1) * nparts * nwl * NV * 64 * 16);
-    auto voff = [&](int q, int k) { return ((((sb * nparts + q) * nwl + wave) * NV + k) * 64 + lane) * 16; };
+    // vector k of part q's state for the rows of wave w
+    auto voffw = [&](int q, int w, int k) { return ((((sb * nparts + q) * nwl + w) * NV + k) * 64 + lane) * 16; };
+    auto voff = [&](int q, int k) { return voffw(q, wave, k); };
     auto st_ws = [&](f32x4 x, int off) {
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), wsr, off, 0, 16);
     };
     auto ld_ws = [&](int off) { return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wsr, off, 0, 16)); };
     auto frag = [](const f32x16& a, int i) { return (f32x4){a[4 * i], a[4 * i + 1], a[4 * i + 2], a[4 * i + 3]}; };
+    if (nwl < NW) {
+      // Rows in fewer waves than the workgroup has (decode steps, packed
+      // query groups): the last part's whole workgroup merges.  The waves
+      // with rows leave their state, the block is counted in once, and each
+      // of the NW waves then merges a share of the (row wave, query block,
+      // 32-column block) units of every part, all read from the exchange, so
+      // the result is the same whichever part is last.  Nobody waits for
+      // another workgroup.  (One wave merging a 256-wide output alone held
+      // its accumulators and one part's loads at a time.)
+      if (wave < nwl) {
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+#pragma unroll
+          for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) st_ws(frag(oacc[qb][db], i), voff(part, qb * NVB + 4 * db + i));
+          st_ws((f32x4){lrow[qb] > 0.f ? mb[qb] : -INFINITY, lrow[qb], 0.f, 0.f}, voff(part, qb * NVB + 4 * NDB));
+        }
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      lds_barrier();  // every wave's state is written and its LDS reads are done
+      int* const flag = (int*)lds;
+      if (tid == 0) {
+        int* const ctr = sa.cnt + 2 * sb * nwl;
+        const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == nparts - 1) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = old == nparts - 1;
+      }
+      lds_barrier();
+      if (__builtin_amdgcn_readfirstlane(*flag) == 0) return;
+      asm volatile("" ::: "memory");  // the exchange loads stay after the count
+      constexpr int CHM = 4;  // parts whose loads are in flight together
+      for (int u = wave; u < nwl * QB * NDB; u += NW) {
+        const int w2 = u / (QB * NDB), r = u - w2 * (QB * NDB), qb = r / NDB, db = r - qb * NDB;
+        float mt = -INFINITY;
+        for (int qa = 0; qa < nparts; qa += CHM) {
+          float mq[CHM];
+#pragma unroll
+          for (int j = 0; j < CHM; ++j) mq[j] = ld_ws(voffw(min(qa + j, nparts - 1), w2, qb * NVB + 4 * NDB))[0];
+#pragma unroll
+          for (int j = 0; j < CHM; ++j) mt = fmaxf(mt, mq[j]);  // clamped repeats change nothing
+        }
+        f32x16 acc = (f32x16){};
+        float l = 0.f;
+        for (int qa = 0; qa < nparts; qa += CHM) {
+          f32x4 ml[CHM], x[CHM][4];
+#pragma unroll
+          for (int j = 0; j < CHM; ++j) {
+            const int qq = min(qa + j, nparts - 1);
+            ml[j] = ld_ws(voffw(qq, w2, qb * NVB + 4 * NDB));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[j][i] = ld_ws(voffw(qq, w2, qb * NVB + 4 * db + i));
+          }
+#pragma unroll
+          for (int j = 0; j < CHM; ++j) {
+            if (qa + j >= nparts) break;
+            const float a = ml[j][0] == -INFINITY ? 0.f : fast_exp2(ml[j][0] - mt);
+            l = __builtin_fmaf(ml[j][1], a, l);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[i] = __builtin_fmaf(x[j][i / 4][i % 4], a, acc[i]);
+          }
+        }
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+        const int qrow = q0 + w2 * QPW + 32 * qb + l32;
+        if (qrow < Sq) {
+          uint16_t* orow = og + row_off(qrow, p.o_g, p.o_s);
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int d = 32 * db + 8 * g + 4 * hh;
+            if (d < D) {
+              u32x2 w;
+              w[0] = Elt<T>::pack(acc[4 * g + 0] * inv, acc[4 * g + 1] * inv);
+              w[1] = Elt<T>::pack(acc[4 * g + 2] * inv, acc[4 * g + 3] * inv);
+              if (ELEM)
+                st_cols16x4(orow + d, w, D - d, p.elem_rows);
+              else
+                *(u32x2*)(orow + d) = w;
+            }
+          }
+        }
+      }
+      return;
+    }
+    // a wave whose rows all lie past Sq has nothing to exchange; every part
+    // of the block agrees on that
+    if (qw0 >= Sq) return;
     int* const ctr = sa.cnt + 2 * (sb * nwl + wave);  // parts in (the second counter is unused here)
     // a row that holds nothing from this part's keys: offset -inf
     float m_own[QB];
@@ -615,18 +700,21 @@ attn_fwd_mfma16(const FwdParams p, const SplitArgs sa) {
 // Key split plan: only when the query blocks leave CUs idle (fewer blocks
 // than CUs), non-causal, into enough parts for up to two workgroups per CU
 // (as many as fit: one at head dims above 128), each part at least
-// kMinTiles16 key tiles long, and at most 32 parts (8 from a 192-wide output
-// up: the last part reads every other part's O back, one part per memory
-// round trip at those widths).  Measured on MI355X, bf16 grouped-query decode
-// over 8 K/V heads (8 packed blocks): D = 256, 16384 keys, 2 / 8 / 32 / 64
-// parts 428 / 178 / 306 / 592 us; D = 160, 32768 keys, 8 / 32 / 64 parts
-// 140 / 66 / 90 us.  Returns the part count (1: no split).
+// kMinTiles16 key tiles long, and at most 32 parts.  When every wave of a
+// block holds rows, the last part's waves each merge their own rows: then
+// at most 8 parts from a 192-wide output up (a wave reads every other part's
+// O back, one part per memory round trip at those widths; measured on
+// MI355X, bf16 grouped-query decode over 8 K/V heads (8 packed blocks):
+// D = 256, 16384 keys, 2 / 8 / 32 / 64 parts 428 / 178 / 306 / 592 us with
+// that merge).  Blocks with rows in fewer waves (`spread`: decode, packed
+// query groups) merge across the whole workgroup and keep the cap of 32.
+// Returns the part count (1: no split).
 constexpr int kMinTiles16 = 4;
-inline int split_parts16(int n, int ntiles, int wg_per_cu, int cus, bool causal, int dp) {
+inline int split_parts16(int n, int ntiles, int wg_per_cu, int cus, bool causal, int dp, bool spread) {
   if (causal || n <= 0 || n >= cus) return 1;
   int parts = (wg_per_cu < 2 ? wg_per_cu : 2) * cus / n;
   if (parts > ntiles / kMinTiles16) parts = ntiles / kMinTiles16;
-  const int cap = dp >= 192 ? 8 : 32;
+  const int cap = dp >= 192 && !spread ? 8 : 32;
   if (parts > cap) parts = cap;
   return parts >= 2 ? parts : 1;
 }
@@ -646,7 +734,7 @@ hipError_t launch_mfma16_cfg(const FwdParams& p0, hipStream_t stream) {
   // waves per block that hold query rows (a single block shorter than BQ has fewer)
   const int nwl = p.n_qblk > 1 ? NW : (p.Sq + QB * 32 - 1) / (QB * 32) < NW ? (p.Sq + QB * 32 - 1) / (QB * 32) : NW;
   SplitArgs sa = {n, 1, nullptr, nullptr, nwl};
-  const int parts = split_parts16(n, (p.Sk + BK - 1) / BK, OCC, device_cus(), CAUSAL, DP);
+  const int parts = split_parts16(n, (p.Sk + BK - 1) / BK, OCC, device_cus(), CAUSAL, DP, nwl < NW);
   if (parts >= 2) {
     // every block is split; one key range of all of them takes part_bytes
     const size_t part_bytes = (size_t)n * nwl * QB * split_vectors(DP) * 64 * sizeof(f32x4);

@@ -62,7 +62,7 @@ bool short16_applies(const FwdParams& p, int dk, bool causal);
 hipError_t launch_short16(const FwdParams& p, int dk, bool bf16, hipStream_t s);
 void describe_short16(int dk, int Sq, int Sk, char* buf, int len);
 hipError_t launch_pipe16(const FwdParams& p, int dk, bool bf16, bool causal, bool prescale, hipStream_t s);
-void describe_pipe16(int dk, int B, int H, int Sq, int Sk, bool causal, char* buf, int len);
+void describe_pipe16(int dk, int B, int H, int Sq, int Sk, bool causal, bool narrow, char* buf, int len);
 bool packs_query_heads(const FwdParams& p, bool causal);
 void pack_query_heads(FwdParams& p);
 
@@ -130,14 +130,16 @@ void describe_mfma16(int D, int B, int H, int Sq, int Sk, bool causal, char* buf
     return;
   }
   if ((!elem || D % 2 == 0) && pipe16_applies(p, dk)) {
-    describe_pipe16(elem ? (dk <= 64 ? 64 : 128) : dk, B, H, Sq, Sk, causal, buf, len);
+    describe_pipe16(elem ? (dk <= 64 ? 64 : 128) : dk, B, H, Sq, Sk, causal, elem, buf, len);
     if (elem) snprintf(buf + strlen(buf), len - strlen(buf), " narrow rows");
     return;
   }
   const Tile16 t = tile16(dk);
   const int bq = t.nw * t.qb * 32;
   const int n = B * H * ((Sq + bq - 1) / bq);
-  const int parts = split_parts16(n, (Sk + t.bk - 1) / t.bk, t.occ, device_cus(), causal, (dk + 31) / 32 * 32);
+  const int nwl = Sq > bq ? t.nw : (Sq + 31) / 32 < t.nw ? (Sq + 31) / 32 : t.nw;
+  const int parts = split_parts16(n, (Sk + t.bk - 1) / t.bk, t.occ, device_cus(), causal, (dk + 31) / 32 * 32,
+                                  nwl < t.nw);
   char split[48] = "";
   if (parts >= 2) snprintf(split, sizeof split, " key-split: %d x %d parts", n, parts);
   snprintf(buf, len,

@@ -74,9 +74,16 @@ namespace cmpext3 {
 // wave issues the same number of these loads per tile and waits for its own
 // with an explicit vmcnt before the barrier that publishes them (the
 // compiler does not track LDS written this way).
+// One workgroup's work on one query block: key tiles [g.tbase, g.tbase +
+// g.ntiles) of block (g.bh, g.qblk).  With g.nparts > 1 that is key range
+// g.part of the block's g.nparts, exchanged through row g.sb of the exchange
+// space (g.pstride part slots per row).
+struct Pipe16Seg {
+  int bh, qblk, part, nparts, pstride, sb, tbase, ntiles;
+};
+
 template <typename T, int DK, int DP, int NW, int BK, int OCC, bool CAUSAL, bool PRESCALE, int OPT = 0>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
-attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
+__device__ __forceinline__ void pipe16_segment(const FwdParams& p, const SplitArgs& sa, const Pipe16Seg& g) {
   constexpr int NT = NW * 64;
   constexpr int BQ = NW * 32;
   constexpr bool SWZ = (OPT & 2) && (DK == DP) && (DK == 32 || DK == 64 || DK == 128);
@@ -103,6 +110,7 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   static_assert(BK % 32 == 0 && DK % 16 == 0 && DP % 32 == 0 && DK <= DP, "tile shape");
   constexpr bool DMA = (OPT & 256) != 0;
   static_assert(!(DMA && (NARROW || MASK || (OPT & 128))), "LDS DMA: plain unmasked launches only");
+  constexpr bool STREAMK = (OPT & 512) != 0;  // segments of an equal-work split (kernel below)
   constexpr int NR = DMA ? 4 : 2;  // K (and V) tiles held in LDS
   // With DMA: one barrier per two tiles.  The barrier before an even
   // iteration t publishes K(t+1), K(t+2), V(t), V(t+1) at once; right after
@@ -121,15 +129,7 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   const int l32 = lane & 31;
   const int hh = lane >> 5;
 
-  int lb = block_x(), part = 0, nparts = 1;
-  if (lb >= sa.nfull) {
-    const int r = lb - sa.nfull;
-    nparts = sa.nparts;
-    lb = sa.nfull + r / nparts;
-    part = r - (lb - sa.nfull) * nparts;
-  }
-  int bh, qblk;
-  wg_tile(lb, p, CAUSAL, bh, qblk);
+  const int bh = g.bh, qblk = g.qblk, part = g.part, nparts = g.nparts;
   const int b = bh / p.H;
   const int h = bh - b * p.H;
   const int q0 = qblk * BQ;
@@ -155,9 +155,7 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
 
   int kend = Sk;
   if (CAUSAL) kend = min(Sk, q0 + BQ);
-  const int ntall = (kend + BK - 1) / BK;
-  const int tbase = part * ntall / nparts;
-  const int ntiles = (part + 1) * ntall / nparts - tbase;
+  const int tbase = g.tbase, ntiles = g.ntiles;
   if (ntiles <= 0) return;  // Sk == 0 is rejected by the host
   // end of this workgroup's key range: the padding tile past it is masked
   const int kpe = min(kend, (tbase + ntiles) * BK);
@@ -799,10 +797,10 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
     // the XCDs' L2s without cache-wide write-back or invalidation.
     constexpr int NV = split_vectors(DP);
     static_assert(NV == NDB * 4 + 1, "O fragments + (m, l)");
-    const int sb = lb - sa.nfull;
+    const int sb = g.sb, ps = g.pstride;
     const int nwl = sa.nwl;  // waves past it hold no rows and left above
-    const __amdgpu_buffer_rsrc_t wsr = uniform_rsrc(sa.ws, (int64_t)(sb + 1) * nparts * nwl * NV * 64 * 16);
-    auto voff = [&](int q, int k) { return ((((sb * nparts + q) * nwl + wave) * NV + k) * 64 + lane) * 16; };
+    const __amdgpu_buffer_rsrc_t wsr = uniform_rsrc(sa.ws, (int64_t)(sb + 1) * ps * nwl * NV * 64 * 16);
+    auto voff = [&](int q, int k) { return ((((sb * ps + q) * nwl + wave) * NV + k) * 64 + lane) * 16; };
     // Every lane moves its vectors, also lanes of rows past Sq (a decode
     // step's wave holds one or two live rows): whole 1 KB runs per
     // instruction measured faster than the sparse 16-byte pieces of the live
@@ -822,9 +820,9 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
     // per lane.  Both parts round their own O this way, so the result does
     // not depend on which one writes (reruns stay bit-identical); rounding O/l
     // to fp16 before the merge adds at most one fp16 rounding to the output.
-    const bool half_x = std::is_same<T, _Float16>::value && nparts == 2;
+    const bool half_x = std::is_same<T, _Float16>::value && (nparts == 2 || STREAMK);
     auto ml_off = [&](int q) {
-      return ((((sb * nparts + q) * nwl + wave) * NV + 2 * NDB) * 64) * 16 + lane * 8;
+      return ((((sb * ps + q) * nwl + wave) * NV + 2 * NDB) * 64) * 16 + lane * 8;
     };
     u32x4 own_h[2 * NDB];  // half_x: this part's O / l in fp16
     if (half_x) {
@@ -907,7 +905,8 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
     constexpr int CH2 = NDB <= 2 ? 2 : 1;   // parts per batch of O loads (registers)
     float mt = m_own;
     if (half_x) {
-      mt = fmaxf(mt, ml_of(1 - part)[0]);
+      for (int q = 0; q < nparts; ++q)
+        if (q != part) mt = fmaxf(mt, ml_of(q)[0]);
     } else {
       for (int q0 = 0; q0 < nparts; q0 += CH) {
         float mq[CH];
@@ -1004,6 +1003,69 @@ attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
   }
 }
 
+// The kernel.  Without OPT bit 512 a workgroup owns one block, or one key
+// range of a block past the whole rounds (SplitArgs::nfull / nparts).  With
+// OPT bit 512 (stream-K, non-causal): the launch is a whole number of rounds
+// of workgroups, and workgroup w takes the w-th of SplitArgs::sk_wgs equal
+// shares of the sequence of (block, key tile) pairs, blocks in order, so
+// every workgroup does the same number of tiles and the chip's slots all end
+// together.  A share runs as segments, one per block it touches (at most two
+// when a share is shorter than a block); a block cut between workgroups
+// merges its parts as any key split does, in part order (part i of a block
+// is the i-th workgroup that touches it), through row `block` of the
+// exchange with SplitArgs::nparts part slots per row.
+template <typename T, int DK, int DP, int NW, int BK, int OCC, bool CAUSAL, bool PRESCALE, int OPT = 0>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
+attn_fwd_pipe16(const FwdParams p, const SplitArgs sa) {
+  if constexpr ((OPT & 512) != 0) {
+    static_assert(!CAUSAL, "stream-K: non-causal launches only");
+    const int W = sa.sk_wgs;
+    const int ntall = (p.Sk + BK - 1) / BK;
+    const int64_t tot = (int64_t)p.n_wg * ntall;  // block-tile pairs
+    // adjacent shares on one XCD (workgroup i runs on XCD i % 8), so the
+    // blocks of a head stream their K/V through one L2
+    const int w = xcd_remap(block_x(), W);
+    const int64_t end = (int64_t)(w + 1) * tot / W;
+    // the first workgroup whose share holds tile position x
+    auto owner = [&](int64_t x) { return (int)(((x + 1) * W - 1) / tot); };
+    // the segment of this share that starts at tile position pos
+    auto segment = [&](int64_t pos) {
+      const int blk = (int)(pos / ntall);
+      const int64_t x0 = (int64_t)blk * ntall;
+      const int t1 = (int)(end - x0 < ntall ? end - x0 : ntall);
+      const int wf = owner(x0);
+      const Pipe16Seg g = {blk / p.n_qblk, blk % p.n_qblk, w - wf, owner(x0 + ntall - 1) - wf + 1,
+                           sa.nparts, blk, (int)(pos - x0), t1 - (int)(pos - x0)};
+      pipe16_segment<T, DK, DP, NW, BK, OCC, CAUSAL, PRESCALE, OPT>(p, sa, g);
+      return x0 + t1;
+    };
+    // a share is at most one block long (the host plans it so), so it
+    // touches at most two blocks
+    const int64_t next = segment((int64_t)w * tot / W);
+    if (next < end) {
+      lds_barrier();  // every wave is done with the first segment's LDS
+      segment(next);
+    }
+  } else {
+    int lb = block_x(), part = 0, nparts = 1;
+    if (lb >= sa.nfull) {
+      const int r = lb - sa.nfull;
+      nparts = sa.nparts;
+      lb = sa.nfull + r / nparts;
+      part = r - (lb - sa.nfull) * nparts;
+    }
+    int bh, qblk;
+    wg_tile(lb, p, CAUSAL, bh, qblk);
+    int kend = p.Sk;
+    if (CAUSAL) kend = min(p.Sk, (qblk + 1) * NW * 32);
+    const int ntall = (kend + BK - 1) / BK;
+    const int tbase = part * ntall / nparts;
+    const Pipe16Seg g = {bh, qblk, part, nparts, nparts, lb - sa.nfull, tbase,
+                         (part + 1) * ntall / nparts - tbase};
+    pipe16_segment<T, DK, DP, NW, BK, OCC, CAUSAL, PRESCALE, OPT>(p, sa, g);
+  }
+}
+
 template <typename T, int DK, int NW, int BK, int OCC, bool CAUSAL, bool PRESCALE, int OPT = 0>
 hipError_t launch_pipe16_cfg(const FwdParams& p0, const SplitArgs& sa, hipStream_t stream) {
   constexpr int DP = (DK + 31) / 32 * 32;
@@ -1016,7 +1078,7 @@ hipError_t launch_pipe16_cfg(const FwdParams& p0, const SplitArgs& sa, hipStream
   const int64_t rs = p.k_s > p.v_s ? p.k_s : p.v_s;
   if ((int64_t)(p.Sk + BK) * rs * 2 >= (int64_t(1) << 31)) return hipErrorInvalidValue;
   if (p.dry) return hipSuccess;
-  const int nwg = sa.nfull + (p.n_wg - sa.nfull) * sa.nparts;
+  const int nwg = (OPT & 512) ? sa.sk_wgs : sa.nfull + (p.n_wg - sa.nfull) * sa.nparts;
   hipLaunchKernelGGL((attn_fwd_pipe16<T, DK, DP, NW, BK, OCC, CAUSAL, PRESCALE, OPT>), dim3(nwg),
                      dim3(NW * 64), 0, stream, p, sa);
   return hipGetLastError();

@@ -37,6 +37,9 @@ constexpr int kMinPartTiles = 8;
 constexpr int kMaxPartsPerCu = 2;
 constexpr int kMi355xCus = 256;  // used when no device is visible (host-only calls)
 
+int n_blocks(int B, int H, int Sq) { return B * H * ((Sq + kPipeNw * 32 - 1) / (kPipeNw * 32)); }
+int n_key_tiles(int Sk) { return (Sk + kPipeBk - 1) / kPipeBk; }
+
 // ---- Exchange storage of the allocation-free entry point
 //
 // One fixed array per device in the library's code object, zero-filled when
@@ -102,6 +105,45 @@ SplitArgs split_plan(int n, int ntiles, int occ, int cus, bool causal) {
   return sa;
 }
 
+// Stream-K (OPT 512): for non-causal, unmasked inference launches of the
+// LDS-DMA buckets whose blocks fill at least the CUs but not whole rounds of
+// the occ * cus workgroup slots.  The launch is then ceil(n / slots) rounds
+// of workgroups, each taking an equal share of the n * ntiles block-tile
+// sequence (with the classic plan the CUs of the last round would idle once
+// their half-blocks end: SDXL self-attention, 640 blocks on 768 slots).
+// Shares of fewer than kMinPartTiles tiles would spend more on prologues and
+// merges than they balance; the counters take 2 per (block, wave).
+constexpr int kMaxStreamkWaves = kExchangeCounters / 2;
+
+bool streamk_applies(const FwdParams& p, int n, int dk, int occ, int cus, bool causal) {
+  if (causal || p.lse || p.elem_rows || p.mask_kind != MASK_NONE || p.pack_sq > 0) return false;
+  if (!(dk == 32 || dk == 64 || dk == 128) || p.Sq <= (kPipeNw - 2) * 32) return false;
+  const int slots = occ * cus;
+  if (cus <= 0 || n < cus || n % slots == 0 || n * kPipeNw > kMaxStreamkWaves) return false;
+  // Only where the classic plan leaves slots idle for the whole launch: one
+  // partial round of whole CUs (n a multiple of the CU count: no block left
+  // to split), or, at two workgroups per CU, a last round at most half full.
+  // Where the classic plan splits the blocks past the whole CUs, it measured
+  // faster (SDXL self-attention 91.1 us against 97.7 us stream-K, same run:
+  // every stream-K share pays a second prologue and every block a merge);
+  // [2,4,4096,4096,64], one block per CU, 54.6 us unsplit against 44.8 us.
+  const bool idle_round = n < slots && n % cus == 0;
+  const bool thin_tail = n > slots && occ == 2 && n % slots <= slots / 2;
+  if (!idle_round && !thin_tail) return false;
+  const int64_t rounds = (n + slots - 1) / slots;
+  return (int64_t)n * n_key_tiles(p.Sk) / (rounds * slots) >= kMinPartTiles;
+}
+
+// The stream-K launch: workgroup count and part slots per block (an upper
+// bound on the shares one block's tiles can touch).
+SplitArgs streamk_plan(int n, int ntiles, int occ, int cus) {
+  const int slots = occ * cus;
+  const int W = (n + slots - 1) / slots * slots;
+  const int share = (int)((int64_t)n * ntiles / W);  // tiles per share, rounded down
+  SplitArgs sa = {0, ntiles / share + 2, nullptr, nullptr, kPipeNw, W};
+  return sa;
+}
+
 template <typename T, int DK, bool CAUSAL, bool PRESCALE, int MOPT>
 hipError_t launch_dk(const FwdParams& p, const SplitArgs& sa, hipStream_t s) {
   // OPT 1: s_setprio around the MFMA blocks; OPT 8: zero K columns past D;
@@ -123,6 +165,14 @@ hipError_t launch_dk(const FwdParams& p, const SplitArgs& sa, hipStream_t s) {
   // instruction per 2 KiB of tile, no bank conflicts; 3-4% faster on SDXL
   // self-attention, 6% on causal bf16 D = 128 than register staging).
   if constexpr (MOPT == 0 && (DK == 32 || DK == 64 || DK == 128)) {
+    // OPT 512: stream-K (equal shares of the block-tile sequence; see
+    // attn_fwd_pipe16.h), planned by launch_pipe16
+    if constexpr (!CAUSAL) {
+      if (sa.sk_wgs > 0) {
+        if (p.D == DK) return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, occ, CAUSAL, PRESCALE, 1 | 2 | 256 | 512>(p, sa, s);
+        return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, occ, CAUSAL, PRESCALE, 1 | 2 | 8 | 256 | 512>(p, sa, s);
+      }
+    }
     if (p.D == DK) return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, occ, CAUSAL, PRESCALE, 1 | 2 | 256>(p, sa, s);
     return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, occ, CAUSAL, PRESCALE, 1 | 2 | 8 | 256>(p, sa, s);
   }
@@ -179,8 +229,6 @@ hipError_t launch_bucket(const FwdParams& p, const SplitArgs& sa, int dk, hipStr
   return hipErrorNotSupported;
 }
 
-int n_blocks(int B, int H, int Sq) { return B * H * ((Sq + kPipeNw * 32 - 1) / (kPipeNw * 32)); }
-int n_key_tiles(int Sk) { return (Sk + kPipeBk - 1) / kPipeBk; }
 
 }  // namespace
 
@@ -294,20 +342,39 @@ hipError_t launch_pipe16(const FwdParams& p0, int dk0, bool bf16, bool causal, b
   const int cus = device_cus();
   const int occ = p.mask_kind != MASK_NONE ? pipe_occ_masked(dk) : pipe_occ(dk);
   const int n = n_blocks(p.B, p.H, p.Sq);
+  const int dp = (dk + 31) / 32 * 32;
+  // stream-K where it applies and its exchange fits the space this call has
+  size_t sk_need = 0;
+  if (streamk_applies(p, n, dk, occ, cus, causal)) {
+    SplitArgs sk = streamk_plan(n, n_key_tiles(p.Sk), occ, cus);
+    const size_t part_bytes = (size_t)n * kPipeNw * split_vectors(dp) * 64 * sizeof(f32x4);
+    const int fit = bind_exchange(p, sk.nparts, part_bytes, 2 * n * kPipeNw, &sk.ws, &sk.cnt);
+    if (p.dry) sk_need = p.dry->need;
+    if (fit == sk.nparts) {
+      if (p.dry) return hipSuccess;
+      return bf16 ? launch_bucket<__bf16, false, false>(p, sk, dk, s)
+                  : prescale ? launch_bucket<_Float16, false, true>(p, sk, dk, s)
+                             : launch_bucket<_Float16, false, false>(p, sk, dk, s);
+    }
+  }
   SplitArgs sa = split_plan(n, n_key_tiles(p.Sk), occ, cus, causal);
   sa.nwl = exchange_waves((p.Sq + kPipeNw * 32 - 1) / (kPipeNw * 32), p.Sq);
+  if (p.dry) *p.dry = SplitInfo{0, 1};  // the stream-K attempt's record, if any, is not this plan
   if (sa.nparts > 1) {
     // Exchange space: the fixed scratch or the caller's workspace, cut to
     // fewer key ranges when the plan does not fit it (an unsplit launch needs
     // none, so no problem is ever refused for want of space).  The plan keeps
     // its whole blocks; only the split blocks' part count changes.
-    const int dp = (dk + 31) / 32 * 32;
     const int nsplit = n - sa.nfull;
     const size_t part_bytes = (size_t)nsplit * sa.nwl * split_vectors(dp) * 64 * sizeof(f32x4);
     sa.nparts = bind_exchange(p, sa.nparts, part_bytes, 2 * nsplit * sa.nwl, &sa.ws, &sa.cnt);
     if (sa.nparts < 2) sa = SplitArgs{n, 1, nullptr, nullptr, sa.nwl};
   }
-  if (p.dry) return hipSuccess;
+  if (p.dry) {
+    // the size query reports the best plan's need (stream-K's, when it applies)
+    if (sk_need > p.dry->need) p.dry->need = sk_need;
+    return hipSuccess;
+  }
   if (p.lse) {  // training forward, masked or not
     if (bf16) return causal ? launch_lse<__bf16, true, false>(p, sa, dk, s) : launch_lse<__bf16, false, false>(p, sa, dk, s);
     if (prescale)
@@ -336,12 +403,23 @@ hipError_t launch_pipe16(const FwdParams& p0, int dk0, bool bf16, bool causal, b
   return causal ? launch_bucket<_Float16, true, false>(p, sa, dk, s) : launch_bucket<_Float16, false, false>(p, sa, dk, s);
 }
 
-void describe_pipe16(int dk, int B, int H, int Sq, int Sk, bool causal, char* buf, int len) {
+void describe_pipe16(int dk, int B, int H, int Sq, int Sk, bool causal, bool narrow, char* buf, int len) {
   const int bq = kPipeNw * 32;
   const int n = n_blocks(B, H, Sq);
   const SplitArgs sa = split_plan(n, n_key_tiles(Sk), pipe_occ(dk), device_cus(), causal);
-  char split[64] = "";
-  if (sa.nparts > 1) snprintf(split, sizeof split, " key-split: %d whole + %d x %d parts", sa.nfull, n - sa.nfull, sa.nparts);
+  char split[96] = "";
+  FwdParams p = {};
+  p.Sq = Sq;
+  p.Sk = Sk;
+  p.mask_kind = MASK_NONE;
+  p.elem_rows = narrow ? 4 : 0;
+  if (streamk_applies(p, n, dk, pipe_occ(dk), device_cus(), causal)) {
+    const SplitArgs sk = streamk_plan(n, n_key_tiles(Sk), pipe_occ(dk), device_cus());
+    snprintf(split, sizeof split, " stream-K: %d workgroups x %lld tiles of %d blocks (with a workspace)", sk.sk_wgs,
+             (long long)n * n_key_tiles(Sk) / sk.sk_wgs, n);
+  } else if (sa.nparts > 1) {
+    snprintf(split, sizeof split, " key-split: %d whole + %d x %d parts", sa.nfull, n - sa.nfull, sa.nparts);
+  }
   snprintf(buf, len,
            "pipe16 mfma 32x32x16 S^T-form, K one tile ahead of V: DK=%d DP=%d waves=%d BQ=%d BK=%d "
            "waves/SIMD=%d qtiles=%d%s",

@@ -58,7 +58,7 @@ struct Mask {
 
 // Key-split workspace of one (device, stream): a byte tensor from torch's
 // caching allocator (so torch.cuda.memory_allocated counts it), zero-filled
-// when made -- its first 16 KiB are the counters every launch leaves at zero
+// when made -- its first 64 KiB are the counters every launch leaves at zero
 // -- and kept for later calls on the stream, replaced by a larger one when a
 // bigger plan arrives.  Calls on one stream run in order, so they can share
 // it.  A stream under graph capture gets none and its launch runs unsplit: a
@@ -398,7 +398,7 @@ int64_t workspace_bytes(int64_t device) {
 
 std::string describe(int64_t dtype, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
                      bool causal) {
-  char buf[256];
+  char buf[384];
   cmpext3_attn_describe((int)dtype, (int)B, (int)H, (int)Sq, (int)Sk, (int)D, causal ? 1 : 0, buf,
                         sizeof buf);
   return std::string(buf);
