@@ -142,6 +142,13 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
       vreg[it] = x;
     }
   };
+  // K rows in LDS: the two 8-byte halves of every 16-byte chunk trade places
+  // in rows 8-15 of each 16.  A 4-byte K fragment read serves 32 lanes (16
+  // rows x lane groups g = 0, 1, or 2, 3) per pass over 32 banks; with a row
+  // stride of 4 * odd floats, rows l and l + 8 start on the same bank, and
+  // the swap moves row l + 8's two lane groups to the other two banks of
+  // each 4-bank group (without it K reads took two passes; measured
+  // SQ_LDS_BANK_CONFLICT ~28-30% of LDS cycles).
   auto store_tile = [&](int buf) {
     float* ks = lds + buf * (KTILE + VTILE);
     float* vs = ks + KTILE;
@@ -150,7 +157,8 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
       const int ci = it * NT + tid;
       if (BK * KCH % NT == 0 || ci < BK * KCH) {
         const int r = ci / KCH, c4 = ci - (ci / KCH) * KCH;
-        *(u32x4*)(ks + r * RSK + 4 * c4) = kreg[it];
+        const u32x4 x = kreg[it];
+        *(u32x4*)(ks + r * RSK + 4 * c4) = (r & 8) ? (u32x4){x[2], x[3], x[0], x[1]} : x;
       }
     }
 #pragma unroll
@@ -182,7 +190,7 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
       for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) sacc[qb][kb] = (f32x4){};
-        const float* krow = ks + (16 * kb + l16) * RSK + g;
+        const float* krow = ks + (16 * kb + l16) * RSK + (g ^ ((l16 >> 2) & 2));
 #pragma unroll
         for (int s = 0; s < NKS; ++s) {
           const float a = krow[4 * s];
