@@ -265,6 +265,15 @@ def test_autoselect_off_runs_the_kernel_without_a_trial(monkeypatch):
     assert torch.equal(cmpext3._dispatch("op", torch.zeros(4), ("sig",), kern, stock), torch.ones(4))
 
 
+def test_unhashable_signature_skips_the_trial(autoselecting):
+    """A signature that cannot key the decision table is served as with
+    autoselect off: the kernel, no measurement, nothing recorded."""
+    kern, stock = Impl(), Impl(torch.ones(4))
+    got = cmpext3._dispatch("op", torch.zeros(4), ("sig", [1, 2]), kern, stock)
+    assert torch.equal(got, torch.zeros(4)) and kern.calls == 1 and stock.calls == 0
+    assert autoselecting._decisions == {}
+
+
 def test_sdpa_signature_and_report(autoselecting, patched, native, monkeypatch):
     force_eligible(monkeypatch)
     q, k, v = torch.randn(1, 2, 5, 8), torch.randn(1, 2, 6, 8), torch.randn(1, 2, 6, 8)

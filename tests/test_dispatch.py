@@ -1,7 +1,7 @@
 """Dispatch-layer tests of the cmpext3 SDPA patch (CPU only, no GPU).
 
 Mirrors the reference's mock-based suite for this path
-(tests/test_cmpext3_monkeypatch.py there: TestGradSafe/TestUsable,
+(tests/test_cmpext3_monkeypatch.py there: the grad and device gates,
 TestEnableDisable :91-180, TestScaledDotProductAttention :857-926),
 written against this package: the
 native module is a fake whose `attention` is a MagicMock (`native` fixture),
@@ -9,6 +9,7 @@ and force_eligible() lets CPU tensors through the GPU/dtype gate.
 """
 from __future__ import annotations
 
+import contextlib
 import os
 import subprocess
 import sys
@@ -37,41 +38,48 @@ def _qkv(*shape):
     return torch.randn(*shape), torch.randn(*shape), torch.randn(*shape)
 
 
-class TestGradSafe:
-    def test_true_when_grad_disabled(self):
-        x = torch.randn(2, requires_grad=True)
-        with torch.no_grad():
-            assert cmpext3._grad_safe(x) is True
-
-    def test_true_in_inference_mode(self):
-        x = torch.randn(2, requires_grad=True)
-        with torch.inference_mode():
-            assert cmpext3._grad_safe(x) is True
-
-    def test_false_when_any_tensor_requires_grad(self):
-        assert cmpext3._grad_safe(torch.randn(2), torch.randn(2, requires_grad=True)) is False
-
-    def test_true_when_no_tensor_requires_grad(self):
-        assert cmpext3._grad_safe(torch.randn(2), torch.randn(2)) is True
-
-    def test_non_tensor_args_are_ignored(self):
-        assert cmpext3._grad_safe(1, "x", None) is True
+def _leaf(needs_grad: bool = False) -> torch.Tensor:
+    return torch.randn(3, requires_grad=needs_grad)
 
 
-class TestUsable:
-    def test_true_for_non_tensor_args(self):
-        assert cmpext3._usable(1, "x", None) is True
+# (what the call looks like, arguments, context it runs in, expected answer)
+_GRAD_CASES = [
+    ("only non-tensors", lambda: (7, "name", None), contextlib.nullcontext, True),
+    ("tensors without grad", lambda: (_leaf(), _leaf()), contextlib.nullcontext, True),
+    ("one tensor needs grad", lambda: (_leaf(), _leaf(True)), contextlib.nullcontext, False),
+    ("grad tensor beside non-tensors", lambda: (None, _leaf(True), 1.5), contextlib.nullcontext,
+     False),
+    ("grad tensor under no_grad", lambda: (_leaf(True),), torch.no_grad, True),
+    ("grad tensor in inference mode", lambda: (_leaf(True),), torch.inference_mode, True),
+]
 
-    def test_false_for_cpu_tensor(self):
-        assert cmpext3._usable(torch.randn(2)) is False
 
-    @pytest.mark.parametrize("dtype,ok", [(torch.int64, False), (torch.float64, False),
-                                          (torch.float16, True), (torch.float32, True),
-                                          (torch.bfloat16, True)])
-    def test_dtype_gate_on_fake_gpu_tensor(self, monkeypatch, dtype, ok):
-        x = torch.zeros(2, dtype=dtype)
-        monkeypatch.setattr(torch.Tensor, "is_cuda", property(lambda self: True))
-        assert cmpext3._usable(x) is ok
+@pytest.mark.parametrize("what,make_args,context,want", _GRAD_CASES,
+                         ids=[case[0] for case in _GRAD_CASES])
+def test_grad_safe(what, make_args, context, want):
+    args = make_args()
+    with context():
+        assert cmpext3._grad_safe(*args) is want, what
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32, torch.bfloat16,
+                                   torch.float64, torch.int64, torch.int8])
+@pytest.mark.parametrize("on_gpu", [True, False])
+def test_usable_accepts_only_gpu_tensors_of_the_three_dtypes(monkeypatch, dtype, on_gpu):
+    monkeypatch.setattr(torch.Tensor, "is_cuda", property(lambda self: on_gpu))
+    t = torch.zeros(2, dtype=dtype)
+    want = on_gpu and dtype in (torch.float16, torch.float32, torch.bfloat16)
+    assert cmpext3._usable(t) is want
+    # non-tensor arguments never change the answer
+    assert cmpext3._usable(None, t, 3, "x") is want
+    assert cmpext3._usable(None, 3, "x") is True
+
+
+def test_usable_needs_every_tensor_to_pass(monkeypatch):
+    monkeypatch.setattr(torch.Tensor, "is_cuda", property(lambda self: self.dtype != torch.int32))
+    good = torch.zeros(2, dtype=torch.float16)
+    assert cmpext3._usable(good, good) is True
+    assert cmpext3._usable(good, torch.zeros(2, dtype=torch.int32)) is False
 
 
 class TestEnableDisable:

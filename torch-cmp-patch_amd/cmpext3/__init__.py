@@ -66,12 +66,18 @@ _SUPPORTED_DTYPES = (torch.float16, torch.float32, torch.bfloat16)
 _ORIGINALS: dict[tuple[Any, str], Callable] = {}
 _ENABLED = False
 
+
+
+def _names_from_env(var: str) -> frozenset:
+    """A comma-separated environment list as a set of names (blanks dropped)."""
+    names = (name.strip() for name in os.environ.get(var, "").split(","))
+    return frozenset(name for name in names if name)
+
+
 # CMPEXT3_DISABLE_OPS=attention (or =scaled_dot_product_attention) keeps SDPA
-# stock; parsed once at import, like the reference (cmpext3/__init__.py:258-261).
+# stock; read once at import, as the reference does (cmpext3/__init__.py:258-261).
 _OP_ALIASES = {"scaled_dot_product_attention": "attention"}
-_DISABLED_OPS = frozenset(
-    part.strip() for part in os.environ.get("CMPEXT3_DISABLE_OPS", "").split(",") if part.strip()
-)
+_DISABLED_OPS = _names_from_env("CMPEXT3_DISABLE_OPS")
 
 
 def _grad_safe(*tensors: Any) -> bool:
@@ -92,12 +98,14 @@ def _usable(*tensors: Any) -> bool:
 
 
 def _install(target: Any, name: str, wrapper: Callable) -> None:
-    if name in _DISABLED_OPS or _OP_ALIASES.get(name, name) in _DISABLED_OPS:
+    """Put `wrapper` in place of target.<name> unless the op is pinned to stock
+    by CMPEXT3_DISABLE_OPS (under its own name or its alias).  The stock
+    callable is remembered the first time only, so enabling twice never
+    records the wrapper as the original (reference: cmpext3/__init__.py:322-329)."""
+    if not _DISABLED_OPS.isdisjoint((name, _OP_ALIASES.get(name, name))):
         return
-    slot = (target, name)
-    if slot not in _ORIGINALS:
-        _ORIGINALS[slot] = getattr(target, name)
-    _keep_scriptable(wrapper, _ORIGINALS[slot])
+    stock = _ORIGINALS.setdefault((target, name), getattr(target, name))
+    _keep_scriptable(wrapper, stock)
     setattr(target, name, wrapper)
 
 
@@ -115,12 +123,6 @@ def _keep_scriptable(wrapper: Callable, original: Callable) -> None:
     op = _builtins._find_builtin(original)
     if op is not None:
         _builtins._register_builtin(wrapper, op)
-
-
-def _restore(target: Any, name: str) -> None:
-    original = _ORIGINALS.pop((target, name), None)
-    if original is not None:
-        setattr(target, name, original)
 
 
 _DTYPE_TAG = {torch.float16: "fp16", torch.float32: "fp32", torch.bfloat16: "bf16"}
@@ -195,24 +197,29 @@ def _training_applies(query, key, value, attn_mask, dropout_p, enable_gqa) -> bo
 
 def _dispatch(op: str, ref: torch.Tensor, key: tuple,
               native_call: Callable, stock_call: Callable) -> Any:
-    """Serve one call from the native kernel or stock torch.
+    """Serve one call from the native kernel or stock torch
+    (reference: cmpext3/__init__.py:376-399).
 
-    With autoselect on, the choice is measured once per signature (correctness
-    first, then speed; see cmpext3/autoselect.py).  With it off: native, and
-    stock only when native raises RuntimeError/TypeError.
+    Autoselect on and a hashable signature: autoselect.choose measures the
+    choice once per signature (correctness first, then speed).  Otherwise
+    (autoselect off, or a signature that cannot key its table): the native
+    kernel, and stock only when it raises RuntimeError or TypeError.
     """
-    if autoselect.enabled():
-        try:
-            return autoselect.choose(f"{op} {_DTYPE_TAG.get(ref.dtype, ref.dtype)}",
-                                     key, native_call, stock_call)
-        except TypeError as exc:
-            if "unhashable" not in str(exc):
-                raise
-            # unhashable signature: skip measuring, behave as autoselect-off
+    if autoselect.enabled() and _hashable(key):
+        tag = _DTYPE_TAG.get(ref.dtype, ref.dtype)
+        return autoselect.choose(f"{op} {tag}", key, native_call, stock_call)
     try:
         return native_call()
     except (RuntimeError, TypeError):
         return stock_call()
+
+
+def _hashable(key: tuple) -> bool:
+    try:
+        hash(key)
+    except TypeError:
+        return False
+    return True
 
 
 def _patched_sdpa(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False,
@@ -267,18 +274,17 @@ def _patched_sdpa(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=Fa
 def enable() -> None:
     """Patch F.scaled_dot_product_attention (idempotent)."""
     global _ENABLED
-    if _ENABLED:
-        return
-    if hasattr(F, "scaled_dot_product_attention"):
+    if not _ENABLED and hasattr(F, "scaled_dot_product_attention"):
         _install(F, "scaled_dot_product_attention", _patched_sdpa)
     _ENABLED = True
 
 
 def disable() -> None:
-    """Restore every patched function to stock (no-op when not enabled)."""
+    """Put every patched function back to stock (no-op when not enabled)."""
     global _ENABLED
-    for target, name in list(_ORIGINALS.keys()):
-        _restore(target, name)
+    while _ORIGINALS:
+        (target, name), stock = _ORIGINALS.popitem()
+        setattr(target, name, stock)
     _ENABLED = False
 
 
