@@ -119,13 +119,21 @@ def test_describe_key_split_plan():
     assert "key-split" not in abi.describe(f32, 1, 8, 1024, 1024, 64, True)[1]
     assert "key-split" not in abi.describe(f32, 2, 8, 4096, 4096, 40)[1]
     assert "key-split: 4 x 5 parts" in abi.describe(f32, 1, 2, 100, 700, 40)[1]
-    # head dims above 128 (one workgroup per CU): fewer blocks than CUs split
-    # into up to CUs / n parts of at least 4 tiles of 32 keys (at most 32; 8
-    # from the 192 bucket up when every wave of a block holds rows, as the
-    # waves then merge their own rows alone), never causal
+    # decode steps (at most 16 rows per head) at head dims above 128 run the
+    # decode kernel: units (batch x heads) x parts fill the CUs' workgroup
+    # slots, each wave keeping at least 4 tiles of 16 keys
+    assert "decode16" in abi.describe(f16, 1, 16, 1, 16384, 256)[1]
     assert "key-split: 16 x 16 parts" in abi.describe(f16, 1, 16, 1, 16384, 256)[1]
-    assert "key-split: 64 x 4 parts" in abi.describe(f16, 1, 8, 1024, 4096, 160)[1]
     assert "key-split: 8 x 32 parts" in abi.describe(f16, 1, 8, 1, 32768, 160)[1]
+    assert "key-split" not in abi.describe(bf16, 64, 8, 1, 4096, 256)[1]   # 512 units: unsplit
+    assert "decode16" in abi.describe(bf16, 1, 8, 16, 4096, 64)[1]         # 8 units at D = 64
+    assert "decode16" not in abi.describe(bf16, 16, 8, 1, 4096, 128)[1]    # 128 units: pipelined
+    assert "decode16" not in abi.describe(bf16, 1, 8, 17, 4096, 256)[1]    # 17 rows
+    # other launches at head dims above 128 (one workgroup per CU): fewer
+    # blocks than CUs split into up to CUs / n parts of at least 4 tiles of
+    # 32 keys (at most 32; 8 from the 192 bucket up when every wave of a block
+    # holds rows, as the waves then merge their own rows alone), never causal
+    assert "key-split: 64 x 4 parts" in abi.describe(f16, 1, 8, 1024, 4096, 160)[1]
     assert "key-split: 4 x 8 parts" in abi.describe(bf16, 1, 4, 100, 3000, 192)[1]
     assert "key-split: 2 x 23 parts" in abi.describe(bf16, 1, 2, 70, 3000, 160)[1]
     assert "key-split" not in abi.describe(f16, 1, 8, 1024, 4096, 160, True)[1]
@@ -329,7 +337,7 @@ def test_workspace_size_and_plan():
     assert need == ctr + 128 * 4 * 4 * 5 * vec
     assert abi.plan(f32, 1, 8, 8, 1024, 1024, 64, need) == (abi.OK, 4)
     assert abi.plan(f32, 1, 8, 8, 1024, 1024, 64, 0) == (abi.OK, 1)
-    # head dim 256 decode: 16 blocks x 16 parts (merged by the whole workgroup)
+    # head dim 256 decode on the decode kernel: 16 units x 16 parts
     assert abi.plan(f16, 1, 16, 16, 1, 16384, 256, 1 << 30) == (abi.OK, 16)
     # never split: causal, whole rounds, short keys
     for args in ((f16, 2, 10, 10, 4096, 4096, 64, -1, True), (f16, 2, 12, 12, 4096, 4096, 64),

@@ -172,7 +172,7 @@ def test_short_keys_layouts_and_scales(dtype, D, layout, scale, shape, run_witho
 
 
 @pytest.mark.parametrize("dtype,B,H,Sq,Sk,D,scale", [
-    ("fp16", 2, 4, 1, 4096, 64, None),     # decode step: three waves hold no rows
+    ("fp16", 2, 4, 17, 4096, 64, None),    # decode-like block: three waves hold no rows
     ("bf16", 1, 3, 33, 1000, 128, None),   # two rowless waves, ragged Sk
     ("fp16", 1, 2, 64, 777, 96, 1.0),      # exactly two rowless waves, D below its bucket, wide scores
     ("bf16", 2, 2, 80, 600, 64, None),     # one rowless wave: the ordinary variant

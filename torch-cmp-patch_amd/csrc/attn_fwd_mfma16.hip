@@ -65,6 +65,9 @@ hipError_t launch_pipe16(const FwdParams& p, int dk, bool bf16, bool causal, boo
 void describe_pipe16(int dk, int B, int H, int Sq, int Sk, bool causal, bool narrow, char* buf, int len);
 bool packs_query_heads(const FwdParams& p, bool causal);
 void pack_query_heads(FwdParams& p);
+bool decode16_applies(const FwdParams& p, bool causal);
+hipError_t launch_decode16(const FwdParams& p, bool bf16, hipStream_t s);
+void describe_decode16(int D, int B, int H, int Sq, int Sk, char* buf, int len);
 
 int mfma16_bucket(int D) {
   for (int dk : kMfma16Dk)
@@ -79,6 +82,10 @@ static bool use_prescale(const FwdParams& p, bool bf16) { return !bf16 && p.c <=
 hipError_t launch_mfma16(const FwdParams& p0, bool bf16, bool causal, hipStream_t s) {
   const int dk = mfma16_bucket(p0.D);
   if (dk < 0) return hipErrorInvalidValue;
+  // decode steps (few query rows per K/V head) above the pipelined kernel's
+  // head dims, and below them where the key split must cut deep: every wave
+  // streams its own key tiles (attn_fwd_decode16.hip)
+  if (decode16_applies(p0, causal)) return launch_decode16(p0, bf16, s);
   // grouped-query launches with few query rows that stay on this kernel run
   // over K/V heads with the group's query rows packed into one problem (the
   // pipelined kernel packs for itself)
@@ -125,6 +132,15 @@ void describe_mfma16(int D, int B, int H, int Sq, int Sk, bool causal, char* buf
   // contiguous rows of a D that is not whole 16-byte chunks are narrow: in
   // 4- or 8-byte pieces (D even) on the pipelined kernel where it applies
   const bool elem = D % 8 != 0;
+  p.B = B;
+  p.H = H;
+  p.D = D;
+  p.Sq = Sq;
+  p.kv_group = 1;
+  if (!elem && decode16_applies(p, causal)) {
+    describe_decode16(D, B, H, Sq, Sk, buf, len);
+    return;
+  }
   if (!elem && short16_applies(p, dk, causal)) {
     describe_short16(dk, Sq, Sk, buf, len);
     return;
