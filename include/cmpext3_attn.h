@@ -68,7 +68,7 @@ extern "C" {
 #define CMPEXT3_E_EMPTY_KEYS       5  /* Sk == 0 with Sq > 0: softmax over nothing */
 #define CMPEXT3_E_LAUNCH           6  /* the HIP launch itself failed */
 #define CMPEXT3_E_TOO_LARGE        7  /* a size does not fit the kernel's index arithmetic */
-#define CMPEXT3_E_MASK             8  /* attention mask with fp32 q or D > 128 */
+#define CMPEXT3_E_MASK             8  /* attention mask the library cannot take (none at present) */
 #define CMPEXT3_E_TRAINING         9  /* training entry point with fp32 or D > 128 */
 
 /*
@@ -138,8 +138,9 @@ int cmpext3_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o,
  * A query row whose keys are all dropped gives zeros (torch's result).
  * With causal != 0 a pair is used only if it is causally visible AND the
  * mask keeps it (torch's rule for attn_mask with is_causal).  Supported for
- * f16/bf16 q/k/v with D <= 128; other calls return CMPEXT3_E_MASK and launch
- * nothing.
+ * every dtype (f16, bf16, f32) and head dim, with the rows of q/k/v/o in
+ * whole 16-byte chunks at 16-byte aligned addresses (else CMPEXT3_E_ALIGN or
+ * CMPEXT3_E_HEAD_DIM, nothing launched).
  *
  * Reference: the reference never ran masks natively: _patched_sdpa sends
  * any attn_mask to stock torch (cmpext3/__init__.py:624).

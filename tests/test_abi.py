@@ -346,7 +346,7 @@ def test_workspace_size_and_plan():
     # errors: the size is 0 and the plan reports the code
     assert abi.workspace_size(f16, 1, 1, 1, 8, 8, 300) == 0
     assert abi.plan(f16, 1, 1, 1, 8, 8, 300, 0) == (abi.E_HEAD_DIM, 0)
-    assert abi.plan(f32, 1, 1, 1, 8, 8, 64, 0, mask_dtype=abi.DTYPE_BOOL) == (abi.E_MASK, 0)
+    assert abi.plan(f32, 1, 1, 1, 8, 8, 64, 0, mask_dtype=abi.DTYPE_BOOL) == (abi.OK, 1)  # fp32 masks run
     assert abi.plan(f16, 1, 4, 3, 8, 8, 64, 0) == (abi.E_INVALID, 0)
 
 

@@ -14,8 +14,8 @@ them empty), grouped-query K/V, head dims below their bucket, and mask
 layouts the ABI cannot read in place (transposed, key count not a multiple
 of 4), which the bindings copy.  With is_causal a pair must be causally
 visible and kept by the mask (torch's CPU rule; the oracle is pinned to it in
-tests/test_oracle.py).  Unsupported masked calls (fp32, D > 128) are rejected
-by the ABI and fall back to stock in the patch.
+tests/test_oracle.py).  fp32 calls run the fp32 kernel's mask path and head
+dims above 128 the wide kernel's (bar 1e-4 for fp32).
 """
 from __future__ import annotations
 
@@ -33,7 +33,7 @@ from oracle import sdpa_oracle as orc
 pytestmark = pytest.mark.gpu
 
 TOL = orc.TOLERANCE
-TDT = {"fp16": torch.float16, "bf16": torch.bfloat16}
+TDT = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}
 
 
 def _inputs(dtype, B, H, Sq, Sk, D, seed, Hkv=None):
@@ -68,6 +68,12 @@ CASES = [
     ("bf16", 1, 2, 130, 300, 128),    # odd tile count
     ("fp16", 1, 2, 256, 2048, 64),    # key split, 8 parts
     ("bf16", 2, 2, 200, 1000, 40),    # D below its bucket, key split
+    ("fp32", 2, 3, 100, 77, 64),      # fp32 kernel, short keys
+    ("fp32", 1, 2, 130, 300, 40),     # fp32, the SD1.5 head dim
+    ("fp32", 1, 2, 256, 2048, 64),    # fp32 key split
+    ("fp16", 1, 2, 130, 300, 160),    # head dims above 128
+    ("bf16", 1, 2, 64, 2048, 256),    # above 128, key split merged by the whole workgroup
+    ("bf16", 2, 2, 200, 700, 192),
 ]
 KINDS = ["bool_pad", "bool_full", "add_heads", "add_2d_f32"]
 
@@ -120,12 +126,17 @@ def test_mask_layouts_that_need_a_copy():
     assert orc.max_abs_err(out.cpu(), ref) <= TOL["fp16"]
 
 
-def test_unsupported_masked_calls_are_rejected():
-    m = torch.ones(64, 64, dtype=torch.bool, device="cuda")
-    q32 = torch.randn(1, 2, 64, 64, device="cuda")
-    assert abi.attn_fwd_raw(q32, q32, q32, torch.empty_like(q32), 0.125, attn_mask=m) == abi.E_MASK
-    q160 = torch.randn(1, 2, 64, 160, device="cuda").half()
-    assert abi.attn_fwd_raw(q160, q160, q160, torch.empty_like(q160), 0.125, attn_mask=m) == abi.E_MASK
+@pytest.mark.parametrize("dtype,D", [("fp32", 64), ("fp16", 256)])
+def test_fully_masked_rows_are_zero_on_every_kernel(dtype, D):
+    q, k, v = _inputs(dtype, 1, 2, 64, 600, D, seed=4)
+    m = torch.ones(1, 2, 64, 600, dtype=torch.bool, device="cuda")
+    m[:, :, 10] = False
+    m[:, 1, 20, :300] = False
+    out = abi.attn_fwd(q, k, v, 0.1, False, attn_mask=m)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out[:, :, 10]) == 0
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), 0.1, attn_mask=m.cpu())
+    assert orc.max_abs_err(out.cpu(), ref) <= TOL[dtype]
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
@@ -154,11 +165,27 @@ def test_masked_sdpa_runs_native(patched, dtype):
     assert orc.max_abs_err(out.cpu(), ref) <= TOL[dtype]
 
 
-def test_unsupported_masked_sdpa_falls_back(patched):
-    """fp32 with a mask: the native op rejects it, stock computes it."""
+def test_fp32_masked_sdpa_runs_native(patched):
+    """fp32 with a mask goes to the native op (one call) and meets the fp32 bar."""
     q, k, v = (torch.randn(1, 2, 50, 64, device="cuda") for _ in range(3))
     m = torch.rand(50, 50, device="cuda") > 0.5
-    with torch.inference_mode():
-        out = F.scaled_dot_product_attention(q, k, v, attn_mask=m)
-        want = cmpext3._ORIGINALS[(F, "scaled_dot_product_attention")](q, k, v, attn_mask=m)
-    assert torch.equal(out, want)
+    calls = {"n": 0}
+    real = cmpext3._C
+
+    class Counting:
+        @staticmethod
+        def attention(*args):
+            calls["n"] += 1
+            return real.attention(*args)
+
+    old = cmpext3._C
+    cmpext3._C = Counting
+    try:
+        with torch.inference_mode():
+            out = F.scaled_dot_product_attention(q, k, v, attn_mask=m)
+    finally:
+        cmpext3._C = old
+    torch.cuda.synchronize()
+    assert calls["n"] == 1
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), None, attn_mask=m.cpu())
+    assert orc.max_abs_err(out.cpu(), ref) <= TOL["fp32"]

@@ -97,10 +97,14 @@ def test_noalloc_passes_argument_checks_like_the_masked_entry_point():
     keep = torch.ones(1, 1, 64, 300, dtype=torch.bool, device="cuda")
     assert abi.attn_fwd_noalloc_raw(bad, k[..., :60], v[..., :60], o[..., :60], 0.1,
                                     attn_mask=keep) == abi.E_HEAD_DIM
-    # fp32 with a mask: refused before any launch
-    m = torch.ones(1, 1, 64, 300, dtype=torch.bool, device="cuda")
+    # fp32 with a mask: the same result as the workspace entry point
+    m = torch.rand(1, 1, 64, 300, device="cuda") > 0.3
     qf, kf, vf = (t.float() for t in (q, k, v))
-    assert abi.attn_fwd_noalloc_raw(qf, kf, vf, torch.empty_like(qf), 0.1, attn_mask=m) == abi.E_MASK
+    got, want = torch.empty_like(qf), torch.empty_like(qf)
+    assert abi.attn_fwd_noalloc_raw(qf, kf, vf, got, 0.1, attn_mask=m) == abi.OK
+    assert abi.attn_fwd_raw(qf, kf, vf, want, 0.1, attn_mask=m) == abi.OK
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
 
 
 # Plans larger than the fixed scratch: cut to fewer key ranges inside the

@@ -16,12 +16,14 @@ What runs where:
   * fp16 / bf16 [B,H,S,D] on the GPU: MFMA kernel (bf16 natively, no cast);
   * fp32 on the GPU: fp32-MFMA kernel (causal included);
   * causal (top-left, torch convention) and cross-attention (Sq != Sk) for
-    every dtype; head dims up to 256;
-  * stock torch for ``attn_mask``, ``dropout_p != 0``, non-4D inputs, live
-    autograd, CPU tensors and any other dtype -- the cases where the reference
-    itself falls back (cmpext3/__init__.py:624-628 there) -- and for any
-    argument the native op rejects (RuntimeError/TypeError), e.g. GQA head
-    counts or an empty key sequence.
+    every dtype; head dims up to 256; ``attn_mask`` (bool or additive) for
+    every dtype, where the reference always fell back
+    (cmpext3/__init__.py:624 there);
+  * stock torch for ``dropout_p != 0``, non-4D inputs, live autograd, CPU
+    tensors and any other dtype -- the cases where the reference itself
+    falls back (cmpext3/__init__.py:624-628 there) -- and for any argument
+    the native op rejects (RuntimeError/TypeError), e.g. GQA head counts or
+    an empty key sequence.
 
 Training (no counterpart in the reference, which is forward-only): with
 ``CMPEXT3_BACKWARD=1`` in the environment, or after ``enable_backward()``,

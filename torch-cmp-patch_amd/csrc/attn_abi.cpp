@@ -62,8 +62,10 @@ int check_mask(const void* mask, int mask_dtype, const int64_t mask_str[3], int 
   if (mask_dtype == -1) return CMPEXT3_OK;
   if (mask_dtype < CMPEXT3_DTYPE_F16 || mask_dtype > CMPEXT3_DTYPE_BOOL) return CMPEXT3_E_DTYPE;
   if (!mask || !mask_str) return CMPEXT3_E_INVALID;
-  // masks run on the pipelined fp16/bf16 kernels only (causal or not)
-  if (dtype == CMPEXT3_DTYPE_F32 || D > 128) return CMPEXT3_E_MASK;
+  // every dtype and head dim takes a mask (causal or not); the rows of Q, K,
+  // V and O must then be whole aligned 16-byte chunks (checked by the caller)
+  (void)dtype;
+  (void)D;
   // every 8-key run of a row is one aligned 8/16/32-byte load
   if (((uintptr_t)mask & 15u) != 0) return CMPEXT3_E_ALIGN;
   for (int i = 0; i < 3; ++i)
@@ -136,7 +138,7 @@ const char* cmpext3_attn_strerror(int code) {
     case CMPEXT3_E_LAUNCH: return "HIP kernel launch failed";
     case CMPEXT3_E_TOO_LARGE: return "problem too large for 32-bit tile indexing";
     case CMPEXT3_E_MASK:
-      return "attention mask not supported here (needs f16/bf16 q and head dim <= 128)";
+      return "attention mask not supported here";
     case CMPEXT3_E_TRAINING:
       return "not supported by the training entry points (need f16/bf16 and head dim <= 128)";
   }
@@ -275,10 +277,8 @@ int plan_impl(int dtype, int B, int H, int H_kv, int Sq, int Sk, int D, int mask
   if (rc != CMPEXT3_OK || (int64_t)B * H * Sq == 0) return rc;
   if (H_kv < 1 || H_kv > H || H % H_kv != 0) return CMPEXT3_E_INVALID;
   if (with_lse && (dtype == CMPEXT3_DTYPE_F32 || D > 128)) return CMPEXT3_E_TRAINING;
-  if (mask_dtype != -1) {
-    if (mask_dtype < CMPEXT3_DTYPE_F16 || mask_dtype > CMPEXT3_DTYPE_BOOL) return CMPEXT3_E_DTYPE;
-    if (dtype == CMPEXT3_DTYPE_F32 || D > 128) return CMPEXT3_E_MASK;
-  }
+  if (mask_dtype != -1 && (mask_dtype < CMPEXT3_DTYPE_F16 || mask_dtype > CMPEXT3_DTYPE_BOOL))
+    return CMPEXT3_E_DTYPE;
   if ((mask_dtype != -1 || with_lse) && elem != 0) return CMPEXT3_E_ALIGN;
   cmpext3::FwdParams p;
   memset(&p, 0, sizeof p);

@@ -111,6 +111,36 @@ __device__ __forceinline__ uint2 lds_tr16_b64(const uint16_t* p) {
   return __builtin_bit_cast(uint2, v);
 }
 
+// Attention mask (FwdParams::mask) of 8 consecutive keys of one query row,
+// applied to the exp2-domain scores sc[r0 .. r0 + 7]: a zero bool removes
+// the key (-inf), float kinds are added times log2(e).  One 8-, 16- or
+// 32-byte read at byte offset `off` of the mask buffer (reads past its end
+// return zero).
+__device__ __forceinline__ void mask_run8(f32x16& sc, int r0, const __amdgpu_buffer_rsrc_t& mrs, int off,
+                                          int kind) {
+  if (kind == MASK_BOOL) {
+    const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(mrs, off, 0, 0));
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (((w[i >> 2] >> (8 * (i & 3))) & 0xffu) == 0u) sc[r0 + i] = -INFINITY;
+  } else if (kind == MASK_F32) {
+#pragma unroll
+    for (int hv = 0; hv < 2; ++hv) {
+      const f32x4 a = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(mrs, off + 16 * hv, 0, 0));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sc[r0 + 4 * hv + i] = __builtin_fmaf(a[i], kLog2e, sc[r0 + 4 * hv + i]);
+    }
+  } else {
+    const u32x4 w = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(mrs, off, 0, 0));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x2 a = kind == MASK_F16 ? Elt<_Float16>::unpack(w[i]) : Elt<__bf16>::unpack(w[i]);
+      sc[r0 + 2 * i] = __builtin_fmaf(a[0], kLog2e, sc[r0 + 2 * i]);
+      sc[r0 + 2 * i + 1] = __builtin_fmaf(a[1], kLog2e, sc[r0 + 2 * i + 1]);
+    }
+  }
+}
+
 constexpr float kSumHi = 256.0f;         // tile row sum above this: offset must rise
 constexpr float kSumLo = 1.0f / 256.0f;  // first tile row sum below this: offset too high
 
@@ -136,7 +166,8 @@ __device__ __forceinline__ int lds_swz(int r) {
 // The padded, max-first form is the default.  OPT bit 6: narrow rows
 // (ld_cols16 / st_cols16x4, FwdParams::elem_rows): any head dim and any
 // 2-byte aligned rows, read and written in 2-, 4- or 8-byte pieces, columns
-// past D never touched.
+// past D never touched.  OPT bit 4: an attention mask (p.mask) on every
+// tile's scores.
 template <typename T, int DK, int DP, int NW, int QB, int BK, int OCC, bool CAUSAL, bool PRESCALE,
           int OPT = 0>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
@@ -148,6 +179,8 @@ attn_fwd_mfma16(const FwdParams p, const SplitArgs sa) {
   // measurable bank conflicts), or unpadded with XOR-swizzled 16-byte chunks.
   constexpr bool SWZ = (OPT & 2) && (DK == DP) && (DK == 32 || DK == 64 || DK == 128);
   constexpr bool ELEM = (OPT & 64) != 0;
+  constexpr bool MASK = (OPT & 16) != 0;
+  static_assert(!(ELEM && MASK), "masked launches have whole 16-byte chunks");
   constexpr int RSK = SWZ ? DK : DK + 8;  // K tile row stride (halves)
   constexpr int RSV = SWZ ? DP : DP + 8;  // V tile row stride (halves)
   constexpr int KTILE = BK * RSK;
@@ -342,6 +375,19 @@ attn_fwd_mfma16(const FwdParams p, const SplitArgs sa) {
       v_rd[db][half] = r * RSV + (SWZ ? 8 * ((col >> 3) ^ lds_swz<DP>(r)) + (col & 7) : col);
     }
 
+  // attention mask (MASK): a lane's 16 keys per 32-key block are 2 runs of 8
+  // consecutive keys (acc_key), one read each; rows past Sq read the last
+  // row (their output is never stored), which is readable up to Sk rounded
+  // up to 8 (the ABI's contract); keys at or past Sk are masked afterwards
+  const int mes = p.mask_kind == MASK_BOOL ? 1 : p.mask_kind == MASK_F32 ? 4 : 2;
+  const __amdgpu_buffer_rsrc_t mrs =
+      uniform_rsrc(MASK ? (const void*)((const char*)p.mask + (b * p.m_b + h * p.m_h) * mes) : p.q,
+                   MASK ? ((int64_t)(Sq - 1) * p.m_q + (Sk + 7) / 8 * 8) * mes : 0);
+  int mrow_off[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb)
+    mrow_off[qb] = MASK ? (int)((int64_t)min(qw0 + 32 * qb + l32, Sq - 1) * p.m_q * mes) : 0;
+
   if (ntiles > 0) load_tile(0);
 
   for (int t = 0; t < ntiles; ++t) {
@@ -380,6 +426,14 @@ attn_fwd_mfma16(const FwdParams p, const SplitArgs sa) {
           for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[kb][r] = __builtin_fmaf(sacc[kb][r], c, -mb[qb]);
+        }
+        if (MASK) {
+#pragma unroll
+          for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int run = 0; run < 2; ++run)
+              mask_run8(sacc[kb], 8 * run, mrs, mrow_off[qb] + (k0 + 32 * kb + 16 * run + 8 * hh) * mes,
+                        p.mask_kind);
         }
         if (need_mask) {
 #pragma unroll

@@ -32,7 +32,8 @@ constexpr Tile16 tile16(int dk) {
 }
 
 // OPT 1: s_setprio(1) around the MFMA blocks (padded LDS rows, max-first
-// rescale); OPT 64: element-granular rows (FwdParams::elem_rows)
+// rescale); OPT 16: attention mask; OPT 64: element-granular rows
+// (FwdParams::elem_rows)
 template <typename T, int DK, bool CAUSAL, bool PRESCALE, int EOPT>
 hipError_t launch_dk(const FwdParams& p, hipStream_t s) {
   constexpr Tile16 tt = tile16(DK);
@@ -51,6 +52,17 @@ hipError_t launch_bucket(const FwdParams& p, int dk, hipStream_t s) {
     case 160: return launch_dk<T, 160, CAUSAL, PRESCALE, EOPT>(p, s);
     case 192: return launch_dk<T, 192, CAUSAL, PRESCALE, EOPT>(p, s);
     case 256: return launch_dk<T, 256, CAUSAL, PRESCALE, EOPT>(p, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+// attention-masked launches (OPT bit 16) of the head dims above 128
+template <typename T, bool CAUSAL, bool PRESCALE>
+hipError_t launch_masked(const FwdParams& p, int dk, hipStream_t s) {
+  switch (dk) {
+    case 160: return launch_dk<T, 160, CAUSAL, PRESCALE, 16>(p, s);
+    case 192: return launch_dk<T, 192, CAUSAL, PRESCALE, 16>(p, s);
+    case 256: return launch_dk<T, 256, CAUSAL, PRESCALE, 16>(p, s);
   }
   return hipErrorInvalidValue;
 }
@@ -108,9 +120,18 @@ hipError_t launch_mfma16(const FwdParams& p0, bool bf16, bool causal, hipStream_
   }
   if (short16_applies(p, dk, causal)) return launch_short16(p, dk, bf16, s);
   if (pipe16_applies(p, dk)) return launch_pipe16(p, dk, bf16, causal, use_prescale(p, bf16), s);
-  // the v2 kernel has neither a log-sum-exp output nor mask code: refuse
-  // rather than run without them (the ABI rejects such calls earlier)
-  if (p.lse || p.mask_kind != MASK_NONE) return hipErrorNotSupported;
+  // this kernel has no log-sum-exp output: refuse rather than run without it
+  // (the ABI rejects such calls earlier); masked launches reach it only above
+  // D = 128 (the pipelined kernel takes every masked launch up to 128)
+  if (p.lse) return hipErrorNotSupported;
+  if (p.mask_kind != MASK_NONE) {
+    if (dk <= 128) return hipErrorNotSupported;
+    if (bf16)
+      return causal ? launch_masked<__bf16, true, false>(p, dk, s) : launch_masked<__bf16, false, false>(p, dk, s);
+    if (use_prescale(p, bf16))
+      return causal ? launch_masked<_Float16, true, true>(p, dk, s) : launch_masked<_Float16, false, true>(p, dk, s);
+    return causal ? launch_masked<_Float16, true, false>(p, dk, s) : launch_masked<_Float16, false, false>(p, dk, s);
+  }
   if (bf16)
     return causal ? launch_bucket<__bf16, true, false>(p, dk, s)
                   : launch_bucket<__bf16, false, false>(p, dk, s);

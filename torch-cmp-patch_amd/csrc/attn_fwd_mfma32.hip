@@ -33,8 +33,10 @@ __device__ __forceinline__ f32x4 mma32(float a, float b, f32x4 c) {
 
 // DK: head dim bucket (multiple of 4, zero-padded above D); NQB: 16-row query
 // blocks per wave.  ELEM: element-granular K/V/O rows (any head dim, any
-// 4-byte aligned rows; ld_cols32), columns past D never touched.
-template <int DK, int NW, int NQB, int BK, bool CAUSAL, bool ELEM>
+// 4-byte aligned rows; ld_cols32), columns past D never touched.  MASK: an
+// attention mask (p.mask: bool keeps, floats are added to the scaled scores)
+// applied to every tile.
+template <int DK, int NW, int NQB, int BK, bool CAUSAL, bool ELEM, bool MASK = false>
 __global__ void __launch_bounds__(NW * 64)
 attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
   constexpr int NT = NW * 64;
@@ -171,6 +173,19 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
     }
   };
 
+  // attention mask rows (MASK): rows past Sq read the last row (their output
+  // is never stored); the last row is readable up to Sk rounded up to 8 (the
+  // ABI's contract), reads past it return zero, and keys at or past Sk are
+  // masked by the key-range rule anyway
+  const int mes = p.mask_kind == MASK_BOOL ? 1 : p.mask_kind == MASK_F32 ? 4 : 2;
+  const __amdgpu_buffer_rsrc_t mrs =
+      uniform_rsrc(MASK ? (const void*)((const char*)p.mask + (b * p.m_b + h * p.m_h) * mes) : p.q,
+                   MASK ? ((int64_t)(Sq - 1) * p.m_q + (Sk + 7) / 8 * 8) * mes : 0);
+  int mrow[NQB];
+#pragma unroll
+  for (int qb = 0; qb < NQB; ++qb)
+    mrow[qb] = MASK ? (int)((int64_t)min(qw0 + 16 * qb + l16, Sq - 1) * p.m_q * mes) : 0;
+
   if (ntiles > 0) load_tile(0);
 
   for (int t = 0; t < ntiles; ++t) {
@@ -199,20 +214,45 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
         }
       }
 
-      const bool need_mask = (k0 + BK > Sk) || (CAUSAL && k0 + BK - 1 > qw0);
+      const bool need_mask = MASK || (k0 + BK > Sk) || (CAUSAL && k0 + BK - 1 > qw0);
       float cm = c;
       if (need_mask) {
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) {
           const int qrow = qw0 + 16 * qb + l16;
 #pragma unroll
-          for (int kb = 0; kb < NKB; ++kb)
+          for (int kb = 0; kb < NKB; ++kb) {
+            // the lane's 4 consecutive keys: one 4/8/16-byte mask read
+            f32x4 madd = {0.f, 0.f, 0.f, 0.f};
+            uint32_t keep = 0x01010101u;
+            if (MASK) {
+              const int key4 = k0 + 16 * kb + 4 * g;
+              if (p.mask_kind == MASK_BOOL) {
+                keep = __builtin_amdgcn_raw_buffer_load_b32(mrs, mrow[qb] + key4, 0, 0);
+              } else if (p.mask_kind == MASK_F32) {
+                madd = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(mrs, mrow[qb] + 4 * key4, 0, 0));
+              } else {
+                const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(mrs, mrow[qb] + 2 * key4, 0, 0));
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                  const uint32_t lo = w[i] << 16, hi = w[i] & 0xffff0000u;
+                  if (p.mask_kind == MASK_BF16) {
+                    madd[2 * i] = __uint_as_float(lo);
+                    madd[2 * i + 1] = __uint_as_float(hi);
+                  } else {
+                    madd[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] & 0xffffu));
+                    madd[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] >> 16));
+                  }
+                }
+              }
+            }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int key = k0 + 16 * kb + 4 * g + r;
-              const bool dead = key >= Sk || (CAUSAL && key > qrow);
-              sacc[qb][kb][r] = dead ? -INFINITY : sacc[qb][kb][r] * c;
+              const bool dead = key >= Sk || (CAUSAL && key > qrow) || ((keep >> (8 * r)) & 0xffu) == 0u;
+              sacc[qb][kb][r] = dead ? -INFINITY : __builtin_fmaf(madd[r], kLog2e, sacc[qb][kb][r] * c);
             }
+          }
         }
         cm = 1.f;
       }
@@ -413,7 +453,7 @@ int tile_keys32(int dk, int n, int Sk, int cus, bool causal) {
   return p64 >= 2 && p64 == split_parts32(n, Sk, def, cus, causal) ? 64 : def;
 }
 
-template <int DK, bool CAUSAL, bool ELEM, int BK>
+template <int DK, bool CAUSAL, bool ELEM, int BK, bool MASK>
 hipError_t launch_mfma32_bk(const FwdParams& p0, hipStream_t stream) {
   // One 16-row query block per wave: measured on MI355X, two per wave only
   // lengthen each wave's dependency chain (1.6x slower on [1,8,1024,1024,64],
@@ -442,20 +482,20 @@ hipError_t launch_mfma32_bk(const FwdParams& p0, hipStream_t stream) {
   }
   if (p.dry) return hipSuccess;
   const int nwg = sa.nfull + (n - sa.nfull) * sa.nparts;
-  hipLaunchKernelGGL((attn_fwd_mfma32<DK, NW, NQB, BK, CAUSAL, ELEM>), dim3(nwg), dim3(NW * 64), 0, stream, p,
-                     sa);
+  hipLaunchKernelGGL((attn_fwd_mfma32<DK, NW, NQB, BK, CAUSAL, ELEM, MASK>), dim3(nwg), dim3(NW * 64), 0, stream,
+                     p, sa);
   return hipGetLastError();
 }
 
-template <int DK, bool CAUSAL, bool ELEM>
+template <int DK, bool CAUSAL, bool ELEM, bool MASK>
 hipError_t launch_mfma32_inst(const FwdParams& p, hipStream_t stream) {
   constexpr int BK = (DK <= 128) ? 32 : 16;
   if constexpr (!CAUSAL && DK <= 64) {
     const int n = p.B * p.H * ((p.Sq + 63) / 64);
     if (tile_keys32(DK, n, p.Sk, device_cus(), CAUSAL) == 64)
-      return launch_mfma32_bk<DK, CAUSAL, ELEM, 64>(p, stream);
+      return launch_mfma32_bk<DK, CAUSAL, ELEM, 64, MASK>(p, stream);
   }
-  return launch_mfma32_bk<DK, CAUSAL, ELEM, BK>(p, stream);
+  return launch_mfma32_bk<DK, CAUSAL, ELEM, BK, MASK>(p, stream);
 }
 
 static const int kMfma32Dk[] = {16, 32, 40, 48, 64, 80, 96, 128, 160, 192, 256};
@@ -466,20 +506,20 @@ int mfma32_bucket(int D) {
   return -1;
 }
 
-template <bool CAUSAL, bool ELEM>
+template <bool CAUSAL, bool ELEM, bool MASK = false>
 static hipError_t launch_mfma32_dk(const FwdParams& p, int dk, hipStream_t s) {
   switch (dk) {
-    case 16: return launch_mfma32_inst<16, CAUSAL, ELEM>(p, s);
-    case 32: return launch_mfma32_inst<32, CAUSAL, ELEM>(p, s);
-    case 40: return launch_mfma32_inst<40, CAUSAL, ELEM>(p, s);
-    case 48: return launch_mfma32_inst<48, CAUSAL, ELEM>(p, s);
-    case 64: return launch_mfma32_inst<64, CAUSAL, ELEM>(p, s);
-    case 80: return launch_mfma32_inst<80, CAUSAL, ELEM>(p, s);
-    case 96: return launch_mfma32_inst<96, CAUSAL, ELEM>(p, s);
-    case 128: return launch_mfma32_inst<128, CAUSAL, ELEM>(p, s);
-    case 160: return launch_mfma32_inst<160, CAUSAL, ELEM>(p, s);
-    case 192: return launch_mfma32_inst<192, CAUSAL, ELEM>(p, s);
-    case 256: return launch_mfma32_inst<256, CAUSAL, ELEM>(p, s);
+    case 16: return launch_mfma32_inst<16, CAUSAL, ELEM, MASK>(p, s);
+    case 32: return launch_mfma32_inst<32, CAUSAL, ELEM, MASK>(p, s);
+    case 40: return launch_mfma32_inst<40, CAUSAL, ELEM, MASK>(p, s);
+    case 48: return launch_mfma32_inst<48, CAUSAL, ELEM, MASK>(p, s);
+    case 64: return launch_mfma32_inst<64, CAUSAL, ELEM, MASK>(p, s);
+    case 80: return launch_mfma32_inst<80, CAUSAL, ELEM, MASK>(p, s);
+    case 96: return launch_mfma32_inst<96, CAUSAL, ELEM, MASK>(p, s);
+    case 128: return launch_mfma32_inst<128, CAUSAL, ELEM, MASK>(p, s);
+    case 160: return launch_mfma32_inst<160, CAUSAL, ELEM, MASK>(p, s);
+    case 192: return launch_mfma32_inst<192, CAUSAL, ELEM, MASK>(p, s);
+    case 256: return launch_mfma32_inst<256, CAUSAL, ELEM, MASK>(p, s);
   }
   return hipErrorInvalidValue;
 }
@@ -487,6 +527,11 @@ static hipError_t launch_mfma32_dk(const FwdParams& p, int dk, hipStream_t s) {
 hipError_t launch_mfma32(const FwdParams& p, bool causal, hipStream_t s) {
   const int dk = mfma32_bucket(p.D);
   if (dk < 0) return hipErrorInvalidValue;
+  if (p.mask_kind != MASK_NONE) {
+    // masked calls arrive with whole, 16-byte aligned rows (the ABI checks)
+    if (p.elem_rows) return hipErrorNotSupported;
+    return causal ? launch_mfma32_dk<true, false, true>(p, dk, s) : launch_mfma32_dk<false, false, true>(p, dk, s);
+  }
   if (p.elem_rows)
     return causal ? launch_mfma32_dk<true, true>(p, dk, s) : launch_mfma32_dk<false, true>(p, dk, s);
   return causal ? launch_mfma32_dk<true, false>(p, dk, s) : launch_mfma32_dk<false, false>(p, dk, s);

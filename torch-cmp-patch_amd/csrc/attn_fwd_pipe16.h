@@ -466,36 +466,11 @@ __device__ __forceinline__ void pipe16_segment(const FwdParams& p, const SplitAr
   const int mrow_off = MASK ? (int)((int64_t)min(qrow, Sq - 1) * p.m_q * mes) : 0;
   auto add_mask = [&](int j, f32x16 (&sc)[NKB]) {
     const int k0 = (tbase + j) * BK;
-    const int kind = p.mask_kind;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-      for (int run = 0; run < 2; ++run) {
-        const int key = k0 + 32 * kb + 16 * run + 8 * hh;  // first of 8 consecutive keys
-        const int r0 = 8 * run;
-        if (kind == MASK_BOOL) {
-          const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(mrs, mrow_off + key, 0, 0));
-#pragma unroll
-          for (int i = 0; i < 8; ++i)
-            if (((w[i >> 2] >> (8 * (i & 3))) & 0xffu) == 0u) sc[kb][r0 + i] = -INFINITY;
-        } else if (kind == MASK_F32) {
-#pragma unroll
-          for (int hv = 0; hv < 2; ++hv) {
-            const f32x4 a = __builtin_bit_cast(
-                f32x4, __builtin_amdgcn_raw_buffer_load_b128(mrs, mrow_off + 4 * (key + 4 * hv), 0, 0));
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sc[kb][r0 + 4 * hv + i] = __builtin_fmaf(a[i], kLog2e, sc[kb][r0 + 4 * hv + i]);
-          }
-        } else {
-          const u32x4 w = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(mrs, mrow_off + 2 * key, 0, 0));
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const f32x2 a = kind == MASK_F16 ? Elt<_Float16>::unpack(w[i]) : Elt<__bf16>::unpack(w[i]);
-            sc[kb][r0 + 2 * i] = __builtin_fmaf(a[0], kLog2e, sc[kb][r0 + 2 * i]);
-            sc[kb][r0 + 2 * i + 1] = __builtin_fmaf(a[1], kLog2e, sc[kb][r0 + 2 * i + 1]);
-          }
-        }
-      }
+      for (int run = 0; run < 2; ++run)  // keys k0 + 32 kb + 16 run + 8 hh .. + 7
+        mask_run8(sc[kb], 8 * run, mrs, mrow_off + (k0 + 32 * kb + 16 * run + 8 * hh) * mes, p.mask_kind);
   };
   // this lane's half of the row max (the two halves meet at the decision)
   auto row_max = [&](const f32x16 (&sc)[NKB]) {
