@@ -123,18 +123,19 @@ int cmpext3_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o,
  * Attention with an explicit mask: as cmpext3_attn_fwd_gqa, plus torch's
  * scaled_dot_product_attention attn_mask.
  *
- *   mask       : device pointer, 16-byte aligned.
+ *   mask       : device pointer, aligned to its element size.
  *   mask_dtype : CMPEXT3_DTYPE_BOOL (one byte per element; non-zero keeps the
  *                (query, key) pair, zero drops it) or CMPEXT3_DTYPE_F16 /
  *                _BF16 / _F32 (added to scale * Q K^T, -inf drops the pair);
  *                -1 means no mask (then mask and mask_str are ignored).
  *   mask_str[3]: element strides of the mask over {batch, head, query}
- *                (0 = broadcast, otherwise multiples of 4); keys are
+ *                (0 = broadcast, otherwise any non-negative value); keys are
  *                contiguous (stride 1).  Element (b, h, i, j) lives at
  *                mask + b*mask_str[0] + h*mask_str[1] + i*mask_str[2] + j.
- *                Keys are read in runs of 8: every row must be readable up
- *                to Sk rounded up to a multiple of 8 (values past Sk are
- *                ignored).
+ *                Nothing past key Sk - 1 of a row is read.  (With a 16-byte
+ *                aligned mask, strides that are multiples of 4 and Sk a
+ *                multiple of 8 the keys are read in runs of 8; any other
+ *                layout element by element.)
  * A query row whose keys are all dropped gives zeros (torch's result).
  * With causal != 0 a pair is used only if it is causally visible AND the
  * mask keeps it (torch's rule for attn_mask with is_causal).  Supported for
@@ -243,7 +244,11 @@ int cmpext3_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* 
  *         softmax; -inf for a row whose keys are all dropped.
  *
  * Supported for f16/bf16 with D <= 128 (else CMPEXT3_E_TRAINING, nothing
- * launched).  Every such call runs the pipelined kernel, whatever Sk.
+ * launched).  Every such call runs the pipelined kernel, whatever Sk.  A mask
+ * is read in runs of 8 keys, as the backward reads it: 16-byte aligned,
+ * strides multiples of 4 elements (else CMPEXT3_E_ALIGN), and every row
+ * readable up to Sk rounded up to a multiple of 8 (values past Sk are
+ * ignored).
  * workspace / workspace_bytes: as in cmpext3_attn_fwd_ws (null: no split;
  * size from cmpext3_attn_fwd_workspace_size with with_lse = 1).
  *
@@ -265,7 +270,7 @@ int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, f
  *   dq : [B, H, Sq, D]   dk, dv : [B, H_kv, Sk, D]   (all `dtype`, overwritten)
  *
  * of sum(o * dout), with the same scale, causal flag, K/V head count and
- * attention mask (same layout rules as cmpext3_attn_fwd_masked; -1 = none) as
+ * attention mask (the layout rules of cmpext3_attn_fwd_lse; -1 = none) as
  * the forward (H_kv must divide H; query head h uses K/V head h / (H / H_kv),
  * and dk, dv sum the contributions of every query head of the group).  A row
  * whose keys were all dropped passes no gradient (its dq row is zero).

@@ -166,14 +166,22 @@ def test_rejections_before_launch():
     assert _call_masked_layout(D=12) == abi.E_HEAD_DIM
     assert _call_masked_layout(q=24) == abi.E_ALIGN
     assert _call_masked_layout(strides=(512, 512, 60)) == abi.E_ALIGN
+    # masks: any layout with element-aligned rows (read element by element
+    # unless they allow runs of 8 keys), but not a misaligned element, a
+    # negative stride, or a mask without runs for the training entry points
+    assert _call_masked_layout(mask=17, mask_dtype=abi.DTYPE_F16) == abi.E_ALIGN
+    assert _call_masked_layout(mask=18, mask_dtype=abi.DTYPE_F32) == abi.E_ALIGN
+    assert _call_masked_layout(mask_str=(0, -8, 0)) == abi.E_ALIGN
+    assert _call_masked(Sk=64, lse=16, mask_str=(0, 0, 66)) == abi.E_ALIGN      # row stride % 4
 
 
-def _call_masked_layout(q=16, D=64, strides=(512, 512, 64)):
+def _call_masked_layout(q=16, D=64, strides=(512, 512, 64), mask=16, mask_dtype=abi.DTYPE_BOOL,
+                        mask_str=(0, 0, 0)):
     st = (ctypes.c_int64 * 3)(*strides)
-    ms = (ctypes.c_int64 * 3)(0, 0, 0)
+    ms = (ctypes.c_int64 * 3)(*mask_str)
     return abi.lib().cmpext3_attn_fwd_masked(ctypes.c_void_p(q), ctypes.c_void_p(16), ctypes.c_void_p(16),
                                              ctypes.c_void_p(16), abi.DTYPE_F16, 1, 1, 1, 8, 8, D, st, st,
-                                             st, st, ctypes.c_void_p(16), abi.DTYPE_BOOL, ms,
+                                             st, st, ctypes.c_void_p(mask), mask_dtype, ms,
                                              ctypes.c_float(0.125), 0, None)
 
 

@@ -114,8 +114,48 @@ def test_mask_with_grouped_query_heads():
     assert orc.max_abs_err(out.cpu(), ref) <= TOL["bf16"]
 
 
+NARROW = [
+    # dtype, B, H, Sq, Sk, D, layout
+    ("fp16", 2, 10, 256, 77, 64, "pad"),     # [B,1,1,77] bool text padding (SDXL cross-attention)
+    ("bf16", 1, 4, 100, 300, 128, "rows"),   # [1,1,Sq,300] additive bf16, rows 600 bytes apart
+    ("fp32", 2, 2, 70, 123, 40, "offset"),   # additive f32 starting one element into its buffer
+    ("fp16", 1, 2, 64, 999, 256, "pad"),     # head dim above 128
+    ("fp32", 1, 2, 40, 45, 64, "pad"),       # fp32, bool padding
+]
+
+
+def _narrow_mask(layout, dtype, B, H, Sq, Sk, seed):
+    g = torch.Generator().manual_seed(seed)
+    if layout == "pad":
+        m = torch.ones(B, 1, 1, Sk, dtype=torch.bool)
+        for b in range(B):
+            m[b, ..., Sk - 1 - (13 * (b + 1)) % Sk:] = False
+        return m.cuda()
+    if layout == "rows":
+        return (torch.randn(1, 1, Sq, Sk, generator=g) * 2).to(TDT[dtype]).cuda()
+    buf = torch.randn(Sq * Sk + 1, generator=g)
+    buf[1::5] = -math.inf
+    return buf.cuda()[1:].view(1, 1, Sq, Sk)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("case", NARROW, ids=[f"{c[0]}-{c[6]}-k{c[4]}d{c[5]}" for c in NARROW])
+def test_masks_read_in_place_element_by_element(case, causal, run_without_copies):
+    """Masks whose rows are not whole runs of 8 keys (a key count that is not
+    a multiple of 8, row strides or a base off 16 bytes) are read in place,
+    element by element: the binding makes no copy, and nothing past the last
+    key of a row is read."""
+    dtype, B, H, Sq, Sk, D, layout = case
+    q, k, v = _inputs(dtype, B, H, Sq, Sk, D, seed=Sk + D)
+    m = _narrow_mask(layout, dtype, B, H, Sq, Sk, seed=D)
+    out = run_without_copies(lambda: cmpext3.ops.attention(q, k, v, 0.1, causal, m))
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), 0.1, causal=causal, attn_mask=m.cpu())
+    assert orc.max_abs_err(out.cpu(), ref) <= TOL[dtype]
+
+
 def test_mask_layouts_that_need_a_copy():
-    """A transposed mask view and a key count that is not a multiple of 4."""
+    """A transposed mask view (key stride not 1) and a key count that is not
+    a multiple of 4."""
     q, k, v = _inputs("fp16", 1, 2, 96, 301, 64, seed=12)
     base = torch.randn(2, 301, 96, device="cuda").to(torch.float16)
     m = base.transpose(1, 2)[None]           # [1, 2, 96, 301], key stride 96

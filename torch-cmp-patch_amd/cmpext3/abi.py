@@ -127,15 +127,17 @@ def dtype_code(dtype) -> int:
             torch.bool: DTYPE_BOOL}[dtype]
 
 
-def prepare_mask(mask, B: int, H: int, Sq: int, Sk: int):
-    """attn_mask broadcast to [B,H,Sq,Sk] in the layout the C ABI takes (unit key
-    stride, other strides multiples of 4 elements, rows readable up to a multiple
-    of 8 keys, 16-byte aligned base): a view when the given tensor already fits,
-    else a compact copy with rows zero-padded to a multiple of 8."""
+def prepare_mask(mask, B: int, H: int, Sq: int, Sk: int, runs: bool = False):
+    """attn_mask broadcast to [B,H,Sq,Sk] in a layout the C ABI takes: a view
+    when the given tensor has a unit key stride (inference calls read any
+    other layout element by element), else a compact copy.  runs=True (the
+    training entry points) also needs rows readable in runs of 8 keys: other
+    strides multiples of 4 elements, Sk a multiple of 8, 16-byte aligned
+    base; the copy's rows are zero-padded to a multiple of 8."""
     import torch
     m = mask.expand(B, H, Sq, Sk)
-    fits = (m.stride(3) == 1 and Sk % 8 == 0 and all(m.stride(i) % 4 == 0 for i in range(3))
-            and m.data_ptr() % 16 == 0)
+    fits = m.stride(3) == 1 and (not runs or (Sk % 8 == 0 and all(m.stride(i) % 4 == 0 for i in range(3))
+                                              and m.data_ptr() % 16 == 0))
     if not fits:
         cb, ch, cq = (1 if m.stride(0) == 0 else B), (1 if m.stride(1) == 0 else H), \
                      (1 if m.stride(2) == 0 else Sq)
@@ -224,11 +226,11 @@ def _handle(t, stream):
     return stream if isinstance(stream, int) else stream.cuda_stream
 
 
-def _mask_args(attn_mask, B, H, Sq, Sk):
+def _mask_args(attn_mask, B, H, Sq, Sk, runs=False):
     """(pointer, dtype code, strides, keep-alive tensor) for an optional mask."""
     if attn_mask is None:
         return ctypes.c_void_p(0), -1, (ctypes.c_int64 * 3)(0, 0, 0), None
-    m = prepare_mask(attn_mask, B, H, Sq, Sk)
+    m = prepare_mask(attn_mask, B, H, Sq, Sk, runs)
     return (ctypes.c_void_p(m.data_ptr()), dtype_code(m.dtype),
             (ctypes.c_int64 * 3)(m.stride(0), m.stride(1), m.stride(2)), m)
 
@@ -244,7 +246,7 @@ def attn_fwd_lse(q, k, v, scale: Optional[float] = None, causal: bool = False, s
     lse = torch.empty(B, H, Sq, dtype=torch.float32, device=q.device)
     if scale is None:
         scale = D ** -0.5
-    mp, mdt, mst, _keep = _mask_args(attn_mask, B, H, Sq, k.shape[2])
+    mp, mdt, mst, _keep = _mask_args(attn_mask, B, H, Sq, k.shape[2], runs=True)
     handle = _handle(q, stream)
     wp, wb = workspace_for(q, handle, workspace_size(dtype_code(q.dtype), B, H, k.shape[1], Sq,
                                                      k.shape[2], D, mdt, causal, with_lse=True))
@@ -264,7 +266,7 @@ def attn_bwd_raw(q, k, v, o, do, lse, dq, dk, dv, delta, scale: float, causal: b
     """Call cmpext3_attn_bwd on caller-allocated tensors; returns the C code."""
     B, H, Sq, D = q.shape
     vp = ctypes.c_void_p
-    mp, mdt, mst, _keep = _mask_args(attn_mask, B, H, Sq, k.shape[2])
+    mp, mdt, mst, _keep = _mask_args(attn_mask, B, H, Sq, k.shape[2], runs=True)
     return lib().cmpext3_attn_bwd(
         *(vp(t.data_ptr()) for t in (q, k, v, o, do, lse, dq, dk, dv, delta)),
         dtype_code(q.dtype), B, H, k.shape[1], Sq, k.shape[2], D,

@@ -57,20 +57,22 @@ bool aligned_to(const void* ptr, int es) { return ((uintptr_t)ptr % (uintptr_t)e
 // rows of whole 16-byte chunks (the pipelined, short-key and training kernels)
 bool whole_chunks(int dtype, int D) { return D % (16 / elem_size(dtype)) == 0; }
 
-// attention-mask arguments (mask_dtype -1 = none): CMPEXT3_OK or an error code
-int check_mask(const void* mask, int mask_dtype, const int64_t mask_str[3], int dtype, int D, int Sq, int Sk) {
+// attention-mask arguments (mask_dtype -1 = none): CMPEXT3_OK or an error code.
+// Every dtype and head dim takes a mask (causal or not; the rows of Q, K, V
+// and O must then be whole aligned 16-byte chunks, checked by the caller).
+// The kernels read a mask in runs of 8 keys when its base is 16-byte aligned
+// and its strides are multiples of 4 elements (*runs_ok); the inference entry
+// points read any other element-aligned layout element by element.
+int check_mask(const void* mask, int mask_dtype, const int64_t mask_str[3], int Sq, int Sk, bool* runs_ok) {
+  *runs_ok = true;
   if (mask_dtype == -1) return CMPEXT3_OK;
   if (mask_dtype < CMPEXT3_DTYPE_F16 || mask_dtype > CMPEXT3_DTYPE_BOOL) return CMPEXT3_E_DTYPE;
   if (!mask || !mask_str) return CMPEXT3_E_INVALID;
-  // every dtype and head dim takes a mask (causal or not); the rows of Q, K,
-  // V and O must then be whole aligned 16-byte chunks (checked by the caller)
-  (void)dtype;
-  (void)D;
-  // every 8-key run of a row is one aligned 8/16/32-byte load
-  if (((uintptr_t)mask & 15u) != 0) return CMPEXT3_E_ALIGN;
-  for (int i = 0; i < 3; ++i)
-    if (mask_str[i] < 0 || mask_str[i] % 4 != 0) return CMPEXT3_E_ALIGN;
   const int mes = mask_dtype == CMPEXT3_DTYPE_BOOL ? 1 : mask_dtype == CMPEXT3_DTYPE_F32 ? 4 : 2;
+  if (((uintptr_t)mask % (uintptr_t)mes) != 0) return CMPEXT3_E_ALIGN;
+  for (int i = 0; i < 3; ++i)
+    if (mask_str[i] < 0) return CMPEXT3_E_ALIGN;
+  *runs_ok = ((uintptr_t)mask & 15u) == 0 && mask_str[0] % 4 == 0 && mask_str[1] % 4 == 0 && mask_str[2] % 4 == 0;
   if (((int64_t)(Sq - 1) * mask_str[2] + Sk + 64) * mes >= INT32_MAX) return CMPEXT3_E_TOO_LARGE;
   return CMPEXT3_OK;
 }
@@ -203,8 +205,14 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
   if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;
   if (H_kv < 1 || H_kv > H || H % H_kv != 0) return CMPEXT3_E_INVALID;
   const bool masked = mask_dtype != -1;
-  rc = check_mask(mask, mask_dtype, mask_str, dtype, D, Sq, Sk);
+  bool runs_ok = true;
+  rc = check_mask(mask, mask_dtype, mask_str, Sq, Sk, &runs_ok);
   if (rc != CMPEXT3_OK) return rc;
+  // The training forward's mask is the backward's too: runs of 8 keys, rows
+  // readable up to Sk rounded up to 8 (the caller pads them).  Inference
+  // calls read runs only where every row ends on a whole run.
+  if (lse && !runs_ok) return CMPEXT3_E_ALIGN;
+  const bool narrow_mask = !lse && (!runs_ok || Sk % 8 != 0);
   if (!q || !k || !v || !o || !q_str || !k_str || !v_str || !o_str) return CMPEXT3_E_INVALID;
   if (!isfinite(scale)) return CMPEXT3_E_INVALID;
   if (workspace && !aligned16(workspace)) return CMPEXT3_E_ALIGN;
@@ -246,6 +254,7 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
     p.mask = mask;
     p.m_b = mask_str[0]; p.m_h = mask_str[1]; p.m_q = mask_str[2];
     p.mask_kind = mask_kind_of(mask_dtype);
+    p.mask_narrow = narrow_mask ? 1 : 0;
   }
   // exp2-domain multiplier; a negative scale is folded into Q's sign bits
   p.c = fabsf(scale) * cmpext3::kLog2e;
@@ -397,8 +406,10 @@ int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
   if (dtype == CMPEXT3_DTYPE_F32 || D > 128) return CMPEXT3_E_TRAINING;
   if (!whole_chunks(dtype, D)) return CMPEXT3_E_HEAD_DIM;
   if (H_kv < 1 || H_kv > H || H % H_kv != 0) return CMPEXT3_E_INVALID;
-  rc = check_mask(mask, mask_dtype, mask_str, dtype, D, Sq, Sk);
+  bool runs_ok = true;
+  rc = check_mask(mask, mask_dtype, mask_str, Sq, Sk, &runs_ok);
   if (rc != CMPEXT3_OK) return rc;
+  if (!runs_ok) return CMPEXT3_E_ALIGN;  // the backward reads runs of 8 keys
   if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv || !delta) return CMPEXT3_E_INVALID;
   if (!q_str || !k_str || !v_str || !o_str || !do_str || !dq_str || !dk_str || !dv_str)
     return CMPEXT3_E_INVALID;

@@ -37,6 +37,11 @@ struct FwdParams {
   const void* mask;
   int64_t m_b, m_h, m_q;
   int mask_kind;
+  // the mask is read element by element, nothing past key Sk - 1 of a row
+  // (any layout with unit key stride); otherwise in runs of 8 keys, every
+  // row readable up to Sk rounded up to 8 (16-byte aligned base, strides a
+  // multiple of 4 elements, Sk a multiple of 8)
+  int mask_narrow;
   // optional [B*H, Sq] fp32 output: natural-log log-sum-exp of each query
   // row's scale * Q K^T over its visible keys (what a backward pass needs to
   // rebuild P); null = not written.  Written by the pipelined kernel only.

@@ -113,11 +113,27 @@ __device__ __forceinline__ uint2 lds_tr16_b64(const uint16_t* p) {
 
 // Attention mask (FwdParams::mask) of 8 consecutive keys of one query row,
 // applied to the exp2-domain scores sc[r0 .. r0 + 7]: a zero bool removes
-// the key (-inf), float kinds are added times log2(e).  One 8-, 16- or
-// 32-byte read at byte offset `off` of the mask buffer (reads past its end
-// return zero).
+// the key (-inf), float kinds are added times log2(e).  `off` is the byte
+// offset of the first key in the mask buffer (reads past its end return
+// zero).  One 8-, 16- or 32-byte read, or (narrow) one read per element.
 __device__ __forceinline__ void mask_run8(f32x16& sc, int r0, const __amdgpu_buffer_rsrc_t& mrs, int off,
-                                          int kind) {
+                                          int kind, bool narrow) {
+  if (narrow) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (kind == MASK_BOOL) {
+        if (__builtin_amdgcn_raw_buffer_load_b8(mrs, off + i, 0, 0) == 0) sc[r0 + i] = -INFINITY;
+      } else if (kind == MASK_F32) {
+        const float a = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(mrs, off + 4 * i, 0, 0));
+        sc[r0 + i] = __builtin_fmaf(a, kLog2e, sc[r0 + i]);
+      } else {
+        const uint32_t hb = __builtin_amdgcn_raw_buffer_load_b16(mrs, off + 2 * i, 0, 0);
+        const float a = kind == MASK_F16 ? (float)__builtin_bit_cast(_Float16, (uint16_t)hb) : __uint_as_float(hb << 16);
+        sc[r0 + i] = __builtin_fmaf(a, kLog2e, sc[r0 + i]);
+      }
+    }
+    return;
+  }
   if (kind == MASK_BOOL) {
     const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(mrs, off, 0, 0));
 #pragma unroll
@@ -139,6 +155,12 @@ __device__ __forceinline__ void mask_run8(f32x16& sc, int r0, const __amdgpu_buf
       sc[r0 + 2 * i + 1] = __builtin_fmaf(a[1], kLog2e, sc[r0 + 2 * i + 1]);
     }
   }
+}
+
+// Bytes of the mask buffer of one (batch, head) that a kernel may read: up
+// to key Sk - 1 of the last row (narrow), or up to Sk rounded up to 8.
+__device__ __forceinline__ int64_t mask_span(const FwdParams& p, int mes) {
+  return ((int64_t)(p.Sq - 1) * p.m_q + (p.mask_narrow ? p.Sk : (p.Sk + 7) / 8 * 8)) * mes;
 }
 
 constexpr float kSumHi = 256.0f;         // tile row sum above this: offset must rise
@@ -376,13 +398,13 @@ attn_fwd_mfma16(const FwdParams p, const SplitArgs sa) {
     }
 
   // attention mask (MASK): a lane's 16 keys per 32-key block are 2 runs of 8
-  // consecutive keys (acc_key), one read each; rows past Sq read the last
-  // row (their output is never stored), which is readable up to Sk rounded
-  // up to 8 (the ABI's contract); keys at or past Sk are masked afterwards
+  // consecutive keys (acc_key), one read each (mask_run8); rows past Sq read
+  // the last row (their output is never stored); reads past the readable span
+  // (mask_span) return zero and keys at or past Sk are masked afterwards
   const int mes = p.mask_kind == MASK_BOOL ? 1 : p.mask_kind == MASK_F32 ? 4 : 2;
   const __amdgpu_buffer_rsrc_t mrs =
       uniform_rsrc(MASK ? (const void*)((const char*)p.mask + (b * p.m_b + h * p.m_h) * mes) : p.q,
-                   MASK ? ((int64_t)(Sq - 1) * p.m_q + (Sk + 7) / 8 * 8) * mes : 0);
+                   MASK ? mask_span(p, mes) : 0);
   int mrow_off[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb)
@@ -433,7 +455,7 @@ attn_fwd_mfma16(const FwdParams p, const SplitArgs sa) {
 #pragma unroll
             for (int run = 0; run < 2; ++run)
               mask_run8(sacc[kb], 8 * run, mrs, mrow_off[qb] + (k0 + 32 * kb + 16 * run + 8 * hh) * mes,
-                        p.mask_kind);
+                        p.mask_kind, p.mask_narrow);
         }
         if (need_mask) {
 #pragma unroll

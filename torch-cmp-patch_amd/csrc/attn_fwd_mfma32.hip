@@ -174,13 +174,14 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
   };
 
   // attention mask rows (MASK): rows past Sq read the last row (their output
-  // is never stored); the last row is readable up to Sk rounded up to 8 (the
-  // ABI's contract), reads past it return zero, and keys at or past Sk are
+  // is never stored); the (batch, head)'s mask is readable up to key Sk - 1
+  // of its last row (a narrow mask, read element by element) or up to Sk
+  // rounded up to 8; reads past that return zero, and keys at or past Sk are
   // masked by the key-range rule anyway
   const int mes = p.mask_kind == MASK_BOOL ? 1 : p.mask_kind == MASK_F32 ? 4 : 2;
   const __amdgpu_buffer_rsrc_t mrs =
       uniform_rsrc(MASK ? (const void*)((const char*)p.mask + (b * p.m_b + h * p.m_h) * mes) : p.q,
-                   MASK ? ((int64_t)(Sq - 1) * p.m_q + (Sk + 7) / 8 * 8) * mes : 0);
+                   MASK ? ((int64_t)(Sq - 1) * p.m_q + (p.mask_narrow ? Sk : (Sk + 7) / 8 * 8)) * mes : 0);
   int mrow[NQB];
 #pragma unroll
   for (int qb = 0; qb < NQB; ++qb)
@@ -225,7 +226,22 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
             // the lane's 4 consecutive keys: one 4/8/16-byte mask read
             f32x4 madd = {0.f, 0.f, 0.f, 0.f};
             uint32_t keep = 0x01010101u;
-            if (MASK) {
+            if (MASK && p.mask_narrow) {
+              const int key4 = k0 + 16 * kb + 4 * g;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int off = mrow[qb] + (key4 + r) * mes;
+                if (p.mask_kind == MASK_BOOL) {
+                  if (__builtin_amdgcn_raw_buffer_load_b8(mrs, off, 0, 0) == 0) keep &= ~(0xffu << (8 * r));
+                } else if (p.mask_kind == MASK_F32) {
+                  madd[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(mrs, off, 0, 0));
+                } else {
+                  const uint32_t hb = __builtin_amdgcn_raw_buffer_load_b16(mrs, off, 0, 0);
+                  madd[r] = p.mask_kind == MASK_F16 ? (float)__builtin_bit_cast(_Float16, (uint16_t)hb)
+                                                    : __uint_as_float(hb << 16);
+                }
+              }
+            } else if (MASK) {
               const int key4 = k0 + 16 * kb + 4 * g;
               if (p.mask_kind == MASK_BOOL) {
                 keep = __builtin_amdgcn_raw_buffer_load_b32(mrs, mrow[qb] + key4, 0, 0);

@@ -454,15 +454,15 @@ __device__ __forceinline__ void pipe16_segment(const FwdParams& p, const SplitAr
   };
   // attention mask of tile j added to (bool: applied to) exp2-domain scores.
   // A lane's 16 keys per 32-key block are 2 runs of 8 consecutive keys
-  // (acc_key: 16j + 8hh + 0..7), so each run is one 8/16/32-byte read; rows
-  // past Sq use the last row (their output is never stored).  The last row is
-  // readable up to Sk rounded up to 8 (the ABI's contract); reads past that
-  // return zero, and every key at or past Sk is masked by the key-range rule
-  // afterwards.
+  // (acc_key: 16j + 8hh + 0..7), so each run is one 8/16/32-byte read (or
+  // one read per element for a narrow mask: mask_run8); rows past Sq use the
+  // last row (their output is never stored).  Reads past the mask's readable
+  // span (mask_span) return zero, and every key at or past Sk is masked by
+  // the key-range rule afterwards.
   const int mes = p.mask_kind == MASK_BOOL ? 1 : p.mask_kind == MASK_F32 ? 4 : 2;
   const __amdgpu_buffer_rsrc_t mrs =
       uniform_rsrc(MASK ? (const void*)((const char*)p.mask + (b * p.m_b + h * p.m_h) * mes) : p.q,
-                   MASK ? ((int64_t)(Sq - 1) * p.m_q + (Sk + 7) / 8 * 8) * mes : 0);
+                   MASK ? mask_span(p, mes) : 0);
   const int mrow_off = MASK ? (int)((int64_t)min(qrow, Sq - 1) * p.m_q * mes) : 0;
   auto add_mask = [&](int j, f32x16 (&sc)[NKB]) {
     const int k0 = (tbase + j) * BK;
@@ -470,7 +470,8 @@ __device__ __forceinline__ void pipe16_segment(const FwdParams& p, const SplitAr
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int run = 0; run < 2; ++run)  // keys k0 + 32 kb + 16 run + 8 hh .. + 7
-        mask_run8(sc[kb], 8 * run, mrs, mrow_off + (k0 + 32 * kb + 16 * run + 8 * hh) * mes, p.mask_kind);
+        mask_run8(sc[kb], 8 * run, mrs, mrow_off + (k0 + 32 * kb + 16 * run + 8 * hh) * mes, p.mask_kind,
+                  p.mask_narrow);
   };
   // this lane's half of the row max (the two halves meet at the decision)
   auto row_max = [&](const f32x16 (&sc)[NKB]) {

@@ -120,9 +120,11 @@ int launch(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& 
 
 // torch's attn_mask broadcast to [B,H,Sq,Sk]; copied into a compact buffer
 // (broadcast dims kept at size 1, rows padded to a multiple of 8 keys) when
-// its layout does not fit the ABI.
+// its layout does not fit the ABI.  Inference calls (runs == false) need
+// only a unit key stride: the ABI reads any other layout element by element.
+// Training calls (runs == true) need rows readable in runs of 8 keys.
 Mask prepare_mask(const torch::Tensor& m0, const torch::Tensor& query, int64_t B, int64_t H,
-                  int64_t Sq, int64_t Sk) {
+                  int64_t Sq, int64_t Sk, bool runs) {
   TORCH_CHECK(m0.device() == query.device(), "cmpext3 attention: attn_mask on another device");
   TORCH_CHECK(m0.dim() <= 4, "cmpext3 attention: attn_mask has more than 4 dims");
   Mask mk;
@@ -136,8 +138,9 @@ Mask prepare_mask(const torch::Tensor& m0, const torch::Tensor& query, int64_t B
   torch::Tensor m = m0.expand({B, H, Sq, Sk});
   // in place only if rows can be read in runs of 8 keys without leaving the
   // tensor: unit key stride and Sk a multiple of 8
-  const bool fits = m.stride(3) == 1 && Sk % 8 == 0 && m.stride(0) % 4 == 0 && m.stride(1) % 4 == 0 &&
-                    m.stride(2) % 4 == 0 && ((uintptr_t)m.data_ptr() & 15u) == 0;
+  const bool fits = m.stride(3) == 1 &&
+                    (!runs || (Sk % 8 == 0 && m.stride(0) % 4 == 0 && m.stride(1) % 4 == 0 &&
+                               m.stride(2) % 4 == 0 && ((uintptr_t)m.data_ptr() & 15u) == 0));
   if (!fits) {
     const int64_t cb = m.stride(0) == 0 ? 1 : B, ch = m.stride(1) == 0 ? 1 : H;
     const int64_t cq = m.stride(2) == 0 ? 1 : Sq, skp = (Sk + 7) / 8 * 8;
@@ -210,7 +213,7 @@ torch::Tensor attention(torch::Tensor query, torch::Tensor key, torch::Tensor va
 
   Mask mask;
   if (attn_mask.has_value() && attn_mask->defined()) {
-    mask = prepare_mask(*attn_mask, query, B, H, Sq, Sk);
+    mask = prepare_mask(*attn_mask, query, B, H, Sq, Sk, false);
   }
 
   torch::Tensor out = is_bshd_view(query)
@@ -310,7 +313,7 @@ std::vector<torch::Tensor> attention_fwd_lse(torch::Tensor query, torch::Tensor 
   Mask mask;
   int64_t ms[3] = {0, 0, 0};
   if (attn_mask.has_value() && attn_mask->defined()) {
-    mask = prepare_mask(*attn_mask, query, B, H, Sq, Sk);
+    mask = prepare_mask(*attn_mask, query, B, H, Sq, Sk, true);
     strides3(mask.t, ms);
   }
   const torch::Tensor q = abi_layout(query, Dp), k = abi_layout(key, Dp), v = abi_layout(value, Dp);
@@ -369,7 +372,7 @@ std::vector<torch::Tensor> attention_bwd(torch::Tensor query, torch::Tensor key,
     Mask mask;
     int64_t ms[3] = {0, 0, 0};
     if (attn_mask.has_value() && attn_mask->defined()) {
-      mask = prepare_mask(*attn_mask, query, B, H, Sq, Sk);
+      mask = prepare_mask(*attn_mask, query, B, H, Sq, Sk, true);
       strides3(mask.t, ms);
     }
     int64_t qs[3], ks[3], vs[3], os[3], gs[3], dqs[3], dks[3], dvs[3];
