@@ -146,7 +146,8 @@ __global__ __launch_bounds__(kDecNw * 64, 1) void attn_fwd_decode16(FwdParams p,
   static_assert(DK % 32 == 0 && DK >= 64 && DK <= 256, "head dim");
   static_assert(BLK % 1024 == 0, "a block is whole DMA instructions");
   static_assert(2 * IB * (NS - 1) <= 63, "vmcnt range");
-  static_assert(kDecNw * kDecRows * DK * 4 + 2 * kDecNw * kDecRows * 4 + 16 <= kDecNw * NS * STAGE,
+  constexpr int MOS = DK + 4;           // row stride (floats) of the waves' merge rows
+  static_assert(kDecNw * kDecRows * MOS * 4 + 2 * kDecNw * kDecRows * 4 + 16 <= kDecNw * NS * STAGE,
                 "the workgroup's merge fits in the ring's LDS");
   static_assert(2 * kDecRows * kDecMaxParts * 4 + 16 + kDecNw * 64 * 16 <= kDecNw * NS * STAGE,
                 "the parts' merge fits in the ring's LDS");
@@ -294,11 +295,13 @@ __global__ __launch_bounds__(kDecNw * 64, 1) void attn_fwd_decode16(FwdParams p,
   lrow += shfl_xor_f(lrow, 32);
   wait_vmcnt<0>();
   lds_barrier();  // every wave is done with its ring
+  // (rows 16 bytes apart mod 128: the 16-byte writes of 8 rows per LDS pass
+  // land on distinct banks)
   float* mo = (float*)lds;
-  float* mm = mo + kDecNw * kDecRows * DK;
+  float* mm = mo + kDecNw * kDecRows * MOS;
   float* ml = mm + kDecNw * kDecRows;
 #pragma unroll
-  for (int db = 0; db < NDB; ++db) *(f32x4*)(mo + (wave * kDecRows + c) * DK + 16 * db + 4 * g) = oacc[db];
+  for (int db = 0; db < NDB; ++db) *(f32x4*)(mo + (wave * kDecRows + c) * MOS + 16 * db + 4 * g) = oacc[db];
   if (g == 0) {
     mm[wave * kDecRows + c] = m_run;
     ml[wave * kDecRows + c] = lrow;
@@ -331,7 +334,7 @@ __global__ __launch_bounds__(kDecNw * 64, 1) void attn_fwd_decode16(FwdParams p,
     for (int w = 0; w < kDecNw; ++w) {
       const float f = mw[w] == -INFINITY ? 0.f : fast_exp2(mw[w] - mx);  // a wave without tiles: 0
       l = __builtin_fmaf(ml[w * kDecRows + r], f, l);
-      o += *(const f32x4*)(mo + (w * kDecRows + r) * DK + 4 * k) * f;
+      o += *(const f32x4*)(mo + (w * kDecRows + r) * MOS + 4 * k) * f;
     }
     if (nparts == 1) {
       store_out(r, k, o, 1.f / l);
