@@ -28,8 +28,10 @@ gradient within that fraction of its own largest oracle magnitude (floor
 each group.
 
 Contract the draws stay inside (include/cmpext3_attn.h): any head dim 1..256
-and element-aligned strides for the unmasked entry points; masks only for
-fp16/bf16 with D <= 128 in whole 16-byte chunks.
+and element-aligned strides for the unmasked entry points; masks for every
+dtype and head dim with rows in whole 16-byte chunks (the masks themselves in
+any layout with unit key stride: key counts that are not a multiple of 8 are
+read element by element).
 """
 from __future__ import annotations
 
@@ -72,7 +74,7 @@ def _draw(rng):
     scale = None if r < 0.5 else 0.0 if r < 0.55 else float(rng.uniform(-0.3, 0.6))
     layout = str(rng.choice(["bhsd", "bshd", "offset"], p=[0.45, 0.35, 0.2]))
     mask = "none"
-    if dtype != "fp32" and D <= 128 and D % 8 == 0 and layout != "offset" and rng.random() < 0.35:
+    if D % (4 if dtype == "fp32" else 8) == 0 and layout != "offset" and rng.random() < 0.35:
         mask = str(rng.choice(["bool_keys", "bool_full", "add_heads", "add_f32"]))
     while B * H * Sq * Sk * D > MAX_WORK:
         if Sq > 64:
