@@ -63,8 +63,8 @@ extern "C" {
 #define CMPEXT3_OK                 0
 #define CMPEXT3_E_INVALID          1  /* null pointer, negative size, bad stride */
 #define CMPEXT3_E_DTYPE            2  /* dtype code not one of the above */
-#define CMPEXT3_E_HEAD_DIM         3  /* D outside 1..256; masked/training calls: D not a multiple of 8 (f16/bf16) / 4 (f32) */
-#define CMPEXT3_E_ALIGN            4  /* a pointer not element-aligned; masked/training calls: base pointer or row stride not 16-byte aligned */
+#define CMPEXT3_E_HEAD_DIM         3  /* D outside 1..256; training calls: D not a multiple of 8 (f16/bf16); masked calls: D odd (f16/bf16) or not a multiple of 4 (f32) */
+#define CMPEXT3_E_ALIGN            4  /* a pointer not element-aligned; training and fp32 masked calls: base pointer or row stride not 16-byte aligned; f16/bf16 masked calls: not 4-byte aligned */
 #define CMPEXT3_E_EMPTY_KEYS       5  /* Sk == 0 with Sq > 0: softmax over nothing */
 #define CMPEXT3_E_LAUNCH           6  /* the HIP launch itself failed */
 #define CMPEXT3_E_TOO_LARGE        7  /* a size does not fit the kernel's index arithmetic */
@@ -139,9 +139,10 @@ int cmpext3_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o,
  * A query row whose keys are all dropped gives zeros (torch's result).
  * With causal != 0 a pair is used only if it is causally visible AND the
  * mask keeps it (torch's rule for attn_mask with is_causal).  Supported for
- * every dtype (f16, bf16, f32) and head dim, with the rows of q/k/v/o in
- * whole 16-byte chunks at 16-byte aligned addresses (else CMPEXT3_E_ALIGN or
- * CMPEXT3_E_HEAD_DIM, nothing launched).
+ * every dtype (f16, bf16, f32) and head dim; the rows of q/k/v/o must be
+ * whole 16-byte chunks at 16-byte aligned addresses for f32, and 4-byte
+ * aligned (even D, base pointers and row strides) for f16/bf16 (else
+ * CMPEXT3_E_ALIGN or CMPEXT3_E_HEAD_DIM, nothing launched).
  *
  * Reference: the reference never ran masks natively: _patched_sdpa sends
  * any attn_mask to stock torch (cmpext3/__init__.py:624).

@@ -150,7 +150,7 @@ def _call(q=16, k=16, v=16, o=16, dtype=abi.DTYPE_F16, B=1, H=1, Sq=8, Sk=8, D=6
 
 # Fake device addresses: every case below must be rejected before any launch.
 # (Odd head dims and 2-byte aligned rows are accepted by the unmasked entry
-# points, so they appear here only with a mask, which needs whole chunks.)
+# points, so they appear here only with a mask, which needs 4-byte pieces.)
 def test_rejections_before_launch():
     assert _call(dtype=5) == abi.E_DTYPE
     assert _call(B=-1) == abi.E_INVALID
@@ -163,9 +163,11 @@ def test_rejections_before_launch():
     assert _call(strides=(512, 512, -64)) == abi.E_INVALID
     assert _call(scale=float("inf")) == abi.E_INVALID
     assert _call(scale=float("nan")) == abi.E_INVALID
-    assert _call_masked_layout(D=12) == abi.E_HEAD_DIM
-    assert _call_masked_layout(q=24) == abi.E_ALIGN
-    assert _call_masked_layout(strides=(512, 512, 60)) == abi.E_ALIGN
+    # masked f16/bf16 calls run rows of 4- or 8-byte pieces in place; 2-byte
+    # pieces (odd head dim, pointer or stride) are refused
+    assert _call_masked_layout(D=13) == abi.E_HEAD_DIM
+    assert _call_masked_layout(q=18) == abi.E_ALIGN
+    assert _call_masked_layout(strides=(512, 512, 61)) == abi.E_ALIGN
     # masks: any layout with element-aligned rows (read element by element
     # unless they allow runs of 8 keys), but not a misaligned element, a
     # negative stride, or a mask without runs for the training entry points

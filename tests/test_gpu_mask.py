@@ -153,6 +153,27 @@ def test_masks_read_in_place_element_by_element(case, causal, run_without_copies
     assert orc.max_abs_err(out.cpu(), ref) <= TOL[dtype]
 
 
+NARROW_ROWS = [
+    # dtype, B, H, Sq, Sk, D: rows of 4- or 8-byte pieces, not whole 16-byte chunks
+    ("fp16", 2, 3, 150, 500, 100),   # 200-byte rows: 8-byte pieces, pipelined kernel
+    ("bf16", 1, 4, 96, 333, 70),     # 140-byte rows: 4-byte pieces
+    ("fp16", 1, 2, 80, 700, 132),    # above 128: the wide kernel's narrow rows
+]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("case", NARROW_ROWS, ids=[f"{c[0]}-d{c[5]}" for c in NARROW_ROWS])
+def test_masked_rows_of_narrow_pieces_run_in_place(case, causal, run_without_copies):
+    """Masked f16/bf16 calls whose head dim is not whole 16-byte chunks run on
+    the narrow-row kernels in place (no padded copy of Q, K, V or O)."""
+    dtype, B, H, Sq, Sk, D = case
+    q, k, v = _inputs(dtype, B, H, Sq, Sk, D, seed=D + Sk)
+    m = _mask("bool_full", dtype, B, H, Sq, Sk, seed=D)
+    out = run_without_copies(lambda: cmpext3.ops.attention(q, k, v, 0.09, causal, m))
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), 0.09, causal=causal, attn_mask=m.cpu())
+    assert orc.max_abs_err(out.cpu(), ref) <= TOL[dtype]
+
+
 def test_mask_layouts_that_need_a_copy():
     """A transposed mask view (key stride not 1) and a key count that is not
     a multiple of 4."""

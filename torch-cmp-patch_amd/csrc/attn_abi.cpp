@@ -131,11 +131,11 @@ const char* cmpext3_attn_strerror(int code) {
     case CMPEXT3_E_INVALID: return "invalid argument (null pointer, negative size or stride)";
     case CMPEXT3_E_DTYPE: return "unsupported dtype (expected f16, bf16 or f32)";
     case CMPEXT3_E_HEAD_DIM:
-      return "unsupported head dim (need 1..256; masked and training calls need a multiple of 8 for f16/bf16, "
-             "4 for f32)";
+      return "unsupported head dim (need 1..256; training calls and fp32 masked calls need a multiple of 8 for "
+             "f16/bf16, 4 for f32; f16/bf16 masked calls an even head dim)";
     case CMPEXT3_E_ALIGN:
-      return "misaligned tensor (pointers must be element-aligned; masked and training calls need 16-byte "
-             "aligned base pointers and row strides)";
+      return "misaligned tensor (pointers must be element-aligned; training calls and fp32 masked calls need "
+             "16-byte aligned base pointers and row strides, f16/bf16 masked calls 4-byte aligned ones)";
     case CMPEXT3_E_EMPTY_KEYS: return "key/value sequence is empty";
     case CMPEXT3_E_LAUNCH: return "HIP kernel launch failed";
     case CMPEXT3_E_TOO_LARGE: return "problem too large for 32-bit tile indexing";
@@ -229,7 +229,10 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
   // row length.  Those exist for unmasked inference only.
   const int piece = piece_bytes(q, k, v, o, D, es, q_str, k_str, v_str, o_str, B, H, H_kv, Sq, Sk);
   const bool chunks = piece == 16;
-  if (!chunks && (masked || lse)) return whole_chunks(dtype, D) ? CMPEXT3_E_ALIGN : CMPEXT3_E_HEAD_DIM;
+  // Training calls need whole aligned chunks; masked ones also run on 4- or
+  // 8-byte pieces of f16/bf16 rows (fp32 and 2-byte pieces: whole chunks).
+  const bool mask_rows_ok = !masked || chunks || (dtype != CMPEXT3_DTYPE_F32 && piece >= 4);
+  if ((!chunks && lse) || !mask_rows_ok) return whole_chunks(dtype, D) ? CMPEXT3_E_ALIGN : CMPEXT3_E_HEAD_DIM;
   // the fp16/bf16 kernel addresses one K/V tile with 32-bit element offsets
   if (dtype != CMPEXT3_DTYPE_F32 &&
       (k_str[2] * 64 + 256 > INT32_MAX || v_str[2] * 64 + 256 > INT32_MAX))
@@ -288,7 +291,8 @@ int plan_impl(int dtype, int B, int H, int H_kv, int Sq, int Sk, int D, int mask
   if (with_lse && (dtype == CMPEXT3_DTYPE_F32 || D > 128)) return CMPEXT3_E_TRAINING;
   if (mask_dtype != -1 && (mask_dtype < CMPEXT3_DTYPE_F16 || mask_dtype > CMPEXT3_DTYPE_BOOL))
     return CMPEXT3_E_DTYPE;
-  if ((mask_dtype != -1 || with_lse) && elem != 0) return CMPEXT3_E_ALIGN;
+  if (elem != 0 && (with_lse || (mask_dtype != -1 && (dtype == CMPEXT3_DTYPE_F32 || elem < 4))))
+    return CMPEXT3_E_ALIGN;
   cmpext3::FwdParams p;
   memset(&p, 0, sizeof p);
   const int64_t rs = elem ? D : (D + 7) / 8 * 8;  // element row stride of the dry run's layout

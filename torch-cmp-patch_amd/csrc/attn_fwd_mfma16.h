@@ -202,7 +202,6 @@ attn_fwd_mfma16(const FwdParams p, const SplitArgs sa) {
   constexpr bool SWZ = (OPT & 2) && (DK == DP) && (DK == 32 || DK == 64 || DK == 128);
   constexpr bool ELEM = (OPT & 64) != 0;
   constexpr bool MASK = (OPT & 16) != 0;
-  static_assert(!(ELEM && MASK), "masked launches have whole 16-byte chunks");
   constexpr int RSK = SWZ ? DK : DK + 8;  // K tile row stride (halves)
   constexpr int RSV = SWZ ? DP : DP + 8;  // V tile row stride (halves)
   constexpr int KTILE = BK * RSK;

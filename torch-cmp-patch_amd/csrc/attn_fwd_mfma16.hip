@@ -56,13 +56,14 @@ hipError_t launch_bucket(const FwdParams& p, int dk, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
-// attention-masked launches (OPT bit 16) of the head dims above 128
-template <typename T, bool CAUSAL, bool PRESCALE>
+// attention-masked launches (OPT bit 16) of the head dims above 128; EOPT 64:
+// narrow rows
+template <typename T, bool CAUSAL, bool PRESCALE, int EOPT = 0>
 hipError_t launch_masked(const FwdParams& p, int dk, hipStream_t s) {
   switch (dk) {
-    case 160: return launch_dk<T, 160, CAUSAL, PRESCALE, 16>(p, s);
-    case 192: return launch_dk<T, 192, CAUSAL, PRESCALE, 16>(p, s);
-    case 256: return launch_dk<T, 256, CAUSAL, PRESCALE, 16>(p, s);
+    case 160: return launch_dk<T, 160, CAUSAL, PRESCALE, 16 | EOPT>(p, s);
+    case 192: return launch_dk<T, 192, CAUSAL, PRESCALE, 16 | EOPT>(p, s);
+    case 256: return launch_dk<T, 256, CAUSAL, PRESCALE, 16 | EOPT>(p, s);
   }
   return hipErrorInvalidValue;
 }
@@ -106,12 +107,20 @@ hipError_t launch_mfma16(const FwdParams& p0, bool bf16, bool causal, hipStream_
                     !((!p0.elem_rows || p0.elem_rows >= 4) && pipe16_applies(p0, dk));
   if (pack) pack_query_heads(p);
   if (p.elem_rows) {
-    // narrow rows (unmasked inference only; the ABI sends masked and training
-    // calls here only with whole aligned chunks): 4- or 8-byte pieces on the
-    // pipelined kernel where it applies, else this kernel in any piece size
-    if (p.lse || p.mask_kind != MASK_NONE) return hipErrorNotSupported;
+    // narrow rows (inference; the ABI sends training calls here only with
+    // whole aligned chunks, and masked ones only in 4- or 8-byte pieces): 4-
+    // or 8-byte pieces on the pipelined kernel where it applies, else this
+    // kernel in any piece size (masked: head dims above 128)
+    if (p.lse) return hipErrorNotSupported;
     if (p.elem_rows >= 4 && pipe16_applies(p, dk))
       return launch_pipe16(p, dk, bf16, causal, use_prescale(p, bf16), s);
+    if (p.mask_kind != MASK_NONE) {
+      if (dk <= 128) return hipErrorNotSupported;
+      return bf16 ? (causal ? launch_masked<__bf16, true, false, 64>(p, dk, s)
+                            : launch_masked<__bf16, false, false, 64>(p, dk, s))
+                  : (causal ? launch_masked<_Float16, true, false, 64>(p, dk, s)
+                            : launch_masked<_Float16, false, false, 64>(p, dk, s));
+    }
     if (bf16)
       return causal ? launch_bucket<__bf16, true, false, 64>(p, dk, s)
                     : launch_bucket<__bf16, false, false, 64>(p, dk, s);

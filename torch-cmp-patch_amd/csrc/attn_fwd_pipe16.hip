@@ -205,14 +205,17 @@ hipError_t launch_lse(const FwdParams& p, const SplitArgs& sa, int dk, hipStream
                                   : launch_lse_m<T, CAUSAL, PRESCALE, 0>(p, sa, dk, s);
 }
 
-// Narrow rows (OPT 64, FwdParams::elem_rows 4 or 8): unmasked inference,
-// buckets 64 and 128 only (other head dims are zero-padded up to them).
-template <typename T, bool CAUSAL>
+// Narrow rows (OPT 64, FwdParams::elem_rows 4 or 8): inference, masked
+// (MOPT 16) or not, buckets 64 and 128 only (other head dims are zero-padded
+// up to them).
+template <typename T, bool CAUSAL, int MOPT = 0>
 hipError_t launch_narrow(const FwdParams& p, const SplitArgs& sa, int dk, hipStream_t s) {
+  constexpr int occ64 = MOPT ? pipe_occ_masked(64) : pipe_occ(64);
+  constexpr int occ128 = MOPT ? pipe_occ_masked(128) : pipe_occ(128);
   if (dk == 64)
-    return launch_pipe16_cfg<T, 64, kPipeNw, kPipeBk, pipe_occ(64), CAUSAL, false, 1 | 64>(p, sa, s);
+    return launch_pipe16_cfg<T, 64, kPipeNw, kPipeBk, occ64, CAUSAL, false, 1 | 64 | MOPT>(p, sa, s);
   if (dk == 128)
-    return launch_pipe16_cfg<T, 128, kPipeNw, kPipeBk, pipe_occ(128), CAUSAL, false, 1 | 64>(p, sa, s);
+    return launch_pipe16_cfg<T, 128, kPipeNw, kPipeBk, occ128, CAUSAL, false, 1 | 64 | MOPT>(p, sa, s);
   return hipErrorNotSupported;
 }
 
@@ -333,7 +336,7 @@ hipError_t launch_pipe16(const FwdParams& p0, int dk0, bool bf16, bool causal, b
   // the training forward and the narrow-row variants have the 64 and 128
   // buckets only
   const int dk = (p.lse || p.elem_rows) ? (dk0 <= 64 ? 64 : 128) : dk0;
-  if (p.elem_rows && (p.elem_rows < 4 || p.lse || p.mask_kind != MASK_NONE)) return hipErrorNotSupported;
+  if (p.elem_rows && (p.elem_rows < 4 || p.lse)) return hipErrorNotSupported;
   // Without pre-scaling, masked keys enter as raw -inf and meet the multiplier
   // c in one FMA; scale 0 would make that 0 * -inf.  A multiplier of 1e-30
   // instead leaves every finite score's exp2 argument within 1e-22 of -m,
@@ -382,6 +385,12 @@ hipError_t launch_pipe16(const FwdParams& p0, int dk0, bool bf16, bool causal, b
     return causal ? launch_lse<_Float16, true, false>(p, sa, dk, s) : launch_lse<_Float16, false, false>(p, sa, dk, s);
   }
   if (p.elem_rows) {  // never pre-scaled: the narrow fp16 kernels then spill
+    if (p.mask_kind != MASK_NONE) {
+      if (bf16)
+        return causal ? launch_narrow<__bf16, true, 16>(p, sa, dk, s) : launch_narrow<__bf16, false, 16>(p, sa, dk, s);
+      return causal ? launch_narrow<_Float16, true, 16>(p, sa, dk, s)
+                    : launch_narrow<_Float16, false, 16>(p, sa, dk, s);
+    }
     if (bf16)
       return causal ? launch_narrow<__bf16, true>(p, sa, dk, s) : launch_narrow<__bf16, false>(p, sa, dk, s);
     return causal ? launch_narrow<_Float16, true>(p, sa, dk, s) : launch_narrow<_Float16, false>(p, sa, dk, s);
