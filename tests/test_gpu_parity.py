@@ -226,14 +226,19 @@ def test_empty_and_rejected_inputs_launch_nothing():
     empty_q = q[:, :, :0]
     assert abi.attn_fwd_raw(empty_q, k, v, o[:, :, :0], 0.125) == abi.OK
     assert abi.attn_fwd_raw(q, k[:, :, :0], v[:, :, :0], o, 0.125) == abi.E_EMPTY_KEYS
-    # a head dim that is not whole 16-byte chunks, and a 2-byte offset view,
-    # are refused with a mask (which needs whole aligned chunks) ...
-    odd = torch.randn(1, 2, 64, 36, dtype=torch.float16, device="cuda")
+    # an odd head dim, and a 2-byte offset view (rows of 2-byte pieces), are
+    # refused with a mask (which needs 4-byte pieces) ...
+    odd = torch.randn(1, 2, 64, 35, dtype=torch.float16, device="cuda")
     keep = torch.ones(1, 1, 64, 64, dtype=torch.bool, device="cuda")
     assert abi.attn_fwd_raw(odd, odd, odd, torch.empty_like(odd), 0.125, attn_mask=keep) == abi.E_HEAD_DIM
     mis = torch.randn(1, 2, 64 * 64 + 1, dtype=torch.float16, device="cuda")[..., 1:]
     mis = mis.view(1, 2, 64, 64)
     assert abi.attn_fwd_raw(mis, k, v, o, 0.125, attn_mask=keep) == abi.E_ALIGN
+    # (an even head dim that is not whole 16-byte chunks runs with the mask)
+    even = torch.randn(1, 2, 64, 36, dtype=torch.float16, device="cuda")
+    oe = torch.empty_like(even)
+    assert abi.attn_fwd_raw(even, even, even, oe, 0.125, attn_mask=keep) == abi.OK
+    assert orc.max_abs_err(oe.cpu(), orc.sdpa_np(even.cpu(), even.cpu(), even.cpu(), 0.125)) <= TOL["fp16"]
     # ... and run in place without one (element-granular rows)
     oo = torch.empty_like(odd)
     assert abi.attn_fwd_raw(odd, odd, odd, oo, 0.125) == abi.OK

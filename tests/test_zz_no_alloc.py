@@ -92,10 +92,10 @@ def test_noalloc_matches_the_workspace_entry_point_on_calls_in_a_row():
 def test_noalloc_passes_argument_checks_like_the_masked_entry_point():
     q, k, v = _inputs("fp16", 1, 2, 2, 64, 300, 64, 0)
     o = torch.empty_like(q)
-    # a masked call whose head dim is not whole 16-byte chunks
-    bad = q[..., :60]
+    # a masked call whose rows are 2-byte pieces (odd head dim)
+    bad = q[..., :59]
     keep = torch.ones(1, 1, 64, 300, dtype=torch.bool, device="cuda")
-    assert abi.attn_fwd_noalloc_raw(bad, k[..., :60], v[..., :60], o[..., :60], 0.1,
+    assert abi.attn_fwd_noalloc_raw(bad, k[..., :59], v[..., :59], o[..., :59], 0.1,
                                     attn_mask=keep) == abi.E_HEAD_DIM
     # fp32 with a mask: the same result as the workspace entry point
     m = torch.rand(1, 1, 64, 300, device="cuda") > 0.3
