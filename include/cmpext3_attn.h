@@ -69,7 +69,7 @@ extern "C" {
 #define CMPEXT3_E_LAUNCH           6  /* the HIP launch itself failed */
 #define CMPEXT3_E_TOO_LARGE        7  /* a size does not fit the kernel's index arithmetic */
 #define CMPEXT3_E_MASK             8  /* attention mask the library cannot take (none at present) */
-#define CMPEXT3_E_TRAINING         9  /* training entry point with fp32 or D > 128 */
+#define CMPEXT3_E_TRAINING         9  /* training entry point with fp32 */
 
 /*
  * Fused attention forward.
@@ -244,8 +244,10 @@ int cmpext3_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* 
  *         scale * Q K^T (+ mask) -- what cmpext3_attn_bwd needs to rebuild the
  *         softmax; -inf for a row whose keys are all dropped.
  *
- * Supported for f16/bf16 with D <= 128 (else CMPEXT3_E_TRAINING, nothing
- * launched).  Every such call runs the pipelined kernel, whatever Sk.  A mask
+ * Supported for f16/bf16 (else CMPEXT3_E_TRAINING, nothing launched).  Every
+ * such call runs the pipelined kernel up to D = 128, whatever Sk, and the
+ * head-dim > 128 kernel above (in the 192 and 256 buckets, never key-split,
+ * so the workspace goes unused there).  A mask
  * is read in runs of 8 keys, as the backward reads it: 16-byte aligned,
  * strides multiples of 4 elements (else CMPEXT3_E_ALIGN), and every row
  * readable up to Sk rounded up to a multiple of 8 (values past Sk are
@@ -282,8 +284,9 @@ int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, f
  * K/V head), dQ
  * (one per 128 queries); each gradient row is written by exactly one
  * workgroup, so results are bit-identical from run to run.  B*H*Sq == 0 is a
- * no-op (dk and dv are then left untouched).  f16/bf16 with D <= 128 only
- * (else CMPEXT3_E_TRAINING).
+ * no-op (dk and dv are then left untouched).  f16/bf16 only (else
+ * CMPEXT3_E_TRAINING); head dims above 128 run in the 192 and 256 buckets at
+ * one wave per SIMD.
  *
  * Reference: none (forward-only reference, cmpext3/__init__.py:115-125).
  */

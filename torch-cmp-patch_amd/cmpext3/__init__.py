@@ -27,7 +27,7 @@ What runs where:
 
 Training (no counterpart in the reference, which is forward-only): with
 ``CMPEXT3_BACKWARD=1`` in the environment, or after ``enable_backward()``,
-SDPA calls with live autograd on fp16/bf16 GPU tensors with D <= 128, equal
+SDPA calls with live autograd on fp16/bf16 GPU tensors with D <= 256, equal
 head counts (or grouped-query K/V under enable_gqa=True), an optional
 attn_mask that needs no gradient, and no dropout run the native forward and
 backward
@@ -177,7 +177,7 @@ def attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
               scale: float | None = None, causal: bool = False,
               attn_mask: torch.Tensor | None = None) -> torch.Tensor:
     """Differentiable native attention (fp16/bf16 GPU tensors [B, H, S, D],
-    D <= 128; K/V may hold fewer heads than Q when that count divides H, with
+    D <= 256; K/V may hold fewer heads than Q when that count divides H, with
     torch's enable_gqa meaning; attn_mask as in SDPA, bool or additive, no
     gradient taken for it).  Raises RuntimeError for anything else."""
     return _Attention.apply(query, key, value, scale, causal, attn_mask)
@@ -194,7 +194,7 @@ def _training_applies(query, key, value, attn_mask, dropout_p, enable_gqa) -> bo
     hq, hkv = query.shape[1], key.shape[1]
     heads_ok = hkv == hq or (enable_gqa and hkv >= 1 and hq % hkv == 0)
     return (heads_ok and key.shape[0] == query.shape[0] and key.shape[3] == query.shape[3]
-            and value.shape == key.shape and 1 <= query.shape[3] <= 128 and key.shape[2] > 0)
+            and value.shape == key.shape and 1 <= query.shape[3] <= 256 and key.shape[2] > 0)
 
 
 def _dispatch(op: str, ref: torch.Tensor, key: tuple,

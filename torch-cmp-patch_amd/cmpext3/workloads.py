@@ -120,6 +120,9 @@ EXTRA_WORKLOADS = [
     Workload("long_decode_d256_bf16", "bf16", 1, 16, 1, 16384, 256, seed=10, Hkv=8,
              note="single-sequence decode, head dim 256, 16 query heads over 8 K/V "
                   "heads, 16384-token KV cache"),
+    Workload("prefill_d256_bf16", "bf16", 1, 16, 4096, 4096, 256, causal=True, seed=11, Hkv=8,
+             note="causal prefill at head dim 256: 16 query heads over 8 K/V heads, "
+                  "4096 tokens (the training pair's head-dim > 128 buckets with --backward)"),
 ]
 BY_NAME = {w.name: w for w in WORKLOADS + EXTRA_WORKLOADS}
 

@@ -142,7 +142,7 @@ const char* cmpext3_attn_strerror(int code) {
     case CMPEXT3_E_MASK:
       return "attention mask not supported here";
     case CMPEXT3_E_TRAINING:
-      return "not supported by the training entry points (need f16/bf16 and head dim <= 128)";
+      return "not supported by the training entry points (need f16/bf16)";
   }
   return "unknown error code";
 }
@@ -237,9 +237,9 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
   if (dtype != CMPEXT3_DTYPE_F32 &&
       (k_str[2] * 64 + 256 > INT32_MAX || v_str[2] * 64 + 256 > INT32_MAX))
     return CMPEXT3_E_TOO_LARGE;
-  // masks and the log-sum-exp exist only in the pipelined kernel, which
-  // addresses every K/V tile of the sweep with 32-bit buffer offsets: a call
-  // beyond that must fail here rather than run a kernel without them
+  // the pipelined kernel (every masked or training call up to D = 128) and
+  // the backward address every K/V tile of the sweep with 32-bit buffer
+  // offsets; masked and training calls keep that one limit at every head dim
   if ((masked || lse) && !tile_offsets_fit(Sk, k_str[2], v_str[2])) return CMPEXT3_E_TOO_LARGE;
 
   cmpext3::FwdParams p;
@@ -288,7 +288,7 @@ int plan_impl(int dtype, int B, int H, int H_kv, int Sq, int Sk, int D, int mask
   int rc = check_shape(dtype, B, H, Sq, Sk, D);
   if (rc != CMPEXT3_OK || (int64_t)B * H * Sq == 0) return rc;
   if (H_kv < 1 || H_kv > H || H % H_kv != 0) return CMPEXT3_E_INVALID;
-  if (with_lse && (dtype == CMPEXT3_DTYPE_F32 || D > 128)) return CMPEXT3_E_TRAINING;
+  if (with_lse && dtype == CMPEXT3_DTYPE_F32) return CMPEXT3_E_TRAINING;
   if (mask_dtype != -1 && (mask_dtype < CMPEXT3_DTYPE_F16 || mask_dtype > CMPEXT3_DTYPE_BOOL))
     return CMPEXT3_E_DTYPE;
   if (elem != 0 && (with_lse || (mask_dtype != -1 && (dtype == CMPEXT3_DTYPE_F32 || elem < 4))))
@@ -382,11 +382,11 @@ int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, f
   const int rc = check_shape(dtype, B, H, Sq, Sk, D);
   if (rc != CMPEXT3_OK) return rc;
   if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;
-  if (dtype == CMPEXT3_DTYPE_F32 || D > 128) return CMPEXT3_E_TRAINING;
+  if (dtype == CMPEXT3_DTYPE_F32) return CMPEXT3_E_TRAINING;
   if (!lse || ((uintptr_t)lse & 3u) != 0) return CMPEXT3_E_INVALID;
   if (!k_str || !v_str) return CMPEXT3_E_INVALID;
-  // the pipelined kernel (the one that writes the log-sum-exp) addresses K/V
-  // tiles with 32-bit buffer offsets, and the backward that consumes this
+  // the pipelined kernel (the one that writes the log-sum-exp up to D = 128)
+  // addresses K/V tiles with 32-bit buffer offsets, and the backward that consumes this
   // forward's state does the same for Q and dO (dO takes O's layout): refuse
   // here what cmpext3_attn_bwd would refuse, so no training step can pass the
   // forward and then fail in its backward
@@ -407,7 +407,7 @@ int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
   int rc = check_shape(dtype, B, H, Sq, Sk, D);
   if (rc != CMPEXT3_OK) return rc;
   if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;
-  if (dtype == CMPEXT3_DTYPE_F32 || D > 128) return CMPEXT3_E_TRAINING;
+  if (dtype == CMPEXT3_DTYPE_F32) return CMPEXT3_E_TRAINING;
   if (!whole_chunks(dtype, D)) return CMPEXT3_E_HEAD_DIM;
   if (H_kv < 1 || H_kv > H || H % H_kv != 0) return CMPEXT3_E_INVALID;
   bool runs_ok = true;

@@ -1,5 +1,5 @@
 // Backward pass of the fused attention, fp16 / bf16 on gfx950
-// (v_mfma_f32_32x32x16_{f16,bf16}), head-dim buckets 64 and 128.
+// (v_mfma_f32_32x32x16_{f16,bf16}), head-dim buckets 64, 128, 192 and 256.
 //
 // Given Q, K, V, the forward output O, its gradient dO and the forward's row
 // log-sum-exp (natural log, written by the forward's training variant), with
@@ -68,6 +68,8 @@ struct BwdParams {
 // LDS row stride (halves) of the Q/dO and K/V tiles: rows padded by 16 bytes,
 // by 48 at D = 128 (fewer bank conflicts there: dK/dV 285 -> 277 us and dQ
 // 125 -> 123 us on causal bf16 [4,16,2048,128]; no change at D = 64).
+// Waves per SIMD of the two gradient kernels: D > 128 holds the dK and dV
+// accumulators alone in 2 * DK registers per lane, so those run one wave.
 constexpr int bwd_lds_stride(int dk) { return dk + (dk == 128 ? 24 : 8); }
 
 // Mask element size in bytes.
@@ -180,10 +182,10 @@ __device__ __forceinline__ void store_rows(uint16_t* base, int64_t row_stride, i
 // registers), 2 causal; D <= 128: 2 with V parked in LDS (the causal and the
 // masked variants spill 8 registers and are still 12-20% faster than at 1),
 // 1 masked causal (its K/V operands and dK/dV accumulators alone take 192
-// registers).
+// registers); D > 128: 1, with V parked in LDS.
 template <typename T, int DK, bool CAUSAL, bool MASK>
 __global__ void __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu(DK <= 64 ? (CAUSAL ? 2 : 3) : (MASK && CAUSAL ? 1 : 2))))
+__attribute__((amdgpu_waves_per_eu(DK <= 64 ? (CAUSAL ? 2 : 3) : (DK > 128 || (MASK && CAUSAL)) ? 1 : 2)))
 attn_bwd_dkdv(const BwdParams p) {
   constexpr int BQ = 32, BKV = 128;
   constexpr int RS = bwd_lds_stride(DK);  // LDS row stride (halves)
@@ -196,9 +198,11 @@ attn_bwd_dkdv(const BwdParams p) {
   // backward 603 -> 481 us) and D <= 64 masked non-causal (three waves
   // instead of two: masked SDXL-shape backward 913 -> 616 us).  Each lane
   // reads back only what it wrote, so no barrier orders the parking stores.
-  // Not for masked causal D > 64 (32 spilled registers at two waves) or
-  // causal D <= 64 (three waves with V parked measured slower: 301 -> 327 us).
-  constexpr bool VLDS = DK > 64 ? !(MASK && CAUSAL) : (MASK && !CAUSAL);
+  // Not for masked causal 64 < D <= 128 (32 spilled registers at two waves)
+  // or causal D <= 64 (three waves with V parked measured slower: 301 -> 327
+  // us).  Above D = 128 always: the K operands (DK / 4 registers) and the
+  // two accumulators (2 * DK) leave little of one wave's 512 registers.
+  constexpr bool VLDS = DK > 128 ? true : DK > 64 ? !(MASK && CAUSAL) : (MASK && !CAUSAL);
   constexpr int RSV = DK + 8;
   __shared__ __attribute__((aligned(16))) uint16_t vpark[VLDS ? BKV * RSV : 8];
   // [slot][-lse2 / c, -Delta][row]: the starting values of the S and dP
@@ -420,7 +424,7 @@ attn_bwd_dkdv(const BwdParams p) {
 // key tiles (32 rows of K and V) through double-buffered LDS.
 template <typename T, int DK, bool CAUSAL, bool MASK>
 __global__ void __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu(DK <= 64 ? (MASK ? 2 : 3) : (MASK && CAUSAL ? 1 : 2))))
+__attribute__((amdgpu_waves_per_eu(DK <= 64 ? (MASK ? 2 : 3) : (DK > 128 || (MASK && CAUSAL)) ? 1 : 2)))
 attn_bwd_dq(const BwdParams p) {
   constexpr int BQ = 128, BK = 32;
   constexpr int RS = bwd_lds_stride(DK);
@@ -432,7 +436,7 @@ attn_bwd_dq(const BwdParams p) {
   // SIMD instead of 1 (masked backward 473 -> 419 us on bf16
   // [2,16,2048,128]; the causal variant would spill 16 registers and gains
   // nothing, so it keeps its registers and 1 wave)
-  constexpr bool DLDS = DK > 64 && MASK && !CAUSAL;
+  constexpr bool DLDS = DK > 64 && DK <= 128 && MASK && !CAUSAL;
   constexpr int RSD = DK + 8;
   __shared__ __attribute__((aligned(16))) uint16_t dpark[DLDS ? BQ * RSD : 8];
 

@@ -1,7 +1,8 @@
 // Launch sequence of the attention backward (templates in attn_bwd16.h):
 // Delta, then dK/dV over key blocks, then dQ over query blocks, all on the
 // caller's stream.  Head dims up to 64 use the 64 bucket, up to 128 the 128
-// bucket (columns past D are zero in every operand and never stored).
+// bucket, up to 192 and 256 those (columns past D are zero in every operand
+// and never stored).
 #include "attn_bwd16.h"
 
 namespace cmpext3 {
@@ -26,6 +27,8 @@ template <typename T, bool MASK>
 hipError_t launch_bwd_mask(const BwdParams& p, int dk, bool causal, hipStream_t s) {
   if (dk == 64) return causal ? launch_bwd_t<T, 64, true, MASK>(p, s) : launch_bwd_t<T, 64, false, MASK>(p, s);
   if (dk == 128) return causal ? launch_bwd_t<T, 128, true, MASK>(p, s) : launch_bwd_t<T, 128, false, MASK>(p, s);
+  if (dk == 192) return causal ? launch_bwd_t<T, 192, true, MASK>(p, s) : launch_bwd_t<T, 192, false, MASK>(p, s);
+  if (dk == 256) return causal ? launch_bwd_t<T, 256, true, MASK>(p, s) : launch_bwd_t<T, 256, false, MASK>(p, s);
   return hipErrorNotSupported;
 }
 
@@ -37,7 +40,7 @@ hipError_t launch_bwd_dtype(const BwdParams& p, int dk, bool causal, hipStream_t
 
 }  // namespace
 
-int bwd16_bucket(int D) { return D <= 0 ? -1 : D <= 64 ? 64 : D <= 128 ? 128 : -1; }
+int bwd16_bucket(int D) { return D <= 0 ? -1 : D <= 64 ? 64 : D <= 128 ? 128 : D <= 192 ? 192 : D <= 256 ? 256 : -1; }
 
 hipError_t launch_bwd16(const BwdParams& p, bool bf16, bool causal, hipStream_t s) {
   if ((int64_t)p.B * p.H * p.Sq == 0) return hipSuccess;

@@ -189,7 +189,8 @@ __device__ __forceinline__ int lds_swz(int r) {
 // (ld_cols16 / st_cols16x4, FwdParams::elem_rows): any head dim and any
 // 2-byte aligned rows, read and written in 2-, 4- or 8-byte pieces, columns
 // past D never touched.  OPT bit 4: an attention mask (p.mask) on every
-// tile's scores.
+// tile's scores.  OPT bit 5: each row's natural-log log-sum-exp goes to
+// p.lse (the training forward; such launches are never key-split).
 template <typename T, int DK, int DP, int NW, int QB, int BK, int OCC, bool CAUSAL, bool PRESCALE,
           int OPT = 0>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
@@ -749,6 +750,13 @@ attn_fwd_mfma16(const FwdParams p, const SplitArgs sa) {
   for (int qb = 0; qb < QB; ++qb) {
     const float inv = lrow[qb] > 0.f ? 1.f / lrow[qb] : 0.f;
     const int qrow = qw0 + 32 * qb + l32;
+    // log-sum-exp in natural log: (offset + log2 of the sum) * ln 2; a row
+    // that saw no key gets -inf (its output is zero)
+    if constexpr ((OPT & 32) != 0) {
+      if (qrow < Sq && hh == 0)
+        p.lse[(int64_t)bh * Sq + qrow] =
+            lrow[qb] > 0.f ? (mb[qb] + __builtin_amdgcn_logf(lrow[qb])) * 0.6931471805599453f : -INFINITY;
+    }
     if (qrow < Sq) {
       uint16_t* orow = og + row_off(qrow, p.o_g, p.o_s);
 #pragma unroll
@@ -809,7 +817,9 @@ hipError_t launch_mfma16_cfg(const FwdParams& p0, hipStream_t stream) {
   // waves per block that hold query rows (a single block shorter than BQ has fewer)
   const int nwl = p.n_qblk > 1 ? NW : (p.Sq + QB * 32 - 1) / (QB * 32) < NW ? (p.Sq + QB * 32 - 1) / (QB * 32) : NW;
   SplitArgs sa = {n, 1, nullptr, nullptr, nwl};
-  const int parts = split_parts16(n, (p.Sk + BK - 1) / BK, OCC, device_cus(), CAUSAL, DP, nwl < NW);
+  // the training forward (OPT bit 5) runs every block whole
+  const int parts =
+      (OPT & 32) ? 1 : split_parts16(n, (p.Sk + BK - 1) / BK, OCC, device_cus(), CAUSAL, DP, nwl < NW);
   if (parts >= 2) {
     // every block is split; one key range of all of them takes part_bytes
     const size_t part_bytes = (size_t)n * nwl * QB * split_vectors(DP) * 64 * sizeof(f32x4);

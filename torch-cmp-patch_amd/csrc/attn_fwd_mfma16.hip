@@ -68,6 +68,17 @@ hipError_t launch_masked(const FwdParams& p, int dk, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
+// training forwards (OPT bit 32: the row log-sum-exp) of the head dims above
+// 128, masked (OPT bit 16) or not, in the backward's buckets 192 and 256; no
+// pre-scaled Q, so one instantiation per dtype serves every scale
+template <typename T, bool CAUSAL>
+hipError_t launch_train(const FwdParams& p, int dk, hipStream_t s) {
+  const bool m = p.mask_kind != MASK_NONE;
+  if (dk <= 192)
+    return m ? launch_dk<T, 192, CAUSAL, false, 32 | 16>(p, s) : launch_dk<T, 192, CAUSAL, false, 32>(p, s);
+  return m ? launch_dk<T, 256, CAUSAL, false, 32 | 16>(p, s) : launch_dk<T, 256, CAUSAL, false, 32>(p, s);
+}
+
 }  // namespace
 
 bool pipe16_applies(const FwdParams& p, int dk);
@@ -129,10 +140,13 @@ hipError_t launch_mfma16(const FwdParams& p0, bool bf16, bool causal, hipStream_
   }
   if (short16_applies(p, dk, causal)) return launch_short16(p, dk, bf16, s);
   if (pipe16_applies(p, dk)) return launch_pipe16(p, dk, bf16, causal, use_prescale(p, bf16), s);
-  // this kernel has no log-sum-exp output: refuse rather than run without it
-  // (the ABI rejects such calls earlier); masked launches reach it only above
-  // D = 128 (the pipelined kernel takes every masked launch up to 128)
-  if (p.lse) return hipErrorNotSupported;
+  // training forwards reach this kernel above D = 128 only (the pipelined
+  // kernel writes the log-sum-exp up to 128); masked launches likewise
+  if (p.lse) {
+    if (dk <= 128) return hipErrorNotSupported;
+    if (bf16) return causal ? launch_train<__bf16, true>(p, dk, s) : launch_train<__bf16, false>(p, dk, s);
+    return causal ? launch_train<_Float16, true>(p, dk, s) : launch_train<_Float16, false>(p, dk, s);
+  }
   if (p.mask_kind != MASK_NONE) {
     if (dk <= 128) return hipErrorNotSupported;
     if (bf16)

@@ -15,13 +15,15 @@
 //     view (the reference's HFMA2 path does this for fp16, :1652);
 //   * head dims that are not a whole number of 16-byte chunks, and tensors
 //     whose base pointer or row strides are not 16-byte aligned, run in place
-//     (narrow-row kernel variants); calls with an attn_mask, and 16-bit rows
-//     with an odd element count or offset (2-byte pieces, slower in place
-//     than copied), repack such inputs into zero-padded contiguous copies;
+//     (narrow-row kernel variants); 16-bit rows with an odd element count or
+//     offset (2-byte pieces, slower in place than copied), and masked fp32
+//     rows off whole 16-byte chunks, repack such inputs into zero-padded
+//     contiguous copies;
 //   * K/V may hold fewer heads than Q (grouped-query attention);
 //   * attn_mask (bool or additive f16/bf16/f32, broadcast like torch's SDPA)
-//     runs natively for f16/bf16 with D <= 128, alone or combined with causal
-//     (the reference sent every mask to stock torch, cmpext3/__init__.py:624).
+//     runs natively for every dtype and head dim, alone or combined with
+//     causal (the reference sent every mask to stock torch,
+//     cmpext3/__init__.py:624).
 //
 // attention_fwd_lse / attention_bwd: the training pair (no reference
 // counterpart: the reference is forward-only, cmpext3/__init__.py:115-125),
@@ -229,9 +231,9 @@ torch::Tensor attention(torch::Tensor query, torch::Tensor key, torch::Tensor va
                ? CMPEXT3_E_ALIGN
                : launch(query, key, value, out, dtype, (int)D, scale, causal, mask, stream);
   if (rc == CMPEXT3_E_ALIGN || rc == CMPEXT3_E_HEAD_DIM) {
-    // Masked calls, and 2-byte rows (the ABI runs any other layout in
-    // place): repack into contiguous copies zero-padded to whole 16-byte
-    // chunks.
+    // 2-byte rows, and masked rows the ABI refuses (fp32 off whole chunks;
+    // it runs any other layout in place): repack into contiguous copies
+    // zero-padded to whole 16-byte chunks.
     // Zero columns add nothing to Q K^T, and the padded V columns only produce
     // output columns that are cut away again; `scale` already used the true D.
     const int64_t chunk = (dtype == CMPEXT3_DTYPE_F32) ? 4 : 8;
@@ -253,7 +255,7 @@ torch::Tensor attention(torch::Tensor query, torch::Tensor key, torch::Tensor va
 namespace {
 
 // Shared checks of the training entry points: 4-D GPU f16/bf16 tensors of one
-// dtype and device, K/V heads dividing the query heads, head dim <= 128.
+// dtype and device, K/V heads dividing the query heads, head dim <= 256.
 int training_dtype(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v) {
   TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4, "cmpext3 attention: q, k, v must be 4D");
   TORCH_CHECK(q.is_cuda() && q.device() == k.device() && q.device() == v.device(),
@@ -267,7 +269,7 @@ int training_dtype(const torch::Tensor& q, const torch::Tensor& k, const torch::
                   k.size(3) == q.size(3) && v.sizes() == k.sizes(),
               "cmpext3 attention: the training path needs K/V of Q's batch and head dim, with a "
               "head count dividing Q's");
-  TORCH_CHECK(q.size(3) >= 1 && q.size(3) <= 128, "cmpext3 attention: the training path needs D <= 128");
+  TORCH_CHECK(q.size(3) >= 1 && q.size(3) <= 256, "cmpext3 attention: the training path needs D <= 256");
   TORCH_CHECK(k.size(2) > 0 || q.size(0) * q.size(1) * q.size(2) == 0,
               "cmpext3 attention: empty key sequence");
   return dtype;
@@ -416,7 +418,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("B"), py::arg("H"), py::arg("Sq"), py::arg("Sk"), py::arg("D"),
         py::arg("causal") = false);
   m.def("attention_fwd_lse", &attention_fwd_lse,
-        "Training forward (fp16/bf16, D <= 128): returns (out, lse), lse = fp32 [B,H,Sq] row "
+        "Training forward (fp16/bf16, D <= 256): returns (out, lse), lse = fp32 [B,H,Sq] row "
         "log-sum-exp (natural log)",
         py::arg("query"), py::arg("key"), py::arg("value"), py::arg("scale") = py::none(),
         py::arg("causal") = false, py::arg("attn_mask") = py::none());
