@@ -247,7 +247,7 @@ def bench_training(wl, args) -> dict:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {"fp16": "f16", "bf16": "bf16"}[wl.dtype],
+        "dtype": {"fp16": "f16", "bf16": "bf16", "fp32": "f32"}[wl.dtype],
         "data": "synthetic (seeded N(0,1) Q/K/V/dO, CPU generator -> device)",
         "config": {"workload": wl.name, "B": wl.B, "H": wl.H, "Sq": wl.Sq, "Sk": wl.Sk, "D": wl.D,
                    "causal": wl.causal, "scale": sc,

@@ -69,7 +69,7 @@ extern "C" {
 #define CMPEXT3_E_LAUNCH           6  /* the HIP launch itself failed */
 #define CMPEXT3_E_TOO_LARGE        7  /* a size does not fit the kernel's index arithmetic */
 #define CMPEXT3_E_MASK             8  /* attention mask the library cannot take (none at present) */
-#define CMPEXT3_E_TRAINING         9  /* training entry point with fp32 */
+#define CMPEXT3_E_TRAINING         9  /* training call the library cannot take (none at present) */
 
 /*
  * Fused attention forward.
@@ -244,10 +244,11 @@ int cmpext3_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* 
  *         scale * Q K^T (+ mask) -- what cmpext3_attn_bwd needs to rebuild the
  *         softmax; -inf for a row whose keys are all dropped.
  *
- * Supported for f16/bf16 (else CMPEXT3_E_TRAINING, nothing launched).  Every
- * such call runs the pipelined kernel up to D = 128, whatever Sk, and the
- * head-dim > 128 kernel above (in the 192 and 256 buckets, never key-split,
- * so the workspace goes unused there).  A mask
+ * Every dtype (rows in whole, 16-byte aligned chunks, else CMPEXT3_E_ALIGN /
+ * CMPEXT3_E_HEAD_DIM).  f16/bf16 calls run the pipelined kernel up to
+ * D = 128, whatever Sk, and the head-dim > 128 kernel above it (in the 192
+ * and 256 buckets, never key-split, so the workspace goes unused there);
+ * fp32 calls run the fp32 kernel, never key-split.  A mask
  * is read in runs of 8 keys, as the backward reads it: 16-byte aligned,
  * strides multiples of 4 elements (else CMPEXT3_E_ALIGN), and every row
  * readable up to Sk rounded up to a multiple of 8 (values past Sk are
@@ -281,12 +282,12 @@ int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, f
  *           receives sum_d dout * o per row).
  *   *_str[3] : element strides over {batch, head, seq} as in cmpext3_attn_fwd.
  * Three kernels on `stream`: Delta, dK/dV (one workgroup per 128 keys of a
- * K/V head), dQ
- * (one per 128 queries); each gradient row is written by exactly one
- * workgroup, so results are bit-identical from run to run.  B*H*Sq == 0 is a
- * no-op (dk and dv are then left untouched).  f16/bf16 only (else
- * CMPEXT3_E_TRAINING); head dims above 128 run in the 192 and 256 buckets at
- * one wave per SIMD.
+ * K/V head; 64 for fp32), dQ (one per 128 queries; 64 for fp32); each
+ * gradient row is written by exactly one workgroup, so results are
+ * bit-identical from run to run.  B*H*Sq == 0 is a no-op (dk and dv are then
+ * left untouched).  Every dtype: f16/bf16 on 32x32x16 MFMAs (head dims above
+ * 128 in the 192 and 256 buckets at one wave per SIMD), fp32 on 16x16x4 fp32
+ * MFMAs (buckets 32, 40, 64, 96, 128, 192, 256).
  *
  * Reference: none (forward-only reference, cmpext3/__init__.py:115-125).
  */

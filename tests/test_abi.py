@@ -231,7 +231,7 @@ def _call_bwd(delta=16, lse=16, dtype=abi.DTYPE_F16, D=64, dq=16, Sq=8, Sk=8, sc
 
 def test_training_entry_points_reject_before_launch():
     """Fake device addresses: each case must be turned down on the host."""
-    assert _call_lse(dtype=abi.DTYPE_F32, D=64) == abi.E_TRAINING
+    assert _call_lse(dtype=abi.DTYPE_F32, D=66) == abi.E_HEAD_DIM   # fp32 training: D a multiple of 4
     assert _call_lse(D=264) == abi.E_HEAD_DIM
     assert _call_lse(lse=0) == abi.E_INVALID
     assert _call_lse(lse=18) == abi.E_INVALID
@@ -239,7 +239,8 @@ def test_training_entry_points_reject_before_launch():
     assert _call_lse(D=36) == abi.E_HEAD_DIM               # training needs whole chunks
     assert _call_lse(Sk=0) == abi.E_EMPTY_KEYS
     assert _call_lse(lse=0, q=0, Sq=0) == abi.OK          # empty problem
-    assert _call_bwd(dtype=abi.DTYPE_F32) == abi.E_TRAINING
+    assert _call_bwd(dtype=abi.DTYPE_F32, D=62) == abi.E_HEAD_DIM
+    assert _call_bwd(dtype=abi.DTYPE_F32, strides=(512, 512, 66)) == abi.E_ALIGN
     assert _call_bwd(D=260) == abi.E_HEAD_DIM
     assert _call_bwd(D=36) == abi.E_HEAD_DIM
     assert _call_bwd(delta=0) == abi.E_INVALID
@@ -258,15 +259,20 @@ def test_training_entry_points_reject_before_launch():
     assert _call_bwd(mask=16, mask_dtype=abi.DTYPE_BOOL, mask_str=(0, 0, 6)) == abi.E_ALIGN
 
 
-def test_training_plans_above_head_dim_128_run_whole():
-    """Training forwards above D = 128 run the head-dim > 128 kernel unsplit
-    (no workspace), f16 and bf16, masked or not; fp32 stays refused."""
+def test_training_plans_that_run_whole():
+    """Training forwards above D = 128 (f16, bf16) and every fp32 training
+    forward run unsplit (no workspace), masked or not."""
     for dt in (abi.DTYPE_F16, abi.DTYPE_BF16):
         for D in (136, 160, 192, 200, 256):
             for mdt in (-1, abi.DTYPE_BOOL):
                 assert abi.workspace_size(dt, 1, 8, 8, 16, 8192, D, mdt, with_lse=True) == 0
                 assert abi.plan(dt, 1, 8, 8, 16, 8192, D, 1 << 30, mdt, with_lse=True) == (abi.OK, 1)
-    assert abi.plan(abi.DTYPE_F32, 1, 8, 8, 16, 8192, 64, 1 << 30, with_lse=True)[0] == abi.E_TRAINING
+    for D in (8, 40, 64, 100, 128, 256):
+        for mdt in (-1, abi.DTYPE_F32):
+            assert abi.workspace_size(abi.DTYPE_F32, 1, 8, 8, 1024, 1024, D, mdt, with_lse=True) == 0
+            assert abi.plan(abi.DTYPE_F32, 1, 8, 8, 1024, 1024, D, 1 << 30, mdt, with_lse=True) == (abi.OK, 1)
+    # the inference forward of the same fp32 problem splits (128 blocks x 4 parts)
+    assert abi.plan(abi.DTYPE_F32, 1, 8, 8, 1024, 1024, 64, 1 << 30) == (abi.OK, 4)
 
 
 def _call_masked(k_row=64, q_row=64, o_row=64, Sk=1 << 17, Sq=1, mask_str=(0, 0, 0), lse=0,

@@ -17,14 +17,14 @@ own elements must still hold the sentinel (no stray writes from tail tiles,
 key-split merges or narrow-row stores).  Cases without K/V grouping or mask
 also run through the torch binding (ops.attention).
 
-Training cases (fp16/bf16, D <= 256 in whole 16-byte chunks, contiguous or
+Training cases (fp16/bf16/fp32, D <= 256 in whole 16-byte chunks, contiguous or
 [B,S,H,D] views, grouped-query K/V, masks) run cmpext3_attn_fwd_lse and then
 cmpext3_attn_bwd against sdpa_np / sdpa_lse_np / sdpa_bwd_np (pinned to torch
 autograd in tests/test_oracle_bwd.py), at the bars of
 tests/test_gpu_backward.py: output and natural-log lse within 1e-2 fp16 /
-2e-2 bf16 (rows with no visible key must give lse -inf exactly), each
+2e-2 bf16 / 1e-4 fp32 (rows with no visible key must give lse -inf exactly), each
 gradient within that fraction of its own largest oracle magnitude (floor
-1e-3); grouped dK/dV are the oracle's per-query-head gradients summed over
+1e-3; 0.1 for fp32); grouped dK/dV are the oracle's per-query-head gradients summed over
 each group.
 
 Contract the draws stay inside (include/cmpext3_attn.h): any head dim 1..256
@@ -89,7 +89,7 @@ def _draw(rng):
 
 
 def _draw_train(rng):
-    dtype = str(rng.choice(["fp16", "bf16"]))
+    dtype = str(rng.choice(["fp16", "bf16", "fp32"], p=[0.4, 0.4, 0.2]))
     B = int(rng.integers(1, 3))
     hkv = int(rng.integers(1, 4))
     H = hkv * int(rng.choice([1, 1, 2, 3]))
@@ -200,8 +200,8 @@ def test_random_case(case):
         assert err2 <= TOL[dtype], f"ops.attention: max abs err {err2:.3g} > {TOL[dtype]}"
 
 
-def _rel_err(got, want):
-    return orc.max_abs_err(got, want) / max(float(np.abs(want).max()) if want.size else 0.0, 1e-3)
+def _rel_err(got, want, floor=1e-3):
+    return orc.max_abs_err(got, want) / max(float(np.abs(want).max()) if want.size else 0.0, floor)
 
 
 @pytest.mark.parametrize("case", TRAIN_CASES, ids=[_case_id(c) for c in TRAIN_CASES])
@@ -237,5 +237,7 @@ def test_random_training_case(case):
     dk_r = dk_r.reshape(B, Hkv, grp, Sk, D).sum(axis=2)
     dv_r = dv_r.reshape(B, Hkv, grp, Sk, D).sum(axis=2)
     for name, got, ref in zip(("dq", "dk", "dv"), (dq, dk, dv), (dq_r, dk_r, dv_r)):
-        err = _rel_err(got.float().cpu().numpy(), ref)
+        # fp32: a gradient that is exactly zero (one key) keeps ~1e-6 of the
+        # cancellation of dP - Delta
+        err = _rel_err(got.float().cpu().numpy(), ref, 0.1 if dtype == "fp32" else 1e-3)
         assert err <= TOL[dtype], f"{name}: relative error {err:.3g}"

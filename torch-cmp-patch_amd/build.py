@@ -30,7 +30,7 @@ HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
 
 HIP_SOURCES = ["attn_fwd_mfma16.hip", "attn_fwd_pipe16.hip", "attn_fwd_short16.hip", "attn_fwd_mfma32.hip",
-               "attn_fwd_decode16.hip", "attn_bwd16.hip", "attn_abi.cpp"]
+               "attn_fwd_decode16.hip", "attn_bwd16.hip", "attn_bwd32.hip", "attn_abi.cpp"]
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -27,7 +27,7 @@ What runs where:
 
 Training (no counterpart in the reference, which is forward-only): with
 ``CMPEXT3_BACKWARD=1`` in the environment, or after ``enable_backward()``,
-SDPA calls with live autograd on fp16/bf16 GPU tensors with D <= 256, equal
+SDPA calls with live autograd on fp16/bf16/fp32 GPU tensors with D <= 256, equal
 head counts (or grouped-query K/V under enable_gqa=True), an optional
 attn_mask that needs no gradient, and no dropout run the native forward and
 backward
@@ -132,7 +132,7 @@ _DTYPE_TAG = {torch.float16: "fp16", torch.float32: "fp32", torch.bfloat16: "bf1
 _MASK_DTYPES = (torch.bool, torch.float16, torch.bfloat16, torch.float32)
 
 
-_TRAIN_DTYPES = (torch.float16, torch.bfloat16)
+_TRAIN_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 _BACKWARD = os.environ.get("CMPEXT3_BACKWARD", "0") == "1"
 
 
@@ -176,7 +176,7 @@ class _Attention(torch.autograd.Function):
 def attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
               scale: float | None = None, causal: bool = False,
               attn_mask: torch.Tensor | None = None) -> torch.Tensor:
-    """Differentiable native attention (fp16/bf16 GPU tensors [B, H, S, D],
+    """Differentiable native attention (fp16/bf16/fp32 GPU tensors [B, H, S, D],
     D <= 256; K/V may hold fewer heads than Q when that count divides H, with
     torch's enable_gqa meaning; attn_mask as in SDPA, bool or additive, no
     gradient taken for it).  Raises RuntimeError for anything else."""

@@ -19,6 +19,7 @@
 
 namespace cmpext3 {
 hipError_t launch_bwd16(const BwdParams& p, bool bf16, bool causal, hipStream_t s);
+hipError_t launch_bwd32(const BwdParams& p, bool causal, hipStream_t s);
 hipError_t launch_mfma16(const FwdParams& p, bool bf16, bool causal, hipStream_t s);
 hipError_t launch_mfma32(const FwdParams& p, bool causal, hipStream_t s);
 int mfma16_bucket(int D);
@@ -142,7 +143,7 @@ const char* cmpext3_attn_strerror(int code) {
     case CMPEXT3_E_MASK:
       return "attention mask not supported here";
     case CMPEXT3_E_TRAINING:
-      return "not supported by the training entry points (need f16/bf16)";
+      return "not supported by the training entry points (none at present)";
   }
   return "unknown error code";
 }
@@ -188,10 +189,11 @@ int cmpext3_attn_fwd_gqa(const void* q, const void* k, const void* v, void* o, i
 namespace {
 
 // Byte offsets of every row of an S-row sweep, plus one 64-row tile past it,
-// stay below 2^31 (the pipelined and backward kernels' 32-bit buffer offsets).
-bool tile_offsets_fit(int S, int64_t s0, int64_t s1) {
+// stay below 2^31 (the pipelined and backward kernels' 32-bit buffer offsets)
+// for es-byte elements.
+bool tile_offsets_fit(int S, int64_t s0, int64_t s1, int es = 2) {
   const int64_t rs = s0 > s1 ? s0 : s1;
-  return (int64_t)(S + 64) * rs * 2 < INT32_MAX;
+  return (int64_t)(S + 64) * rs * es < INT32_MAX;
 }
 
 // Forward with every option; lse (may be null) receives the row log-sum-exp.
@@ -240,7 +242,7 @@ int fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, i
   // the pipelined kernel (every masked or training call up to D = 128) and
   // the backward address every K/V tile of the sweep with 32-bit buffer
   // offsets; masked and training calls keep that one limit at every head dim
-  if ((masked || lse) && !tile_offsets_fit(Sk, k_str[2], v_str[2])) return CMPEXT3_E_TOO_LARGE;
+  if ((masked || lse) && !tile_offsets_fit(Sk, k_str[2], v_str[2], es)) return CMPEXT3_E_TOO_LARGE;
 
   cmpext3::FwdParams p;
   memset(&p, 0, sizeof p);
@@ -288,7 +290,6 @@ int plan_impl(int dtype, int B, int H, int H_kv, int Sq, int Sk, int D, int mask
   int rc = check_shape(dtype, B, H, Sq, Sk, D);
   if (rc != CMPEXT3_OK || (int64_t)B * H * Sq == 0) return rc;
   if (H_kv < 1 || H_kv > H || H % H_kv != 0) return CMPEXT3_E_INVALID;
-  if (with_lse && dtype == CMPEXT3_DTYPE_F32) return CMPEXT3_E_TRAINING;
   if (mask_dtype != -1 && (mask_dtype < CMPEXT3_DTYPE_F16 || mask_dtype > CMPEXT3_DTYPE_BOOL))
     return CMPEXT3_E_DTYPE;
   if (elem != 0 && (with_lse || (mask_dtype != -1 && (dtype == CMPEXT3_DTYPE_F32 || elem < 4))))
@@ -382,7 +383,6 @@ int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, f
   const int rc = check_shape(dtype, B, H, Sq, Sk, D);
   if (rc != CMPEXT3_OK) return rc;
   if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;
-  if (dtype == CMPEXT3_DTYPE_F32) return CMPEXT3_E_TRAINING;
   if (!lse || ((uintptr_t)lse & 3u) != 0) return CMPEXT3_E_INVALID;
   if (!k_str || !v_str) return CMPEXT3_E_INVALID;
   // the pipelined kernel (the one that writes the log-sum-exp up to D = 128)
@@ -391,7 +391,8 @@ int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, f
   // here what cmpext3_attn_bwd would refuse, so no training step can pass the
   // forward and then fail in its backward
   if (!q_str || !o_str) return CMPEXT3_E_INVALID;
-  if (!tile_offsets_fit(Sk, k_str[2], v_str[2]) || !tile_offsets_fit(Sq, q_str[2], o_str[2]))
+  const int es = elem_size(dtype);
+  if (!tile_offsets_fit(Sk, k_str[2], v_str[2], es) || !tile_offsets_fit(Sq, q_str[2], o_str[2], es))
     return CMPEXT3_E_TOO_LARGE;
   return fwd_impl(q, k, v, o, lse, dtype, B, H, H_kv, Sq, Sk, D, q_str, k_str, v_str, o_str, mask,
                   mask_dtype, mask_str, scale, causal, stream, workspace, workspace_bytes);
@@ -407,7 +408,6 @@ int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
   int rc = check_shape(dtype, B, H, Sq, Sk, D);
   if (rc != CMPEXT3_OK) return rc;
   if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;
-  if (dtype == CMPEXT3_DTYPE_F32) return CMPEXT3_E_TRAINING;
   if (!whole_chunks(dtype, D)) return CMPEXT3_E_HEAD_DIM;
   if (H_kv < 1 || H_kv > H || H % H_kv != 0) return CMPEXT3_E_INVALID;
   bool runs_ok = true;
@@ -422,12 +422,13 @@ int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
   const void* ptrs[] = {q, k, v, o, dout, dq, dk, dv};
   for (const void* ptr : ptrs)
     if (!aligned16(ptr)) return CMPEXT3_E_ALIGN;
-  if (!stride_ok(q_str, B, H, Sq, 2) || !stride_ok(o_str, B, H, Sq, 2) || !stride_ok(do_str, B, H, Sq, 2) ||
-      !stride_ok(dq_str, B, H, Sq, 2) || !stride_ok(k_str, B, H_kv, Sk, 2) || !stride_ok(v_str, B, H_kv, Sk, 2) ||
-      !stride_ok(dk_str, B, H_kv, Sk, 2) || !stride_ok(dv_str, B, H_kv, Sk, 2))
+  const int es = elem_size(dtype);
+  if (!stride_ok(q_str, B, H, Sq, es) || !stride_ok(o_str, B, H, Sq, es) || !stride_ok(do_str, B, H, Sq, es) ||
+      !stride_ok(dq_str, B, H, Sq, es) || !stride_ok(k_str, B, H_kv, Sk, es) || !stride_ok(v_str, B, H_kv, Sk, es) ||
+      !stride_ok(dk_str, B, H_kv, Sk, es) || !stride_ok(dv_str, B, H_kv, Sk, es))
     return CMPEXT3_E_ALIGN;
   // Q/dO tiles (dK/dV kernel) and K/V tiles (dQ kernel) use 32-bit buffer offsets
-  if (!tile_offsets_fit(Sq, q_str[2], do_str[2]) || !tile_offsets_fit(Sk, k_str[2], v_str[2]))
+  if (!tile_offsets_fit(Sq, q_str[2], do_str[2], es) || !tile_offsets_fit(Sk, k_str[2], v_str[2], es))
     return CMPEXT3_E_TOO_LARGE;
 
   cmpext3::BwdParams p;
@@ -451,13 +452,15 @@ int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
     p.m_b = mask_str[0]; p.m_h = mask_str[1]; p.m_q = mask_str[2];
     p.mask_kind = mask_kind_of(mask_dtype);
   }
-  // The dK/dV kernel divides by c.  For |scale| * log2(e) below 1e-30 (scale 0
+  // The fp16/bf16 dK/dV kernel divides by c.  For |scale| * log2(e) below 1e-30 (scale 0
   // and denormal scales) c = 1e-30 moves each exp2 argument by at most
   // 1e-30 * |score|, and keeps -lse2 / c finite
   p.c = fmaxf(fabsf(scale) * cmpext3::kLog2e, 1e-30f);
   p.scale = scale;
-  p.sign = scale < 0.f ? 0x80008000u : 0u;
-  const hipError_t err = cmpext3::launch_bwd16(p, dtype == CMPEXT3_DTYPE_BF16, causal != 0, stream);
+  p.sign = scale < 0.f ? (dtype == CMPEXT3_DTYPE_F32 ? 0x80000000u : 0x80008000u) : 0u;
+  const hipError_t err = dtype == CMPEXT3_DTYPE_F32
+                             ? cmpext3::launch_bwd32(p, causal != 0, stream)
+                             : cmpext3::launch_bwd16(p, dtype == CMPEXT3_DTYPE_BF16, causal != 0, stream);
   return err == hipSuccess ? CMPEXT3_OK : CMPEXT3_E_LAUNCH;
 }
 

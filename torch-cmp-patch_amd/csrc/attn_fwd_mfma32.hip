@@ -11,6 +11,9 @@
 // V stays row-major in LDS: a PV A-operand element is V[key][d] with d along
 // the 16 lanes of a group, which is a conflict-free LDS read.
 //
+// With p.lse set (the training forward) each row's natural-log log-sum-exp
+// is written too, and the launch is never key-split.
+//
 // Key split (non-causal launches with at most as many query blocks as CUs,
 // such as [1, 8, 1024, 64]): each block's key range is cut into parts run by
 // separate workgroups, which shortens every wave's dependency chain over the
@@ -423,6 +426,12 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
     // a row that saw no key at all gives zeros, as torch does
     const float inv = lrow[qb] > 0.f ? 1.f / lrow[qb] : 0.f;
     const int qrow = qw0 + 16 * qb + l16;
+    // training forward: log-sum-exp in natural log, (m + log2 l) * ln 2
+    // (m is the exp2-domain offset, equal in the row's four lane groups);
+    // -inf for a row that saw no key
+    if (p.lse && qrow < Sq && g == 0)
+      p.lse[(int64_t)bh * Sq + qrow] =
+          lrow[qb] > 0.f ? (m_run[qb] + __builtin_amdgcn_logf(lrow[qb])) * 0.6931471805599453f : -INFINITY;
     if (qrow < Sq) {
       float* orow = og + (int64_t)qrow * p.o_s;
 #pragma unroll
@@ -493,7 +502,8 @@ hipError_t launch_mfma32_bk(const FwdParams& p0, hipStream_t stream) {
   // waves per block that hold query rows (a single block shorter than BQ has fewer)
   const int nwl = p.n_qblk > 1 ? NW : (p.Sq + 15) / 16 < NW ? (p.Sq + 15) / 16 : NW;
   SplitArgs sa = {n, 1, nullptr, nullptr, nwl};
-  const int parts = split_parts32(n, p.Sk, BK, device_cus(), CAUSAL);
+  // the training forward (p.lse) runs every block whole
+  const int parts = p.lse ? 1 : split_parts32(n, p.Sk, BK, device_cus(), CAUSAL);
   if (parts >= 2) {
     // every block is split; one key range of all of them takes part_bytes
     const size_t part_bytes = (size_t)n * nwl * NQB * (NDB + 1) * 64 * sizeof(f32x4);

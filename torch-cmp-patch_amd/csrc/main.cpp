@@ -254,8 +254,8 @@ torch::Tensor attention(torch::Tensor query, torch::Tensor key, torch::Tensor va
 
 namespace {
 
-// Shared checks of the training entry points: 4-D GPU f16/bf16 tensors of one
-// dtype and device, K/V heads dividing the query heads, head dim <= 256.
+// Shared checks of the training entry points: 4-D GPU f16/bf16/fp32 tensors of
+// one dtype and device, K/V heads dividing the query heads, head dim <= 256.
 int training_dtype(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v) {
   TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4, "cmpext3 attention: q, k, v must be 4D");
   TORCH_CHECK(q.is_cuda() && q.device() == k.device() && q.device() == v.device(),
@@ -263,8 +263,8 @@ int training_dtype(const torch::Tensor& q, const torch::Tensor& k, const torch::
   TORCH_CHECK(q.scalar_type() == k.scalar_type() && q.scalar_type() == v.scalar_type(),
               "cmpext3 attention: q, k, v must share one dtype");
   const int dtype = dtype_code(q.scalar_type());
-  TORCH_CHECK(dtype == CMPEXT3_DTYPE_F16 || dtype == CMPEXT3_DTYPE_BF16,
-              "cmpext3 attention: the training path takes fp16/bf16 only");
+  TORCH_CHECK(dtype == CMPEXT3_DTYPE_F16 || dtype == CMPEXT3_DTYPE_BF16 || dtype == CMPEXT3_DTYPE_F32,
+              "cmpext3 attention: the training path takes fp16/bf16/fp32 only");
   TORCH_CHECK(k.size(0) == q.size(0) && k.size(1) >= 1 && q.size(1) % k.size(1) == 0 &&
                   k.size(3) == q.size(3) && v.sizes() == k.sizes(),
               "cmpext3 attention: the training path needs K/V of Q's batch and head dim, with a "
@@ -275,14 +275,22 @@ int training_dtype(const torch::Tensor& q, const torch::Tensor& k, const torch::
   return dtype;
 }
 
-// The ABI's layout: unit head-dim stride, 16-byte aligned base and row strides,
-// head dim a multiple of 8 (zero-padded to Dp otherwise).
+// The ABI's training layout: unit head-dim stride, 16-byte aligned base and
+// row strides, head dim a whole number of 16-byte chunks (zero-padded to Dp
+// otherwise).
 torch::Tensor abi_layout(const torch::Tensor& t, int64_t Dp) {
   const int64_t D = t.size(3);
   if (Dp != D) return at::constant_pad_nd(t, {0, Dp - D}, 0).contiguous();
-  const bool ok = t.stride(3) == 1 && ((uintptr_t)t.data_ptr() & 15u) == 0 && t.stride(0) % 8 == 0 &&
-                  t.stride(1) % 8 == 0 && t.stride(2) % 8 == 0;
+  const int64_t chunk = 16 / t.element_size();
+  const bool ok = t.stride(3) == 1 && ((uintptr_t)t.data_ptr() & 15u) == 0 && t.stride(0) % chunk == 0 &&
+                  t.stride(1) % chunk == 0 && t.stride(2) % chunk == 0;
   return ok ? t : t.contiguous();
+}
+
+// Head dim padded to whole 16-byte chunks of the training dtype.
+int64_t chunk_dim(const torch::Tensor& t) {
+  const int64_t chunk = 16 / t.element_size();
+  return (t.size(3) + chunk - 1) / chunk * chunk;
 }
 
 void strides3(const torch::Tensor& t, int64_t s[3]) {
@@ -304,7 +312,7 @@ std::vector<torch::Tensor> attention_fwd_lse(torch::Tensor query, torch::Tensor 
                                              c10::optional<torch::Tensor> attn_mask) {
   const int dtype = training_dtype(query, key, value);
   const int64_t B = query.size(0), H = query.size(1), Sq = query.size(2), D = query.size(3);
-  const int64_t Sk = key.size(2), Hkv = key.size(1), Dp = (D + 7) / 8 * 8;
+  const int64_t Sk = key.size(2), Hkv = key.size(1), Dp = chunk_dim(query);
   const float scale = resolve_scale(scale_arg, D);
   const at::hip::HIPGuardMasqueradingAsCUDA guard(query.device());
   hipStream_t stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA(query.device().index()).stream();
@@ -342,7 +350,7 @@ std::vector<torch::Tensor> attention_bwd(torch::Tensor query, torch::Tensor key,
                                          c10::optional<torch::Tensor> attn_mask) {
   const int dtype = training_dtype(query, key, value);
   const int64_t B = query.size(0), H = query.size(1), Sq = query.size(2), D = query.size(3);
-  const int64_t Sk = key.size(2), Hkv = key.size(1), Dp = (D + 7) / 8 * 8;
+  const int64_t Sk = key.size(2), Hkv = key.size(1), Dp = chunk_dim(query);
   TORCH_CHECK(out.sizes() == query.sizes() && grad_out.sizes() == query.sizes() &&
                   out.scalar_type() == query.scalar_type() && grad_out.scalar_type() == query.scalar_type(),
               "cmpext3 attention: out / grad_out must match query");
@@ -368,7 +376,7 @@ std::vector<torch::Tensor> attention_bwd(torch::Tensor query, torch::Tensor key,
     // exotic layout is packed rather than refused
     const torch::Tensor o = abi_layout(out, Dp);
     torch::Tensor g = abi_layout(grad_out, Dp);
-    if ((Sq + 64) * std::max<int64_t>(g.stride(2), 1) * 2 >= INT32_MAX) g = g.contiguous();
+    if ((Sq + 64) * std::max<int64_t>(g.stride(2), 1) * g.element_size() >= INT32_MAX) g = g.contiguous();
     const torch::Tensor l = lse.contiguous();
     torch::Tensor delta = torch::empty({B, H, Sq}, query.options().dtype(at::kFloat));
     Mask mask;
@@ -418,7 +426,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("B"), py::arg("H"), py::arg("Sq"), py::arg("Sk"), py::arg("D"),
         py::arg("causal") = false);
   m.def("attention_fwd_lse", &attention_fwd_lse,
-        "Training forward (fp16/bf16, D <= 256): returns (out, lse), lse = fp32 [B,H,Sq] row "
+        "Training forward (fp16/bf16/fp32, D <= 256): returns (out, lse), lse = fp32 [B,H,Sq] row "
         "log-sum-exp (natural log)",
         py::arg("query"), py::arg("key"), py::arg("value"), py::arg("scale") = py::none(),
         py::arg("causal") = false, py::arg("attn_mask") = py::none());
