@@ -129,15 +129,23 @@ def test_describe_key_split_plan():
     assert "decode16" in abi.describe(bf16, 1, 8, 16, 4096, 64)[1]         # 8 units at D = 64
     assert "decode16" not in abi.describe(bf16, 16, 8, 1, 4096, 128)[1]    # 128 units: pipelined
     assert "decode16" not in abi.describe(bf16, 1, 8, 17, 4096, 256)[1]    # 17 rows
-    # other launches at head dims above 128 (one workgroup per CU): fewer
-    # blocks than CUs split into up to CUs / n parts of at least 4 tiles of
-    # 32 keys (at most 32; 8 from the 192 bucket up when every wave of a block
-    # holds rows, as the waves then merge their own rows alone), never causal
-    assert "key-split: 64 x 4 parts" in abi.describe(f16, 1, 8, 1024, 4096, 160)[1]
-    assert "key-split: 4 x 8 parts" in abi.describe(bf16, 1, 4, 100, 3000, 192)[1]
-    assert "key-split: 2 x 23 parts" in abi.describe(bf16, 1, 2, 70, 3000, 160)[1]
+    # prefills at head dims above 128 (rows in at least three waves of a
+    # block, 256+ keys) run the pipelined kernel at one workgroup per CU:
+    # fewer blocks than CUs split into up to CUs / n parts of at least 8
+    # tiles of 32 keys, never causal
+    assert "key-split: 0 whole + 64 x 4 parts" in abi.describe(f16, 1, 8, 1024, 4096, 160)[1]
+    assert "key-split: 0 whole + 4 x 11 parts" in abi.describe(bf16, 1, 4, 100, 3000, 192)[1]
+    assert "key-split: 0 whole + 2 x 11 parts" in abi.describe(bf16, 1, 2, 70, 3000, 160)[1]
     assert "key-split" not in abi.describe(f16, 1, 8, 1024, 4096, 160, True)[1]
     assert "key-split" not in abi.describe(f16, 2, 10, 1024, 1024, 160)[1]
+    assert "pipe16" in abi.describe(f16, 1, 4, 300, 1000, 192, True)[1]
+    # causal bf16 192 keeps the plain kernel (two waves per SIMD fit there),
+    # and so do blocks with rows in at most two waves: up to CUs / n parts of
+    # at least 4 tiles (at most 32; 8 from the 192 bucket up when every wave
+    # of a block holds rows)
+    assert "mfma16" in abi.describe(bf16, 1, 4, 300, 1000, 192, True)[1]
+    assert "mfma16" in abi.describe(bf16, 1, 4, 40, 3000, 192)[1]
+    assert "key-split: 4 x 23 parts" in abi.describe(bf16, 1, 4, 40, 3000, 192)[1]
 
 
 def _call(q=16, k=16, v=16, o=16, dtype=abi.DTYPE_F16, B=1, H=1, Sq=8, Sk=8, D=64,

@@ -12,7 +12,10 @@ inputs):
   * head dims 160, 192 and 256 over long key sweeps (>= 1024 keys, many
     tiles, scores wide enough to force offset rescales), causal and not; the
     reference serves D = 160 at any key length
-    (src/cuda/fp16_flash_attention_hfma2.cu:278-285);
+    (src/cuda/fp16_flash_attention_hfma2.cu:278-285); prefills above 128 on
+    the pipelined kernel (head dims below their bucket, ragged tiles,
+    grouped-query K/V, views, a key split, reruns bit-identical) and the one
+    case kept on the plain kernel;
   * the reference's production sequence length S = 17402
     (cmpext3/__init__.py:16-20, tests_hardware/test_attention_bf16_routing.py:240-243),
     bf16 [1, 4, 17402, 64], causal and not: ragged in every tiling here
@@ -128,6 +131,50 @@ def test_large_head_dims_long_key_sweeps(dtype, D, causal, Sq, Sk, scale):
     ref = orc.sdpa_c(q.cpu(), k.cpu(), v.cpu(), eff, causal)
     err = orc.max_abs_err(out.cpu(), ref)
     assert err <= TOL[dtype], f"max abs err {err:.3e}"
+
+
+WIDE_PREFILL = [
+    # dtype, B, H, Hkv, Sq, Sk, D, causal, layout: head dims above 128 on the
+    # pipelined kernel (unmasked inference, at least three waves of rows,
+    # 256+ keys), D below its bucket (zeroed K columns), ragged tiles,
+    # grouped-query K/V, [B,S,H,D] views, a key split (fewer blocks than CUs)
+    ("bf16", 1, 4, 4, 300, 1000, 256, False, "bhsd"),
+    ("fp16", 2, 4, 2, 257, 257, 136, True, "bhsd"),
+    ("bf16", 1, 8, 2, 65, 700, 200, False, "bhsd"),     # three waves of rows
+    ("fp16", 1, 2, 2, 512, 4096, 248, False, "bshd"),   # key split
+    ("fp16", 1, 3, 3, 200, 333, 192, True, "bshd"),     # fp16 pre-scaled causal 192: pipelined
+    ("bf16", 1, 2, 2, 130, 900, 160, True, "bhsd"),
+]
+
+
+@pytest.mark.parametrize("case", WIDE_PREFILL, ids=[f"{c[0]}-H{c[2]}of{c[3]}-q{c[4]}k{c[5]}d{c[6]}"
+                                                    f"{'c' if c[7] else ''}-{c[8]}" for c in WIDE_PREFILL])
+def test_wide_prefill_on_the_pipelined_kernel(case):
+    dtype, B, H, Hkv, Sq, Sk, D, causal, layout = case
+    text = abi.describe(abi.dtype_code(W.DTYPES[dtype]), B, H, Sq, Sk, D, causal)[1]
+    assert "pipe16" in text and f"DK={(160 if D <= 160 else 192 if D <= 192 else 256)}" in text, text
+    print(f"wide prefill {case}", flush=True)
+    q = W.Workload("wq", dtype, B, H, Sq, Sk, D, seed=Sq + D).make_inputs("cuda", layout=layout)[0]
+    _, k, v = W.Workload("wk", dtype, B, Hkv, Sq, Sk, D, seed=Sk + D).make_inputs("cuda", layout=layout)
+    scale = 1.0 / math.sqrt(D)
+    out = abi.attn_fwd(q, k, v, scale, causal)
+    again = abi.attn_fwd(q, k, v, scale, causal)
+    torch.cuda.synchronize()
+    g = H // Hkv
+    kx, vx = (t.cpu().repeat_interleave(g, dim=1) for t in (k, v))
+    err = orc.max_abs_err(out.cpu(), orc.sdpa_np(q.cpu(), kx, vx, scale, causal))
+    assert err <= TOL[dtype], f"max abs err {err:.3e}"
+    assert torch.equal(out, again)
+
+
+def test_wide_prefill_exception_stays_on_the_plain_kernel():
+    """Causal bf16 launches of the 192 bucket keep the plain head-dim > 128
+    kernel (two waves per SIMD there); its output matches the oracle."""
+    assert "mfma16" in abi.describe(abi.dtype_code(torch.bfloat16), 1, 4, 300, 1000, 192, True)[1]
+    q, k, v = _inputs("bf16", 1, 2, 300, 1000, 192, seed=5)
+    out = abi.attn_fwd(q, k, v, 0.07, True)
+    torch.cuda.synchronize()
+    assert orc.max_abs_err(out.cpu(), orc.sdpa_c(q.cpu(), k.cpu(), v.cpu(), 0.07, True)) <= TOL["bf16"]
 
 
 @pytest.mark.parametrize("Sk", [1, 17, 48, 49, 64, 65, 77, 80, 81, 100, 112, 113, 128])

@@ -145,5 +145,7 @@ def test_describe_names_the_kernel():
     # SDXL cross-attention (77 keys): all of K/V in LDS, one pass per row
     assert "short16" in cmpext3.ops.describe(0, 2, 10, 4096, 77, 64, False)
     assert "short16" not in cmpext3.ops.describe(0, 2, 10, 4096, 77, 64, True)
-    assert "mfma16" in cmpext3.ops.describe(0, 2, 10, 4096, 4096, 256, False)
+    # head dims above 128: prefills on the pipelined kernel, one wave per SIMD
+    assert "pipe16" in cmpext3.ops.describe(0, 2, 10, 4096, 4096, 256, False)
+    assert "mfma16" in cmpext3.ops.describe(0, 2, 10, 64, 4096, 256, False)  # two waves of rows
     assert "mfma32" in cmpext3.ops.describe(2, 2, 8, 4096, 4096, 40, False)

@@ -24,7 +24,7 @@ hipError_t launch_mfma16(const FwdParams& p, bool bf16, bool causal, hipStream_t
 hipError_t launch_mfma32(const FwdParams& p, bool causal, hipStream_t s);
 int mfma16_bucket(int D);
 int mfma32_bucket(int D);
-void describe_mfma16(int D, int B, int H, int Sq, int Sk, bool causal, char* buf, int len);
+void describe_mfma16(int D, int B, int H, int Sq, int Sk, bool causal, bool bf16, char* buf, int len);
 void describe_mfma32(int D, int B, int H, int Sq, int Sk, bool causal, char* buf, int len);
 }  // namespace cmpext3
 
@@ -161,7 +161,7 @@ int cmpext3_attn_describe(int dtype, int B, int H, int Sq, int Sk, int D, int ca
       if (dtype == CMPEXT3_DTYPE_F32)
         cmpext3::describe_mfma32(D, B, H, Sq, Sk, causal != 0, kb, sizeof kb);
       else
-        cmpext3::describe_mfma16(D, B, H, Sq, Sk, causal != 0, kb, sizeof kb);
+        cmpext3::describe_mfma16(D, B, H, Sq, Sk, causal != 0, dtype == CMPEXT3_DTYPE_BF16, kb, sizeof kb);
       snprintf(buf, len, "%s%s", kb, causal ? " causal" : "");
     }
   }

@@ -1,8 +1,9 @@
 // Instantiations and tile table of the fp16/bf16 MFMA attention kernel
 // (kernel template in attn_fwd_mfma16.h), and the fp16/bf16 entry point:
-// head dims up to 128 go to the software-pipelined kernel
-// (attn_fwd_pipe16.hip); larger head dims, and K/V row strides too large for
-// its 32-bit buffer offsets, run this one.
+// head dims up to 128, and unmasked inference prefills above 128, go to the
+// software-pipelined kernel (attn_fwd_pipe16.hip); the other launches above
+// 128 (masked, training, few query rows, short key sweeps), and K/V row
+// strides too large for its 32-bit buffer offsets, run this one.
 //
 // The tile table replaces the reference's hard-coded per-head-dim template
 // table (src/cuda/fp16_flash_attention_hfma2.cu:278-285) and its build-time
@@ -103,6 +104,13 @@ int mfma16_bucket(int D) {
 // path is taken for fp16 (for bf16 the scaled Q would keep only 8 mantissa bits).
 static bool use_prescale(const FwdParams& p, bool bf16) { return !bf16 && p.c <= 1.0f; }
 
+// Head-dim > 128 prefills go to the pipelined kernel except causal launches
+// of the 192 bucket without pre-scaled Q: there this kernel's instantiation
+// fits two waves per SIMD (252 registers) and measured faster on MI355X
+// (bf16 [1,32/8,4096,4096,192] causal 221 against 254 us, same run; fp16
+// pre-scaled, at one wave per SIMD here, 307 against 266 us).
+static bool keeps_wide(int dk, bool causal, bool prescale) { return dk == 192 && causal && !prescale; }
+
 hipError_t launch_mfma16(const FwdParams& p0, bool bf16, bool causal, hipStream_t s) {
   const int dk = mfma16_bucket(p0.D);
   if (dk < 0) return hipErrorInvalidValue;
@@ -139,7 +147,8 @@ hipError_t launch_mfma16(const FwdParams& p0, bool bf16, bool causal, hipStream_
                   : launch_bucket<_Float16, false, false, 64>(p, dk, s);
   }
   if (short16_applies(p, dk, causal)) return launch_short16(p, dk, bf16, s);
-  if (pipe16_applies(p, dk)) return launch_pipe16(p, dk, bf16, causal, use_prescale(p, bf16), s);
+  if (pipe16_applies(p, dk) && !keeps_wide(dk, causal, use_prescale(p, bf16)))
+    return launch_pipe16(p, dk, bf16, causal, use_prescale(p, bf16), s);
   // training forwards reach this kernel above D = 128 only (the pipelined
   // kernel writes the log-sum-exp up to 128); masked launches likewise
   if (p.lse) {
@@ -167,7 +176,7 @@ hipError_t launch_mfma16(const FwdParams& p0, bool bf16, bool causal, hipStream_
 
 int mfma16_max_bk() { return 64; }
 
-void describe_mfma16(int D, int B, int H, int Sq, int Sk, bool causal, char* buf, int len) {
+void describe_mfma16(int D, int B, int H, int Sq, int Sk, bool causal, bool bf16, char* buf, int len) {
   const int dk = mfma16_bucket(D);
   FwdParams p = {};
   p.Sk = Sk;
@@ -189,7 +198,9 @@ void describe_mfma16(int D, int B, int H, int Sq, int Sk, bool causal, char* buf
     describe_short16(dk, Sq, Sk, buf, len);
     return;
   }
-  if ((!elem || D % 2 == 0) && pipe16_applies(p, dk)) {
+  // (narrow rows above 128 stay here; the default scale: fp16 pre-scales Q)
+  const bool wide = dk > 128;
+  if ((!elem || (D % 2 == 0 && !wide)) && pipe16_applies(p, dk) && !(wide && keeps_wide(dk, causal, !bf16))) {
     describe_pipe16(elem ? (dk <= 64 ? 64 : 128) : dk, B, H, Sq, Sk, causal, elem, buf, len);
     if (elem) snprintf(buf + strlen(buf), len - strlen(buf), " narrow rows");
     return;

@@ -1,12 +1,14 @@
 // Instantiations, tile table and key-split plan of the software-pipelined
 // fp16/bf16 kernel (template in attn_fwd_pipe16.h), used for head dims up to
-// 128.
+// 128, and for the unmasked inference prefills above 128 (instantiations in
+// attn_fwd_pipe16w.hip).
 //
 // Like the v2 table in attn_fwd_mfma16.hip this replaces the reference's
 // per-head-dim template table (src/cuda/fp16_flash_attention_hfma2.cu:278-285);
 // entries come from an offline sweep on an MI355X.  All buckets use 4-wave
 // workgroups and 32-key tiles; the waves per SIMD are the most the registers
-// allow without spilling (D = 32: 4, D <= 64: 3, D <= 128: 2).
+// allow without spilling (D = 32: 4, D <= 64: 3, D <= 128: 2; above 128 one,
+// with accumulation registers as the spill space).
 //
 // The key split (no counterpart in the reference) needs exchange space, and
 // the library allocates none: the workspace entry points take it from the
@@ -26,7 +28,7 @@ namespace {
 
 constexpr int kPipeNw = 4;
 constexpr int kPipeBk = 32;
-constexpr int pipe_occ(int dk) { return dk <= 32 ? 4 : dk <= 64 ? 3 : 2; }
+constexpr int pipe_occ(int dk) { return dk <= 32 ? 4 : dk <= 64 ? 3 : dk <= 128 ? 2 : 1; }
 // masked launches need a few more registers: D = 32 drops to 3 waves per SIMD
 constexpr int pipe_occ_masked(int dk) { return dk <= 64 ? 3 : 2; }
 
@@ -235,6 +237,9 @@ hipError_t launch_bucket(const FwdParams& p, const SplitArgs& sa, int dk, hipStr
 
 }  // namespace
 
+hipError_t launch_pipe16_wide(const FwdParams& p, const SplitArgs& sa, int dk, bool bf16, bool causal,
+                              bool prescale, hipStream_t s);
+
 // Compute units of the current device (256 on MI355X), cached per device.
 int device_cus() {
   static int cus[64] = {};
@@ -292,12 +297,18 @@ int bind_exchange(const FwdParams& p, int parts, size_t part_bytes, int ncnt, f3
 // True when the pipelined kernel takes this problem: head-dim bucket <= 128,
 // a key sweep long enough for its prologue (four tiles in flight) to pay off
 // (shorter sweeps run faster on the short-key and v2 kernels) unless an
-// attention mask or the log-sum-exp output is asked for (only this kernel
-// has them), and K/V tiles addressable with 32-bit buffer offsets.
+// attention mask or the log-sum-exp output is asked for (up to D = 128 only
+// this kernel has them), and K/V tiles addressable with 32-bit buffer
+// offsets.  Above D = 128: unmasked inference launches whose query blocks
+// hold rows in at least three of their four waves (fewer rows: the decode
+// and packed-row paths) and sweep at least kPipeMinSk keys.
 constexpr int kPipeMinSk = 256;
 
 bool pipe16_applies(const FwdParams& p, int dk) {
-  if (dk > 128 || (p.Sk < kPipeMinSk && p.mask_kind == MASK_NONE && !p.lse)) return false;
+  if (dk > 128 && (p.lse || p.elem_rows || p.mask_kind != MASK_NONE || p.Sq <= (kPipeNw - 2) * 32 ||
+                   p.Sk < kPipeMinSk))
+    return false;
+  if (p.Sk < kPipeMinSk && p.mask_kind == MASK_NONE && !p.lse) return false;
   const int64_t rs = p.k_s > p.v_s ? p.k_s : p.v_s;
   return (int64_t)(p.Sk + kPipeBk) * rs * 2 < (int64_t(1) << 31);
 }
@@ -378,6 +389,7 @@ hipError_t launch_pipe16(const FwdParams& p0, int dk0, bool bf16, bool causal, b
     if (sk_need > p.dry->need) p.dry->need = sk_need;
     return hipSuccess;
   }
+  if (dk > 128) return launch_pipe16_wide(p, sa, dk, bf16, causal, prescale, s);
   if (p.lse) {  // training forward, masked or not
     if (bf16) return causal ? launch_lse<__bf16, true, false>(p, sa, dk, s) : launch_lse<__bf16, false, false>(p, sa, dk, s);
     if (prescale)
