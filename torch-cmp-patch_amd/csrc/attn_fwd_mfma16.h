@@ -157,6 +157,55 @@ __device__ __forceinline__ void mask_run8(f32x16& sc, int r0, const __amdgpu_buf
   }
 }
 
+// The mask words of one run of 8 keys (whole runs: an 8-, 16- or 32-byte
+// read), split from their use so that a tile can test them first.
+struct MaskRun8 {
+  u32x4 w0, w1;  // bool: w0.xy; f16/bf16: w0; f32: w0, w1
+};
+__device__ __forceinline__ MaskRun8 mask_load8(const __amdgpu_buffer_rsrc_t& mrs, int off, int kind) {
+  MaskRun8 m;
+  m.w1 = (u32x4){0u, 0u, 0u, 0u};
+  if (kind == MASK_BOOL) {
+    const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(mrs, off, 0, 0));
+    m.w0 = (u32x4){w[0], w[1], 0x01010101u, 0x01010101u};
+  } else {
+    m.w0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(mrs, off, 0, 0));
+    if (kind == MASK_F32) m.w1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(mrs, off + 16, 0, 0));
+  }
+  return m;
+}
+// True when the run leaves every score as it is: no zero bool byte, or every
+// additive value +0 (bit pattern zero).
+__device__ __forceinline__ bool mask_run_keeps(const MaskRun8& m, int kind) {
+  if (kind == MASK_BOOL) {
+    uint32_t z = 0;  // high bit of every zero byte (the classic has-zero-byte test)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) z |= (m.w0[i] - 0x01010101u) & ~m.w0[i] & 0x80808080u;
+    return z == 0u;
+  }
+  const u32x4 o = m.w0 | m.w1;
+  return (o[0] | o[1] | o[2] | o[3]) == 0u;
+}
+// Apply a loaded run to sc[r0 .. r0 + 7] as mask_run8 does.
+__device__ __forceinline__ void mask_apply8(f32x16& sc, int r0, const MaskRun8& m, int kind) {
+  if (kind == MASK_BOOL) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (((m.w0[i >> 2] >> (8 * (i & 3))) & 0xffu) == 0u) sc[r0 + i] = -INFINITY;
+  } else if (kind == MASK_F32) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      sc[r0 + i] = __builtin_fmaf(__uint_as_float(i < 4 ? m.w0[i] : m.w1[i - 4]), kLog2e, sc[r0 + i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x2 a = kind == MASK_F16 ? Elt<_Float16>::unpack(m.w0[i]) : Elt<__bf16>::unpack(m.w0[i]);
+      sc[r0 + 2 * i] = __builtin_fmaf(a[0], kLog2e, sc[r0 + 2 * i]);
+      sc[r0 + 2 * i + 1] = __builtin_fmaf(a[1], kLog2e, sc[r0 + 2 * i + 1]);
+    }
+  }
+}
+
 // Bytes of the mask buffer of one (batch, head) that a kernel may read: up
 // to key Sk - 1 of the last row (narrow), or up to Sk rounded up to 8.
 __device__ __forceinline__ int64_t mask_span(const FwdParams& p, int mes) {

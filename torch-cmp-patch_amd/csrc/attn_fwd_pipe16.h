@@ -109,7 +109,7 @@ __device__ __forceinline__ void pipe16_segment(const FwdParams& p, const SplitAr
   constexpr int NKS = DK / 16;            // score k-steps
   static_assert(BK % 32 == 0 && DK % 16 == 0 && DP % 32 == 0 && DK <= DP, "tile shape");
   constexpr bool DMA = (OPT & 256) != 0;
-  static_assert(!(DMA && (NARROW || MASK || (OPT & 128))), "LDS DMA: plain unmasked launches only");
+  static_assert(!(DMA && (NARROW || (OPT & 128))), "LDS DMA: whole-chunk rows, every wave computing");
   constexpr bool STREAMK = (OPT & 512) != 0;  // segments of an equal-work split (kernel below)
   constexpr int NR = DMA ? 4 : 2;  // K (and V) tiles held in LDS
   // With DMA: one barrier per two tiles.  The barrier before an even
@@ -464,14 +464,35 @@ __device__ __forceinline__ void pipe16_segment(const FwdParams& p, const SplitAr
       uniform_rsrc(MASK ? (const void*)((const char*)p.mask + (b * p.m_b + h * p.m_h) * mes) : p.q,
                    MASK ? mask_span(p, mes) : 0);
   const int mrow_off = MASK ? (int)((int64_t)min(qrow, Sq - 1) * p.m_q * mes) : 0;
+  // Whole runs are loaded first and applied only when some lane's keys of
+  // the tile are dropped or biased (a wave-uniform test): a key-padding mask
+  // leaves every tile before its padding untouched, and those tiles skip the
+  // 16 selects or FMAs per 32-key block.
   auto add_mask = [&](int j, f32x16 (&sc)[NKB]) {
     const int k0 = (tbase + j) * BK;
+    if (p.mask_narrow) {
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int run = 0; run < 2; ++run)  // keys k0 + 32 kb + 16 run + 8 hh .. + 7
+          mask_run8(sc[kb], 8 * run, mrs, mrow_off + (k0 + 32 * kb + 16 * run + 8 * hh) * mes, p.mask_kind, true);
+      return;
+    }
+    MaskRun8 mr[NKB][2];
+    bool keeps = true;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-      for (int run = 0; run < 2; ++run)  // keys k0 + 32 kb + 16 run + 8 hh .. + 7
-        mask_run8(sc[kb], 8 * run, mrs, mrow_off + (k0 + 32 * kb + 16 * run + 8 * hh) * mes, p.mask_kind,
-                  p.mask_narrow);
+      for (int run = 0; run < 2; ++run) {
+        mr[kb][run] = mask_load8(mrs, mrow_off + (k0 + 32 * kb + 16 * run + 8 * hh) * mes, p.mask_kind);
+        keeps = keeps && mask_run_keeps(mr[kb][run], p.mask_kind);
+      }
+    if (__builtin_amdgcn_ballot_w64(!keeps)) {
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int run = 0; run < 2; ++run) mask_apply8(sc[kb], 8 * run, mr[kb][run], p.mask_kind);
+    }
   };
   // this lane's half of the row max (the two halves meet at the decision)
   auto row_max = [&](const f32x16 (&sc)[NKB]) {

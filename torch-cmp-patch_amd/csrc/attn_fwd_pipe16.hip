@@ -178,6 +178,14 @@ hipError_t launch_dk(const FwdParams& p, const SplitArgs& sa, hipStream_t s) {
     if (p.D == DK) return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, occ, CAUSAL, PRESCALE, 1 | 2 | 256>(p, sa, s);
     return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, occ, CAUSAL, PRESCALE, 1 | 2 | 8 | 256>(p, sa, s);
   }
+  // masked launches of those buckets: the same LDS DMA, whose freed staging
+  // registers the mask words use (masked fp16 D = 64 spilled 3-21 registers
+  // with register staging; SDXL self-attention with a key-padding mask
+  // 162 -> 121 us with the mask test of attn_fwd_pipe16.h)
+  if constexpr (MOPT != 0 && (DK == 32 || DK == 64 || DK == 128)) {
+    if (p.D == DK) return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, occ, CAUSAL, PRESCALE, 1 | 2 | 256 | MOPT>(p, sa, s);
+    return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, occ, CAUSAL, PRESCALE, 1 | 2 | 8 | 256 | MOPT>(p, sa, s);
+  }
   if (p.D == DK) return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, occ, CAUSAL, PRESCALE, 1 | MOPT>(p, sa, s);
   return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, occ, CAUSAL, PRESCALE, 1 | 8 | MOPT>(p, sa, s);
 }
@@ -186,8 +194,8 @@ hipError_t launch_dk(const FwdParams& p, const SplitArgs& sa, hipStream_t s) {
 // attention mask): buckets 64 and 128 only.
 template <typename T, bool CAUSAL, bool PRESCALE, int MOPT>
 hipError_t launch_lse_m(const FwdParams& p, const SplitArgs& sa, int dk, hipStream_t s) {
-  // unmasked: K/V straight into swizzled LDS, as for inference
-  constexpr int LD = MOPT ? 0 : 2 | 256;
+  // K/V straight into swizzled LDS, as for inference
+  constexpr int LD = 2 | 256;
   if (dk == 64) {
     if (p.D == 64)
       return launch_pipe16_cfg<T, 64, kPipeNw, kPipeBk, pipe_occ(64), CAUSAL, PRESCALE, 1 | 32 | MOPT | LD>(p, sa, s);
