@@ -29,7 +29,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["attn_fwd_mfma16.hip", "attn_fwd_pipe16.hip", "attn_fwd_pipe16w.hip", "attn_fwd_short16.hip", "attn_fwd_mfma32.hip",
+HIP_SOURCES = ["attn_fwd_mfma16.hip", "attn_fwd_pipe16.hip", "attn_fwd_pipe16w.hip", "attn_fwd_pipe16wm.hip", "attn_fwd_short16.hip", "attn_fwd_mfma32.hip",
                "attn_fwd_decode16.hip", "attn_bwd16.hip", "attn_bwd32.hip", "attn_abi.cpp"]
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall",
@@ -45,7 +45,8 @@ HIP_FLAGS = [
 # fp16 D <= 64 instantiations into spills at 3 waves per SIMD.  Its common
 # path has no max operations, so the quieting instructions cost nothing there.
 FILE_FLAGS_DROP = {"attn_fwd_pipe16.hip": {"-mno-amdgpu-ieee", "-fno-honor-nans"},
-                   "attn_fwd_pipe16w.hip": {"-mno-amdgpu-ieee", "-fno-honor-nans"}}
+                   "attn_fwd_pipe16w.hip": {"-mno-amdgpu-ieee", "-fno-honor-nans"},
+                   "attn_fwd_pipe16wm.hip": {"-mno-amdgpu-ieee", "-fno-honor-nans"}}
 
 LIB_NAME = "libcmpext3_attn.so"
 

@@ -307,15 +307,14 @@ int bind_exchange(const FwdParams& p, int parts, size_t part_bytes, int ncnt, f3
 // (shorter sweeps run faster on the short-key and v2 kernels) unless an
 // attention mask or the log-sum-exp output is asked for (up to D = 128 only
 // this kernel has them), and K/V tiles addressable with 32-bit buffer
-// offsets.  Above D = 128: unmasked inference launches whose query blocks
-// hold rows in at least three of their four waves (fewer rows: the decode
-// and packed-row paths) and sweep at least kPipeMinSk keys.
+// offsets.  Above D = 128: launches with whole-chunk rows whose query
+// blocks hold rows in at least three of their four waves (fewer rows: the
+// decode and packed-row paths) and sweep at least kPipeMinSk keys, masked or
+// not, inference or training.
 constexpr int kPipeMinSk = 256;
 
 bool pipe16_applies(const FwdParams& p, int dk) {
-  if (dk > 128 && (p.lse || p.elem_rows || p.mask_kind != MASK_NONE || p.Sq <= (kPipeNw - 2) * 32 ||
-                   p.Sk < kPipeMinSk))
-    return false;
+  if (dk > 128 && (p.elem_rows || p.Sq <= (kPipeNw - 2) * 32 || p.Sk < kPipeMinSk)) return false;
   if (p.Sk < kPipeMinSk && p.mask_kind == MASK_NONE && !p.lse) return false;
   const int64_t rs = p.k_s > p.v_s ? p.k_s : p.v_s;
   return (int64_t)(p.Sk + kPipeBk) * rs * 2 < (int64_t(1) << 31);
@@ -353,8 +352,12 @@ hipError_t launch_pipe16(const FwdParams& p0, int dk0, bool bf16, bool causal, b
   FwdParams p = p0;
   if (packs_query_heads(p, causal)) pack_query_heads(p);
   // the training forward and the narrow-row variants have the 64 and 128
-  // buckets only
-  const int dk = (p.lse || p.elem_rows) ? (dk0 <= 64 ? 64 : 128) : dk0;
+  // buckets only up to D = 128; above it the training forward has 192 and
+  // 256, and neither it nor masked launches pre-scale Q (one instantiation
+  // per dtype)
+  const int dk = dk0 > 128 ? (p.lse && dk0 < 192 ? 192 : dk0)
+                           : (p.lse || p.elem_rows) ? (dk0 <= 64 ? 64 : 128) : dk0;
+  if (dk > 128 && (p.lse || p.mask_kind != MASK_NONE)) prescale = false;
   if (p.elem_rows && (p.elem_rows < 4 || p.lse)) return hipErrorNotSupported;
   // Without pre-scaling, masked keys enter as raw -inf and meet the multiplier
   // c in one FMA; scale 0 would make that 0 * -inf.  A multiplier of 1e-30

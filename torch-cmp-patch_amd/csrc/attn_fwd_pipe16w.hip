@@ -1,6 +1,7 @@
 // Instantiations of the software-pipelined fp16/bf16 kernel (template in
 // attn_fwd_pipe16.h) for head dims above 128: unmasked inference prefills of
-// the 160, 192 and 256 buckets (plan and dispatch in attn_fwd_pipe16.hip).
+// the 160, 192 and 256 buckets (plan and dispatch in attn_fwd_pipe16.hip;
+// masked and training launches in attn_fwd_pipe16wm.hip).
 // One wave per SIMD (the O accumulator alone takes DK registers per lane, and
 // the compiler parks what does not fit in the accumulation registers), K/V
 // tiles straight into LDS with padded rows (no swizzle above 128), 32-key
@@ -33,8 +34,13 @@ hipError_t launch_wide(const FwdParams& p, const SplitArgs& sa, int dk, hipStrea
 
 }  // namespace
 
+hipError_t launch_pipe16_wide_mt(const FwdParams& p, const SplitArgs& sa, int dk, bool bf16, bool causal,
+                                 hipStream_t s);
+
 hipError_t launch_pipe16_wide(const FwdParams& p, const SplitArgs& sa, int dk, bool bf16, bool causal,
                               bool prescale, hipStream_t s) {
+  // masked and training launches: attn_fwd_pipe16wm.hip (never pre-scaled)
+  if (p.lse || p.mask_kind != MASK_NONE) return launch_pipe16_wide_mt(p, sa, dk, bf16, causal, s);
   if (bf16) return causal ? launch_wide<__bf16, true, false>(p, sa, dk, s) : launch_wide<__bf16, false, false>(p, sa, dk, s);
   if (prescale)
     return causal ? launch_wide<_Float16, true, true>(p, sa, dk, s) : launch_wide<_Float16, false, true>(p, sa, dk, s);
