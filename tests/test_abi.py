@@ -281,6 +281,11 @@ def test_training_plans_that_run_whole():
             assert abi.plan(abi.DTYPE_F32, 1, 8, 8, 1024, 1024, D, 1 << 30, mdt, with_lse=True) == (abi.OK, 1)
     # the inference forward of the same fp32 problem splits (128 blocks x 4 parts)
     assert abi.plan(abi.DTYPE_F32, 1, 8, 8, 1024, 1024, 64, 1 << 30) == (abi.OK, 4)
+    # f16/bf16 training prefills above D = 128 take the pipelined kernel,
+    # which splits small grids like the inference launch (64 blocks x 4 parts)
+    need = abi.workspace_size(abi.DTYPE_BF16, 1, 8, 8, 1024, 4096, 256, with_lse=True)
+    assert need > 0
+    assert abi.plan(abi.DTYPE_BF16, 1, 8, 8, 1024, 4096, 256, need, with_lse=True) == (abi.OK, 4)
 
 
 def _call_masked(k_row=64, q_row=64, o_row=64, Sk=1 << 17, Sq=1, mask_str=(0, 0, 0), lse=0,

@@ -1,6 +1,7 @@
 """GPU parity of the training pair at head dims above 128: the forward that
-keeps the row log-sum-exp (cmpext3_attn_fwd_lse, here on the head-dim > 128
-kernel in its 192 and 256 buckets, never key-split) and the backward
+keeps the row log-sum-exp (cmpext3_attn_fwd_lse, in its 192 and 256 buckets:
+the pipelined kernel for prefills of more than 64 rows and 256+ keys, key
+split included, else the head-dim > 128 kernel) and the backward
 (cmpext3_attn_bwd, gradient kernels in the 192 and 256 buckets at one wave per
 SIMD), through the C ABI, plus the autograd Function and the SDPA route.
 
@@ -70,6 +71,7 @@ CASES = [
     ("bf16", 1, 8, 2, 150, 260, 256, True, None),     # grouped-query K/V
     ("fp16", 1, 4, 1, 100, 300, 160, False, None),    # multi-query
     ("bf16", 1, 4, 4, 1024, 1024, 256, True, None),   # a long causal sweep
+    ("fp16", 1, 2, 2, 512, 4096, 200, False, None),   # pipelined forward, key split (8 blocks x 16 parts)
 ]
 
 
@@ -144,6 +146,7 @@ def _mask(kind, B, H, Sq, Sk, dtype, seed):
 MASK_CASES = [
     # dtype, B, H, Hkv, Sq, Sk, D, kind
     ("bf16", 2, 2, 2, 160, 300, 256, "bool_pad"),
+    ("fp16", 1, 2, 2, 300, 2048, 192, "add_heads"),   # pipelined forward, key split when non-causal
     ("fp16", 1, 4, 2, 120, 264, 192, "bool_full"),
     ("bf16", 1, 2, 1, 90, 200, 160, "add_heads"),
 ]
