@@ -92,6 +92,51 @@ def test_mask_parity(case, kind, causal):
     assert orc.max_abs_err(out.cpu(), ref) <= TOL[dtype]
 
 
+BCAST = [
+    # dtype, B, H, Sq, Sk, D, causal, mask: masks that are the same for every
+    # query row (key padding, per-head biases, a single query row) and are
+    # read in whole runs: their tile slices ride the pipelined kernel's LDS
+    # ring (D = 32/64/128 buckets)
+    ("fp16", 2, 3, 300, 1000, 64, False, "pad_bool"),
+    ("bf16", 1, 4, 200, 777, 128, True, "head_bias_bf16"),     # [1,H,1,Sk] expanded, ragged Sk
+    ("fp16", 2, 2, 130, 2056, 32, False, "pad_f32"),           # additive fp32, key split
+    ("bf16", 2, 4, 1, 4096, 128, False, "row_bool"),           # one query row, [B,H,1,Sk]
+    ("fp16", 1, 2, 96, 520, 80, True, "pad_bool"),             # 96 bucket: register-staged loads
+]
+
+
+@pytest.mark.parametrize("case", BCAST, ids=[f"{c[0]}-B{c[1]}H{c[2]}-q{c[3]}k{c[4]}d{c[5]}{'c' if c[6] else ''}-{c[7]}"
+                                             for c in BCAST])
+def test_query_broadcast_masks(case):
+    dtype, B, H, Sq, Sk, D, causal, kind = case
+    q, k, v = _inputs(dtype, B, H, Sq, Sk, D, seed=Sq + Sk + D)
+    g = torch.Generator().manual_seed(Sk)
+    if kind == "pad_bool":
+        m = torch.ones(B, 1, 1, Sk, dtype=torch.bool)
+        for b in range(B):
+            m[b, ..., Sk - 37 * (b + 1):] = False
+            m[b, ..., 3] = False
+    elif kind == "head_bias_bf16":
+        m = (torch.randn(1, H, 1, Sk, generator=g) * 3).bfloat16()
+        m[..., 5::7] = -math.inf
+        m = m.expand(B, H, Sq, Sk)
+    elif kind == "pad_f32":
+        m = torch.zeros(B, 1, 1, Sk)
+        m[..., -100:] = -math.inf
+        m[0, ..., :40] = -2.5
+    else:
+        m = torch.rand(B, H, 1, Sk, generator=g) > 0.5
+        m[..., 0] = True
+    m = m.cuda()
+    scale = 1.0 / math.sqrt(D)
+    out = abi.attn_fwd(q, k, v, scale, causal, attn_mask=m)
+    again = abi.attn_fwd(q, k, v, scale, causal, attn_mask=m)
+    torch.cuda.synchronize()
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), scale, causal=causal, attn_mask=m.cpu())
+    assert orc.max_abs_err(out.cpu(), ref) <= TOL[dtype]
+    assert torch.equal(out, again)
+
+
 def test_fully_masked_rows_are_zero():
     q, k, v = _inputs("fp16", 1, 2, 64, 600, 64, seed=3)
     m = torch.ones(1, 2, 64, 600, dtype=torch.bool, device="cuda")

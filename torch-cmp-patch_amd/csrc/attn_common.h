@@ -184,6 +184,14 @@ __device__ __forceinline__ void lds_dma16(const u32x4& rs, uint32_t lds_byte, in
                : "memory");
 }
 
+// 4 bytes per lane from the buffer straight into LDS at lds_byte + 4 i (as
+// lds_dma16; used for the small per-tile slices of attention masks).
+__device__ __forceinline__ void lds_dma4(const u32x4& rs, uint32_t lds_byte, int voff, int soff) {
+  asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, %2 offen lds"
+               ::"v"(voff), "s"(rs), "s"(soff), "{m0}"(lds_byte)
+               : "memory");
+}
+
 // Narrow row access (FwdParams::elem_rows = a, the largest of 2, 4, 8 bytes
 // that divides every base pointer, every row stride and the row length D *
 // element size): for head dims that are not a whole number of 16-byte chunks

@@ -73,7 +73,10 @@ namespace cmpext3 {
 // barrier, with no staging registers and no LDS store instructions; every
 // wave issues the same number of these loads per tile and waits for its own
 // with an explicit vmcnt before the barrier that publishes them (the
-// compiler does not track LDS written this way).
+// compiler does not track LDS written this way).  OPT bit 10 (with bits 4
+// and 8): the mask is the same for every query row (m_q = 0, or one row)
+// and read in whole runs: wave 0 loads each tile's slice of the mask row
+// into a ring beside K, and the waves read it from LDS after the barrier.
 // One workgroup's work on one query block: key tiles [g.tbase, g.tbase +
 // g.ntiles) of block (g.bh, g.qblk).  With g.nparts > 1 that is key range
 // g.part of the block's g.nparts, exchanged through row g.sb of the exchange
@@ -119,9 +122,13 @@ __device__ __forceinline__ void pipe16_segment(const FwdParams& p, const SplitAr
   // of its loads before the next barrier, two iterations later (measured
   // 2-4% faster than a barrier per tile with loads three tiles ahead)
 
-  __shared__ __attribute__((aligned(16))) uint16_t lds[NR * KTILE + NR * VTILE];
+  // masked DMA launches: a ring of NR 128-byte slices of the mask, one per
+  // tile (query-broadcast masks; see add_mask)
+  constexpr int MSLOT = (MASK && DMA) ? 64 : 0;  // halves per mask slice
+  __shared__ __attribute__((aligned(16))) uint16_t lds[NR * KTILE + NR * VTILE + NR * MSLOT];
   uint16_t* const kbase = lds;                // K(j) at kbase + (j % NR) * KTILE
   uint16_t* const vbase = lds + NR * KTILE;   // V(j) at vbase + (j % NR) * VTILE
+  uint16_t* const mbase = lds + NR * (KTILE + VTILE);  // mask slice of tile j at mbase + (j % NR) * MSLOT
 
   const int tid = thread_x();
   const int wave = tid >> 6;
@@ -328,6 +335,25 @@ __device__ __forceinline__ void pipe16_segment(const FwdParams& p, const SplitAr
       if (64 * i + lane < SPWV)
         lds_dma16(vrw, lds0 + 2 * (NR * KTILE + slot * VTILE + (wv * SPWV + 64 * i) * 8), dvo[i], so);
   };
+  // Query-broadcast masks (every row the same: m_q = 0, or one row) read in
+  // whole runs: wave 0 brings tile j's BK keys of the mask row (BK * element
+  // size bytes, at most 128) into ring slot `slot` with K(j), 4 bytes per
+  // lane, so that the waves read them from LDS after the barrier that
+  // publishes K(j) instead of waiting on a memory load inside the step.
+  constexpr bool MBC = (OPT & 1024) != 0;  // the host sends only such masks with this bit
+  static_assert(!MBC || (MASK && DMA), "mask slices ride the LDS DMA ring");
+  const bool mbc = MBC;
+  const int mbytes = p.mask_kind == MASK_BOOL ? 1 : p.mask_kind == MASK_F32 ? 4 : 2;
+  const u32x4 mrw = uniform_rsrc_words(MASK ? (const void*)((const char*)p.mask + (b * p.m_b + h * p.m_h) * mbytes)
+                                            : (const void*)p.q,
+                                       MASK ? mask_span(p, mbytes) : 0);
+  auto dma_m = [&](int j, int slot) {
+    if (mbc && wv == 0 && lane < BK * mbytes / 4) {
+      int vo = 4 * lane;
+      asm volatile("" : "+v"(vo));  // computed here, not held through the loop
+      lds_dma4(mrw, lds0 + 2 * (NR * (KTILE + VTILE) + slot * MSLOT), vo, (tbase + min(j, ntiles - 1)) * BK * mbytes);
+    }
+  };
 
   // OPT 128: the rowless waves (ltid = their thread index, nlt = their
   // thread count, at least 128) move every chunk of a tile.  Chunks past the
@@ -470,6 +496,39 @@ __device__ __forceinline__ void pipe16_segment(const FwdParams& p, const SplitAr
   // 16 selects or FMAs per 32-key block.
   auto add_mask = [&](int j, f32x16 (&sc)[NKB]) {
     const int k0 = (tbase + j) * BK;
+    if constexpr (MBC) {
+      // the tile's slice of the (query-broadcast) mask row, from LDS: tested
+      // first, read again only to apply (LDS reads are cheap; registers are not)
+      int o8 = 8 * hh * mes;
+      asm volatile("" : "+v"(o8));  // computed here, not held through the loop
+      const char* ms = (const char*)(mbase + (j & (NR - 1)) * MSLOT) + o8;
+      auto run_at = [&](int kb, int run) {
+        const char* r8 = ms + (32 * kb + 16 * run) * mes;
+        MaskRun8 m;
+        m.w1 = (u32x4){0u, 0u, 0u, 0u};
+        if (p.mask_kind == MASK_BOOL) {
+          const u32x2 w = *(const u32x2*)r8;
+          m.w0 = (u32x4){w[0], w[1], 0x01010101u, 0x01010101u};
+        } else {
+          m.w0 = *(const u32x4*)r8;
+          if (p.mask_kind == MASK_F32) m.w1 = *(const u32x4*)(r8 + 16);
+        }
+        return m;
+      };
+      bool keeps = true;
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int run = 0; run < 2; ++run) keeps = keeps && mask_run_keeps(run_at(kb, run), p.mask_kind);
+      if (__builtin_amdgcn_ballot_w64(!keeps)) {
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+          for (int run = 0; run < 2; ++run) mask_apply8(sc[kb], 8 * run, run_at(kb, run), p.mask_kind);
+      }
+      return;
+    }
+    if constexpr (MBC) return;
     if (p.mask_narrow) {
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb)
@@ -547,6 +606,9 @@ __device__ __forceinline__ void pipe16_segment(const FwdParams& p, const SplitAr
     dma_v(0, 0);
     dma_k(2, 2);
     dma_v(1, 1);
+    dma_m(0, 0);
+    dma_m(1, 1);
+    dma_m(2, 2);
     wait_vmcnt<0>();
   } else {
     load_k(0, kA);
@@ -650,6 +712,8 @@ __device__ __forceinline__ void pipe16_segment(const FwdParams& p, const SplitAr
         dma_v(t + 2, (t + 2) & (NR - 1));
         dma_k(t + 4, (t + 4) & (NR - 1));
         dma_v(t + 3, (t + 3) & (NR - 1));
+        dma_m(t + 3, (t + 3) & (NR - 1));  // with K: read in the step before K's
+        dma_m(t + 4, (t + 4) & (NR - 1));
       }
     } else if constexpr (!LOADERS) {
       // this iteration's register set holds K(t+2), V(t+1) (loaded two

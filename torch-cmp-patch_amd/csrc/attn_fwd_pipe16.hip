@@ -146,6 +146,11 @@ SplitArgs streamk_plan(int n, int ntiles, int occ, int cus) {
   return sa;
 }
 
+// The mask is the same for every query row and is read in whole runs.
+bool mask_bcast(const FwdParams& p) {
+  return p.mask_kind != MASK_NONE && !p.mask_narrow && (p.m_q == 0 || p.Sq == 1);
+}
+
 template <typename T, int DK, bool CAUSAL, bool PRESCALE, int MOPT>
 hipError_t launch_dk(const FwdParams& p, const SplitArgs& sa, hipStream_t s) {
   // OPT 1: s_setprio around the MFMA blocks; OPT 8: zero K columns past D;
@@ -183,6 +188,12 @@ hipError_t launch_dk(const FwdParams& p, const SplitArgs& sa, hipStream_t s) {
   // with register staging; SDXL self-attention with a key-padding mask
   // 162 -> 121 us with the mask test of attn_fwd_pipe16.h)
   if constexpr (MOPT != 0 && (DK == 32 || DK == 64 || DK == 128)) {
+    // OPT 1024: a query-broadcast mask read in runs (key padding [B,1,1,Sk]
+    // and the like): its tile slices ride the DMA ring, no loads in the step
+    if (mask_bcast(p)) {
+      if (p.D == DK) return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, occ, CAUSAL, PRESCALE, 1 | 2 | 256 | 1024 | MOPT>(p, sa, s);
+      return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, occ, CAUSAL, PRESCALE, 1 | 2 | 8 | 256 | 1024 | MOPT>(p, sa, s);
+    }
     if (p.D == DK) return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, occ, CAUSAL, PRESCALE, 1 | 2 | 256 | MOPT>(p, sa, s);
     return launch_pipe16_cfg<T, DK, kPipeNw, kPipeBk, occ, CAUSAL, PRESCALE, 1 | 2 | 8 | 256 | MOPT>(p, sa, s);
   }
