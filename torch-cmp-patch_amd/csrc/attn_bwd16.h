@@ -347,9 +347,17 @@ attn_bwd_dkdv(const BwdParams p) {
         const int h = h0 + cg;
         const __amdgpu_buffer_rsrc_t mrs = uniform_rsrc(
             (const char*)p.mask + (b * p.m_b + h * p.m_h) * mes, ((int64_t)(Sq - 1) * p.m_q + (Sk + 7) / 8 * 8) * mes);
+        if (p.m_q == 0 || Sq == 1) {
+          // the same row for every query (key padding, per-head biases): one
+          // element per lane serves all 16 rows
+          const float a = mask_elem(mrs, key * mes, kind);
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          madd[r] = mask_elem(mrs, (int)(((int64_t)(q0 + acc_key(r, hh)) * p.m_q + key) * mes), kind);
+          for (int r = 0; r < 16; ++r) madd[r] = a;
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            madd[r] = mask_elem(mrs, (int)(((int64_t)(q0 + acc_key(r, hh)) * p.m_q + key) * mes), kind);
+        }
       }
       // register r holds query q0 + acc_key(r, hh): two runs of 8 consecutive rows
       f32x16 s, dp;

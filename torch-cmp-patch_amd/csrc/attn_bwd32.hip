@@ -297,9 +297,15 @@ __global__ void __launch_bounds__(256) attn_bwd32_dkdv(const BwdParams p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) x[i] = __builtin_fmaf(s[i], c, -l2[i]);
       if (masked) {
+        if (p.m_q == 0 || Sq == 1) {  // one row for every query: one element per lane
+          const float a = mask_elem(mrs, key * mes, p.mask_kind);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          x[i] += mask_elem(mrs, (int)(((int64_t)(qlo + 4 * g + i) * p.m_q + key) * mes), p.mask_kind);
+          for (int i = 0; i < 4; ++i) x[i] += a;
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            x[i] += mask_elem(mrs, (int)(((int64_t)(qlo + 4 * g + i) * p.m_q + key) * mes), p.mask_kind);
+        }
       }
       // causal diagonal: one wave-uniform branch around the four checks
       if (CAUSAL && qlo < kw0 + 15) {

@@ -205,8 +205,24 @@ hipError_t launch_dk(const FwdParams& p, const SplitArgs& sa, hipStream_t s) {
 // attention mask): buckets 64 and 128 only.
 template <typename T, bool CAUSAL, bool PRESCALE, int MOPT>
 hipError_t launch_lse_m(const FwdParams& p, const SplitArgs& sa, int dk, hipStream_t s) {
-  // K/V straight into swizzled LDS, as for inference
+  // K/V straight into swizzled LDS, as for inference; query-broadcast masks
+  // with K (OPT 1024)
   constexpr int LD = 2 | 256;
+  if constexpr (MOPT != 0) {
+    if (mask_bcast(p)) {
+      if (dk == 64) {
+        if (p.D == 64)
+          return launch_pipe16_cfg<T, 64, kPipeNw, kPipeBk, pipe_occ(64), CAUSAL, PRESCALE, 1 | 32 | MOPT | LD | 1024>(p, sa, s);
+        return launch_pipe16_cfg<T, 64, kPipeNw, kPipeBk, pipe_occ(64), CAUSAL, PRESCALE, 1 | 8 | 32 | MOPT | LD | 1024>(p, sa, s);
+      }
+      if (dk == 128) {
+        if (p.D == 128)
+          return launch_pipe16_cfg<T, 128, kPipeNw, kPipeBk, pipe_occ(128), CAUSAL, PRESCALE, 1 | 32 | MOPT | LD | 1024>(p, sa, s);
+        return launch_pipe16_cfg<T, 128, kPipeNw, kPipeBk, pipe_occ(128), CAUSAL, PRESCALE, 1 | 8 | 32 | MOPT | LD | 1024>(p, sa, s);
+      }
+      return hipErrorNotSupported;
+    }
+  }
   if (dk == 64) {
     if (p.D == 64)
       return launch_pipe16_cfg<T, 64, kPipeNw, kPipeBk, pipe_occ(64), CAUSAL, PRESCALE, 1 | 32 | MOPT | LD>(p, sa, s);
