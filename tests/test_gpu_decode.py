@@ -8,8 +8,9 @@ the CUs.  The oracle is float64 SDPA on the CPU over
 K/V repeated per query head, with the usual bar (max abs error <= 1e-2 fp16,
 2e-2 bf16).  Covers ragged key counts (one key, fewer than a tile, a tile
 and one), 1 to 16 rows, grouped and multi-query K/V, negative and zero
-scales, [B,S,H,D] views, the key split against the unsplit launch, and
-bit-identical reruns of the split.
+scales, [B,S,H,D] views, the key split against the unsplit launch,
+bit-identical reruns of the split, and the two-level merge of deep splits
+(up to 256 parts, a last group shorter than the others).
 """
 from __future__ import annotations
 
@@ -110,6 +111,36 @@ def test_decode_split_matches_unsplit_and_reruns_bit_identical(D):
     want = _oracle(q, k, v, 0.1)
     assert orc.max_abs_err(split1.cpu(), want) <= TOL["fp16"]
     assert orc.max_abs_err(whole.cpu(), want) <= TOL["fp16"]
+
+
+DEEP = [
+    # dtype, B, H, Hkv, Sq, Sk, D, merge groups: deep splits of many rows
+    ("bf16", 1, 32, 4, 1, 65536, 256, 8),    # 4 units x 64 parts of 8 rows
+    ("fp16", 1, 16, 1, 1, 65536, 256, 16),   # 1 unit x 256 parts (the most) of 16 rows
+    ("bf16", 5, 8, 1, 1, 20000, 256, 8),     # 5 units x 52 parts: a last group of 4, ragged keys
+]
+
+
+@pytest.mark.parametrize("case", DEEP, ids=[f"{c[0]}-b{c[1]}h{c[2]}of{c[3]}-k{c[5]}d{c[6]}" for c in DEEP])
+def test_decode_two_level_merge(case):
+    """Deep splits merge per group of parts, then over the groups: the output
+    meets the oracle, a rerun is bit-identical (fixed groups and order, whichever
+    part arrives last), and the unsplit launch agrees within the same bar."""
+    dtype, B, H, Hkv, Sq, Sk, D, groups = case
+    desc = _describe(case[:7])
+    assert f"merged in groups of {groups}" in desc, desc
+    print(f"decode two-level merge {case}", flush=True)
+    q, k, v = _inputs(dtype, B, H, Hkv, Sq, Sk, D, seed=D + B)
+    scale = 1.0 / math.sqrt(D)
+    split1, split2, whole = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    assert abi.attn_fwd_raw(q, k, v, split1, scale, False) == 0
+    assert abi.attn_fwd_raw(q, k, v, split2, scale, False) == 0
+    assert abi.attn_fwd_raw(q, k, v, whole, scale, False, workspace=False) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(split1, split2)
+    want = _oracle(q, k, v, scale)
+    assert orc.max_abs_err(split1.cpu(), want) <= TOL[dtype]
+    assert orc.max_abs_err(whole.cpu(), want) <= TOL[dtype]
 
 
 def test_seventeen_rows_stay_on_the_prefill_kernel():

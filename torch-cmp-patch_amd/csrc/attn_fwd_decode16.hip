@@ -90,6 +90,7 @@ constexpr int kDecRows = 16;        // query rows per unit at most
 constexpr int kDecBk = 16;          // keys per tile
 constexpr int kDecMinTiles = 4;     // tiles per wave at least, when keys are split
 constexpr int kDecMaxParts = 256;   // key ranges per unit at most (the merge's LDS)
+constexpr int kDecMergeLoads = 8;   // exchange loads of one merging thread in flight together
 constexpr int kDecLds = 160 * 1024; // LDS of one CU
 
 // Ring stages per wave: as deep as 128 KB of LDS per workgroup allows, at
@@ -117,7 +118,10 @@ struct DecArgs {
   int nt;      // 16-key tiles per unit
   int parts;   // workgroups per unit (key ranges)
   f32x4* ws;   // exchange: [unit][part][row] (DK / 4 + 1) float4: O, then (m, l, 0, 0)
-  int* cnt;    // one counter per unit, zero between launches
+  int* cnt;    // one counter per unit, then (two-level merge) one per group of
+               // each unit from cnt + gbase; zero between launches
+  int gsize;   // parts per merge group (>= parts: one-level merge)
+  int gbase;   // index of the first group counter
 };
 
 __device__ __forceinline__ float shfl_xor_f(float x, int m) { return __shfl_xor(x, m); }
@@ -149,7 +153,7 @@ __global__ __launch_bounds__(kDecNw * 64, 1) void attn_fwd_decode16(FwdParams p,
   constexpr int MOS = DK + 4;           // row stride (floats) of the waves' merge rows
   static_assert(kDecNw * kDecRows * MOS * 4 + 2 * kDecNw * kDecRows * 4 + 16 <= kDecNw * NS * STAGE,
                 "the workgroup's merge fits in the ring's LDS");
-  static_assert(2 * kDecRows * kDecMaxParts * 4 + 16 + kDecNw * 64 * 16 <= kDecNw * NS * STAGE,
+  static_assert(2 * kDecRows * kDecMaxParts * 4 + 2 * kDecRows * 4 + 16 + kDecNw * 64 * 16 <= kDecNw * NS * STAGE,
                 "the parts' merge fits in the ring's LDS");
   __shared__ __attribute__((aligned(16))) unsigned char lds[kDecNw * NS * STAGE];
 
@@ -348,90 +352,126 @@ __global__ __launch_bounds__(kDecNw * 64, 1) void attn_fwd_decode16(FwdParams p,
   }
   if (nparts == 1) return;
 
-  // ---- key split: count in; the last part of the unit merges every part
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  lds_barrier();  // every wave's stores are done (and its LDS reads)
+  // ---- key split: count in; the last arriver merges.  One level: the last
+  // part of the unit merges every part.  Two levels (deep splits, a.gsize <
+  // nparts): the last part of each group of a.gsize consecutive parts merges
+  // the group into the group's first slot, unnormalised, and counts the group
+  // in; the last group merges the groups.  Counters go back to zero.
   int* const flag = (int*)(ml + kDecNw * kDecRows);
-  if (tid == 0) {
-    int* const ctr = a.cnt + unit;
-    const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (old == nparts - 1) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *flag = old == nparts - 1;
-  }
-  lds_barrier();
-  if (__builtin_amdgcn_readfirstlane(*flag) == 0) return;
-  asm volatile("" ::: "memory");  // the exchange loads stay after the count
-  lds_barrier();                  // every wave has read the flag before its LDS is reused
+  const int gs = a.gsize, ng = (nparts + gs - 1) / gs;
+  auto count_in = [&](int* ctr, int n) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();  // every wave's stores are done (and its LDS reads)
+    if (tid == 0) {
+      const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (old == n - 1) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *flag = old == n - 1;
+    }
+    lds_barrier();
+    const bool last = __builtin_amdgcn_readfirstlane(*flag) != 0;
+    asm volatile("" ::: "memory");  // the exchange loads stay after the count
+    if (last) lds_barrier();        // every wave has read the flag before its LDS is reused
+    return last;
+  };
   auto ld = [&](int off) {
     return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wsr, off, 0, 16));
   };
-  // The merge is the launch's tail (only this workgroup is left), so it is
-  // laid out for few dependent memory round trips: (1) every part's (m, l)
-  // of every row in one load per thread, then per row (one wave each) the
-  // normalised weight of each part, exp2(m_q - max m) / sum of the weighted
-  // row sums; (2) every thread loads all of its share of the partial outputs
-  // at once: the parts of an output vector are spread over S thread groups
-  // whose sums meet in LDS.  Fixed assignment and summation order: the same
-  // result whichever part merges.
-  float* const wq = (float*)lds;      // [row][part] offsets, then weights
-  float* const lq = wq + R * nparts;  // [row][part] row sums
-  for (int i = tid; i < R * nparts; i += kDecNw * 64) {
-    const int r = i / nparts, q = i - r * nparts;
-    const f32x4 ml = ld(slot(q, r, DQ));
-    wq[i] = ml[0];
-    lq[i] = ml[1];
-  }
-  lds_barrier();
-  for (int r = wave; r < R; r += kDecNw) {
-    float* const wr = wq + r * nparts;
-    const float* const lr = lq + r * nparts;
-    float mx = -INFINITY;
-    for (int q = lane; q < nparts; q += 64) mx = fmaxf(mx, wr[q]);  // every part has keys: finite
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, shfl_xor_f(mx, m));
-    float L = 0.f;
-    for (int q = lane; q < nparts; q += 64) L = __builtin_fmaf(lr[q], fast_exp2(wr[q] - mx), L);
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) L += shfl_xor_f(L, m);
-    const float inv = 1.f / L;
-    for (int q = lane; q < nparts; q += 64) wr[q] = fast_exp2(wr[q] - mx) * inv;  // this lane's own entries
-  }
-  lds_barrier();
-  constexpr int NT = kDecNw * 64;
-  constexpr int CH = 8;  // loads of one thread in flight together
-  const int S = nu >= NT ? 1 : NT / nu;
-  f32x4* const acc = (f32x4*)(lds + ((2 * R * nparts * 4 + 15) & ~15));  // [S][nu] partial sums
-  for (int u0 = 0; u0 < nu; u0 += NT / S) {
-    const int t = tid % (NT / S), sg = tid / (NT / S), u = u0 + t;
-    f32x4 o = {0.f, 0.f, 0.f, 0.f};
-    if (u < nu && sg < S) {
-      const int r = u / DQ, k = u - r * DQ;
-      const float* const wr = wq + r * nparts;
-      for (int q0 = sg; q0 < nparts; q0 += CH * S) {
-        f32x4 x[CH];
-#pragma unroll
-        for (int j = 0; j < CH; ++j) {
-          const int q = q0 + j * S;
-          x[j] = q < nparts ? ld(slot(q, r, k)) : (f32x4){0.f, 0.f, 0.f, 0.f};
-        }
-#pragma unroll
-        for (int j = 0; j < CH; ++j) {
-          const int q = q0 + j * S;
-          if (q < nparts) o += x[j] * wr[q];
-        }
-      }
-      if (S == 1) store_out(r, k, o, 1.f);
+  // Merge the n entries q0, q0 + qs, ... of this unit's exchange.  The merge
+  // is on the launch's tail, so it is laid out for few dependent memory round
+  // trips: (1) every entry's (m, l) of every row in one load per thread, then
+  // per row (one wave each) the weight of each entry, exp2(m_q - max m),
+  // divided by the weighted row-sum total for the output; (2) every thread
+  // loads all of its share of the partial outputs at once: the entries of an
+  // output vector are spread over S thread groups whose sums meet in LDS.
+  // `fin` writes the output; otherwise the unnormalised (O, max m, total)
+  // goes to entry q0.  Fixed assignment and summation order: the same result
+  // whichever part merges.
+  auto merge = [&](int q0, int qs, int n, bool fin) {
+    float* const wq = (float*)lds;  // [row][entry] offsets, then weights
+    float* const lq = wq + R * n;   // [row][entry] row sums
+    float* const rt = lq + R * n;   // [row] (max m, total) of a group merge
+    for (int i = tid; i < R * n; i += kDecNw * 64) {
+      const int r = i / n, j = i - r * n;
+      const f32x4 e = ld(slot(q0 + j * qs, r, DQ));
+      wq[i] = e[0];
+      lq[i] = e[1];
     }
-    if (S > 1) {
-      if (sg < S && u < nu) acc[sg * nu + u] = o;  // S > 1: nu < NT, one pass (u0 = 0)
-      lds_barrier();
-      if (tid < nu) {
-        f32x4 sum = acc[tid];
-        for (int g2 = 1; g2 < S; ++g2) sum += acc[g2 * nu + tid];
-        store_out(tid / DQ, tid - tid / DQ * DQ, sum, 1.f);
+    lds_barrier();
+    for (int r = wave; r < R; r += kDecNw) {
+      float* const wr = wq + r * n;
+      const float* const lr = lq + r * n;
+      float mx = -INFINITY;
+      for (int j = lane; j < n; j += 64) mx = fmaxf(mx, wr[j]);  // every part has keys: finite
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, shfl_xor_f(mx, m));
+      float L = 0.f;
+      for (int j = lane; j < n; j += 64) L = __builtin_fmaf(lr[j], fast_exp2(wr[j] - mx), L);
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) L += shfl_xor_f(L, m);
+      const float inv = fin ? 1.f / L : 1.f;
+      for (int j = lane; j < n; j += 64) wr[j] = fast_exp2(wr[j] - mx) * inv;  // this lane's own entries
+      if (!fin && lane == 0) {
+        rt[2 * r] = mx;
+        rt[2 * r + 1] = L;
       }
     }
+    lds_barrier();
+    constexpr int NT = kDecNw * 64;
+    constexpr int CH = kDecMergeLoads;
+    const int S = nu >= NT ? 1 : NT / nu;
+    f32x4* const acc = (f32x4*)(lds + ((2 * R * n * 4 + 2 * R * 4 + 15) & ~15));  // [S][nu] partial sums
+    auto put = [&](int r, int k, f32x4 o) {
+      if (fin) {
+        store_out(r, k, o, 1.f);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), wsr, slot(q0, r, k), 0, 16);
+        if (k == 0)
+          __builtin_amdgcn_raw_buffer_store_b128(
+              __builtin_bit_cast(u32x4, ((f32x4){rt[2 * r], rt[2 * r + 1], 0.f, 0.f})), wsr, slot(q0, r, DQ), 0,
+              16);
+      }
+    };
+    for (int u0 = 0; u0 < nu; u0 += NT / S) {
+      const int t = tid % (NT / S), sg = tid / (NT / S), u = u0 + t;
+      f32x4 o = {0.f, 0.f, 0.f, 0.f};
+      if (u < nu && sg < S) {
+        const int r = u / DQ, k = u - r * DQ;
+        const float* const wr = wq + r * n;
+        for (int j0 = sg; j0 < n; j0 += CH * S) {
+          f32x4 x[CH];
+#pragma unroll
+          for (int i = 0; i < CH; ++i) {
+            const int j = j0 + i * S;
+            x[i] = j < n ? ld(slot(q0 + j * qs, r, k)) : (f32x4){0.f, 0.f, 0.f, 0.f};
+          }
+#pragma unroll
+          for (int i = 0; i < CH; ++i) {
+            const int j = j0 + i * S;
+            if (j < n) o += x[i] * wr[j];
+          }
+        }
+        if (S == 1) put(r, k, o);
+      }
+      if (S > 1) {
+        if (sg < S && u < nu) acc[sg * nu + u] = o;  // S > 1: nu < NT, one pass (u0 = 0)
+        lds_barrier();
+        if (tid < nu) {
+          f32x4 sum = acc[tid];
+          for (int g2 = 1; g2 < S; ++g2) sum += acc[g2 * nu + tid];
+          put(tid / DQ, tid - tid / DQ * DQ, sum);
+        }
+      }
+    }
+  };
+  if (gs >= nparts) {
+    if (count_in(a.cnt + unit, nparts)) merge(0, 1, nparts, true);
+    return;
   }
+  const int grp = part / gs, g0 = grp * gs;
+  const int gn = nparts - g0 < gs ? nparts - g0 : gs;
+  if (!count_in(a.cnt + a.gbase + unit * ng + grp, gn)) return;
+  merge(g0, 1, gn, false);
+  if (count_in(a.cnt + unit, ng)) merge(0, gs, ng, true);
 }
 
 template <typename T, int DK>
@@ -509,6 +549,23 @@ int dec_parts(int units, int nt, int D, int cus) {
   return parts >= 2 ? parts : 1;
 }
 
+// Parts per merge group.  The merging workgroup loads kDecMergeLoads partial
+// vectors per thread at a time; a split whose one-level merge needs eight or
+// more such batches per thread (deep splits of many rows: 64 parts of 8 rows
+// at D = 256 take 16) merges in two levels of about sqrt(parts) entries each
+// (on MI355X, [1,32/4,1,65536,256]: the one-level merge took 16.6 us of a
+// 60.9 us launch).  Otherwise one level (returns parts).
+int dec_group(int parts, int rows, int D) {
+  const int nt = kDecNw * 64, nu = rows * (D / 4);
+  const int S = nu >= nt ? 1 : nt / nu;
+  const int passes = S == 1 ? (nu + nt - 1) / nt : 1;  // output vectors per thread
+  const int batches = passes * ((parts + kDecMergeLoads * S - 1) / (kDecMergeLoads * S));
+  if (batches < 8) return parts;
+  int g = 1;
+  while (g * g < parts) ++g;
+  return g;
+}
+
 }  // namespace
 
 hipError_t launch_decode16(const FwdParams& p0, bool bf16, hipStream_t s) {
@@ -517,12 +574,18 @@ hipError_t launch_decode16(const FwdParams& p0, bool bf16, hipStream_t s) {
   if (p.Sk == 1) p.k_s = p.v_s = p.D;  // one row: rows past it must lie past the buffer
   const int units = p.B * p.H;
   if (units == 0) return hipSuccess;
-  DecArgs a = {p.Sq, (p.Sk + kDecBk - 1) / kDecBk, 1, nullptr, nullptr};
+  DecArgs a = {p.Sq, (p.Sk + kDecBk - 1) / kDecBk, 1, nullptr, nullptr, 1, units};
   const int parts = dec_parts(units, a.nt, p.D, device_cus());
   if (parts >= 2) {
     const size_t part_bytes = (size_t)units * a.rows * (p.D / 4 + 1) * sizeof(f32x4);
-    const int fit = bind_exchange(p, parts, part_bytes, units, &a.ws, &a.cnt);
-    if (fit >= 2) a.parts = fit;
+    // counters for the two-level merge of the deepest plan (fewer parts need fewer)
+    const int gs = dec_group(parts, a.rows, p.D);
+    const int ncnt = units * (1 + (parts + gs - 1) / gs);
+    const int fit = bind_exchange(p, parts, part_bytes, ncnt, &a.ws, &a.cnt);
+    if (fit >= 2) {
+      a.parts = fit;
+      a.gsize = dec_group(fit, a.rows, p.D);
+    }
   } else if (p.dry) {
     *p.dry = SplitInfo{0, 1};
   }
@@ -533,8 +596,12 @@ hipError_t launch_decode16(const FwdParams& p0, bool bf16, hipStream_t s) {
 void describe_decode16(int D, int B, int H, int Sq, int Sk, char* buf, int len) {
   const int nt = (Sk + kDecBk - 1) / kDecBk;
   const int parts = dec_parts(B * H, nt, D, device_cus());
-  char split[48] = "";
-  if (parts >= 2) snprintf(split, sizeof split, " key-split: %d x %d parts", B * H, parts);
+  char split[64] = "";
+  if (parts >= 2) {
+    const int gs = dec_group(parts, Sq, D);
+    const int n = snprintf(split, sizeof split, " key-split: %d x %d parts", B * H, parts);
+    if (gs < parts) snprintf(split + n, sizeof split - n, ", merged in groups of %d", gs);
+  }
   snprintf(buf, len,
            "decode16 16x16 S^T-form: DK=%d rows=%d waves=%d BK=%d, a %d-stage LDS DMA ring per wave, "
            "workgroups/CU=%d%s",
