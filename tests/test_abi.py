@@ -128,7 +128,7 @@ def test_describe_key_split_plan():
     assert "merged in groups" not in abi.describe(f16, 1, 8, 1, 32768, 160)[1]
     # deep splits of many rows merge in two levels of about sqrt(parts)
     assert "key-split: 4 x 64 parts, merged in groups of 8" in abi.describe(bf16, 1, 4, 8, 65536, 256)[1]
-    assert "key-split: 1 x 256 parts, merged in groups of 16" in abi.describe(f16, 1, 1, 16, 65536, 256)[1]
+    assert "key-split: 1 x 128 parts, merged in groups of 12" in abi.describe(f16, 1, 1, 16, 65536, 256)[1]
     assert "key-split" not in abi.describe(bf16, 64, 8, 1, 4096, 256)[1]   # 512 units: unsplit
     assert "decode16" in abi.describe(bf16, 1, 8, 16, 4096, 64)[1]         # 8 units at D = 64
     assert "decode16" not in abi.describe(bf16, 16, 8, 1, 4096, 128)[1]    # 128 units: pipelined

@@ -10,7 +10,7 @@ K/V repeated per query head, with the usual bar (max abs error <= 1e-2 fp16,
 and one), 1 to 16 rows, grouped and multi-query K/V, negative and zero
 scales, [B,S,H,D] views, the key split against the unsplit launch,
 bit-identical reruns of the split, and the two-level merge of deep splits
-(up to 256 parts, a last group shorter than the others).
+(up to 128 parts, a last group shorter than the others).
 """
 from __future__ import annotations
 
@@ -116,7 +116,7 @@ def test_decode_split_matches_unsplit_and_reruns_bit_identical(D):
 DEEP = [
     # dtype, B, H, Hkv, Sq, Sk, D, merge groups: deep splits of many rows
     ("bf16", 1, 32, 4, 1, 65536, 256, 8),    # 4 units x 64 parts of 8 rows
-    ("fp16", 1, 16, 1, 1, 65536, 256, 16),   # 1 unit x 256 parts (the most) of 16 rows
+    ("fp16", 1, 16, 1, 1, 65536, 256, 12),   # 1 unit x 128 parts (the most) of 16 rows, last group 8
     ("bf16", 5, 8, 1, 1, 20000, 256, 8),     # 5 units x 52 parts: a last group of 4, ragged keys
 ]
 

@@ -89,7 +89,7 @@ constexpr int kDecNw = 4;           // waves per workgroup
 constexpr int kDecRows = 16;        // query rows per unit at most
 constexpr int kDecBk = 16;          // keys per tile
 constexpr int kDecMinTiles = 4;     // tiles per wave at least, when keys are split
-constexpr int kDecMaxParts = 256;   // key ranges per unit at most (the merge's LDS)
+constexpr int kDecMaxParts = 128;   // key ranges per unit at most
 constexpr int kDecMergeLoads = 8;   // exchange loads of one merging thread in flight together
 constexpr int kDecLds = 160 * 1024; // LDS of one CU
 
