@@ -119,10 +119,11 @@ def host_info() -> dict:
 
 
 def config_cpu_and_error(wl, out_gpu, budget_s: float = 4.0) -> dict:
-    """Per-config CPU figures: stock torch SDPA on the
-    host CPU in the config's own dtype (1 warmup + timed calls, ~budget_s),
-    and the GPU output's max abs error against torch's CPU math SDPA on the
-    fp32-upcast inputs (BASELINE.md section 2's reference)."""
+    """Per-config CPU figures: stock torch SDPA on the host CPU in the
+    config's own dtype (1 warmup + timed calls, ~budget_s; the reference's
+    own CPU figures are quoted this way), and the GPU output's max abs error
+    against torch's CPU math SDPA on the fp32-upcast inputs (the reference's
+    accuracy check)."""
     import torch
     import torch.nn.functional as F
     torch.set_num_threads(os.cpu_count() or 1)
@@ -282,7 +283,7 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (attention forward shards per "
-              "(batch, head) with no exchange; see DESIGN.md). Run with --gpus 1.",
+              "(batch, head) with no exchange). Run with --gpus 1.",
               file=sys.stderr)
         return 2
 
