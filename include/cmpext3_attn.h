@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define CMPEXT3_ATTN_ABI_VERSION 8
+#define CMPEXT3_ATTN_ABI_VERSION 9
 
 /* dtype codes (CMPEXT3_DTYPE_BOOL: attention masks only) */
 #define CMPEXT3_DTYPE_F16  0
@@ -285,7 +285,8 @@ int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, f
  * Three kernels on `stream`: Delta, dK/dV (one workgroup per 128 keys of a
  * K/V head; 64 for fp32), dQ (one per 128 queries; 64 for fp32); each
  * gradient row is written by exactly one workgroup, so results are
- * bit-identical from run to run.  B*H*Sq == 0 is a no-op (dk and dv are then
+ * bit-identical from run to run.  This entry point takes no workspace and
+ * never splits a sweep (cmpext3_attn_bwd_ws below can).  B*H*Sq == 0 is a no-op (dk and dv are then
  * left untouched).  Every dtype: f16/bf16 on 32x32x16 MFMAs (head dims above
  * 128 in the 192 and 256 buckets at one wave per SIMD), fp32 on 16x16x4 fp32
  * MFMAs (buckets 32, 40, 64, 96, 128, 192, 256).
@@ -301,6 +302,41 @@ int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
                      const int64_t dk_str[3], const int64_t dv_str[3],
                      const void* mask, int mask_dtype, const int64_t mask_str[3],
                      float scale, int causal, hipStream_t stream);
+
+/*
+ * cmpext3_attn_bwd with a caller-owned workspace (16-byte aligned; NULL or 0
+ * bytes = none).  f16/bf16 problems with too few key blocks for the CUs
+ * (grouped-query K/V of one or two sequences, causal sweeps whose length
+ * falls with the key block) cut each block's dK/dV sweep over (query head,
+ * query tile) into up to 8 contiguous parts on separate workgroups; the parts
+ * leave fp32 partial dK/dV rows in the workspace and a fourth kernel sums
+ * them in part order (still bit-identical from run to run; the sums differ
+ * from the unsplit launch's only by rounding).  A workspace smaller than
+ * cmpext3_attn_bwd_workspace_size runs unsplit.  Otherwise the arguments,
+ * results and return codes of cmpext3_attn_bwd (CMPEXT3_E_ALIGN also for a
+ * misaligned workspace).
+ *
+ * Reference: none (forward-only reference, cmpext3/__init__.py:115-125).
+ */
+int cmpext3_attn_bwd_ws(const void* q, const void* k, const void* v, const void* o,
+                        const void* dout, const float* lse, void* dq, void* dk, void* dv,
+                        float* delta, int dtype, int B, int H, int H_kv, int Sq, int Sk, int D,
+                        const int64_t q_str[3], const int64_t k_str[3],
+                        const int64_t v_str[3], const int64_t o_str[3],
+                        const int64_t do_str[3], const int64_t dq_str[3],
+                        const int64_t dk_str[3], const int64_t dv_str[3],
+                        const void* mask, int mask_dtype, const int64_t mask_str[3],
+                        float scale, int causal, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream);
+
+/*
+ * Workspace bytes cmpext3_attn_bwd_ws needs to split this problem's dK/dV
+ * sweeps (mask_dtype -1 = no mask); 0 when it never splits (fp32, enough key
+ * blocks) or the arguments are invalid.  Depends on the current device's CU
+ * count (256, MI355X's, when none is visible).  Host-only.
+ */
+size_t cmpext3_attn_bwd_workspace_size(int dtype, int B, int H, int H_kv, int Sq, int Sk, int D,
+                                       int mask_dtype, int causal);
 
 /* Human-readable text for a return code (static storage). */
 const char* cmpext3_attn_strerror(int code);

@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version_and_messages():
-    assert abi.lib().cmpext3_attn_abi_version() == 8
+    assert abi.lib().cmpext3_attn_abi_version() == 9
     for code in range(10):
         assert abi.strerror(code) and abi.strerror(code) != "unknown error code"
     assert abi.strerror(99) == "unknown error code"
@@ -401,3 +401,33 @@ def test_workspace_alignment_is_checked_before_launch():
                                        st, st, st, st, vp(0), -1, st, ctypes.c_float(0.125), 0,
                                        vp(24), 1 << 20, None)
     assert rc == abi.E_ALIGN
+
+
+def test_bwd_workspace_plan():
+    """The backward splits its dK/dV sweeps only with too few key blocks for
+    the CU slots (256 CUs without a visible device): grouped-query and
+    single-sequence launches ask for ns x B x H_kv x Sk x D x 2 fp32 partials;
+    the Qwen3 and SDXL training shapes, fp32 and invalid arguments ask for
+    nothing."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("plan depends on the visible device's CU count")
+    f16, bf16, f32 = abi.DTYPE_F16, abi.DTYPE_BF16, abi.DTYPE_F32
+    part = lambda ns, B, Hkv, Sk, D: ns * B * Hkv * Sk * D * 2 * 4
+    assert abi.bwd_workspace_size(bf16, 4, 16, 16, 2048, 2048, 128, -1, True) == 0     # Qwen3 shape
+    assert abi.bwd_workspace_size(f16, 2, 10, 10, 4096, 4096, 64, -1, False) == 0      # SDXL shape
+    assert abi.bwd_workspace_size(f32, 1, 8, 8, 1024, 1024, 64, -1, False) == 0
+    assert abi.bwd_workspace_size(bf16, 1, 32, 7, 4096, 4096, 128, -1, True) == 0      # 7 does not divide 32
+    assert abi.bwd_workspace_size(bf16, 1, 32, 8, 4096, 4096, 129, -1, True) == 0      # rows off 16 bytes
+    # causal: two rounds of the 512 slots (2 waves per SIMD at D = 128)
+    assert abi.bwd_workspace_size(bf16, 1, 32, 8, 4096, 4096, 128, -1, True) == part(4, 1, 8, 4096, 128)
+    assert abi.bwd_workspace_size(bf16, 2, 32, 8, 4096, 4096, 128, -1, True) == part(2, 2, 8, 4096, 128)
+    # non-causal: one round
+    assert abi.bwd_workspace_size(bf16, 1, 32, 8, 4096, 4096, 128, -1, False) == part(2, 1, 8, 4096, 128)
+    # one wave per SIMD: D = 256, and masked causal D = 128
+    assert abi.bwd_workspace_size(bf16, 1, 16, 8, 4096, 4096, 256, -1, True) == part(2, 1, 8, 4096, 256)
+    assert abi.bwd_workspace_size(bf16, 2, 32, 8, 4096, 4096, 128, 3, True) == 0
+    # at most 8 parts, each at least 4 query tiles of the longest sweep
+    assert abi.bwd_workspace_size(f16, 1, 2, 2, 4096, 4096, 64, -1, False) == part(8, 1, 2, 4096, 64)
+    assert abi.bwd_workspace_size(f16, 1, 2, 2, 260, 200, 64, -1, False) == part(2, 1, 2, 200, 64)
+    assert abi.bwd_workspace_size(f16, 1, 2, 2, 100, 200, 64, -1, False) == 0

@@ -1,0 +1,111 @@
+"""GPU parity of the split dK/dV sweeps of the backward (cmpext3_attn_bwd_ws).
+
+With too few key blocks for the CUs (one or two sequences, grouped-query K/V,
+causal sweeps whose length falls with the key block) the dK/dV sweep of a
+block over (query head of the group, query tile) is cut into up to 8
+contiguous parts whose fp32 partials a fourth kernel sums in part order.
+Oracle: float64 sdpa_bwd_np on K/V repeated per query head, the repeats'
+gradients summed; bar: max abs error <= 1e-2 (fp16) / 2e-2 (bf16) times the
+gradient's largest oracle magnitude (at least 1e-3), as for the unsplit
+backward.  Also: the split launch agrees with the unsplit one (no workspace)
+within the same bar, reruns are bit-identical, dQ is untouched by the split
+(bit-identical to the unsplit launch), and a workspace below the size query
+runs unsplit.  The plan itself (which problems split) is a CPU test in
+test_abi.py.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from cmpext3 import abi
+from oracle import sdpa_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"fp16": 1e-2, "bf16": 2e-2}
+TDT = {"fp16": torch.float16, "bf16": torch.bfloat16}
+
+
+def _rel_err(got, want):
+    want = torch.as_tensor(want)
+    return orc.max_abs_err(got.cpu(), want) / max(float(want.abs().max()), 1e-3)
+
+
+CASES = [
+    # dtype, B, H, Hkv, Sq, Sk, D, causal, mask
+    ("bf16", 1, 8, 2, 1024, 1024, 128, True, None),     # grouped-query causal, 8 parts
+    ("fp16", 1, 4, 4, 1000, 777, 64, False, None),      # ragged non-causal
+    ("fp16", 2, 8, 1, 300, 1500, 64, True, None),       # multi-query, causal Sq < Sk (empty parts)
+    ("bf16", 1, 4, 2, 700, 300, 128, True, None),       # causal Sq > Sk
+    ("bf16", 1, 4, 2, 600, 900, 256, True, None),       # D = 256 bucket, one wave per SIMD
+    ("fp16", 1, 2, 1, 333, 520, 160, False, None),      # D = 160 in the 192 bucket
+    ("fp16", 2, 4, 2, 500, 700, 64, False, "pad"),      # key-padding mask
+    ("bf16", 1, 4, 2, 400, 400, 128, True, "full"),     # per-row bool mask with causal
+    ("fp16", 1, 2, 2, 260, 200, 64, False, None),       # short sweeps: 2 parts of 4 and 5 tiles
+]
+
+
+def _mask(kind, B, H, Sq, Sk, seed):
+    if kind is None:
+        return None
+    g = torch.Generator().manual_seed(seed)
+    if kind == "pad":
+        m = torch.ones(B, 1, 1, Sk, dtype=torch.bool)
+        m[..., Sk - Sk // 5:] = False
+    else:
+        m = torch.rand(B, H, Sq, Sk, generator=g) > 0.3
+        m[..., 0] = True
+    return m.cuda()
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}-b{c[1]}h{c[2]}of{c[3]}-q{c[4]}k{c[5]}d{c[6]}"
+                                             f"{'c' if c[7] else ''}{'-' + c[8] if c[8] else ''}" for c in CASES])
+def test_split_backward(case):
+    dtype, B, H, Hkv, Sq, Sk, D, causal, mk = case
+    dt = abi.dtype_code(TDT[dtype])
+    mdt = -1 if mk is None else abi.DTYPE_BOOL
+    assert abi.bwd_workspace_size(dt, B, H, Hkv, Sq, Sk, D, mdt, causal) > 0
+    print(f"split backward {case}", flush=True)
+    g = torch.Generator().manual_seed(Sq + Sk + D)
+    rnd = lambda h, S: torch.randn(B, h, S, D, generator=g).to(TDT[dtype]).cuda()
+    q, k, v, do = rnd(H, Sq), rnd(Hkv, Sk), rnd(Hkv, Sk), rnd(H, Sq)
+    m = _mask(mk, B, H, Sq, Sk, seed=D)
+    s = D ** -0.5
+    out, lse = abi.attn_fwd_lse(q, k, v, s, causal, attn_mask=m)
+    split1 = abi.attn_bwd(q, k, v, out, do, lse, s, causal, attn_mask=m, workspace=True)
+    split2 = abi.attn_bwd(q, k, v, out, do, lse, s, causal, attn_mask=m, workspace=True)
+    whole = abi.attn_bwd(q, k, v, out, do, lse, s, causal, attn_mask=m, workspace=None)
+    torch.cuda.synchronize()
+    for a, b in zip(split1, split2):
+        assert torch.equal(a, b)
+    assert torch.equal(split1[0], whole[0])  # dQ does not depend on the split
+    grp = H // Hkv
+    kr, vr = (t.cpu().repeat_interleave(grp, dim=1) for t in (k, v))
+    want = orc.sdpa_bwd_np(q.cpu(), kr, vr, do.cpu(), s, causal, attn_mask=None if m is None else m.cpu())
+    dq_r, dk_r, dv_r = want
+    dk_r = dk_r.reshape(B, Hkv, grp, Sk, D).sum(axis=2)
+    dv_r = dv_r.reshape(B, Hkv, grp, Sk, D).sum(axis=2)
+    for name, got, alt, ref in zip(("dq", "dk", "dv"), split1, whole, (dq_r, dk_r, dv_r)):
+        assert _rel_err(got, ref) <= TOL[dtype], name
+        assert _rel_err(alt, ref) <= TOL[dtype], name
+        assert _rel_err(got, alt.cpu()) <= TOL[dtype], name
+
+
+def test_workspace_smaller_than_asked_runs_unsplit():
+    """A workspace below the query's size runs the unsplit sweep: the same
+    gradients as no workspace, bit for bit."""
+    B, H, Hkv, Sq, Sk, D = 1, 4, 2, 512, 512, 64
+    dt = abi.dtype_code(torch.float16)
+    need = abi.bwd_workspace_size(dt, B, H, Hkv, Sq, Sk, D, -1, True)
+    assert need > 0
+    g = torch.Generator().manual_seed(3)
+    rnd = lambda h, S: torch.randn(B, h, S, D, generator=g).half().cuda()
+    q, k, v, do = rnd(H, Sq), rnd(Hkv, Sk), rnd(Hkv, Sk), rnd(H, Sq)
+    out, lse = abi.attn_fwd_lse(q, k, v, 0.125, True)
+    small = torch.empty(need - 16, dtype=torch.uint8, device="cuda")
+    a = abi.attn_bwd(q, k, v, out, do, lse, 0.125, True, workspace=small)
+    b = abi.attn_bwd(q, k, v, out, do, lse, 0.125, True, workspace=None)
+    torch.cuda.synchronize()
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)

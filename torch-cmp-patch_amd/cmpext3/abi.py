@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcmpext3_
 SYMBOLS = ("cmpext3_attn_fwd", "cmpext3_attn_fwd_gqa", "cmpext3_attn_fwd_masked",
            "cmpext3_attn_fwd_ws", "cmpext3_attn_fwd_workspace_size", "cmpext3_attn_fwd_plan",
            "cmpext3_attn_fwd_noalloc", "cmpext3_attn_fwd_lse", "cmpext3_attn_bwd",
+           "cmpext3_attn_bwd_ws", "cmpext3_attn_bwd_workspace_size",
            "cmpext3_attn_strerror", "cmpext3_attn_abi_version", "cmpext3_attn_describe")
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_BOOL = 0, 1, 2, 3
@@ -64,6 +65,11 @@ def lib() -> ctypes.CDLL:
         L.cmpext3_attn_bwd.argtypes = ([vp] * 10 + [ci] * 7 + [i64p] * 8 + [vp, ci, i64p]
                                        + [ctypes.c_float, ci, vp])
         L.cmpext3_attn_bwd.restype = ci
+        L.cmpext3_attn_bwd_ws.argtypes = ([vp] * 10 + [ci] * 7 + [i64p] * 8 + [vp, ci, i64p]
+                                          + [ctypes.c_float, ci, vp, sz, vp])
+        L.cmpext3_attn_bwd_ws.restype = ci
+        L.cmpext3_attn_bwd_workspace_size.argtypes = [ci] * 9
+        L.cmpext3_attn_bwd_workspace_size.restype = sz
         L.cmpext3_attn_strerror.argtypes = [ci]
         L.cmpext3_attn_strerror.restype = ctypes.c_char_p
         L.cmpext3_attn_abi_version.argtypes = []
@@ -261,23 +267,41 @@ def attn_fwd_lse(q, k, v, scale: Optional[float] = None, causal: bool = False, s
     return o, lse
 
 
+def bwd_workspace_size(dtype: int, B: int, H: int, H_kv: int, Sq: int, Sk: int, D: int,
+                       mask_dtype: int = -1, causal: bool = False) -> int:
+    """cmpext3_attn_bwd_workspace_size: bytes that let the backward split its
+    dK/dV sweeps (0 = it never splits)."""
+    return lib().cmpext3_attn_bwd_workspace_size(dtype, B, H, H_kv, Sq, Sk, D, mask_dtype, int(causal))
+
+
 def attn_bwd_raw(q, k, v, o, do, lse, dq, dk, dv, delta, scale: float, causal: bool = False,
-                 stream=None, attn_mask=None) -> int:
-    """Call cmpext3_attn_bwd on caller-allocated tensors; returns the C code."""
+                 stream=None, attn_mask=None, workspace=None) -> int:
+    """Call cmpext3_attn_bwd (workspace None) or cmpext3_attn_bwd_ws (a byte
+    tensor, or True for one of cmpext3_attn_bwd_workspace_size bytes made
+    here) on caller-allocated tensors; returns the C code."""
     B, H, Sq, D = q.shape
     vp = ctypes.c_void_p
     mp, mdt, mst, _keep = _mask_args(attn_mask, B, H, Sq, k.shape[2], runs=True)
-    return lib().cmpext3_attn_bwd(
-        *(vp(t.data_ptr()) for t in (q, k, v, o, do, lse, dq, dk, dv, delta)),
-        dtype_code(q.dtype), B, H, k.shape[1], Sq, k.shape[2], D,
-        *(_strides(t) for t in (q, k, v, o, do, dq, dk, dv)),
-        mp, mdt, mst, ctypes.c_float(scale), int(causal), vp(_handle(q, stream)))
+    args = [*(vp(t.data_ptr()) for t in (q, k, v, o, do, lse, dq, dk, dv, delta)),
+            dtype_code(q.dtype), B, H, k.shape[1], Sq, k.shape[2], D,
+            *(_strides(t) for t in (q, k, v, o, do, dq, dk, dv)),
+            mp, mdt, mst, ctypes.c_float(scale), int(causal)]
+    if workspace is None:
+        return lib().cmpext3_attn_bwd(*args, vp(_handle(q, stream)))
+    if workspace is True:
+        import torch
+        n = bwd_workspace_size(dtype_code(q.dtype), B, H, k.shape[1], Sq, k.shape[2], D, mdt, causal)
+        workspace = torch.empty(max(n, 16), dtype=torch.uint8, device=q.device)
+    return lib().cmpext3_attn_bwd_ws(*args, vp(workspace.data_ptr()), workspace.numel(),
+                                     vp(_handle(q, stream)))
 
 
 def attn_bwd(q, k, v, o, do, lse, scale: Optional[float] = None, causal: bool = False, stream=None,
-             attn_mask=None):
-    """Gradients (dq, dk, dv) through cmpext3_attn_bwd (outputs contiguous, a
-    delta workspace allocated here).  Raises RuntimeError on a non-zero code."""
+             attn_mask=None, workspace=True):
+    """Gradients (dq, dk, dv) through cmpext3_attn_bwd_ws (outputs contiguous;
+    the delta workspace and, with workspace=True, the split workspace
+    allocated here; workspace=None: cmpext3_attn_bwd, never split).  Raises
+    RuntimeError on a non-zero code."""
     import torch
     B, H, Sq, D = q.shape
     dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
@@ -286,7 +310,7 @@ def attn_bwd(q, k, v, o, do, lse, scale: Optional[float] = None, causal: bool = 
     delta = torch.empty(B, H, Sq, dtype=torch.float32, device=q.device)
     if scale is None:
         scale = D ** -0.5
-    rc = attn_bwd_raw(q, k, v, o, do, lse, dq, dk, dv, delta, scale, causal, stream, attn_mask)
+    rc = attn_bwd_raw(q, k, v, o, do, lse, dq, dk, dv, delta, scale, causal, stream, attn_mask, workspace)
     if rc != OK:
         raise RuntimeError(f"cmpext3_attn_bwd: {strerror(rc)} (code {rc})")
     return dq, dk, dv

@@ -19,6 +19,8 @@
 
 namespace cmpext3 {
 hipError_t launch_bwd16(const BwdParams& p, bool bf16, bool causal, hipStream_t s);
+int bwd16_split(int B, int Hkv, int group, int Sq, int Sk, int D, bool causal, bool masked, int cus);
+size_t bwd16_split_bytes(int B, int Hkv, int Sk, int D, int ns);
 hipError_t launch_bwd32(const BwdParams& p, bool causal, hipStream_t s);
 hipError_t launch_mfma16(const FwdParams& p, bool bf16, bool causal, hipStream_t s);
 hipError_t launch_mfma32(const FwdParams& p, bool causal, hipStream_t s);
@@ -398,6 +400,15 @@ int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, f
                   mask_dtype, mask_str, scale, causal, stream, workspace, workspace_bytes);
 }
 
+size_t cmpext3_attn_bwd_workspace_size(int dtype, int B, int H, int H_kv, int Sq, int Sk, int D,
+                                       int mask_dtype, int causal) {
+  if (check_shape(dtype, B, H, Sq, Sk, D) != CMPEXT3_OK || dtype == CMPEXT3_DTYPE_F32) return 0;
+  if (!whole_chunks(dtype, D) || H_kv < 1 || H_kv > H || H % H_kv != 0) return 0;
+  const int ns = cmpext3::bwd16_split(B, H_kv, H / H_kv, Sq, Sk, D, causal != 0, mask_dtype != -1,
+                                      cmpext3::device_cus());
+  return cmpext3::bwd16_split_bytes(B, H_kv, Sk, D, ns);
+}
+
 int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
                      const float* lse, void* dq, void* dk, void* dv, float* delta, int dtype, int B,
                      int H, int H_kv, int Sq, int Sk, int D, const int64_t q_str[3], const int64_t k_str[3],
@@ -405,6 +416,18 @@ int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
                      const int64_t dq_str[3], const int64_t dk_str[3], const int64_t dv_str[3],
                      const void* mask, int mask_dtype, const int64_t mask_str[3], float scale, int causal,
                      hipStream_t stream) {
+  return cmpext3_attn_bwd_ws(q, k, v, o, dout, lse, dq, dk, dv, delta, dtype, B, H, H_kv, Sq, Sk, D, q_str,
+                             k_str, v_str, o_str, do_str, dq_str, dk_str, dv_str, mask, mask_dtype, mask_str,
+                             scale, causal, nullptr, 0, stream);
+}
+
+int cmpext3_attn_bwd_ws(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                        const float* lse, void* dq, void* dk, void* dv, float* delta, int dtype, int B,
+                        int H, int H_kv, int Sq, int Sk, int D, const int64_t q_str[3], const int64_t k_str[3],
+                        const int64_t v_str[3], const int64_t o_str[3], const int64_t do_str[3],
+                        const int64_t dq_str[3], const int64_t dk_str[3], const int64_t dv_str[3],
+                        const void* mask, int mask_dtype, const int64_t mask_str[3], float scale, int causal,
+                        void* workspace, size_t workspace_bytes, hipStream_t stream) {
   int rc = check_shape(dtype, B, H, Sq, Sk, D);
   if (rc != CMPEXT3_OK) return rc;
   if ((int64_t)B * H * Sq == 0) return CMPEXT3_OK;
@@ -419,6 +442,7 @@ int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
     return CMPEXT3_E_INVALID;
   if (!isfinite(scale)) return CMPEXT3_E_INVALID;
   if (((uintptr_t)lse & 3u) != 0 || ((uintptr_t)delta & 3u) != 0) return CMPEXT3_E_ALIGN;
+  if (workspace && !aligned16(workspace)) return CMPEXT3_E_ALIGN;
   const void* ptrs[] = {q, k, v, o, dout, dq, dk, dv};
   for (const void* ptr : ptrs)
     if (!aligned16(ptr)) return CMPEXT3_E_ALIGN;
@@ -458,6 +482,16 @@ int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
   p.c = fmaxf(fabsf(scale) * cmpext3::kLog2e, 1e-30f);
   p.scale = scale;
   p.sign = scale < 0.f ? (dtype == CMPEXT3_DTYPE_F32 ? 0x80000000u : 0x80008000u) : 0u;
+  // split dK/dV sweeps when the workspace holds their partials (else unsplit)
+  p.nsplit = 1;
+  if (workspace && dtype != CMPEXT3_DTYPE_F32) {
+    const int ns = cmpext3::bwd16_split(B, H_kv, H / H_kv, Sq, Sk, D, causal != 0,
+                                        p.mask_kind != cmpext3::MASK_NONE, cmpext3::device_cus());
+    if (ns > 1 && workspace_bytes >= cmpext3::bwd16_split_bytes(B, H_kv, Sk, D, ns)) {
+      p.nsplit = ns;
+      p.part = (float*)workspace;
+    }
+  }
   const hipError_t err = dtype == CMPEXT3_DTYPE_F32
                              ? cmpext3::launch_bwd32(p, causal != 0, stream)
                              : cmpext3::launch_bwd16(p, dtype == CMPEXT3_DTYPE_BF16, causal != 0, stream);

@@ -11,8 +11,10 @@
 //   with dP = dO V^T and dS = P * (dP - Delta).
 // P is recomputed from the scores and the saved log-sum-exp, so nothing of
 // size Sq x Sk is stored.  The two gradient kernels each own their output rows
-// outright (no atomics, no accumulation across workgroups), so the results are
-// bit-identical from run to run.  The reference is forward-only (its patch
+// outright (no atomics), so the results are bit-identical from run to run;
+// where a dK/dV sweep is split over several workgroups (few key blocks for
+// the CUs), their fp32 partials go to a caller workspace and
+// attn_bwd_dkdv_reduce adds them in a fixed order.  The reference is forward-only (its patch
 // hands calls with live autograd to stock torch, cmpext3/__init__.py:115-125);
 // this is the gradient of the same forward, checked against the float64
 // restatement in oracle/sdpa_oracle.py (sdpa_bwd_np).
@@ -28,8 +30,9 @@
 // dQ^T = K^T dS^T.  A negative scale is folded into the sign of the operand
 // held in registers (K in dK/dV, Q in dQ), and the signed scale multiplies the
 // result.  Grouped-query K/V (Hkv heads shared by H / Hkv query heads each):
-// a dK/dV workgroup sweeps the query tiles of every query head of its group,
-// so the group's contributions are summed in registers.
+// a dK/dV workgroup sweeps the query tiles of every query head of its group
+// (or its part of that sequence), so the group's contributions are summed in
+// registers.
 #pragma once
 
 #include "attn_fwd_pipe16.h"
@@ -54,7 +57,7 @@ struct BwdParams {
   int Hkv;          // K/V heads (dk, dv have Hkv heads); query head h uses K/V head h / group
   int group;        // H / Hkv
   int n_blk;        // key blocks (dK/dV, per K/V head) or query blocks (dQ, per query head)
-  int n_wg;         // workgroups launched = B * H * n_blk
+  int n_wg;         // workgroups launched = B * H * n_blk (dK/dV: times nsplit)
   float c;          // |scale| * log2(e)
   float scale;      // signed scale: dK = scale * dS^T Q, dQ = scale * dS K
   uint32_t sign;    // 0x80008000 when scale < 0 (XORed into K or Q words), else 0
@@ -63,6 +66,11 @@ struct BwdParams {
   const void* mask;
   int64_t m_b, m_h, m_q;
   int mask_kind;
+  // dK/dV split sweeps (f16/bf16): nsplit > 1 workgroups per key block, each
+  // leaving fp32 partial dK / dV rows in `part` ([nsplit][B * Hkv][Sk][D] for
+  // dK, then the same for dV) that attn_bwd_dkdv_reduce sums
+  int nsplit;
+  float* part;
 };
 
 // LDS row stride (halves) of the Q/dO and K/V tiles: rows padded by 16 bytes,
@@ -176,6 +184,24 @@ __device__ __forceinline__ void store_rows(uint16_t* base, int64_t row_stride, i
     }
 }
 
+// The same accumulator set unscaled, as fp32 rows of D floats (row = lane's
+// key; rows past nrows are not stored).
+template <int NDB>
+__device__ __forceinline__ void store_rows_f32(float* base, int row, int nrows, int D, int hh,
+                                               const f32x16 (&acc)[NDB]) {
+  if (row >= nrows) return;
+  float* dst = base + (int64_t)row * D;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = 32 * db + 8 * g + 4 * hh;
+      if (d < D)
+        *(f32x4*)(dst + d) =
+            (f32x4){acc[db][4 * g + 0], acc[db][4 * g + 1], acc[db][4 * g + 2], acc[db][4 * g + 3]};
+    }
+}
+
 // ---- dK, dV for one block of 128 keys (4 waves x 32 keys), sweeping the
 // query tiles (32 rows of Q, dO, lse, Delta) through double-buffered LDS.
 // Waves per SIMD: D <= 64: 3 (masked with V parked in LDS; 4 spilled
@@ -214,7 +240,11 @@ attn_bwd_dkdv(const BwdParams p) {
   // they start first); XCD-contiguous ranges share Q/dO in L2
   // (the divisions run on the vector unit: readfirstlane keeps the indices,
   // and the per-head address arithmetic of the sweep, in scalar registers)
-  const int tile = __builtin_amdgcn_readfirstlane(xcd_remap(block_x(), p.n_wg));
+  // split sweeps: workgroups (tile, part) of one block are adjacent
+  const int ns = p.nsplit > 1 ? p.nsplit : 1;
+  const int widx = __builtin_amdgcn_readfirstlane(xcd_remap(block_x(), p.n_wg));
+  const int tile = __builtin_amdgcn_readfirstlane(widx / ns);
+  const int part = widx - tile * ns;
   const int bhk = __builtin_amdgcn_readfirstlane(tile / p.n_blk);  // (batch, K/V head)
   const int kb = tile - bhk * p.n_blk;                             // key block
   const int b = __builtin_amdgcn_readfirstlane(bhk / p.Hkv), hk = bhk - b * p.Hkv;
@@ -266,17 +296,20 @@ attn_bwd_dkdv(const BwdParams p) {
   for (int db = 0; db < NDB; ++db) dva[db] = dka[db] = (f32x16){};
 
   // The sweep: query tiles t0 .. t1-1 of each query head of the group, as one
-  // sequence of nj tiles.  (fg, ft) is the head and tile of the next fetch,
-  // (cg, ct) those of the tile being computed: running counters, no divisions.
+  // sequence of nj tiles, of which this workgroup takes [jb, je) (all of it
+  // unless the sweep is split).  (fg, ft) is the head and tile of the next
+  // fetch, (cg, ct) those of the tile being computed: running counters.
   const int t0 = CAUSAL ? kb * (BKV / BQ) : 0;  // query tiles before the block see none of its keys
   const int t1 = (Sq + BQ - 1) / BQ;
   const int nt = t1 > t0 ? t1 - t0 : 0;
   const int nj = nt * p.group;
+  const int jb = (int)((int64_t)part * nj / ns), je = (int)((int64_t)(part + 1) * nj / ns);
+  const int jg0 = nt > 0 ? jb / nt : 0;
   u32x4 xq[TileLoader<DK>::N], xd[TileLoader<DK>::N];
   float xl = -INFINITY, xdl = 0.f;  // raw lse / Delta of the fetched rows
   const float inv_c = 1.f / p.c;    // c > 0 (the caller floors it for tiny |scale|)
   const int h0 = hk * p.group;      // first query head of the group
-  int fg = 0, ft = t0;
+  int fg = jg0, ft = t0 + (jb - jg0 * nt);
   auto fetch = [&]() {
     const int h = h0 + fg;
     const uint16_t* qg = (const uint16_t*)p.q + b * p.q_b + h * p.q_h;
@@ -319,9 +352,20 @@ attn_bwd_dkdv(const BwdParams p) {
   // lane = key, registers = head-dim columns
   uint16_t* dkg = (uint16_t*)p.dk + b * p.dk_b + hk * p.dk_h;
   uint16_t* dvg = (uint16_t*)p.dv + b * p.dv_b + hk * p.dv_h;
-  if (nj == 0) {  // no query sees this block (causal): zero gradients
-    store_rows<T, NDB>(dvg, p.dv_s, key, Sk, D, hh, dva, 1.f);
-    store_rows<T, NDB>(dkg, p.dk_s, key, Sk, D, hh, dka, p.scale);
+  // the result: gradients, or this part's fp32 partials (dK unscaled)
+  auto finish = [&]() {
+    if (ns > 1) {
+      const int64_t rows = (int64_t)p.B * p.Hkv * Sk;
+      float* const pk = p.part + ((int64_t)part * p.B * p.Hkv + bhk) * Sk * D;
+      store_rows_f32<NDB>(pk, key, Sk, D, hh, dka);
+      store_rows_f32<NDB>(pk + ns * rows * D, key, Sk, D, hh, dva);
+    } else {
+      store_rows<T, NDB>(dvg, p.dv_s, key, Sk, D, hh, dva, 1.f);
+      store_rows<T, NDB>(dkg, p.dk_s, key, Sk, D, hh, dka, p.scale);
+    }
+  };
+  if (je == jb) {  // no query of this range sees the block (causal): zeros
+    finish();
     return;
   }
   // (the loop is entered only past put(0), whose waits cover the operand
@@ -329,10 +373,10 @@ attn_bwd_dkdv(const BwdParams p) {
   fetch();
   put(0);
   lds_barrier();
-  int cg = 0, ct = t0;
-  for (int j = 0; j < nj; ++j) {
-    const int slot = j & 1;
-    if (j + 1 < nj) fetch();
+  int cg = jg0, ct = t0 + (jb - jg0 * nt);
+  for (int j = jb; j < je; ++j) {
+    const int slot = (j - jb) & 1;
+    if (j + 1 < je) fetch();
     const int q0 = ct * BQ;
     // causal: a tile whose last query precedes this wave's first key adds nothing
     if (!CAUSAL || q0 + BQ - 1 >= kw0) {
@@ -416,16 +460,42 @@ attn_bwd_dkdv(const BwdParams p) {
           dka[db] = Elt<T>::mma(tr_frag(qsl, t_rd[db][0], t_rd[db][1]), ps[ks], dka[db]);
         }
     }
-    if (j + 1 < nj) put(slot ^ 1);
+    if (j + 1 < je) put(slot ^ 1);
     lds_barrier();
     if (++ct == t1) {
       ct = t0;
       ++cg;
     }
   }
+  finish();
+}
 
-  store_rows<T, NDB>(dvg, p.dv_s, key, Sk, D, hh, dva, 1.f);
-  store_rows<T, NDB>(dkg, p.dk_s, key, Sk, D, hh, dka, p.scale);
+// ---- Sum of the split dK/dV sweeps' partials, in part order (the same
+// result on every run), times the signed scale for dK; 4 columns per thread.
+template <typename T>
+__global__ void __launch_bounds__(256) attn_bwd_dkdv_reduce(const BwdParams p) {
+  const int D = p.D, Sk = p.Sk, ns = p.nsplit;
+  const int64_t rows = (int64_t)p.B * p.Hkv * Sk, n4 = rows * D / 4;
+  const int64_t i4 = (int64_t)block_x() * 256 + thread_x();
+  if (i4 >= n4) return;
+  const int64_t row = i4 * 4 / D;
+  const int d = (int)(i4 * 4 - row * D);
+  const int bhk = (int)(row / Sk), key = (int)(row - (int64_t)bhk * Sk);
+  const int b = bhk / p.Hkv, hk = bhk - b * p.Hkv;
+  const f32x4* const pk = (const f32x4*)p.part + i4;
+  const int64_t step = rows * D / 4;  // one part's vectors
+  f32x4 gk = pk[0], gv = pk[ns * step];
+  for (int q = 1; q < ns; ++q) {
+    gk += pk[q * step];
+    gv += pk[(ns + q) * step];
+  }
+  u32x2 wk, wv;
+  wk[0] = Elt<T>::pack(gk[0] * p.scale, gk[1] * p.scale);
+  wk[1] = Elt<T>::pack(gk[2] * p.scale, gk[3] * p.scale);
+  wv[0] = Elt<T>::pack(gv[0], gv[1]);
+  wv[1] = Elt<T>::pack(gv[2], gv[3]);
+  *(u32x2*)((uint16_t*)p.dk + b * p.dk_b + hk * p.dk_h + (int64_t)key * p.dk_s + d) = wk;
+  *(u32x2*)((uint16_t*)p.dv + b * p.dv_b + hk * p.dv_h + (int64_t)key * p.dv_s + d) = wv;
 }
 
 // ---- dQ for one block of 128 queries (4 waves x 32 queries), sweeping the

@@ -388,12 +388,18 @@ std::vector<torch::Tensor> attention_bwd(torch::Tensor query, torch::Tensor key,
     int64_t qs[3], ks[3], vs[3], os[3], gs[3], dqs[3], dks[3], dvs[3];
     strides3(q, qs); strides3(k, ks); strides3(v, vs); strides3(o, os); strides3(g, gs);
     strides3(dq, dqs); strides3(dk, dks); strides3(dv, dvs);
-    const int rc = cmpext3_attn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), g.data_ptr(),
-                                    l.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                                    delta.data_ptr<float>(), dtype, (int)B, (int)H, (int)Hkv, (int)Sq,
-                                    (int)Sk, (int)Dp, qs, ks, vs, os, gs, dqs, dks, dvs,
-                                    mask.dtype >= 0 ? mask.t.data_ptr() : nullptr, mask.dtype, ms, scale,
-                                    causal ? 1 : 0, stream);
+    // split dK/dV sweeps (few key blocks for the CUs) sum fp32 partials kept
+    // in a workspace from torch's caching allocator, on this stream
+    const size_t wsb = cmpext3_attn_bwd_workspace_size(dtype, (int)B, (int)H, (int)Hkv, (int)Sq, (int)Sk,
+                                                       (int)Dp, mask.dtype, causal ? 1 : 0);
+    torch::Tensor ws;
+    if (wsb > 0) ws = torch::empty({(int64_t)wsb}, query.options().dtype(at::kByte));
+    const int rc = cmpext3_attn_bwd_ws(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), g.data_ptr(),
+                                       l.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                       delta.data_ptr<float>(), dtype, (int)B, (int)H, (int)Hkv, (int)Sq,
+                                       (int)Sk, (int)Dp, qs, ks, vs, os, gs, dqs, dks, dvs,
+                                       mask.dtype >= 0 ? mask.t.data_ptr() : nullptr, mask.dtype, ms, scale,
+                                       causal ? 1 : 0, wsb > 0 ? ws.data_ptr() : nullptr, wsb, stream);
     TORCH_CHECK(rc == CMPEXT3_OK, "cmpext3 attention backward: ", cmpext3_attn_strerror(rc));
   }
   if (Dp != D) {
