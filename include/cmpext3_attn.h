@@ -305,7 +305,7 @@ int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
 
 /*
  * cmpext3_attn_bwd with a caller-owned workspace (16-byte aligned; NULL or 0
- * bytes = none).  f16/bf16 problems with too few key blocks for the CUs
+ * bytes = none).  Problems with too few key blocks for the CUs
  * (grouped-query K/V of one or two sequences, causal sweeps whose length
  * falls with the key block) cut each block's dK/dV sweep over (query head,
  * query tile) into up to 8 contiguous parts on separate workgroups; the parts
@@ -331,7 +331,7 @@ int cmpext3_attn_bwd_ws(const void* q, const void* k, const void* v, const void*
 
 /*
  * Workspace bytes cmpext3_attn_bwd_ws needs to split this problem's dK/dV
- * sweeps (mask_dtype -1 = no mask); 0 when it never splits (fp32, enough key
+ * sweeps (mask_dtype -1 = no mask); 0 when it never splits (enough key
  * blocks) or the arguments are invalid.  Depends on the current device's CU
  * count (256, MI355X's, when none is visible).  Host-only.
  */

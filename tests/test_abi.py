@@ -407,7 +407,7 @@ def test_bwd_workspace_plan():
     """The backward splits its dK/dV sweeps only with too few key blocks for
     the CU slots (256 CUs without a visible device): grouped-query and
     single-sequence launches ask for ns x B x H_kv x Sk x D x 2 fp32 partials;
-    the Qwen3 and SDXL training shapes, fp32 and invalid arguments ask for
+    the Qwen3 and SDXL training shapes and invalid arguments ask for
     nothing."""
     import torch
     if torch.cuda.is_available():
@@ -416,7 +416,10 @@ def test_bwd_workspace_plan():
     part = lambda ns, B, Hkv, Sk, D: ns * B * Hkv * Sk * D * 2 * 4
     assert abi.bwd_workspace_size(bf16, 4, 16, 16, 2048, 2048, 128, -1, True) == 0     # Qwen3 shape
     assert abi.bwd_workspace_size(f16, 2, 10, 10, 4096, 4096, 64, -1, False) == 0      # SDXL shape
-    assert abi.bwd_workspace_size(f32, 1, 8, 8, 1024, 1024, 64, -1, False) == 0
+    # fp32: 64-key blocks, 3 workgroups per CU at D = 64 non-causal: BASELINE
+    # config 1's 128 blocks take 6 parts; SD1.5's 1024 blocks none
+    assert abi.bwd_workspace_size(f32, 1, 8, 8, 1024, 1024, 64, -1, False) == part(6, 1, 8, 1024, 64)
+    assert abi.bwd_workspace_size(f32, 2, 8, 8, 4096, 4096, 40, -1, False) == 0
     assert abi.bwd_workspace_size(bf16, 1, 32, 7, 4096, 4096, 128, -1, True) == 0      # 7 does not divide 32
     assert abi.bwd_workspace_size(bf16, 1, 32, 8, 4096, 4096, 129, -1, True) == 0      # rows off 16 bytes
     # causal: two rounds of the 512 slots (2 waves per SIMD at D = 128)

@@ -20,7 +20,13 @@
 namespace cmpext3 {
 hipError_t launch_bwd16(const BwdParams& p, bool bf16, bool causal, hipStream_t s);
 int bwd16_split(int B, int Hkv, int group, int Sq, int Sk, int D, bool causal, bool masked, int cus);
-size_t bwd16_split_bytes(int B, int Hkv, int Sk, int D, int ns);
+int bwd32_split(int B, int Hkv, int group, int Sq, int Sk, int D, bool causal, int cus);
+size_t bwd_split_bytes(int B, int Hkv, int Sk, int D, int ns);
+// Parts per key block of the dK/dV sweep (1 = unsplit).
+int bwd_split(int dtype, int B, int Hkv, int group, int Sq, int Sk, int D, bool causal, bool masked) {
+  return dtype == CMPEXT3_DTYPE_F32 ? bwd32_split(B, Hkv, group, Sq, Sk, D, causal, device_cus())
+                                    : bwd16_split(B, Hkv, group, Sq, Sk, D, causal, masked, device_cus());
+}
 hipError_t launch_bwd32(const BwdParams& p, bool causal, hipStream_t s);
 hipError_t launch_mfma16(const FwdParams& p, bool bf16, bool causal, hipStream_t s);
 hipError_t launch_mfma32(const FwdParams& p, bool causal, hipStream_t s);
@@ -402,11 +408,10 @@ int cmpext3_attn_fwd_lse(const void* q, const void* k, const void* v, void* o, f
 
 size_t cmpext3_attn_bwd_workspace_size(int dtype, int B, int H, int H_kv, int Sq, int Sk, int D,
                                        int mask_dtype, int causal) {
-  if (check_shape(dtype, B, H, Sq, Sk, D) != CMPEXT3_OK || dtype == CMPEXT3_DTYPE_F32) return 0;
+  if (check_shape(dtype, B, H, Sq, Sk, D) != CMPEXT3_OK) return 0;
   if (!whole_chunks(dtype, D) || H_kv < 1 || H_kv > H || H % H_kv != 0) return 0;
-  const int ns = cmpext3::bwd16_split(B, H_kv, H / H_kv, Sq, Sk, D, causal != 0, mask_dtype != -1,
-                                      cmpext3::device_cus());
-  return cmpext3::bwd16_split_bytes(B, H_kv, Sk, D, ns);
+  const int ns = cmpext3::bwd_split(dtype, B, H_kv, H / H_kv, Sq, Sk, D, causal != 0, mask_dtype != -1);
+  return cmpext3::bwd_split_bytes(B, H_kv, Sk, D, ns);
 }
 
 int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
@@ -484,10 +489,10 @@ int cmpext3_attn_bwd_ws(const void* q, const void* k, const void* v, const void*
   p.sign = scale < 0.f ? (dtype == CMPEXT3_DTYPE_F32 ? 0x80000000u : 0x80008000u) : 0u;
   // split dK/dV sweeps when the workspace holds their partials (else unsplit)
   p.nsplit = 1;
-  if (workspace && dtype != CMPEXT3_DTYPE_F32) {
-    const int ns = cmpext3::bwd16_split(B, H_kv, H / H_kv, Sq, Sk, D, causal != 0,
-                                        p.mask_kind != cmpext3::MASK_NONE, cmpext3::device_cus());
-    if (ns > 1 && workspace_bytes >= cmpext3::bwd16_split_bytes(B, H_kv, Sk, D, ns)) {
+  if (workspace) {
+    const int ns = cmpext3::bwd_split(dtype, B, H_kv, H / H_kv, Sq, Sk, D, causal != 0,
+                                      p.mask_kind != cmpext3::MASK_NONE);
+    if (ns > 1 && workspace_bytes >= cmpext3::bwd_split_bytes(B, H_kv, Sk, D, ns)) {
       p.nsplit = ns;
       p.part = (float*)workspace;
     }

@@ -71,7 +71,8 @@ int bwd16_split(int B, int Hkv, int group, int Sq, int Sk, int D, bool causal, b
   return ns >= 2 ? (int)ns : 1;
 }
 
-size_t bwd16_split_bytes(int B, int Hkv, int Sk, int D, int ns) {
+// Workspace of a split backward: fp32 partial dK and dV rows of every part.
+size_t bwd_split_bytes(int B, int Hkv, int Sk, int D, int ns) {
   return ns > 1 ? (size_t)ns * B * Hkv * Sk * D * 2 * sizeof(float) : 0;
 }
 

@@ -172,7 +172,11 @@ __global__ void __launch_bounds__(256) attn_bwd32_dkdv(const BwdParams p) {
   const int tid = thread_x(), wave = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
   // key blocks in order (causal: the first blocks see the most queries);
   // XCD-contiguous ranges share Q/dO in L2
-  const int tile = __builtin_amdgcn_readfirstlane(xcd_remap(block_x(), p.n_wg));
+  // split sweeps: workgroups (tile, part) of one block are adjacent
+  const int ns = p.nsplit > 1 ? p.nsplit : 1;
+  const int widx = __builtin_amdgcn_readfirstlane(xcd_remap(block_x(), p.n_wg));
+  const int tile = __builtin_amdgcn_readfirstlane(widx / ns);
+  const int part = widx - tile * ns;
   const int bhk = __builtin_amdgcn_readfirstlane(tile / p.n_blk);
   const int kb = tile - bhk * p.n_blk;
   const int b = __builtin_amdgcn_readfirstlane(bhk / p.Hkv), hk = bhk - b * p.Hkv;
@@ -207,16 +211,19 @@ __global__ void __launch_bounds__(256) attn_bwd32_dkdv(const BwdParams p) {
   for (int db = 0; db < NDB; ++db) dva[db] = dka[db] = (f32x4){};
 
   // the sweep: query tiles t0 .. t1-1 of each query head of the group as one
-  // sequence of nj tiles; (fg, ft) = head and tile of the next fetch, (cg, ct)
-  // those of the tile being computed
+  // sequence of nj tiles, of which this workgroup takes [jb, je) (all of it
+  // unless the sweep is split); (fg, ft) = head and tile of the next fetch,
+  // (cg, ct) those of the tile being computed
   const int t0 = CAUSAL ? kb * (BKV / BQ) : 0;  // earlier query tiles see none of the block's keys
   const int t1 = (Sq + BQ - 1) / BQ;
   const int nt = t1 > t0 ? t1 - t0 : 0;
   const int nj = nt * p.group;
+  const int jb = (int)((int64_t)part * nj / ns), je = (int)((int64_t)(part + 1) * nj / ns);
+  const int jg0 = nt > 0 ? jb / nt : 0;
   u32x4 xq[Tile::N], xd[Tile::N];
   float xl = INFINITY, xdl = 0.f;
   const int h0 = hk * p.group;
-  int fg = 0, ft = t0;
+  int fg = jg0, ft = t0 + (jb - jg0 * nt);
   auto fetch = [&]() {
     const int h = h0 + fg;
     const float* qg = (const float*)p.q + b * p.q_b + h * p.q_h;
@@ -254,9 +261,20 @@ __global__ void __launch_bounds__(256) attn_bwd32_dkdv(const BwdParams p) {
 
   float* dkg = (float*)p.dk + b * p.dk_b + hk * p.dk_h;
   float* dvg = (float*)p.dv + b * p.dv_b + hk * p.dv_h;
-  if (nj == 0) {  // no query sees this block (causal): zero gradients
-    store_rows32<NDB>(dvg, p.dv_s, key, Sk, D, g, dva, 1.f);
-    store_rows32<NDB>(dkg, p.dk_s, key, Sk, D, g, dka, p.scale);
+  // the result: gradients, or this part's partial rows (dK unscaled)
+  auto finish = [&]() {
+    if (ns > 1) {
+      const int64_t rows = (int64_t)p.B * p.Hkv * Sk;
+      float* const pk = p.part + ((int64_t)part * p.B * p.Hkv + bhk) * Sk * D;
+      store_rows32<NDB>(pk, D, key, Sk, D, g, dka, 1.f);
+      store_rows32<NDB>(pk + ns * rows * D, D, key, Sk, D, g, dva, 1.f);
+    } else {
+      store_rows32<NDB>(dvg, p.dv_s, key, Sk, D, g, dva, 1.f);
+      store_rows32<NDB>(dkg, p.dk_s, key, Sk, D, g, dka, p.scale);
+    }
+  };
+  if (je == jb) {  // no query of this range sees the block (causal): zeros
+    finish();
     return;
   }
   const bool masked = p.mask_kind != MASK_NONE;
@@ -265,10 +283,10 @@ __global__ void __launch_bounds__(256) attn_bwd32_dkdv(const BwdParams p) {
   fetch();
   put(0);
   lds_barrier();
-  int cg = 0, ct = t0;
-  for (int j = 0; j < nj; ++j) {
-    const int slot = j & 1;
-    if (j + 1 < nj) fetch();
+  int cg = jg0, ct = t0 + (jb - jg0 * nt);
+  for (int j = jb; j < je; ++j) {
+    const int slot = (j - jb) & 1;
+    if (j + 1 < je) fetch();
     const int q0 = ct * BQ;
     const float* qs = lds + slot * 2 * BQ * RS;
     const float* dos = qs + BQ * RS;
@@ -329,16 +347,36 @@ __global__ void __launch_bounds__(256) attn_bwd32_dkdv(const BwdParams p) {
           dka[db] = mma4(qs[pos], ds[r], dka[db]);
         }
     }
-    if (j + 1 < nj) put(slot ^ 1);
+    if (j + 1 < je) put(slot ^ 1);
     lds_barrier();
     if (++ct == t1) {
       ct = t0;
       ++cg;
     }
   }
+  finish();
+}
 
-  store_rows32<NDB>(dvg, p.dv_s, key, Sk, D, g, dva, 1.f);
-  store_rows32<NDB>(dkg, p.dk_s, key, Sk, D, g, dka, p.scale);
+// ---- Sum of the split dK/dV sweeps' partials, in part order (the same
+// result on every run), times the signed scale for dK; 4 columns per thread.
+__global__ void __launch_bounds__(256) attn_bwd32_dkdv_reduce(const BwdParams p) {
+  const int D = p.D, Sk = p.Sk, ns = p.nsplit;
+  const int64_t rows = (int64_t)p.B * p.Hkv * Sk, n4 = rows * D / 4;
+  const int64_t i4 = (int64_t)block_x() * 256 + thread_x();
+  if (i4 >= n4) return;
+  const int64_t row = i4 * 4 / D;
+  const int d = (int)(i4 * 4 - row * D);
+  const int bhk = (int)(row / Sk), key = (int)(row - (int64_t)bhk * Sk);
+  const int b = bhk / p.Hkv, hk = bhk - b * p.Hkv;
+  const f32x4* const pk = (const f32x4*)p.part + i4;
+  const int64_t step = rows * D / 4;  // one part's vectors
+  f32x4 gk = pk[0], gv = pk[ns * step];
+  for (int q = 1; q < ns; ++q) {
+    gk += pk[q * step];
+    gv += pk[(ns + q) * step];
+  }
+  *(f32x4*)((float*)p.dk + b * p.dk_b + hk * p.dk_h + (int64_t)key * p.dk_s + d) = gk * p.scale;
+  *(f32x4*)((float*)p.dv + b * p.dv_b + hk * p.dv_h + (int64_t)key * p.dv_s + d) = gv;
 }
 
 // ---- dQ for one block of 64 queries (4 waves x 16 queries), sweeping
@@ -482,8 +520,14 @@ hipError_t launch_bwd32_t(const BwdParams& p0, hipStream_t s) {
   const int64_t rows = (int64_t)p.B * p.H * p.Sq;
   hipLaunchKernelGGL(attn_bwd32_delta, dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, s, p);
   p.n_blk = (p.Sk + 63) / 64;
-  p.n_wg = p.B * p.Hkv * p.n_blk;
+  const int ns = p.nsplit > 1 && p.part ? p.nsplit : 1;
+  p.nsplit = ns;
+  p.n_wg = p.B * p.Hkv * p.n_blk * ns;
   hipLaunchKernelGGL((attn_bwd32_dkdv<DK, CAUSAL>), dim3(p.n_wg), dim3(256), 0, s, p);
+  if (ns > 1) {
+    const int64_t n4 = (int64_t)p.B * p.Hkv * p.Sk * p.D / 4;
+    hipLaunchKernelGGL(attn_bwd32_dkdv_reduce, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, p);
+  }
   p.n_blk = (p.Sq + 63) / 64;
   p.n_wg = p.B * p.H * p.n_blk;
   hipLaunchKernelGGL((attn_bwd32_dq<DK, CAUSAL>), dim3(p.n_wg), dim3(256), 0, s, p);
@@ -510,6 +554,27 @@ int bwd32_bucket(int D) {
   for (int dk : {32, 40, 64, 96, 128, 192, 256})
     if (D <= dk) return dk;
   return -1;
+}
+
+// Workgroups of the fp32 dK/dV sweep per 64-key block, as bwd16_split plans
+// the f16/bf16 one: with too few key blocks for the CU slots (the kernel's
+// workgroups per CU from its registers and LDS: 5 at D <= 32, 4 up to 40, 3-4
+// up to 64, 2 up to 128, then 1), non-causal sweeps are cut
+// into as many parts as fill one round, causal ones two rounds; at most 8
+// parts, each at least 4 query tiles of the longest sweep.
+int bwd32_split(int B, int Hkv, int group, int Sq, int Sk, int D, bool causal, int cus) {
+  const int dk = bwd32_bucket(D);
+  if (dk < 0 || (int64_t)B * Hkv * Sq == 0) return 1;
+  const int occ = dk <= 32 ? 5 : dk <= 40 ? 4 : dk <= 64 ? (causal ? 4 : 3) : dk <= 128 ? 2 : 1;
+  const int64_t n_wg = (int64_t)B * Hkv * ((Sk + 63) / 64);
+  const int64_t slots = (int64_t)cus * occ;
+  const int64_t want = causal ? 2 * slots : slots;
+  if (n_wg * 2 > want) return 1;
+  int64_t ns = causal ? (want + n_wg - 1) / n_wg : want / n_wg;
+  const int64_t nj = (int64_t)group * ((Sq + 31) / 32);
+  if (ns > 8) ns = 8;
+  if (ns > nj / 4) ns = nj / 4;
+  return ns >= 2 ? (int)ns : 1;
 }
 
 hipError_t launch_bwd32(const BwdParams& p, bool causal, hipStream_t s) {
