@@ -308,11 +308,13 @@ int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
  * bytes = none).  Problems with too few key blocks for the CUs
  * (grouped-query K/V of one or two sequences, causal sweeps whose length
  * falls with the key block) cut each block's dK/dV sweep over (query head,
- * query tile) into up to 8 contiguous parts on separate workgroups; the parts
- * leave fp32 partial dK/dV rows in the workspace and a fourth kernel sums
- * them in part order (still bit-identical from run to run; the sums differ
- * from the unsplit launch's only by rounding).  A workspace smaller than
- * cmpext3_attn_bwd_workspace_size runs unsplit.  Otherwise the arguments,
+ * query tile) into up to 8 contiguous parts on separate workgroups, and
+ * likewise the dQ sweeps of few query blocks over key tiles; the parts leave
+ * fp32 partial rows in the workspace that a further kernel sums in part
+ * order (still bit-identical from run to run; the sums differ from the
+ * unsplit launch's only by rounding).  With a workspace smaller than
+ * cmpext3_attn_bwd_workspace_size, a sweep whose partials do not fit runs
+ * unsplit (the dK/dV partials take the workspace first).  Otherwise the arguments,
  * results and return codes of cmpext3_attn_bwd (CMPEXT3_E_ALIGN also for a
  * misaligned workspace).
  *
@@ -330,9 +332,9 @@ int cmpext3_attn_bwd_ws(const void* q, const void* k, const void* v, const void*
                         hipStream_t stream);
 
 /*
- * Workspace bytes cmpext3_attn_bwd_ws needs to split this problem's dK/dV
- * sweeps (mask_dtype -1 = no mask); 0 when it never splits (enough key
- * blocks) or the arguments are invalid.  Depends on the current device's CU
+ * Workspace bytes cmpext3_attn_bwd_ws needs to split this problem's gradient
+ * sweeps (mask_dtype -1 = no mask); 0 when it never splits (enough blocks)
+ * or the arguments are invalid.  Depends on the current device's CU
  * count (256, MI355X's, when none is visible).  Host-only.
  */
 size_t cmpext3_attn_bwd_workspace_size(int dtype, int B, int H, int H_kv, int Sq, int Sk, int D,

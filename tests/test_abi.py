@@ -404,33 +404,40 @@ def test_workspace_alignment_is_checked_before_launch():
 
 
 def test_bwd_workspace_plan():
-    """The backward splits its dK/dV sweeps only with too few key blocks for
-    the CU slots (256 CUs without a visible device): grouped-query and
-    single-sequence launches ask for ns x B x H_kv x Sk x D x 2 fp32 partials;
-    the Qwen3 and SDXL training shapes and invalid arguments ask for
-    nothing."""
+    """The backward splits a gradient sweep only with too few blocks for the
+    CU slots (256 CUs without a visible device): a split dK/dV sweep asks for
+    ns x B x H_kv x Sk x D x 2 fp32 partials, a split dQ sweep for
+    ns_q x B x H x Sq x D; the Qwen3 and SDXL training shapes and invalid
+    arguments ask for nothing."""
     import torch
     if torch.cuda.is_available():
         pytest.skip("plan depends on the visible device's CU count")
     f16, bf16, f32 = abi.DTYPE_F16, abi.DTYPE_BF16, abi.DTYPE_F32
-    part = lambda ns, B, Hkv, Sk, D: ns * B * Hkv * Sk * D * 2 * 4
+    kv = lambda ns, B, Hkv, Sk, D: ns * B * Hkv * Sk * D * 2 * 4
+    dq = lambda ns, B, H, Sq, D: ns * B * H * Sq * D * 4
     assert abi.bwd_workspace_size(bf16, 4, 16, 16, 2048, 2048, 128, -1, True) == 0     # Qwen3 shape
     assert abi.bwd_workspace_size(f16, 2, 10, 10, 4096, 4096, 64, -1, False) == 0      # SDXL shape
-    # fp32: 64-key blocks, 3 workgroups per CU at D = 64 non-causal: BASELINE
-    # config 1's 128 blocks take 6 parts; SD1.5's 1024 blocks none
-    assert abi.bwd_workspace_size(f32, 1, 8, 8, 1024, 1024, 64, -1, False) == part(6, 1, 8, 1024, 64)
+    # fp32: 64-row blocks; BASELINE config 1's 128 key blocks (3 workgroups per
+    # CU) take 6 parts and its 128 query blocks (4 per CU) 8; SD1.5's none
+    assert abi.bwd_workspace_size(f32, 1, 8, 8, 1024, 1024, 64, -1, False) == \
+        kv(6, 1, 8, 1024, 64) + dq(8, 1, 8, 1024, 64)
     assert abi.bwd_workspace_size(f32, 2, 8, 8, 4096, 4096, 40, -1, False) == 0
     assert abi.bwd_workspace_size(bf16, 1, 32, 7, 4096, 4096, 128, -1, True) == 0      # 7 does not divide 32
+    assert abi.bwd_workspace_size(bf16, 1, 32, 8, 4096, 4096, 128, -1, True) == kv(4, 1, 8, 4096, 128)
     assert abi.bwd_workspace_size(bf16, 1, 32, 8, 4096, 4096, 129, -1, True) == 0      # rows off 16 bytes
-    # causal: two rounds of the 512 slots (2 waves per SIMD at D = 128)
-    assert abi.bwd_workspace_size(bf16, 1, 32, 8, 4096, 4096, 128, -1, True) == part(4, 1, 8, 4096, 128)
-    assert abi.bwd_workspace_size(bf16, 2, 32, 8, 4096, 4096, 128, -1, True) == part(2, 2, 8, 4096, 128)
-    # non-causal: one round
-    assert abi.bwd_workspace_size(bf16, 1, 32, 8, 4096, 4096, 128, -1, False) == part(2, 1, 8, 4096, 128)
+    # grouped-query K/V: only the dK/dV grid is small (the dQ grid has every
+    # query head); causal: two rounds of the 512 slots (2 waves per SIMD at
+    # D = 128), non-causal one
+    assert abi.bwd_workspace_size(bf16, 2, 32, 8, 4096, 4096, 128, -1, True) == kv(2, 2, 8, 4096, 128)
+    assert abi.bwd_workspace_size(bf16, 1, 32, 8, 4096, 4096, 128, -1, False) == kv(2, 1, 8, 4096, 128)
     # one wave per SIMD: D = 256, and masked causal D = 128
-    assert abi.bwd_workspace_size(bf16, 1, 16, 8, 4096, 4096, 256, -1, True) == part(2, 1, 8, 4096, 256)
+    assert abi.bwd_workspace_size(bf16, 1, 16, 8, 4096, 4096, 256, -1, True) == kv(2, 1, 8, 4096, 256)
     assert abi.bwd_workspace_size(bf16, 2, 32, 8, 4096, 4096, 128, 3, True) == 0
-    # at most 8 parts, each at least 4 query tiles of the longest sweep
-    assert abi.bwd_workspace_size(f16, 1, 2, 2, 4096, 4096, 64, -1, False) == part(8, 1, 2, 4096, 64)
-    assert abi.bwd_workspace_size(f16, 1, 2, 2, 260, 200, 64, -1, False) == part(2, 1, 2, 200, 64)
+    # few sequences and heads: both sweeps split, at most 8 parts each, each
+    # part at least 4 tiles of the longest sweep
+    assert abi.bwd_workspace_size(f16, 1, 2, 2, 4096, 4096, 64, -1, False) == \
+        kv(8, 1, 2, 4096, 64) + dq(8, 1, 2, 4096, 64)
+    assert abi.bwd_workspace_size(f16, 1, 2, 2, 260, 200, 64, -1, False) == kv(2, 1, 2, 200, 64)
+    assert abi.bwd_workspace_size(f16, 1, 2, 2, 260, 700, 64, -1, False) == \
+        kv(2, 1, 2, 700, 64) + dq(5, 1, 2, 260, 64)
     assert abi.bwd_workspace_size(f16, 1, 2, 2, 100, 200, 64, -1, False) == 0

@@ -1,16 +1,16 @@
-"""GPU parity of the split dK/dV sweeps of the backward (cmpext3_attn_bwd_ws).
+"""GPU parity of the split gradient sweeps of the backward (cmpext3_attn_bwd_ws).
 
-With too few key blocks for the CUs (one or two sequences, grouped-query K/V,
-causal sweeps whose length falls with the key block) the dK/dV sweep of a
-block over (query head of the group, query tile) is cut into up to 8
-contiguous parts whose fp32 partials a fourth kernel sums in part order.
+With too few blocks for the CUs (one or two sequences, grouped-query K/V,
+causal sweeps whose length runs from one tile to all of them) the dK/dV sweep
+of a key block over (query head of the group, query tile), and the dQ sweep
+of a query block over key tiles, are cut into up to 8 contiguous parts whose
+fp32 partials a further kernel sums in part order.
 Oracle: float64 sdpa_bwd_np on K/V repeated per query head, the repeats'
 gradients summed; bar: max abs error <= 1e-2 (fp16) / 2e-2 (bf16) / 1e-4
 (fp32) times the gradient's largest oracle magnitude (at least 1e-3; 0.1 for
 fp32, as in test_gpu_backward32.py), as for the unsplit backward.  Also: the split launch agrees with the unsplit one (no workspace)
-within the same bar, reruns are bit-identical, dQ is untouched by the split
-(bit-identical to the unsplit launch), and a workspace below the size query
-runs unsplit.  The plan itself (which problems split) is a CPU test in
+within the same bar, reruns are bit-identical, and a workspace below the
+size query runs unsplit.  The plan itself (which problems split) is a CPU test in
 test_abi.py.
 """
 from __future__ import annotations
@@ -35,7 +35,7 @@ def _rel_err(got, want, dtype):
 CASES = [
     # dtype, B, H, Hkv, Sq, Sk, D, causal, mask
     ("bf16", 1, 8, 2, 1024, 1024, 128, True, None),     # grouped-query causal, 8 parts
-    ("fp16", 1, 4, 4, 1000, 777, 64, False, None),      # ragged non-causal
+    ("fp16", 1, 4, 4, 1000, 777, 64, False, None),      # ragged non-causal, dQ split too
     ("fp16", 2, 8, 1, 300, 1500, 64, True, None),       # multi-query, causal Sq < Sk (empty parts)
     ("bf16", 1, 4, 2, 700, 300, 128, True, None),       # causal Sq > Sk
     ("bf16", 1, 4, 2, 600, 900, 256, True, None),       # D = 256 bucket, one wave per SIMD
@@ -43,7 +43,7 @@ CASES = [
     ("fp16", 2, 4, 2, 500, 700, 64, False, "pad"),      # key-padding mask
     ("bf16", 1, 4, 2, 400, 400, 128, True, "full"),     # per-row bool mask with causal
     ("fp16", 1, 2, 2, 260, 200, 64, False, None),       # short sweeps: 2 parts of 4 and 5 tiles
-    ("fp32", 1, 8, 8, 1024, 1024, 64, False, None),     # BASELINE config 1 shape: 6 parts
+    ("fp32", 1, 8, 8, 1024, 1024, 64, False, None),     # BASELINE config 1 shape: 6 + 8 parts
     ("fp32", 1, 4, 2, 700, 500, 40, True, None),        # SD1.5 head dim, grouped-query causal
     ("fp32", 1, 2, 1, 300, 400, 128, True, "pad"),      # masked causal D = 128
 ]
@@ -82,7 +82,6 @@ def test_split_backward(case):
     torch.cuda.synchronize()
     for a, b in zip(split1, split2):
         assert torch.equal(a, b)
-    assert torch.equal(split1[0], whole[0])  # dQ does not depend on the split
     grp = H // Hkv
     kr, vr = (t.cpu().repeat_interleave(grp, dim=1) for t in (k, v))
     want = orc.sdpa_bwd_np(q.cpu(), kr, vr, do.cpu(), s, causal, attn_mask=None if m is None else m.cpu())
@@ -96,8 +95,10 @@ def test_split_backward(case):
 
 
 def test_workspace_smaller_than_asked_runs_unsplit():
-    """A workspace below the query's size runs the unsplit sweep: the same
-    gradients as no workspace, bit for bit."""
+    """A sweep whose partials do not fit the workspace runs unsplit (dK/dV's
+    take the workspace first, then dQ's): with a few bytes short of the size
+    query only dK/dV split, so dQ is bit for bit the unsplit launch's; with a
+    tiny workspace nothing splits and all three gradients are."""
     B, H, Hkv, Sq, Sk, D = 1, 4, 2, 512, 512, 64
     dt = abi.dtype_code(torch.float16)
     need = abi.bwd_workspace_size(dt, B, H, Hkv, Sq, Sk, D, -1, True)
@@ -106,9 +107,14 @@ def test_workspace_smaller_than_asked_runs_unsplit():
     rnd = lambda h, S: torch.randn(B, h, S, D, generator=g).half().cuda()
     q, k, v, do = rnd(H, Sq), rnd(Hkv, Sk), rnd(Hkv, Sk), rnd(H, Sq)
     out, lse = abi.attn_fwd_lse(q, k, v, 0.125, True)
-    small = torch.empty(need - 16, dtype=torch.uint8, device="cuda")
-    a = abi.attn_bwd(q, k, v, out, do, lse, 0.125, True, workspace=small)
-    b = abi.attn_bwd(q, k, v, out, do, lse, 0.125, True, workspace=None)
+    short = torch.empty(need - 16, dtype=torch.uint8, device="cuda")
+    tiny = torch.empty(1024, dtype=torch.uint8, device="cuda")
+    a = abi.attn_bwd(q, k, v, out, do, lse, 0.125, True, workspace=short)
+    t = abi.attn_bwd(q, k, v, out, do, lse, 0.125, True, workspace=tiny)
+    w = abi.attn_bwd(q, k, v, out, do, lse, 0.125, True, workspace=None)
+    full = abi.attn_bwd(q, k, v, out, do, lse, 0.125, True, workspace=True)
     torch.cuda.synchronize()
-    for x, y in zip(a, b):
+    assert torch.equal(a[0], w[0])
+    assert not torch.equal(full[0], w[0])  # the full workspace splits dQ too
+    for x, y in zip(t, w):
         assert torch.equal(x, y)

@@ -19,13 +19,12 @@
 
 namespace cmpext3 {
 hipError_t launch_bwd16(const BwdParams& p, bool bf16, bool causal, hipStream_t s);
-int bwd16_split(int B, int Hkv, int group, int Sq, int Sk, int D, bool causal, bool masked, int cus);
-int bwd32_split(int B, int Hkv, int group, int Sq, int Sk, int D, bool causal, int cus);
-size_t bwd_split_bytes(int B, int Hkv, int Sk, int D, int ns);
-// Parts per key block of the dK/dV sweep (1 = unsplit).
-int bwd_split(int dtype, int B, int Hkv, int group, int Sq, int Sk, int D, bool causal, bool masked) {
-  return dtype == CMPEXT3_DTYPE_F32 ? bwd32_split(B, Hkv, group, Sq, Sk, D, causal, device_cus())
-                                    : bwd16_split(B, Hkv, group, Sq, Sk, D, causal, masked, device_cus());
+BwdSplit bwd16_split(int B, int H, int Hkv, int Sq, int Sk, int D, bool causal, bool masked, int cus);
+BwdSplit bwd32_split(int B, int H, int Hkv, int Sq, int Sk, int D, bool causal, int cus);
+// Split plan of the backward's gradient sweeps.
+BwdSplit bwd_split(int dtype, int B, int H, int Hkv, int Sq, int Sk, int D, bool causal, bool masked) {
+  return dtype == CMPEXT3_DTYPE_F32 ? bwd32_split(B, H, Hkv, Sq, Sk, D, causal, device_cus())
+                                    : bwd16_split(B, H, Hkv, Sq, Sk, D, causal, masked, device_cus());
 }
 hipError_t launch_bwd32(const BwdParams& p, bool causal, hipStream_t s);
 hipError_t launch_mfma16(const FwdParams& p, bool bf16, bool causal, hipStream_t s);
@@ -410,8 +409,8 @@ size_t cmpext3_attn_bwd_workspace_size(int dtype, int B, int H, int H_kv, int Sq
                                        int mask_dtype, int causal) {
   if (check_shape(dtype, B, H, Sq, Sk, D) != CMPEXT3_OK) return 0;
   if (!whole_chunks(dtype, D) || H_kv < 1 || H_kv > H || H % H_kv != 0) return 0;
-  const int ns = cmpext3::bwd_split(dtype, B, H_kv, H / H_kv, Sq, Sk, D, causal != 0, mask_dtype != -1);
-  return cmpext3::bwd_split_bytes(B, H_kv, Sk, D, ns);
+  const cmpext3::BwdSplit sp = cmpext3::bwd_split(dtype, B, H, H_kv, Sq, Sk, D, causal != 0, mask_dtype != -1);
+  return sp.kv_bytes(B, H_kv, Sk, D) + sp.q_bytes(B, H, Sq, D);
 }
 
 int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
@@ -487,14 +486,22 @@ int cmpext3_attn_bwd_ws(const void* q, const void* k, const void* v, const void*
   p.c = fmaxf(fabsf(scale) * cmpext3::kLog2e, 1e-30f);
   p.scale = scale;
   p.sign = scale < 0.f ? (dtype == CMPEXT3_DTYPE_F32 ? 0x80000000u : 0x80008000u) : 0u;
-  // split dK/dV sweeps when the workspace holds their partials (else unsplit)
-  p.nsplit = 1;
+  // split sweeps where the workspace holds their partials (dK/dV first, then
+  // dQ; a sweep whose partials do not fit runs unsplit)
+  p.nsplit = p.nsplit_q = 1;
   if (workspace) {
-    const int ns = cmpext3::bwd_split(dtype, B, H_kv, H / H_kv, Sq, Sk, D, causal != 0,
-                                      p.mask_kind != cmpext3::MASK_NONE);
-    if (ns > 1 && workspace_bytes >= cmpext3::bwd_split_bytes(B, H_kv, Sk, D, ns)) {
-      p.nsplit = ns;
+    const cmpext3::BwdSplit sp =
+        cmpext3::bwd_split(dtype, B, H, H_kv, Sq, Sk, D, causal != 0, p.mask_kind != cmpext3::MASK_NONE);
+    const size_t kvb = sp.kv_bytes(B, H_kv, Sk, D), qb = sp.q_bytes(B, H, Sq, D);
+    size_t used = 0;
+    if (kvb > 0 && kvb <= workspace_bytes) {
+      p.nsplit = sp.ns_kv;
       p.part = (float*)workspace;
+      used = kvb;
+    }
+    if (qb > 0 && used + qb <= workspace_bytes) {
+      p.nsplit_q = sp.ns_q;
+      p.part_q = (float*)((char*)workspace + used);
     }
   }
   const hipError_t err = dtype == CMPEXT3_DTYPE_F32

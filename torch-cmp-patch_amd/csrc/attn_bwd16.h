@@ -12,10 +12,10 @@
 // P is recomputed from the scores and the saved log-sum-exp, so nothing of
 // size Sq x Sk is stored.  The two gradient kernels each own their output rows
 // outright (no atomics), so the results are bit-identical from run to run;
-// where a dK/dV sweep is split over several workgroups (few key blocks for
-// the CUs), their fp32 partials go to a caller workspace and
-// attn_bwd_dkdv_reduce adds them in a fixed order.  The reference is forward-only (its patch
-// hands calls with live autograd to stock torch, cmpext3/__init__.py:115-125);
+// where a sweep is split over several workgroups (few blocks for the CUs),
+// their fp32 partials go to a caller workspace and attn_bwd_part_sum adds
+// them in a fixed order.  The reference is forward-only (its patch hands
+// calls with live autograd to stock torch, cmpext3/__init__.py:115-125);
 // this is the gradient of the same forward, checked against the float64
 // restatement in oracle/sdpa_oracle.py (sdpa_bwd_np).
 //
@@ -66,11 +66,56 @@ struct BwdParams {
   const void* mask;
   int64_t m_b, m_h, m_q;
   int mask_kind;
-  // dK/dV split sweeps (f16/bf16): nsplit > 1 workgroups per key block, each
-  // leaving fp32 partial dK / dV rows in `part` ([nsplit][B * Hkv][Sk][D] for
-  // dK, then the same for dV) that attn_bwd_dkdv_reduce sums
-  int nsplit;
+  // split sweeps: nsplit > 1 dK/dV workgroups per key block, each leaving
+  // fp32 partial dK / dV rows in `part` ([nsplit][B * Hkv][Sk][D] for dK, then
+  // the same for dV); nsplit_q > 1 dQ workgroups per query block, partial dQ
+  // rows in `part_q` ([nsplit_q][B * H][Sq][D]); attn_bwd_part_sum adds them
+  int nsplit, nsplit_q;
   float* part;
+  float* part_q;
+};
+
+// Parts per block of a gradient sweep (1 = unsplit).  With too few blocks
+// (n_wg) for the CU slots the kernel's occupancy allows (one 4-wave workgroup
+// per wave per SIMD), each block's sweep is cut into contiguous parts whose
+// fp32 partials are summed afterwards: non-causal, as many parts as fill one
+// round of slots; causal, enough for two rounds, so that longest-first
+// dispatch pairs long parts with short ones (causal sweeps' lengths run from
+// one tile to all of them).  At most 8 parts, each at least 4 tiles of the
+// longest sweep (`tiles`).
+inline int split_sweep(int64_t n_wg, int occ, int cus, bool causal, int64_t tiles) {
+  const int64_t slots = (int64_t)cus * occ;
+  const int64_t want = causal ? 2 * slots : slots;
+  if (n_wg <= 0 || n_wg * 2 > want) return 1;
+  int64_t ns = causal ? (want + n_wg - 1) / n_wg : want / n_wg;
+  if (ns > 8) ns = 8;
+  if (ns > tiles / 4) ns = tiles / 4;
+  return ns >= 2 ? (int)ns : 1;
+}
+
+// Split plan of a backward launch and its workspace: the dK/dV partials
+// (2 x ns_kv x B x Hkv x Sk x D floats), then the dQ partials (ns_q x B x H
+// x Sq x D floats).
+struct BwdSplit {
+  int ns_kv = 1, ns_q = 1;
+  size_t kv_bytes(int B, int Hkv, int Sk, int D) const {
+    return ns_kv > 1 ? (size_t)2 * ns_kv * B * Hkv * Sk * D * sizeof(float) : 0;
+  }
+  size_t q_bytes(int B, int H, int Sq, int D) const {
+    return ns_q > 1 ? (size_t)ns_q * B * H * Sq * D * sizeof(float) : 0;
+  }
+};
+
+// fp32 partial rows of a split sweep ([ns][rows][D], rows = B x heads x S)
+// and where their sum goes: T rows with element strides {batch, head, seq},
+// times `mul`.
+struct PartSum {
+  const float* part;
+  void* out;
+  int64_t ob, oh, os;
+  int64_t rows;
+  int heads, S, D, ns;
+  float mul;
 };
 
 // LDS row stride (halves) of the Q/dO and K/V tiles: rows padded by 16 bytes,
@@ -470,32 +515,56 @@ attn_bwd_dkdv(const BwdParams p) {
   finish();
 }
 
-// ---- Sum of the split dK/dV sweeps' partials, in part order (the same
-// result on every run), times the signed scale for dK; 4 columns per thread.
+// ---- Sums of split sweeps' partials, in part order (the same result on every
+// run): vector i4 (4 columns) of one or two outputs (b.out null: one).
 template <typename T>
-__global__ void __launch_bounds__(256) attn_bwd_dkdv_reduce(const BwdParams p) {
-  const int D = p.D, Sk = p.Sk, ns = p.nsplit;
-  const int64_t rows = (int64_t)p.B * p.Hkv * Sk, n4 = rows * D / 4;
-  const int64_t i4 = (int64_t)block_x() * 256 + thread_x();
-  if (i4 >= n4) return;
-  const int64_t row = i4 * 4 / D;
-  const int d = (int)(i4 * 4 - row * D);
-  const int bhk = (int)(row / Sk), key = (int)(row - (int64_t)bhk * Sk);
-  const int b = bhk / p.Hkv, hk = bhk - b * p.Hkv;
-  const f32x4* const pk = (const f32x4*)p.part + i4;
-  const int64_t step = rows * D / 4;  // one part's vectors
-  f32x4 gk = pk[0], gv = pk[ns * step];
-  for (int q = 1; q < ns; ++q) {
-    gk += pk[q * step];
-    gv += pk[(ns + q) * step];
+__device__ __forceinline__ void part_sum_store(const PartSum& a, int64_t i4) {
+  const int64_t row = i4 * 4 / a.D;
+  const int d = (int)(i4 * 4 - row * a.D);
+  const int64_t bh = row / a.S;
+  const int s = (int)(row - bh * a.S);
+  const int b = (int)(bh / a.heads), h = (int)(bh - (int64_t)b * a.heads);
+  const f32x4* const pk = (const f32x4*)a.part + i4;
+  const int64_t step = a.rows * a.D / 4;  // one part's vectors
+  f32x4 x = pk[0];
+  for (int q = 1; q < a.ns; ++q) x += pk[q * step];
+  x = x * a.mul;
+  T* const dst = (T*)a.out + b * a.ob + h * a.oh + (int64_t)s * a.os + d;
+  if constexpr (sizeof(T) == 4) {
+    *(f32x4*)dst = x;
+  } else {
+    u32x2 w;
+    w[0] = Elt<T>::pack(x[0], x[1]);
+    w[1] = Elt<T>::pack(x[2], x[3]);
+    *(u32x2*)dst = w;
   }
-  u32x2 wk, wv;
-  wk[0] = Elt<T>::pack(gk[0] * p.scale, gk[1] * p.scale);
-  wk[1] = Elt<T>::pack(gk[2] * p.scale, gk[3] * p.scale);
-  wv[0] = Elt<T>::pack(gv[0], gv[1]);
-  wv[1] = Elt<T>::pack(gv[2], gv[3]);
-  *(u32x2*)((uint16_t*)p.dk + b * p.dk_b + hk * p.dk_h + (int64_t)key * p.dk_s + d) = wk;
-  *(u32x2*)((uint16_t*)p.dv + b * p.dv_b + hk * p.dv_h + (int64_t)key * p.dv_s + d) = wv;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) attn_bwd_part_sum(const PartSum a, const PartSum b) {
+  const int64_t i4 = (int64_t)block_x() * 256 + thread_x();
+  if (i4 >= a.rows * a.D / 4) return;
+  part_sum_store<T>(a, i4);
+  if (b.out) part_sum_store<T>(b, i4);
+}
+
+// Launch the sums of the dK/dV partials (sweeps split nsplit ways) or of the
+// dQ partials (nsplit_q ways) that a launch's split sweeps left (errors show
+// in the caller's final hipGetLastError).
+template <typename T>
+void launch_part_sums(const BwdParams& p, bool dkdv, hipStream_t s) {
+  PartSum a = {}, b = {};
+  if (dkdv) {
+    const int64_t rows = (int64_t)p.B * p.Hkv * p.Sk;
+    a = PartSum{p.part, p.dk, p.dk_b, p.dk_h, p.dk_s, rows, p.Hkv, p.Sk, p.D, p.nsplit, p.scale};
+    b = PartSum{p.part + (int64_t)p.nsplit * rows * p.D, p.dv, p.dv_b, p.dv_h, p.dv_s, rows, p.Hkv, p.Sk, p.D,
+                p.nsplit, 1.f};
+  } else {
+    const int64_t rows = (int64_t)p.B * p.H * p.Sq;
+    a = PartSum{p.part_q, p.dq, p.dq_b, p.dq_h, p.dq_s, rows, p.H, p.Sq, p.D, p.nsplit_q, p.scale};
+  }
+  const int64_t n4 = a.rows * a.D / 4;
+  hipLaunchKernelGGL(attn_bwd_part_sum<T>, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, a, b);
 }
 
 // ---- dQ for one block of 128 queries (4 waves x 32 queries), sweeping the
@@ -519,11 +588,16 @@ attn_bwd_dq(const BwdParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t dpark[DLDS ? BQ * RSD : 8];
 
   const int tid = thread_x(), wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-  int bh, qblk;
+  // split sweeps: (query block, part) pairs as ns virtual blocks per block
+  const int ns = p.nsplit_q > 1 ? p.nsplit_q : 1;
+  int bh, qblk, part;
   {
     FwdParams fp;
-    fp.B = p.B; fp.H = p.H; fp.n_qblk = p.n_blk; fp.n_wg = p.n_wg;
-    wg_tile(block_x(), fp, CAUSAL, bh, qblk);  // causal: longest key sweeps first
+    fp.B = p.B; fp.H = p.H; fp.n_qblk = p.n_blk * ns; fp.n_wg = p.n_wg;
+    int vblk;
+    wg_tile(block_x(), fp, CAUSAL, bh, vblk);  // causal: longest key sweeps first
+    qblk = vblk / ns;
+    part = vblk - qblk * ns;
   }
   const int b = bh / p.H, h = bh - b * p.H;
   const int Sq = p.Sq, Sk = p.Sk, D = p.D;
@@ -602,14 +676,16 @@ attn_bwd_dq(const BwdParams p) {
   };
 
   const float c = p.c;
-  if (nt > 0) {
-    fetch(0);
+  // this workgroup's key tiles [kt0, kt1) (all of them unless the sweep is split)
+  const int kt0 = (int)((int64_t)part * nt / ns), kt1 = (int)((int64_t)(part + 1) * nt / ns);
+  if (kt1 > kt0) {
+    fetch(kt0);
     put(0);
   }
   lds_barrier();
-  for (int t = 0; t < nt; ++t) {
-    const int slot = t & 1;
-    if (t + 1 < nt) fetch(t + 1);
+  for (int t = kt0; t < kt1; ++t) {
+    const int slot = (t - kt0) & 1;
+    if (t + 1 < kt1) fetch(t + 1);
     const int k0 = t * BK;
     if (!CAUSAL || k0 <= wlast) {  // causal: tiles past this wave's last query add nothing
       const uint16_t* ks = lds + slot * 2 * BK * RS;
@@ -691,10 +767,14 @@ attn_bwd_dq(const BwdParams p) {
         for (int db = 0; db < NDB; ++db)
           dqa[db] = Elt<T>::mma(tr_frag(ks + 16 * ks2 * RS, t_rd[db][0], t_rd[db][1]), ps[ks2], dqa[db]);
     }
-    if (t + 1 < nt) put(slot ^ 1);
+    if (t + 1 < kt1) put(slot ^ 1);
     lds_barrier();
   }
 
+  if (ns > 1) {  // this part's partial rows, unscaled
+    store_rows_f32<NDB>(p.part_q + ((int64_t)part * p.B * p.H + bh) * Sq * D, qrow, Sq, D, hh, dqa);
+    return;
+  }
   uint16_t* dqg = (uint16_t*)p.dq + b * p.dq_b + h * p.dq_h;
   store_rows<T, NDB>(dqg, p.dq_s, qrow, Sq, D, hh, dqa, p.scale);
 }

@@ -19,13 +19,13 @@ hipError_t launch_bwd_t(const BwdParams& p0, hipStream_t s) {
   p.nsplit = ns;
   p.n_wg = p.B * p.Hkv * p.n_blk * ns;
   hipLaunchKernelGGL((attn_bwd_dkdv<T, DK, CAUSAL, MASK>), dim3(p.n_wg), dim3(256), 0, s, p);
-  if (ns > 1) {
-    const int64_t n4 = (int64_t)p.B * p.Hkv * p.Sk * p.D / 4;
-    hipLaunchKernelGGL(attn_bwd_dkdv_reduce<T>, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, p);
-  }
+  if (ns > 1) launch_part_sums<T>(p, true, s);
   p.n_blk = (p.Sq + 127) / 128;
-  p.n_wg = p.B * p.H * p.n_blk;
+  const int nsq = p.nsplit_q > 1 && p.part_q ? p.nsplit_q : 1;
+  p.nsplit_q = nsq;
+  p.n_wg = p.B * p.H * p.n_blk * nsq;
   hipLaunchKernelGGL((attn_bwd_dq<T, DK, CAUSAL, MASK>), dim3(p.n_wg), dim3(256), 0, s, p);
+  if (nsq > 1) launch_part_sums<T>(p, false, s);
   return hipGetLastError();
 }
 
@@ -48,32 +48,20 @@ hipError_t launch_bwd_dtype(const BwdParams& p, int dk, bool causal, hipStream_t
 
 int bwd16_bucket(int D) { return D <= 0 ? -1 : D <= 64 ? 64 : D <= 128 ? 128 : D <= 192 ? 192 : D <= 256 ? 256 : -1; }
 
-// Workgroups of the dK/dV sweep per key block.  With too few key blocks for
-// the CU slots the kernel's occupancy allows (one 4-wave workgroup per wave
-// per SIMD), each block's sweep over (query head of the group, query tile)
-// is cut into contiguous parts whose fp32 partials are summed afterwards:
-// non-causal, as many parts as fill one round of slots; causal, enough for
-// two rounds, so that the longest-first order evens out sweeps whose length
-// falls with the key block (the first blocks see every query).  At most 8
-// parts, each at least 4 query tiles of the longest sweep.
-int bwd16_split(int B, int Hkv, int group, int Sq, int Sk, int D, bool causal, bool masked, int cus) {
+// Split plan of the f16/bf16 gradient sweeps (split_sweep): dK/dV over
+// 128-key blocks, each sweeping (query head of the group, 32-query tile);
+// dQ over 128-query blocks, each sweeping 32-key tiles.  Workgroups per CU
+// follow the kernels' waves per SIMD.
+BwdSplit bwd16_split(int B, int H, int Hkv, int Sq, int Sk, int D, bool causal, bool masked, int cus) {
+  BwdSplit sp;
   const int dk = bwd16_bucket(D);
-  if (dk < 0 || (int64_t)B * Hkv * Sq == 0) return 1;
-  const int occ = dk <= 64 ? (causal ? 2 : 3) : dk <= 128 ? (masked && causal ? 1 : 2) : 1;
-  const int64_t n_wg = (int64_t)B * Hkv * ((Sk + 127) / 128);
-  const int64_t slots = (int64_t)cus * occ;
-  const int64_t want = causal ? 2 * slots : slots;
-  if (n_wg * 2 > want) return 1;
-  int64_t ns = causal ? (want + n_wg - 1) / n_wg : want / n_wg;
-  const int64_t nj = (int64_t)group * ((Sq + 31) / 32);
-  if (ns > 8) ns = 8;
-  if (ns > nj / 4) ns = nj / 4;
-  return ns >= 2 ? (int)ns : 1;
-}
-
-// Workspace of a split backward: fp32 partial dK and dV rows of every part.
-size_t bwd_split_bytes(int B, int Hkv, int Sk, int D, int ns) {
-  return ns > 1 ? (size_t)ns * B * Hkv * Sk * D * 2 * sizeof(float) : 0;
+  if (dk < 0 || (int64_t)B * H * Sq == 0 || Hkv < 1) return sp;
+  const int occ_kv = dk <= 64 ? (causal ? 2 : 3) : dk <= 128 ? (masked && causal ? 1 : 2) : 1;
+  const int occ_q = dk <= 64 ? (masked ? 2 : 3) : dk <= 128 ? (masked && causal ? 1 : 2) : 1;
+  sp.ns_kv = split_sweep((int64_t)B * Hkv * ((Sk + 127) / 128), occ_kv, cus, causal,
+                         (int64_t)(H / Hkv) * ((Sq + 31) / 32));
+  sp.ns_q = split_sweep((int64_t)B * H * ((Sq + 127) / 128), occ_q, cus, causal, (Sk + 31) / 32);
+  return sp;
 }
 
 hipError_t launch_bwd16(const BwdParams& p, bool bf16, bool causal, hipStream_t s) {

@@ -357,28 +357,6 @@ __global__ void __launch_bounds__(256) attn_bwd32_dkdv(const BwdParams p) {
   finish();
 }
 
-// ---- Sum of the split dK/dV sweeps' partials, in part order (the same
-// result on every run), times the signed scale for dK; 4 columns per thread.
-__global__ void __launch_bounds__(256) attn_bwd32_dkdv_reduce(const BwdParams p) {
-  const int D = p.D, Sk = p.Sk, ns = p.nsplit;
-  const int64_t rows = (int64_t)p.B * p.Hkv * Sk, n4 = rows * D / 4;
-  const int64_t i4 = (int64_t)block_x() * 256 + thread_x();
-  if (i4 >= n4) return;
-  const int64_t row = i4 * 4 / D;
-  const int d = (int)(i4 * 4 - row * D);
-  const int bhk = (int)(row / Sk), key = (int)(row - (int64_t)bhk * Sk);
-  const int b = bhk / p.Hkv, hk = bhk - b * p.Hkv;
-  const f32x4* const pk = (const f32x4*)p.part + i4;
-  const int64_t step = rows * D / 4;  // one part's vectors
-  f32x4 gk = pk[0], gv = pk[ns * step];
-  for (int q = 1; q < ns; ++q) {
-    gk += pk[q * step];
-    gv += pk[(ns + q) * step];
-  }
-  *(f32x4*)((float*)p.dk + b * p.dk_b + hk * p.dk_h + (int64_t)key * p.dk_s + d) = gk * p.scale;
-  *(f32x4*)((float*)p.dv + b * p.dv_b + hk * p.dv_h + (int64_t)key * p.dv_s + d) = gv;
-}
-
 // ---- dQ for one block of 64 queries (4 waves x 16 queries), sweeping
 // 32-key tiles of K and V through double-buffered LDS.
 template <int DK, bool CAUSAL>
@@ -392,11 +370,16 @@ __global__ void __launch_bounds__(256) attn_bwd32_dq(const BwdParams p) {
   __shared__ __attribute__((aligned(16))) float lds[2 * 2 * BK * RS];  // [slot][K, V][row][col]
 
   const int tid = thread_x(), wave = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
-  int bh, qblk;
+  // split sweeps: (query block, part) pairs as ns virtual blocks per block
+  const int ns = p.nsplit_q > 1 ? p.nsplit_q : 1;
+  int bh, qblk, part;
   {
     FwdParams fp;
-    fp.B = p.B; fp.H = p.H; fp.n_qblk = p.n_blk; fp.n_wg = p.n_wg;
-    wg_tile(block_x(), fp, CAUSAL, bh, qblk);  // causal: longest key sweeps first
+    fp.B = p.B; fp.H = p.H; fp.n_qblk = p.n_blk * ns; fp.n_wg = p.n_wg;
+    int vblk;
+    wg_tile(block_x(), fp, CAUSAL, bh, vblk);  // causal: longest key sweeps first
+    qblk = vblk / ns;
+    part = vblk - qblk * ns;
   }
   const int b = bh / p.H, h = bh - b * p.H;
   const int Sq = p.Sq, Sk = p.Sk, D = p.D;
@@ -459,14 +442,16 @@ __global__ void __launch_bounds__(256) attn_bwd32_dq(const BwdParams p) {
   };
 
   const float c = p.c;
-  if (nt > 0) {
-    fetch(0);
+  // this workgroup's key tiles [kt0, kt1) (all of them unless the sweep is split)
+  const int kt0 = (int)((int64_t)part * nt / ns), kt1 = (int)((int64_t)(part + 1) * nt / ns);
+  if (kt1 > kt0) {
+    fetch(kt0);
     put(0);
   }
   lds_barrier();
-  for (int t = 0; t < nt; ++t) {
-    const int slot = t & 1;
-    if (t + 1 < nt) fetch(t + 1);
+  for (int t = kt0; t < kt1; ++t) {
+    const int slot = (t - kt0) & 1;
+    if (t + 1 < kt1) fetch(t + 1);
     const float* ks = lds + slot * 2 * BK * RS;
     const float* vs = ks + BK * RS;
 #pragma unroll
@@ -506,10 +491,14 @@ __global__ void __launch_bounds__(256) attn_bwd32_dq(const BwdParams p) {
         for (int db = 0; db < NDB; ++db)
           dqa[db] = mma4(ks[tb[r] + 16 * kb * RS + 16 * db], ds[r], dqa[db]);
     }
-    if (t + 1 < nt) put(slot ^ 1);
+    if (t + 1 < kt1) put(slot ^ 1);
     lds_barrier();
   }
 
+  if (ns > 1) {  // this part's partial rows, unscaled
+    store_rows32<NDB>(p.part_q + ((int64_t)part * p.B * p.H + bh) * Sq * D, D, qrow, Sq, D, g, dqa, 1.f);
+    return;
+  }
   float* dqg = (float*)p.dq + b * p.dq_b + h * p.dq_h;
   store_rows32<NDB>(dqg, p.dq_s, qrow, Sq, D, g, dqa, p.scale);
 }
@@ -524,13 +513,13 @@ hipError_t launch_bwd32_t(const BwdParams& p0, hipStream_t s) {
   p.nsplit = ns;
   p.n_wg = p.B * p.Hkv * p.n_blk * ns;
   hipLaunchKernelGGL((attn_bwd32_dkdv<DK, CAUSAL>), dim3(p.n_wg), dim3(256), 0, s, p);
-  if (ns > 1) {
-    const int64_t n4 = (int64_t)p.B * p.Hkv * p.Sk * p.D / 4;
-    hipLaunchKernelGGL(attn_bwd32_dkdv_reduce, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, p);
-  }
+  if (ns > 1) launch_part_sums<float>(p, true, s);
   p.n_blk = (p.Sq + 63) / 64;
-  p.n_wg = p.B * p.H * p.n_blk;
+  const int nsq = p.nsplit_q > 1 && p.part_q ? p.nsplit_q : 1;
+  p.nsplit_q = nsq;
+  p.n_wg = p.B * p.H * p.n_blk * nsq;
   hipLaunchKernelGGL((attn_bwd32_dq<DK, CAUSAL>), dim3(p.n_wg), dim3(256), 0, s, p);
+  if (nsq > 1) launch_part_sums<float>(p, false, s);
   return hipGetLastError();
 }
 
@@ -556,25 +545,21 @@ int bwd32_bucket(int D) {
   return -1;
 }
 
-// Workgroups of the fp32 dK/dV sweep per 64-key block, as bwd16_split plans
-// the f16/bf16 one: with too few key blocks for the CU slots (the kernel's
-// workgroups per CU from its registers and LDS: 5 at D <= 32, 4 up to 40, 3-4
-// up to 64, 2 up to 128, then 1), non-causal sweeps are cut
-// into as many parts as fill one round, causal ones two rounds; at most 8
-// parts, each at least 4 query tiles of the longest sweep.
-int bwd32_split(int B, int Hkv, int group, int Sq, int Sk, int D, bool causal, int cus) {
+// Split plan of the fp32 gradient sweeps (split_sweep): dK/dV over 64-key
+// blocks sweeping 32-query tiles, dQ over 64-query blocks sweeping 32-key
+// tiles.  Workgroups per CU from the kernels' registers and LDS: dK/dV 5 at
+// D <= 32, 4 up to 40, 3 (causal 4) up to 64, 2 up to 128, then 1; dQ 7, 5,
+// 4, 3 up to 96, 2 up to 128, then 1.
+BwdSplit bwd32_split(int B, int H, int Hkv, int Sq, int Sk, int D, bool causal, int cus) {
+  BwdSplit sp;
   const int dk = bwd32_bucket(D);
-  if (dk < 0 || (int64_t)B * Hkv * Sq == 0) return 1;
-  const int occ = dk <= 32 ? 5 : dk <= 40 ? 4 : dk <= 64 ? (causal ? 4 : 3) : dk <= 128 ? 2 : 1;
-  const int64_t n_wg = (int64_t)B * Hkv * ((Sk + 63) / 64);
-  const int64_t slots = (int64_t)cus * occ;
-  const int64_t want = causal ? 2 * slots : slots;
-  if (n_wg * 2 > want) return 1;
-  int64_t ns = causal ? (want + n_wg - 1) / n_wg : want / n_wg;
-  const int64_t nj = (int64_t)group * ((Sq + 31) / 32);
-  if (ns > 8) ns = 8;
-  if (ns > nj / 4) ns = nj / 4;
-  return ns >= 2 ? (int)ns : 1;
+  if (dk < 0 || (int64_t)B * H * Sq == 0 || Hkv < 1) return sp;
+  const int occ_kv = dk <= 32 ? 5 : dk <= 40 ? 4 : dk <= 64 ? (causal ? 4 : 3) : dk <= 128 ? 2 : 1;
+  const int occ_q = dk <= 32 ? 7 : dk <= 40 ? 5 : dk <= 64 ? 4 : dk <= 96 ? 3 : dk <= 128 ? 2 : 1;
+  sp.ns_kv = split_sweep((int64_t)B * Hkv * ((Sk + 63) / 64), occ_kv, cus, causal,
+                         (int64_t)(H / Hkv) * ((Sq + 31) / 32));
+  sp.ns_q = split_sweep((int64_t)B * H * ((Sq + 63) / 64), occ_q, cus, causal, (Sk + 31) / 32);
+  return sp;
 }
 
 hipError_t launch_bwd32(const BwdParams& p, bool causal, hipStream_t s) {
