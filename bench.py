@@ -253,7 +253,7 @@ def bench_training(wl, args) -> dict:
         "config": {"workload": wl.name, "B": wl.B, "H": wl.H, "Sq": wl.Sq, "Sk": wl.Sk, "D": wl.D,
                    "causal": wl.causal, "scale": sc,
                    "entry": "cmpext3.ops.attention_fwd_lse + attention_bwd -> cmpext3_attn_fwd_lse, "
-                            "cmpext3_attn_bwd"},
+                            "cmpext3_attn_bwd_ws"},
         "roofline": {"bound": "mfma", "achieved": round(f_bwd / dev_bwd / 1e12, 3), "peak": peak,
                      "unit": "TFLOP/s", "frac": round(f_bwd / dev_bwd / 1e12 / peak, 4), "traffic": None,
                      "kernel_us": round(dev_bwd * 1e6, 3), "flops_per_launch": f_bwd,
