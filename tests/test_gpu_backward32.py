@@ -1,5 +1,5 @@
 """GPU parity of the fp32 training pair: the fp32 forward that keeps the row
-log-sum-exp (cmpext3_attn_fwd_lse on the fp32 kernel, never key-split) and the
+log-sum-exp (cmpext3_attn_fwd_lse on the fp32 kernel, key-split on small grids) and the
 fp32 backward (cmpext3_attn_bwd: attn_bwd32_delta / _dkdv / _dq on 16x16x4
 fp32 MFMAs), through the C ABI, plus the autograd Function and the SDPA route.
 
@@ -241,3 +241,35 @@ def test_fp32_autograd_function_with_odd_head_dim():
     for got, ref in zip((q.grad, k.grad, v.grad), want):
         assert got.shape == (1, 2, 150, 41)
         assert _rel_err(got, ref) <= TOL
+
+
+def test_fp32_training_forward_key_split():
+    """Grids of few query blocks key-split the fp32 training forward too: the
+    merging part writes the log-sum-exp of the merged (m, l).  BASELINE config
+    1's shape (128 blocks, 4 parts) and a masked ragged one: output and lse
+    meet the oracle, agree with the unsplit launch, and reruns are
+    bit-identical."""
+    dt = abi.DTYPE_F32
+    for B, H, Sq, Sk, D, masked in ((1, 8, 1024, 1024, 64, False), (1, 2, 100, 700, 40, True)):
+        ws = abi.workspace_size(dt, B, H, H, Sq, Sk, D, abi.DTYPE_BOOL if masked else -1, False, with_lse=True)
+        assert abi.plan(dt, B, H, H, Sq, Sk, D, ws, abi.DTYPE_BOOL if masked else -1, False, with_lse=True)[1] >= 2
+        g = torch.Generator().manual_seed(Sk + D)
+        q, k, v = _t(B, H, Sq, D, g), _t(B, H, Sk, D, g), _t(B, H, Sk, D, g)
+        m = None
+        if masked:
+            m = torch.ones(B, 1, 1, Sk, dtype=torch.bool)
+            m[..., Sk - 150:] = False
+            m = m.cuda()
+        s = D ** -0.5
+        o1, l1 = abi.attn_fwd_lse(q, k, v, s, False, attn_mask=m)
+        o2, l2 = abi.attn_fwd_lse(q, k, v, s, False, attn_mask=m)
+        ow, lw = abi.attn_fwd_lse(q, k, v, s, False, attn_mask=m, workspace=False)
+        torch.cuda.synchronize()
+        assert torch.equal(o1, o2) and torch.equal(l1, l2)
+        mc = None if m is None else m.cpu()
+        qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
+        want_o = orc.sdpa_np(qc, kc, vc, s, False, attn_mask=mc)
+        want_l = orc.sdpa_lse_np(qc, kc, s, False, attn_mask=mc)
+        for o, l in ((o1, l1), (ow, lw)):
+            assert orc.max_abs_err(o.cpu(), want_o) <= TOL
+            assert orc.max_abs_err(l.cpu(), want_l) <= TOL

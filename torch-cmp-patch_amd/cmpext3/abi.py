@@ -242,10 +242,11 @@ def _mask_args(attn_mask, B, H, Sq, Sk, runs=False):
 
 
 def attn_fwd_lse(q, k, v, scale: Optional[float] = None, causal: bool = False, stream=None,
-                 attn_mask=None):
+                 attn_mask=None, workspace: bool = True):
     """Training forward through cmpext3_attn_fwd_lse: returns (O, lse) with
     lse the fp32 [B,H,Sq] natural-log row log-sum-exp (k, v may hold fewer
-    heads than q: grouped-query).  Raises RuntimeError on a non-zero code."""
+    heads than q: grouped-query); workspace=False passes none (no key split).
+    Raises RuntimeError on a non-zero code."""
     import torch
     B, H, Sq, D = q.shape
     o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
@@ -255,7 +256,8 @@ def attn_fwd_lse(q, k, v, scale: Optional[float] = None, causal: bool = False, s
     mp, mdt, mst, _keep = _mask_args(attn_mask, B, H, Sq, k.shape[2], runs=True)
     handle = _handle(q, stream)
     wp, wb = workspace_for(q, handle, workspace_size(dtype_code(q.dtype), B, H, k.shape[1], Sq,
-                                                     k.shape[2], D, mdt, causal, with_lse=True))
+                                                     k.shape[2], D, mdt, causal, with_lse=True)) \
+        if workspace else (None, 0)
     rc = lib().cmpext3_attn_fwd_lse(
         ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()),
         ctypes.c_void_p(o.data_ptr()), ctypes.c_void_p(lse.data_ptr()), dtype_code(q.dtype),
@@ -270,7 +272,7 @@ def attn_fwd_lse(q, k, v, scale: Optional[float] = None, causal: bool = False, s
 def bwd_workspace_size(dtype: int, B: int, H: int, H_kv: int, Sq: int, Sk: int, D: int,
                        mask_dtype: int = -1, causal: bool = False) -> int:
     """cmpext3_attn_bwd_workspace_size: bytes that let the backward split its
-    dK/dV sweeps (0 = it never splits)."""
+    gradient sweeps (0 = it never splits)."""
     return lib().cmpext3_attn_bwd_workspace_size(dtype, B, H, H_kv, Sq, Sk, D, mask_dtype, int(causal))
 
 

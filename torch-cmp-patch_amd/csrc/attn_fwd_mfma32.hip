@@ -12,7 +12,8 @@
 // the 16 lanes of a group, which is a conflict-free LDS read.
 //
 // With p.lse set (the training forward) each row's natural-log log-sum-exp
-// is written too, and the launch is never key-split.
+// is written too (by the merging part where the keys are split: the merged
+// offset and row sum).
 //
 // Key split (non-causal launches with at most as many query blocks as CUs,
 // such as [1, 8, 1024, 64]): each block's key range is cut into parts run by
@@ -418,6 +419,7 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
         }
       }
       lrow[qb] = l;
+      m_run[qb] = mt;  // the merged offset, for the log-sum-exp
     }
   }
 
@@ -502,8 +504,7 @@ hipError_t launch_mfma32_bk(const FwdParams& p0, hipStream_t stream) {
   // waves per block that hold query rows (a single block shorter than BQ has fewer)
   const int nwl = p.n_qblk > 1 ? NW : (p.Sq + 15) / 16 < NW ? (p.Sq + 15) / 16 : NW;
   SplitArgs sa = {n, 1, nullptr, nullptr, nwl};
-  // the training forward (p.lse) runs every block whole
-  const int parts = p.lse ? 1 : split_parts32(n, p.Sk, BK, device_cus(), CAUSAL);
+  const int parts = split_parts32(n, p.Sk, BK, device_cus(), CAUSAL);
   if (parts >= 2) {
     // every block is split; one key range of all of them takes part_bytes
     const size_t part_bytes = (size_t)n * nwl * NQB * (NDB + 1) * 64 * sizeof(f32x4);
