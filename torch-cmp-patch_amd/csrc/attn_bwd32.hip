@@ -170,15 +170,18 @@ __global__ void __launch_bounds__(256) attn_bwd32_dkdv(const BwdParams p) {
   __shared__ __attribute__((aligned(16))) float lsd[2][2][BQ];
 
   const int tid = thread_x(), wave = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
-  // key blocks in order (causal: the first blocks see the most queries);
-  // XCD-contiguous ranges share Q/dO in L2
-  // split sweeps: workgroups (tile, part) of one block are adjacent
+  // (batch, K/V head) and key block; split sweeps: (block, part) pairs as
+  // virtual blocks.  Causal: longest sweeps first (kv_tile)
   const int ns = p.nsplit > 1 ? p.nsplit : 1;
-  const int widx = __builtin_amdgcn_readfirstlane(xcd_remap(block_x(), p.n_wg));
-  const int tile = __builtin_amdgcn_readfirstlane(widx / ns);
-  const int part = widx - tile * ns;
-  const int bhk = __builtin_amdgcn_readfirstlane(tile / p.n_blk);
-  const int kb = tile - bhk * p.n_blk;
+  int bhk, kb, part;
+  {
+    int bh0, vb;
+    kv_tile(block_x(), p.B * p.Hkv, p.n_blk * ns, CAUSAL, bh0, vb);
+    bhk = __builtin_amdgcn_readfirstlane(bh0);
+    vb = __builtin_amdgcn_readfirstlane(vb);
+    kb = __builtin_amdgcn_readfirstlane(vb / ns);
+    part = vb - kb * ns;
+  }
   const int b = __builtin_amdgcn_readfirstlane(bhk / p.Hkv), hk = bhk - b * p.Hkv;
   const int Sq = p.Sq, Sk = p.Sk, D = p.D;
   const int kw0 = kb * BKV + wave * 16;  // first key of this wave

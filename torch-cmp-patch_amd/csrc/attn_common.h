@@ -132,6 +132,25 @@ __device__ __forceinline__ void wg_tile(int wg, const FwdParams& p, bool causal,
   if (causal) qblk = p.n_qblk - 1 - qblk;
 }
 
+// Which (batch*K/V head, key block) a dK/dV workgroup of the backward computes,
+// nvb blocks per head (with split sweeps, (block, part) pairs as virtual
+// blocks).  Causal: key block j is seen by every query from j on, so the
+// first blocks have the longest sweeps; like wg_tile, when the heads split
+// evenly over the XCDs each XCD starts its heads' blocks longest first across
+// those heads (list scheduling per XCD).  Otherwise the xcd_remap ranges.
+__device__ __forceinline__ void kv_tile(int wg, int BH, int nvb, bool causal, int& bh, int& vb) {
+  if (causal && BH % kNumXcd == 0) {
+    const int x = wg % kNumXcd, i = wg / kNumXcd, hx = BH / kNumXcd;
+    const int r = i / hx;  // blocks handed out so far on this XCD, per head
+    bh = x + kNumXcd * (i - r * hx);
+    vb = r;
+    return;
+  }
+  const int tile = xcd_remap(wg, BH * nvb);
+  bh = tile / nvb;
+  vb = tile - bh * nvb;
+}
+
 // max / sum of a value with its partner 32 lanes away (v_permlane32_swap):
 // lane L receives {x[L mod 32], x[32 + L mod 32]} in the two results.
 __device__ __forceinline__ float xhalf_max(float x) {
