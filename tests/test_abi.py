@@ -271,9 +271,11 @@ def test_training_entry_points_reject_before_launch():
     assert _call_bwd(mask=16, mask_dtype=abi.DTYPE_BOOL, mask_str=(0, 0, 6)) == abi.E_ALIGN
 
 
-def test_training_plans_that_run_whole():
-    """Training forwards above D = 128 (f16, bf16) and every fp32 training
-    forward run unsplit (no workspace), masked or not."""
+def test_training_plans():
+    """Short-query training forwards above D = 128 (f16, bf16; the
+    head-dim > 128 kernel) run unsplit (no workspace), masked or not; the fp32
+    training forward key-splits small non-causal grids like the inference
+    forward (the merging part writes the log-sum-exp), causal ones never."""
     for dt in (abi.DTYPE_F16, abi.DTYPE_BF16):
         for D in (136, 160, 192, 200, 256):
             for mdt in (-1, abi.DTYPE_BOOL):
@@ -281,10 +283,14 @@ def test_training_plans_that_run_whole():
                 assert abi.plan(dt, 1, 8, 8, 16, 8192, D, 1 << 30, mdt, with_lse=True) == (abi.OK, 1)
     for D in (8, 40, 64, 100, 128, 256):
         for mdt in (-1, abi.DTYPE_F32):
-            assert abi.workspace_size(abi.DTYPE_F32, 1, 8, 8, 1024, 1024, D, mdt, with_lse=True) == 0
-            assert abi.plan(abi.DTYPE_F32, 1, 8, 8, 1024, 1024, D, 1 << 30, mdt, with_lse=True) == (abi.OK, 1)
-    # the inference forward of the same fp32 problem splits (128 blocks x 4 parts)
+            train = abi.plan(abi.DTYPE_F32, 1, 8, 8, 1024, 1024, D, 1 << 30, mdt, with_lse=True)
+            assert train == abi.plan(abi.DTYPE_F32, 1, 8, 8, 1024, 1024, D, 1 << 30, mdt)
+            assert train[0] == abi.OK and train[1] >= 2
+            assert abi.workspace_size(abi.DTYPE_F32, 1, 8, 8, 1024, 1024, D, mdt, with_lse=True) > 0
+            assert abi.plan(abi.DTYPE_F32, 1, 8, 8, 1024, 1024, D, 1 << 30, mdt, True, with_lse=True) == (abi.OK, 1)
+    # BASELINE config 1's shape: 128 blocks x 4 parts, training or not
     assert abi.plan(abi.DTYPE_F32, 1, 8, 8, 1024, 1024, 64, 1 << 30) == (abi.OK, 4)
+    assert abi.plan(abi.DTYPE_F32, 1, 8, 8, 1024, 1024, 64, 1 << 30, with_lse=True) == (abi.OK, 4)
     # f16/bf16 training prefills above D = 128 take the pipelined kernel,
     # which splits small grids like the inference launch (64 blocks x 4 parts)
     need = abi.workspace_size(abi.DTYPE_BF16, 1, 8, 8, 1024, 4096, 256, with_lse=True)
