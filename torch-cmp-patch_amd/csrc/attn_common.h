@@ -115,21 +115,29 @@ __device__ __forceinline__ int xcd_remap(int wg, int n) {
 // When the heads split evenly over the XCDs, XCD x owns heads x, x+8, ... and
 // starts their query blocks longest first across those heads; an XCD starts
 // its workgroups in order as slots free up, so this is longest-first list
-// scheduling per XCD.  Otherwise each head's blocks run longest first inside
-// the contiguous range.
+// scheduling per XCD.  Otherwise the whole grid runs longest first, head
+// after head within a length, so that every XCD gets its share of long and
+// short blocks (each head's blocks then land on 8 / gcd(B*H, 8) XCDs; the
+// contiguous per-XCD ranges gave, e.g. for 4 heads, the first XCD the longest
+// half of a head and the second its shortest half).
 __device__ __forceinline__ void wg_tile(int wg, const FwdParams& p, bool causal, int& bh, int& qblk) {
   const int BH = p.B * p.H;
-  if (causal && BH % kNumXcd == 0) {
-    const int x = wg % kNumXcd, i = wg / kNumXcd, hx = BH / kNumXcd;
-    const int r = i / hx;  // query blocks handed out so far on this XCD, per head
-    bh = x + kNumXcd * (i - r * hx);
+  if (causal) {
+    int r;
+    if (BH % kNumXcd == 0) {
+      const int x = wg % kNumXcd, i = wg / kNumXcd, hx = BH / kNumXcd;
+      r = i / hx;  // query blocks handed out so far on this XCD, per head
+      bh = x + kNumXcd * (i - r * hx);
+    } else {
+      r = wg / BH;
+      bh = wg - r * BH;
+    }
     qblk = p.n_qblk - 1 - r;
     return;
   }
   const int tile = xcd_remap(wg, p.n_wg);
   bh = tile / p.n_qblk;
   qblk = tile - bh * p.n_qblk;
-  if (causal) qblk = p.n_qblk - 1 - qblk;
 }
 
 // Which (batch*K/V head, key block) a dK/dV workgroup of the backward computes,
@@ -137,13 +145,18 @@ __device__ __forceinline__ void wg_tile(int wg, const FwdParams& p, bool causal,
 // blocks).  Causal: key block j is seen by every query from j on, so the
 // first blocks have the longest sweeps; like wg_tile, when the heads split
 // evenly over the XCDs each XCD starts its heads' blocks longest first across
-// those heads (list scheduling per XCD).  Otherwise the xcd_remap ranges.
+// those heads (list scheduling per XCD), otherwise the whole grid runs
+// longest first.  Non-causal: the xcd_remap ranges.
 __device__ __forceinline__ void kv_tile(int wg, int BH, int nvb, bool causal, int& bh, int& vb) {
-  if (causal && BH % kNumXcd == 0) {
-    const int x = wg % kNumXcd, i = wg / kNumXcd, hx = BH / kNumXcd;
-    const int r = i / hx;  // blocks handed out so far on this XCD, per head
-    bh = x + kNumXcd * (i - r * hx);
-    vb = r;
+  if (causal) {
+    if (BH % kNumXcd == 0) {
+      const int x = wg % kNumXcd, i = wg / kNumXcd, hx = BH / kNumXcd;
+      vb = i / hx;  // blocks handed out so far on this XCD, per head
+      bh = x + kNumXcd * (i - vb * hx);
+    } else {
+      vb = wg / BH;
+      bh = wg - vb * BH;
+    }
     return;
   }
   const int tile = xcd_remap(wg, BH * nvb);
