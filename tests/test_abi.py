@@ -93,6 +93,12 @@ def test_describe_key_split_plan():
     # shares under 8 tiles: the classic plan (16 blocks past one round in 2 parts)
     assert "key-split: 256 whole + 16 x 2 parts" in abi.describe(f16, 1, 17, 2048, 512, 64)[1]
     assert "key-split" not in abi.describe(f16, 2, 10, 4096, 4096, 64, True)[1]
+    # causal grids of few blocks: every block in the same number of parts,
+    # where they leave most CUs without a block or sweep long key ranges
+    assert "key-split: 0 whole + 64 x 2 parts" in abi.describe(f16, 1, 8, 1024, 1024, 64, True)[1]
+    assert "key-split: 0 whole + 256 x 2 parts" in abi.describe(bf16, 1, 8, 4096, 4096, 128, True)[1]
+    assert "key-split" not in abi.describe(bf16, 1, 32, 1024, 1024, 128, True)[1]
+    assert "key-split" not in abi.describe(bf16, 4, 16, 2048, 2048, 128, True)[1]
     assert "key-split" not in abi.describe(f16, 1, 2, 256, 300, 64)[1]
     assert "key-split: 0 whole + 4 x 8 parts" in abi.describe(f16, 1, 2, 256, 2048, 64)[1]
     bf16 = abi.DTYPE_BF16
@@ -136,11 +142,12 @@ def test_describe_key_split_plan():
     # prefills at head dims above 128 (rows in at least three waves of a
     # block, 256+ keys) run the pipelined kernel at one workgroup per CU:
     # fewer blocks than CUs split into up to CUs / n parts of at least 8
-    # tiles of 32 keys, never causal
+    # tiles of 32 keys; causal into parts of at least 16 tiles of the last
+    # block's sweep (1024 keys: 2 parts)
     assert "key-split: 0 whole + 64 x 4 parts" in abi.describe(f16, 1, 8, 1024, 4096, 160)[1]
     assert "key-split: 0 whole + 4 x 11 parts" in abi.describe(bf16, 1, 4, 100, 3000, 192)[1]
     assert "key-split: 0 whole + 2 x 11 parts" in abi.describe(bf16, 1, 2, 70, 3000, 160)[1]
-    assert "key-split" not in abi.describe(f16, 1, 8, 1024, 4096, 160, True)[1]
+    assert "key-split: 0 whole + 64 x 2 parts" in abi.describe(f16, 1, 8, 1024, 4096, 160, True)[1]
     assert "key-split" not in abi.describe(f16, 2, 10, 1024, 1024, 160)[1]
     assert "pipe16" in abi.describe(f16, 1, 4, 300, 1000, 192, True)[1]
     # causal bf16 192 keeps the plain kernel (two waves per SIMD fit there),

@@ -9,8 +9,9 @@ These cases drive that path (describe() must name the split) with the same
 bar as every other parity test: max |kernel - oracle| <= 1e-2 fp16, 2e-2 bf16,
 oracle = float64 SDPA on the CPU over the same rounded inputs.
 
-Shapes: fewer blocks than CUs (every block split, up to 8 parts), one whole
-round plus a remainder, ragged key counts whose parts get odd tile counts
+Shapes: fewer blocks than CUs (every block split, up to 8 parts), causal
+grids of few blocks (every block cut into the same number of parts), one
+whole round plus a remainder, ragged key counts whose parts get odd tile counts
 (a masked padding tile inside a part), scores spread over tens of log2 units
 (parts settle on different offsets before the merge), back-to-back
 launches of different plans (the per-wave counters must come back to zero),
@@ -115,6 +116,7 @@ def test_split_bshd_views():
 
 def test_causal_and_whole_rounds_do_not_split():
     q = torch.empty(1, dtype=torch.float16)
+    # causal sweeps too short for two parts of 16 tiles
     assert not _splits(_split_text(q, 1, 2, 256, 2048, 64, causal=True))
     if torch.cuda.get_device_properties(0).multi_processor_count == 256:
         # 2 x 12 x 32 blocks = one whole round at three workgroups per CU
@@ -123,6 +125,53 @@ def test_causal_and_whole_rounds_do_not_split():
         # equal shares of the block-tile sequence for all 768 slots
         assert "key-split: 512 whole + 128 x 2 parts" in _split_text(q, 2, 10, 4096, 4096, 64)
         assert "stream-K: 768 workgroups x 42 tiles of 256 blocks" in _split_text(q, 2, 4, 4096, 4096, 64)
+
+
+CAUSAL_SPLIT = [
+    # dtype, B, H, Sq, Sk, D, parts: causal grids filling at most half the
+    # slots with long sweeps, or leaving most CUs without a block
+    ("fp16", 1, 8, 1024, 1024, 64, 2),     # 64 blocks
+    ("bf16", 1, 2, 4096, 4096, 128, 4),    # 64 blocks, 4 parts: the count-in merge
+    ("bf16", 1, 8, 4096, 4096, 128, 2),    # 256 blocks of up to 128 tiles
+    ("fp16", 1, 4, 1000, 3000, 64, 2),     # Sq < Sk (top-left): keys past the last query unseen
+    ("fp16", 1, 4, 3000, 1000, 64, 2),     # Sq > Sk: later blocks see every key
+    ("bf16", 1, 8, 2048, 2048, 256, 2),    # head dim 256, one wave per SIMD
+]
+
+
+@pytest.mark.parametrize("case", CAUSAL_SPLIT, ids=[f"{c[0]}-B{c[1]}H{c[2]}-q{c[3]}k{c[4]}d{c[5]}"
+                                                     for c in CAUSAL_SPLIT])
+def test_causal_split_parity(case):
+    """Causal blocks cut into key ranges: a part's rows either see a key in
+    its first tile or none of its keys (no weight in the merge); the merged
+    output meets the oracle, a rerun is bit-identical, and the training
+    forward's log-sum-exp (the merging part's offset and row sum) too."""
+    dtype, B, H, Sq, Sk, D, parts = case
+    q, k, v = _inputs(dtype, B, H, Sq, Sk, D, seed=Sq + Sk + D)
+    text = _split_text(q, B, H, Sq, Sk, D, causal=True)
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert f"x {parts} parts" in text, text
+    s = 1.0 / math.sqrt(D)
+    out = _check(q, k, v, s, True, dtype)
+    again = abi.attn_fwd(q, k, v, s, True)
+    o2, lse = abi.attn_fwd_lse(q, k, v, s, True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, again)
+    qc, kc = q.cpu(), k.cpu()
+    assert orc.max_abs_err(o2.cpu(), orc.sdpa_np(qc, kc, v.cpu(), s, True)) <= TOL[dtype]
+    assert orc.max_abs_err(lse.cpu(), orc.sdpa_lse_np(qc, kc, s, True)) <= TOL[dtype]
+
+
+def test_causal_split_with_mask():
+    """A key-padding mask and causal together on a split causal grid."""
+    B, H, Sq, Sk, D = 1, 8, 1024, 1024, 64
+    q, k, v = _inputs("fp16", B, H, Sq, Sk, D, seed=5)
+    m = torch.ones(B, 1, 1, Sk, dtype=torch.bool, device="cuda")
+    m[..., 900:] = False
+    out = abi.attn_fwd(q, k, v, 0.125, True, attn_mask=m)
+    torch.cuda.synchronize()
+    ref = orc.sdpa_np(q.cpu(), k.cpu(), v.cpu(), 0.125, True, attn_mask=m.cpu())
+    assert orc.max_abs_err(out.cpu(), ref) <= TOL["fp16"]
 
 
 def test_fewer_blocks_than_cus_take_two_parts_per_cu():

@@ -845,7 +845,7 @@ __device__ __forceinline__ void pipe16_segment(const FwdParams& p, const SplitAr
   // a wave whose rows all lie past Sq (short or packed query sweeps) has
   // nothing to exchange or store; every part of the block agrees on that
   if (qlo >= Sq) return;
-  if (!CAUSAL && nparts > 1) {  // causal launches never split
+  if (nparts > 1) {
     // Leave this part's state, then let the last part of the block merge
     // (its own state straight from its registers); no part ever waits for
     // another workgroup.  Two parts (the tail of a whole-round grid, where
