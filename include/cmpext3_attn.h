@@ -7,7 +7,9 @@
  * of its own.  Launches that split key ranges across workgroups (non-causal,
  * when the query blocks do not fill whole rounds of the GPU; fp16/bf16 with
  * D <= 128, fp16/bf16 with D > 128 and fewer query blocks than CUs, and fp32
- * with at most as many query blocks as CUs) exchange partial results through
+ * with at most as many query blocks as CUs; causal fp16/bf16 grids that fill
+ * at most half of the workgroup slots with long sweeps or on few CUs)
+ * exchange partial results through
  * a caller-owned workspace (cmpext3_attn_fwd_ws, sized by
  * cmpext3_attn_fwd_workspace_size) or, in the allocation-free entry point,
  * through a fixed per-device array inside the library.  Every other call, and
