@@ -122,7 +122,10 @@ def test_describe_key_split_plan():
     assert "BK=32" in abi.describe(f32, 2, 10, 1024, 1024, 64, True)[1]
     assert "BK=32" in abi.describe(f32, 1, 2, 100, 700, 40)[1]
     assert "BK=32" in abi.describe(f32, 2, 8, 4096, 4096, 64)[1]
-    assert "key-split" not in abi.describe(f32, 1, 8, 1024, 1024, 64, True)[1]
+    # causal fp32: every block in the same number of parts where most CUs
+    # idle (128 blocks of up to 32 tiles: 2 parts) or sweeps are long
+    assert "key-split: 128 x 2 parts" in abi.describe(f32, 1, 8, 1024, 1024, 64, True)[1]
+    assert "key-split" not in abi.describe(f32, 1, 12, 2048, 2048, 64, True)[1]   # 384 blocks
     assert "key-split" not in abi.describe(f32, 2, 8, 4096, 4096, 40)[1]
     assert "key-split: 4 x 5 parts" in abi.describe(f32, 1, 2, 100, 700, 40)[1]
     # decode steps (at most 16 rows per head) at head dims above 128 run the
@@ -282,7 +285,8 @@ def test_training_plans():
     """Short-query training forwards above D = 128 (f16, bf16; the
     head-dim > 128 kernel) run unsplit (no workspace), masked or not; the fp32
     training forward key-splits small non-causal grids like the inference
-    forward (the merging part writes the log-sum-exp), causal ones never."""
+    forward (the merging part writes the log-sum-exp), causal ones by the
+    causal plan of the inference forward."""
     for dt in (abi.DTYPE_F16, abi.DTYPE_BF16):
         for D in (136, 160, 192, 200, 256):
             for mdt in (-1, abi.DTYPE_BOOL):
@@ -294,7 +298,8 @@ def test_training_plans():
             assert train == abi.plan(abi.DTYPE_F32, 1, 8, 8, 1024, 1024, D, 1 << 30, mdt)
             assert train[0] == abi.OK and train[1] >= 2
             assert abi.workspace_size(abi.DTYPE_F32, 1, 8, 8, 1024, 1024, D, mdt, with_lse=True) > 0
-            assert abi.plan(abi.DTYPE_F32, 1, 8, 8, 1024, 1024, D, 1 << 30, mdt, True, with_lse=True) == (abi.OK, 1)
+            assert abi.plan(abi.DTYPE_F32, 1, 8, 8, 1024, 1024, D, 1 << 30, mdt, True, with_lse=True) == \
+                abi.plan(abi.DTYPE_F32, 1, 8, 8, 1024, 1024, D, 1 << 30, mdt, True)
     # BASELINE config 1's shape: 128 blocks x 4 parts, training or not
     assert abi.plan(abi.DTYPE_F32, 1, 8, 8, 1024, 1024, 64, 1 << 30) == (abi.OK, 4)
     assert abi.plan(abi.DTYPE_F32, 1, 8, 8, 1024, 1024, 64, 1 << 30, with_lse=True) == (abi.OK, 4)

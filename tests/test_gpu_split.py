@@ -136,6 +136,9 @@ CAUSAL_SPLIT = [
     ("fp16", 1, 4, 1000, 3000, 64, 2),     # Sq < Sk (top-left): keys past the last query unseen
     ("fp16", 1, 4, 3000, 1000, 64, 2),     # Sq > Sk: later blocks see every key
     ("bf16", 1, 8, 2048, 2048, 256, 2),    # head dim 256, one wave per SIMD
+    ("fp32", 1, 8, 1024, 1024, 64, 2),     # the fp32 kernel's 64-row blocks
+    ("fp32", 1, 8, 1024, 1024, 256, 4),    # fp32, 16-key tiles
+    ("fp32", 1, 4, 4096, 4096, 128, 2),    # fp32, 256 blocks of long sweeps
 ]
 
 
@@ -208,7 +211,7 @@ def test_split_parity_fp32(case):
 
 def test_split_fp32_wide_scores_and_causal_unsplit():
     """Scores over tens of log2 units (each part settles on its own offset),
-    and causal fp32 launches, which never split."""
+    and a causal fp32 launch of short sweeps, which stays whole."""
     q, k, v = _inputs("fp32", 1, 2, 128, 1500, 64, seed=31)
     q = q * 6
     _check(q, k, v, 0.125, False, "fp32")
@@ -285,7 +288,7 @@ FP32_PLANS = [
     (2, 8, 1000, 1500, 128, False, ("key-split: 256 x 2 parts", "BK=32")),  # ragged, D = 128
     (1, 8, 2048, 2048, 40, False, ("key-split: 256 x 2 parts", "BK=64")),   # the D = 40 bucket
     (2, 10, 1024, 1000, 64, False, ("BK=64",)),                             # 320 blocks: unsplit
-    (2, 8, 1024, 1024, 64, True, ("BK=32",)),                               # causal: never split
+    (2, 8, 1024, 1024, 64, True, ("BK=32",)),                               # causal, short sweeps: whole
 ]
 
 

@@ -15,8 +15,9 @@
 // is written too (by the merging part where the keys are split: the merged
 // offset and row sum).
 //
-// Key split (non-causal launches with at most as many query blocks as CUs,
-// such as [1, 8, 1024, 64]): each block's key range is cut into parts run by
+// Key split (launches with at most as many query blocks as CUs, such as
+// [1, 8, 1024, 64]; causal ones where most CUs idle or sweeps are long): each
+// block's key range is cut into parts run by
 // separate workgroups, which shortens every wave's dependency chain over the
 // keys and fills the idle CUs.  Every part leaves its fp32 (O, m, l) in the exchange
 // buffer; the last part of a (block, wave) to finish merges all of them in
@@ -91,7 +92,7 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
 
   int kend = Sk;
   if (CAUSAL) kend = min(Sk, q0 + BQ);
-  // this workgroup's key tiles [tbase, tbase + ntiles) (causal launches never split)
+  // this workgroup's key tiles [tbase, tbase + ntiles)
   const int ntall = (kend + BK - 1) / BK;
   const int tbase = part * ntall / nparts;
   const int ntiles = (part + 1) * ntall / nparts - tbase;
@@ -337,7 +338,7 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
     l += __shfl_xor(l, 32);
     lrow[qb] = l;
   }
-  if (!CAUSAL && nparts > 1) {
+  if (nparts > 1) {
     // a wave whose rows all lie past Sq has nothing to exchange; every part
     // of the block agrees on that
     if (qw0 >= Sq) return;
@@ -452,18 +453,38 @@ attn_fwd_mfma32(const FwdParams p, const SplitArgs sa) {
 }
 
 // Key split plan: only when the query blocks leave CUs idle or alone (at most
-// one block per CU), non-causal, into enough parts for about two workgroups
-// per CU, each part at least kMinTiles32 key tiles long.  Returns the part
+// one block per CU), into enough parts for about two workgroups per CU, each
+// part at least kMinTiles32 key tiles long (causal: below).  Returns the part
 // count (1: no split) for n query blocks and bk-key tiles.  Measured on
 // MI355X at one block per CU (n = 256, 2 parts, 64-key tiles against the
 // unsplit launch): [2,8,1024,1024,64] 60.8 -> 54.1 us, [2,8,1024,4096,64]
 // 215 -> 172 us, [1,8,2048,2048,40] 95.5 -> 69.2 us, [2,8,1024,1024,128]
 // (32-key tiles) 107 -> 101 us; between one and two blocks per CU a split
 // changes nothing.
+//
+// Causal launches (query blocks of 64 rows whose sweeps end at their last
+// row): every block is cut into the same number of parts where the blocks
+// leave more than half of the CUs idle or sweep long key ranges (the last
+// block at least kLongCausal32 tiles), the longest part keeping at least
+// kMinCausalTiles32 tiles and every part at least one (a causal row sees a
+// key in the first tile of a part or none of its keys; the kernel gives such
+// a row's part no weight in the merge).
 constexpr int kMinTiles32 = 4;
-int split_parts32(int n, int Sk, int bk, int cus, bool causal) {
-  if (causal || n <= 0 || n > cus) return 1;
+constexpr int kMinCausalTiles32 = 8;
+constexpr int kLongCausal32 = 64;
+int split_parts32(int n, int Sk, int bk, int cus, bool causal, int Sq) {
+  if (n <= 0 || n > cus) return 1;
   int parts = 2 * cus / n;
+  if (causal) {
+    const int64_t last = (int64_t)(Sq + 63) / 64 * 64;  // keys the last block's rows can see
+    const int tmax = (int)(((last < Sk ? last : Sk) + bk - 1) / bk);
+    const int tmin = ((Sk < 64 ? Sk : 64) + bk - 1) / bk;
+    if (n * 2 > cus && tmax < kLongCausal32) return 1;
+    if (parts > tmax / kMinCausalTiles32) parts = tmax / kMinCausalTiles32;
+    if (parts > tmin) parts = tmin;
+    if (parts > 8) parts = 8;
+    return parts >= 2 ? parts : 1;
+  }
   const int ntiles = (Sk + bk - 1) / bk;
   if (parts > ntiles / kMinTiles32) parts = ntiles / kMinTiles32;
   return parts >= 2 ? parts : 1;
@@ -480,10 +501,10 @@ int split_parts32(int n, int Sk, int bk, int cus, bool causal) {
 // 601 us with 32, 635 with 64.
 int tile_keys32(int dk, int n, int Sk, int cus, bool causal) {
   const int def = dk <= 128 ? 32 : 16;
-  if (dk > 64) return def;
+  if (dk > 64 || causal) return def;
   if (!causal && n > cus) return n <= 2 * cus ? 64 : def;
-  const int p64 = split_parts32(n, Sk, 64, cus, causal);
-  return p64 >= 2 && p64 == split_parts32(n, Sk, def, cus, causal) ? 64 : def;
+  const int p64 = split_parts32(n, Sk, 64, cus, false, 0);
+  return p64 >= 2 && p64 == split_parts32(n, Sk, def, cus, false, 0) ? 64 : def;
 }
 
 template <int DK, bool CAUSAL, bool ELEM, int BK, bool MASK>
@@ -504,7 +525,7 @@ hipError_t launch_mfma32_bk(const FwdParams& p0, hipStream_t stream) {
   // waves per block that hold query rows (a single block shorter than BQ has fewer)
   const int nwl = p.n_qblk > 1 ? NW : (p.Sq + 15) / 16 < NW ? (p.Sq + 15) / 16 : NW;
   SplitArgs sa = {n, 1, nullptr, nullptr, nwl};
-  const int parts = split_parts32(n, p.Sk, BK, device_cus(), CAUSAL);
+  const int parts = split_parts32(n, p.Sk, BK, device_cus(), CAUSAL, p.Sq);
   if (parts >= 2) {
     // every block is split; one key range of all of them takes part_bytes
     const size_t part_bytes = (size_t)n * nwl * NQB * (NDB + 1) * 64 * sizeof(f32x4);
@@ -575,7 +596,7 @@ void describe_mfma32(int D, int B, int H, int Sq, int Sk, bool causal, char* buf
   const int bq = 64;
   const int n = B * H * ((Sq + bq - 1) / bq), cus = device_cus();
   const int bk = tile_keys32(dk, n, Sk, cus, causal);
-  const int parts = split_parts32(n, Sk, bk, cus, causal);
+  const int parts = split_parts32(n, Sk, bk, cus, causal, Sq);
   char split[48] = "";
   if (parts >= 2) snprintf(split, sizeof split, " key-split: %d x %d parts", n, parts);
   snprintf(buf, len, "mfma32 16x16x4f32 S^T-form: DK=%d DPV=%d waves=4 BQ=%d BK=%d qblocks=%d%s%s", dk,
