@@ -136,6 +136,7 @@ CAUSAL_SPLIT = [
     ("fp16", 1, 4, 1000, 3000, 64, 2),     # Sq < Sk (top-left): keys past the last query unseen
     ("fp16", 1, 4, 3000, 1000, 64, 2),     # Sq > Sk: later blocks see every key
     ("bf16", 1, 8, 2048, 2048, 256, 2),    # head dim 256, one wave per SIMD
+    ("bf16", 1, 4, 2048, 2048, 192, 4),    # causal D = 192 on the head-dim > 128 kernel
     ("fp32", 1, 8, 1024, 1024, 64, 2),     # the fp32 kernel's 64-row blocks
     ("fp32", 1, 8, 1024, 1024, 256, 4),    # fp32, 16-key tiles
     ("fp32", 1, 4, 4096, 4096, 128, 2),    # fp32, 256 blocks of long sweeps

@@ -275,9 +275,9 @@ attn_fwd_mfma16(const FwdParams p, const SplitArgs sa) {
   const int hh = lane >> 5;
 
   // ---- which (batch, head, query block) and which part of its keys this
-  // workgroup owns (causal launches never split)
+  // workgroup owns
   int lb = block_x(), part = 0, nparts = 1;
-  if (!CAUSAL && lb >= sa.nfull) {
+  if (lb >= sa.nfull) {
     const int r = lb - sa.nfull;
     nparts = sa.nparts;
     lb = sa.nfull + r / nparts;
@@ -622,7 +622,7 @@ attn_fwd_mfma16(const FwdParams p, const SplitArgs sa) {
   float lrow[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) lrow[qb] = xhalf_sum(lsum[qb]);
-  if (!CAUSAL && nparts > 1) {
+  if (nparts > 1) {
     // Every part leaves its state and counts itself in; the last one in
     // merges and writes the output.  Device-scope (aux 16 = sc1) 16-byte
     // accesses, coherent across the XCDs' L2s.
@@ -830,7 +830,7 @@ attn_fwd_mfma16(const FwdParams p, const SplitArgs sa) {
 
 // Launch one instance: grid = B*H*ceil(Sq/BQ) workgroups of NW waves.
 // Key split plan: only when the query blocks leave CUs idle (fewer blocks
-// than CUs), non-causal, into enough parts for up to two workgroups per CU
+// than CUs), into enough parts for up to two workgroups per CU
 // (as many as fit: one at head dims above 128), each part at least
 // kMinTiles16 key tiles long, and at most 32 parts.  When every wave of a
 // block holds rows, the last part's waves each merge their own rows: then
@@ -840,11 +840,23 @@ attn_fwd_mfma16(const FwdParams p, const SplitArgs sa) {
 // D = 256, 16384 keys, 2 / 8 / 32 / 64 parts 428 / 178 / 306 / 592 us with
 // that merge).  Blocks with rows in fewer waves (`spread`: decode, packed
 // query groups) merge across the whole workgroup and keep the cap of 32.
-// Returns the part count (1: no split).
+// Causal launches: below.  Returns the part count (1: no split).
 constexpr int kMinTiles16 = 4;
-inline int split_parts16(int n, int ntiles, int wg_per_cu, int cus, bool causal, int dp, bool spread) {
-  if (causal || n <= 0 || n >= cus) return 1;
+inline int split_parts16(int n, int ntiles, int wg_per_cu, int cus, bool causal, int dp, bool spread,
+                         int ntiles_min) {
+  if (n <= 0 || n >= cus) return 1;
   int parts = (wg_per_cu < 2 ? wg_per_cu : 2) * cus / n;
+  if (causal) {
+    // ntiles: the last block's sweep (to its last row), ntiles_min the
+    // first's; every part keeps a tile, the longest at least 16 (a causal row
+    // sees a key in a part's first tile or none of the part's keys, and then
+    // has no weight in the merge); only where most CUs idle or sweeps are long
+    if (n * 2 > cus && ntiles < 64) return 1;
+    if (parts > ntiles / 16) parts = ntiles / 16;
+    if (parts > ntiles_min) parts = ntiles_min;
+    if (parts > 8) parts = 8;
+    return parts >= 2 ? parts : 1;
+  }
   if (parts > ntiles / kMinTiles16) parts = ntiles / kMinTiles16;
   const int cap = dp >= 192 && !spread ? 8 : 32;
   if (parts > cap) parts = cap;
@@ -867,8 +879,11 @@ hipError_t launch_mfma16_cfg(const FwdParams& p0, hipStream_t stream) {
   const int nwl = p.n_qblk > 1 ? NW : (p.Sq + QB * 32 - 1) / (QB * 32) < NW ? (p.Sq + QB * 32 - 1) / (QB * 32) : NW;
   SplitArgs sa = {n, 1, nullptr, nullptr, nwl};
   // the training forward (OPT bit 5) runs every block whole
-  const int parts =
-      (OPT & 32) ? 1 : split_parts16(n, (p.Sk + BK - 1) / BK, OCC, device_cus(), CAUSAL, DP, nwl < NW);
+  const int kmax = CAUSAL && (int64_t)p.n_qblk * BQ < p.Sk ? p.n_qblk * BQ : p.Sk;  // the last block's keys
+  const int kmin = CAUSAL && BQ < p.Sk ? BQ : p.Sk;                                 // the first block's
+  const int parts = (OPT & 32) ? 1
+                               : split_parts16(n, (kmax + BK - 1) / BK, OCC, device_cus(), CAUSAL, DP, nwl < NW,
+                                               (kmin + BK - 1) / BK);
   if (parts >= 2) {
     // every block is split; one key range of all of them takes part_bytes
     const size_t part_bytes = (size_t)n * nwl * QB * split_vectors(DP) * 64 * sizeof(f32x4);

@@ -209,8 +209,10 @@ void describe_mfma16(int D, int B, int H, int Sq, int Sk, bool causal, bool bf16
   const int bq = t.nw * t.qb * 32;
   const int n = B * H * ((Sq + bq - 1) / bq);
   const int nwl = Sq > bq ? t.nw : (Sq + 31) / 32 < t.nw ? (Sq + 31) / 32 : t.nw;
-  const int parts = split_parts16(n, (Sk + t.bk - 1) / t.bk, t.occ, device_cus(), causal, (dk + 31) / 32 * 32,
-                                  nwl < t.nw);
+  const int64_t nb = (Sq + bq - 1) / bq;
+  const int kmax = causal && nb * bq < Sk ? (int)(nb * bq) : Sk, kmin = causal && bq < Sk ? bq : Sk;
+  const int parts = split_parts16(n, (kmax + t.bk - 1) / t.bk, t.occ, device_cus(), causal, (dk + 31) / 32 * 32,
+                                  nwl < t.nw, (kmin + t.bk - 1) / t.bk);
   char split[48] = "";
   if (parts >= 2) snprintf(split, sizeof split, " key-split: %d x %d parts", n, parts);
   snprintf(buf, len,
