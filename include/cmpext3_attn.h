@@ -250,8 +250,8 @@ int cmpext3_attn_fwd_noalloc(const void* q, const void* k, const void* v, void* 
  * CMPEXT3_E_HEAD_DIM).  f16/bf16 calls run the pipelined kernel up to
  * D = 128, whatever Sk, and above it (192 and 256 buckets) when Sq > 64 and
  * Sk >= 256 (both may key-split through the workspace); other f16/bf16
- * calls above D = 128 run the head-dim > 128 kernel, and fp32 calls the
- * fp32 kernel, both never key-split.  A mask
+ * calls above D = 128 run the head-dim > 128 kernel (never key-split here),
+ * and fp32 calls the fp32 kernel (key-split like its inference launch).  A mask
  * is read in runs of 8 keys, as the backward reads it: 16-byte aligned,
  * strides multiples of 4 elements (else CMPEXT3_E_ALIGN), and every row
  * readable up to Sk rounded up to a multiple of 8 (values past Sk are

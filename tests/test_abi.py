@@ -72,7 +72,8 @@ def test_describe_key_split_plan():
     """Without a visible device the plan assumes MI355X's 256 CUs.  SDXL
     self-attention: 640 blocks of 128 queries = 2 whole rounds + 128 blocks
     cut in 2 key ranges (one part per CU); 2*4*32 = 256 blocks fill whole
-    rounds; causal launches and short key sweeps never split; 4 blocks of
+    rounds; causal launches of many blocks and short key sweeps never split;
+    4 blocks of
     2048 keys (64 tiles) get 8 parts of 8 tiles.  With no whole round every
     CU holds two parts: 128 blocks of 4096 keys (a packed decode step) get
     4 parts each, 200 blocks get 2."""
@@ -401,7 +402,7 @@ def test_workspace_size_and_plan():
     assert abi.plan(f32, 1, 8, 8, 1024, 1024, 64, 0) == (abi.OK, 1)
     # head dim 256 decode on the decode kernel: 16 units x 16 parts
     assert abi.plan(f16, 1, 16, 16, 1, 16384, 256, 1 << 30) == (abi.OK, 16)
-    # never split: causal, whole rounds, short keys
+    # never split: causal grids of many blocks, whole rounds, short keys
     for args in ((f16, 2, 10, 10, 4096, 4096, 64, -1, True), (f16, 2, 12, 12, 4096, 4096, 64),
                  (f16, 2, 10, 10, 4096, 77, 64)):
         assert abi.workspace_size(*args) == 0
