@@ -311,7 +311,9 @@ int cmpext3_attn_bwd(const void* q, const void* k, const void* v, const void* o,
  * (grouped-query K/V of one or two sequences, causal sweeps whose length
  * falls with the key block) cut each block's dK/dV sweep over (query head,
  * query tile) into up to 8 contiguous parts on separate workgroups, and
- * likewise the dQ sweeps of few query blocks over key tiles; the parts leave
+ * likewise the dQ sweeps of few query blocks over key tiles (f16/bf16
+ * non-causal grids past one round split only their last, partial round of
+ * blocks); the parts leave
  * fp32 partial rows in the workspace that a further kernel sums in part
  * order (still bit-identical from run to run; the sums differ from the
  * unsplit launch's only by rounding).  With a workspace smaller than

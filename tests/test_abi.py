@@ -435,7 +435,12 @@ def test_bwd_workspace_plan():
     kv = lambda ns, B, Hkv, Sk, D: ns * B * Hkv * Sk * D * 2 * 4
     dq = lambda ns, B, H, Sq, D: ns * B * H * Sq * D * 4
     assert abi.bwd_workspace_size(bf16, 4, 16, 16, 2048, 2048, 128, -1, True) == 0     # Qwen3 shape
-    assert abi.bwd_workspace_size(f16, 2, 10, 10, 4096, 4096, 64, -1, False) == 0      # SDXL shape
+    # SDXL shape: 640 blocks at three per CU, the last 128 in 2 parts (split
+    # tails: block-indexed partials of 128 rows)
+    tail = lambda ns, nsb, D: ns * nsb * 128 * D * 4
+    assert abi.bwd_workspace_size(f16, 2, 10, 10, 4096, 4096, 64, -1, False) == \
+        2 * tail(2, 128, 64) + tail(2, 128, 64)
+    assert abi.bwd_workspace_size(f16, 2, 12, 12, 4096, 4096, 64, -1, False) == 0      # whole rounds
     # fp32: 64-row blocks; BASELINE config 1's 128 key blocks (3 workgroups per
     # CU) take 6 parts and its 128 query blocks (4 per CU) 8; SD1.5's none
     assert abi.bwd_workspace_size(f32, 1, 8, 8, 1024, 1024, 64, -1, False) == \

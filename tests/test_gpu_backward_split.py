@@ -4,7 +4,9 @@ With too few blocks for the CUs (one or two sequences, grouped-query K/V,
 causal sweeps whose length runs from one tile to all of them) the dK/dV sweep
 of a key block over (query head of the group, query tile), and the dQ sweep
 of a query block over key tiles, are cut into up to 8 contiguous parts whose
-fp32 partials a further kernel sums in part order.
+fp32 partials a further kernel sums in part order; non-causal f16/bf16 grids
+past one round split only the blocks of their last, partial round (split
+tails, block-indexed partials).
 Oracle: float64 sdpa_bwd_np on K/V repeated per query head, the repeats'
 gradients summed; bar: max abs error <= 1e-2 (fp16) / 2e-2 (bf16) / 1e-4
 (fp32) times the gradient's largest oracle magnitude (at least 1e-3; 0.1 for
@@ -43,6 +45,10 @@ CASES = [
     ("fp16", 2, 4, 2, 500, 700, 64, False, "pad"),      # key-padding mask
     ("bf16", 1, 4, 2, 400, 400, 128, True, "full"),     # per-row bool mask with causal
     ("fp16", 1, 2, 2, 260, 200, 64, False, None),       # short sweeps: 2 parts of 4 and 5 tiles
+    ("fp16", 1, 36, 36, 2048, 2048, 64, False, None),   # split tails: 512 whole + 64 x 4 parts
+    ("fp16", 1, 36, 36, 2048, 2048, 64, False, "pad"),  # a dK/dV split tail with a mask
+    ("bf16", 1, 20, 20, 2048, 2048, 128, False, None),  # split tails at two workgroups per CU
+    ("bf16", 1, 40, 20, 2048, 2048, 128, False, None),  # a dK/dV split tail, grouped-query K/V
     ("fp32", 1, 8, 8, 1024, 1024, 64, False, None),     # BASELINE config 1 shape: 6 + 8 parts
     ("fp32", 1, 4, 2, 700, 500, 40, True, None),        # SD1.5 head dim, grouped-query causal
     ("fp32", 1, 2, 1, 300, 400, 128, True, "pad"),      # masked causal D = 128

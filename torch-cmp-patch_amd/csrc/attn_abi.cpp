@@ -496,11 +496,13 @@ int cmpext3_attn_bwd_ws(const void* q, const void* k, const void* v, const void*
     size_t used = 0;
     if (kvb > 0 && kvb <= workspace_bytes) {
       p.nsplit = sp.ns_kv;
+      p.nfull = sp.nfull_kv;
       p.part = (float*)workspace;
       used = kvb;
     }
     if (qb > 0 && used + qb <= workspace_bytes) {
       p.nsplit_q = sp.ns_q;
+      p.nfull_q = sp.nfull_q;
       p.part_q = (float*)((char*)workspace + used);
     }
   }

@@ -73,6 +73,11 @@ struct BwdParams {
   int nsplit, nsplit_q;
   float* part;
   float* part_q;
+  // f16/bf16, non-causal: with nfull > 0 only the blocks past the first nfull
+  // (the last, partial round of workgroup slots) are split, and their
+  // partials are block-indexed: [nsplit][blocks - nfull][128][D] (likewise
+  // nfull_q for dQ)
+  int nfull, nfull_q;
 };
 
 // Parts per block of a gradient sweep (1 = unsplit).  With too few blocks
@@ -98,13 +103,38 @@ inline int split_sweep(int64_t n_wg, int occ, int cus, bool causal, int64_t tile
 // x Sq x D floats).
 struct BwdSplit {
   int ns_kv = 1, ns_q = 1;
+  int nfull_kv = 0, nfull_q = 0;  // split tails: whole blocks before them
   size_t kv_bytes(int B, int Hkv, int Sk, int D) const {
-    return ns_kv > 1 ? (size_t)2 * ns_kv * B * Hkv * Sk * D * sizeof(float) : 0;
+    if (ns_kv < 2) return 0;
+    if (nfull_kv > 0)
+      return (size_t)2 * ns_kv * ((int64_t)B * Hkv * ((Sk + 127) / 128) - nfull_kv) * 128 * D * sizeof(float);
+    return (size_t)2 * ns_kv * B * Hkv * Sk * D * sizeof(float);
   }
   size_t q_bytes(int B, int H, int Sq, int D) const {
-    return ns_q > 1 ? (size_t)ns_q * B * H * Sq * D * sizeof(float) : 0;
+    if (ns_q < 2) return 0;
+    if (nfull_q > 0) return (size_t)ns_q * ((int64_t)B * H * ((Sq + 127) / 128) - nfull_q) * 128 * D * sizeof(float);
+    return (size_t)ns_q * B * H * Sq * D * sizeof(float);
   }
 };
+
+// Split tail of a non-causal grid of n equal sweeps that fills more than one
+// but not a whole number of rounds of one workgroup per CU, within the occ
+// workgroups per CU the kernel allows (SDXL self-attention: 640 blocks at
+// three per CU): the blocks past the whole rounds are cut into parts, one
+// per CU, so every CU holds the same work (as the forward's key split does).
+// Returns the parts (1 = none) and sets *nfull.
+inline int split_tail(int64_t n, int occ, int cus, int64_t tiles, int* nfull) {
+  *nfull = 0;
+  if (cus <= 0) return 1;
+  const int64_t full = n / cus, rem = n - full * cus;
+  if (full == 0 || rem == 0 || full + 1 > occ) return 1;
+  int64_t ns = cus / rem;
+  if (ns > 8) ns = 8;
+  if (ns > tiles / 8) ns = tiles / 8;
+  if (ns < 2) return 1;
+  *nfull = (int)(full * cus);
+  return (int)ns;
+}
 
 // fp32 partial rows of a split sweep ([ns][rows][D], rows = B x heads x S)
 // and where their sum goes: T rows with element strides {batch, head, seq},
@@ -285,9 +315,27 @@ attn_bwd_dkdv(const BwdParams p) {
   // virtual blocks.  Causal: longest sweeps first (kv_tile).  (The divisions
   // run on the vector unit: readfirstlane keeps the indices, and the per-head
   // address arithmetic of the sweep, in scalar registers.)
-  const int ns = p.nsplit > 1 ? p.nsplit : 1;
-  int bhk, kb, part;
-  {
+  int ns = p.nsplit > 1 ? p.nsplit : 1;
+  int bhk, kb, part, sb = -1;  // sb: index among a split tail's blocks
+  if (!CAUSAL && p.nfull > 0) {
+    // split tail: the first nfull workgroups take whole blocks, the rest
+    // ns-way parts of the remaining blocks
+    const int w = block_x();
+    int tile = w;
+    part = 0;
+    if (w >= p.nfull) {
+      const int r = w - p.nfull;
+      tile = p.nfull + r / ns;
+      part = r - (tile - p.nfull) * ns;
+      sb = tile - p.nfull;
+    } else {
+      ns = 1;
+    }
+    int bh0, kb0;
+    kv_tile(tile, p.B * p.Hkv, p.n_blk, false, bh0, kb0);
+    bhk = __builtin_amdgcn_readfirstlane(bh0);
+    kb = __builtin_amdgcn_readfirstlane(kb0);
+  } else {
     int bh0, vb;
     kv_tile(block_x(), p.B * p.Hkv, p.n_blk * ns, CAUSAL, bh0, vb);
     bhk = __builtin_amdgcn_readfirstlane(bh0);
@@ -402,7 +450,13 @@ attn_bwd_dkdv(const BwdParams p) {
   uint16_t* dvg = (uint16_t*)p.dv + b * p.dv_b + hk * p.dv_h;
   // the result: gradients, or this part's fp32 partials (dK unscaled)
   auto finish = [&]() {
-    if (ns > 1) {
+    if (ns > 1 && sb >= 0) {  // split tail: block-indexed rows
+      const int64_t nsb = (int64_t)p.B * p.Hkv * p.n_blk - p.nfull;
+      float* const pk = p.part + ((int64_t)part * nsb + sb) * 128 * D;
+      const int kl = key - kb * 128;
+      store_rows_f32<NDB>(pk, kl, Sk - kb * 128, D, hh, dka);
+      store_rows_f32<NDB>(pk + ns * nsb * 128 * D, kl, Sk - kb * 128, D, hh, dva);
+    } else if (ns > 1) {
       const int64_t rows = (int64_t)p.B * p.Hkv * Sk;
       float* const pk = p.part + ((int64_t)part * p.B * p.Hkv + bhk) * Sk * D;
       store_rows_f32<NDB>(pk, key, Sk, D, hh, dka);
@@ -551,6 +605,52 @@ __global__ void __launch_bounds__(256) attn_bwd_part_sum(const PartSum a, const 
   if (b.out) part_sum_store<T>(b, i4);
 }
 
+// ---- Sums of a split tail's block-indexed partials ([ns][blocks][128][D]),
+// in part order: split block sb is logical block nfull + sb, mapped to its
+// (head, block) as the gradient kernel maps it; rows past Sk (Sq) are not
+// stored.  KV: dK (times the signed scale) and dV; otherwise dQ.
+template <typename T, bool KV>
+__global__ void __launch_bounds__(256) attn_bwd_tail_sum(const BwdParams p) {
+  const int D = p.D, ns = KV ? p.nsplit : p.nsplit_q, nfull = KV ? p.nfull : p.nfull_q;
+  const int heads = KV ? p.Hkv : p.H;
+  const int64_t nsb = (int64_t)p.B * heads * p.n_blk - nfull;
+  const int64_t i4 = (int64_t)block_x() * 256 + thread_x();
+  if (i4 >= nsb * 128 * D / 4) return;
+  const int64_t row = i4 * 4 / D;
+  const int d = (int)(i4 * 4 - row * D);
+  const int sbi = (int)(row / 128), rl = (int)(row - (int64_t)sbi * 128);
+  int bh, blk;
+  if (KV) {
+    kv_tile(nfull + sbi, p.B * heads, p.n_blk, false, bh, blk);
+  } else {
+    FwdParams fp;
+    fp.B = p.B; fp.H = p.H; fp.n_qblk = p.n_blk; fp.n_wg = p.B * p.H * p.n_blk;
+    wg_tile(nfull + sbi, fp, false, bh, blk);
+  }
+  const int s = blk * 128 + rl;
+  if (s >= (KV ? p.Sk : p.Sq)) return;
+  const int b = bh / heads, h = bh - b * heads;
+  const float* const src = (KV ? p.part : p.part_q) + row * D + d;
+  const int64_t step = nsb * 128 * D;  // one part's floats
+  auto sum = [&](const float* base) {
+    f32x4 x = *(const f32x4*)base;
+    for (int q = 1; q < ns; ++q) x += *(const f32x4*)(base + q * step);
+    return x;
+  };
+  auto put = [&](void* out, int64_t ob, int64_t oh, int64_t os, f32x4 x) {
+    u32x2 w;
+    w[0] = Elt<T>::pack(x[0], x[1]);
+    w[1] = Elt<T>::pack(x[2], x[3]);
+    *(u32x2*)((uint16_t*)out + b * ob + h * oh + (int64_t)s * os + d) = w;
+  };
+  if (KV) {
+    put(p.dk, p.dk_b, p.dk_h, p.dk_s, sum(src) * p.scale);
+    put(p.dv, p.dv_b, p.dv_h, p.dv_s, sum(src + ns * step));
+  } else {
+    put(p.dq, p.dq_b, p.dq_h, p.dq_s, sum(src) * p.scale);
+  }
+}
+
 // Launch the sums of the dK/dV partials (sweeps split nsplit ways) or of the
 // dQ partials (nsplit_q ways) that a launch's split sweeps left (errors show
 // in the caller's final hipGetLastError).
@@ -592,9 +692,26 @@ attn_bwd_dq(const BwdParams p) {
 
   const int tid = thread_x(), wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   // split sweeps: (query block, part) pairs as ns virtual blocks per block
-  const int ns = p.nsplit_q > 1 ? p.nsplit_q : 1;
-  int bh, qblk, part;
-  {
+  int ns = p.nsplit_q > 1 ? p.nsplit_q : 1;
+  int bh, qblk, part, sb = -1;  // sb: index among a split tail's blocks
+  if (!CAUSAL && p.nfull_q > 0) {
+    // split tail: the first nfull_q workgroups take whole blocks, the rest
+    // ns-way parts of the remaining blocks
+    const int w = block_x();
+    int lb = w;
+    part = 0;
+    if (w >= p.nfull_q) {
+      const int r = w - p.nfull_q;
+      lb = p.nfull_q + r / ns;
+      part = r - (lb - p.nfull_q) * ns;
+      sb = lb - p.nfull_q;
+    } else {
+      ns = 1;
+    }
+    FwdParams fp;
+    fp.B = p.B; fp.H = p.H; fp.n_qblk = p.n_blk; fp.n_wg = p.B * p.H * p.n_blk;
+    wg_tile(lb, fp, false, bh, qblk);
+  } else {
     FwdParams fp;
     fp.B = p.B; fp.H = p.H; fp.n_qblk = p.n_blk * ns; fp.n_wg = p.n_wg;
     int vblk;
@@ -774,6 +891,12 @@ attn_bwd_dq(const BwdParams p) {
     lds_barrier();
   }
 
+  if (ns > 1 && sb >= 0) {  // split tail: block-indexed partial rows, unscaled
+    const int64_t nsb = (int64_t)p.B * p.H * p.n_blk - p.nfull_q;
+    store_rows_f32<NDB>(p.part_q + ((int64_t)part * nsb + sb) * BQ * D, qrow - qblk * BQ, Sq - qblk * BQ, D, hh,
+                        dqa);
+    return;
+  }
   if (ns > 1) {  // this part's partial rows, unscaled
     store_rows_f32<NDB>(p.part_q + ((int64_t)part * p.B * p.H + bh) * Sq * D, qrow, Sq, D, hh, dqa);
     return;

@@ -17,15 +17,33 @@ hipError_t launch_bwd_t(const BwdParams& p0, hipStream_t s) {
   p.n_blk = (p.Sk + 127) / 128;
   const int ns = p.nsplit > 1 && p.part ? p.nsplit : 1;
   p.nsplit = ns;
-  p.n_wg = p.B * p.Hkv * p.n_blk * ns;
+  if (ns == 1 || CAUSAL) p.nfull = 0;
+  const int n_kv = p.B * p.Hkv * p.n_blk;
+  p.n_wg = p.nfull > 0 ? p.nfull + (n_kv - p.nfull) * ns : n_kv * ns;
   hipLaunchKernelGGL((attn_bwd_dkdv<T, DK, CAUSAL, MASK>), dim3(p.n_wg), dim3(256), 0, s, p);
-  if (ns > 1) launch_part_sums<T>(p, true, s);
+  if (ns > 1) {
+    if (p.nfull > 0) {
+      const int64_t n4 = (int64_t)(n_kv - p.nfull) * 128 * p.D / 4;
+      hipLaunchKernelGGL((attn_bwd_tail_sum<T, true>), dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, p);
+    } else {
+      launch_part_sums<T>(p, true, s);
+    }
+  }
   p.n_blk = (p.Sq + 127) / 128;
   const int nsq = p.nsplit_q > 1 && p.part_q ? p.nsplit_q : 1;
   p.nsplit_q = nsq;
-  p.n_wg = p.B * p.H * p.n_blk * nsq;
+  if (nsq == 1 || CAUSAL) p.nfull_q = 0;
+  const int n_q = p.B * p.H * p.n_blk;
+  p.n_wg = p.nfull_q > 0 ? p.nfull_q + (n_q - p.nfull_q) * nsq : n_q * nsq;
   hipLaunchKernelGGL((attn_bwd_dq<T, DK, CAUSAL, MASK>), dim3(p.n_wg), dim3(256), 0, s, p);
-  if (nsq > 1) launch_part_sums<T>(p, false, s);
+  if (nsq > 1) {
+    if (p.nfull_q > 0) {
+      const int64_t n4 = (int64_t)(n_q - p.nfull_q) * 128 * p.D / 4;
+      hipLaunchKernelGGL((attn_bwd_tail_sum<T, false>), dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, p);
+    } else {
+      launch_part_sums<T>(p, false, s);
+    }
+  }
   return hipGetLastError();
 }
 
@@ -58,9 +76,13 @@ BwdSplit bwd16_split(int B, int H, int Hkv, int Sq, int Sk, int D, bool causal, 
   if (dk < 0 || (int64_t)B * H * Sq == 0 || Hkv < 1) return sp;
   const int occ_kv = dk <= 64 ? (causal ? 2 : 3) : dk <= 128 ? (masked && causal ? 1 : 2) : 1;
   const int occ_q = dk <= 64 ? (masked ? 2 : 3) : dk <= 128 ? (masked && causal ? 1 : 2) : 1;
-  sp.ns_kv = split_sweep((int64_t)B * Hkv * ((Sk + 127) / 128), occ_kv, cus, causal,
-                         (int64_t)(H / Hkv) * ((Sq + 31) / 32));
-  sp.ns_q = split_sweep((int64_t)B * H * ((Sq + 127) / 128), occ_q, cus, causal, (Sk + 31) / 32);
+  const int64_t n_kv = (int64_t)B * Hkv * ((Sk + 127) / 128), n_q = (int64_t)B * H * ((Sq + 127) / 128);
+  const int64_t t_kv = (int64_t)(H / Hkv) * ((Sq + 31) / 32), t_q = (Sk + 31) / 32;
+  sp.ns_kv = split_sweep(n_kv, occ_kv, cus, causal, t_kv);
+  sp.ns_q = split_sweep(n_q, occ_q, cus, causal, t_q);
+  // non-causal grids past one round: split only the last, partial round
+  if (!causal && sp.ns_kv == 1) sp.ns_kv = split_tail(n_kv, occ_kv, cus, t_kv, &sp.nfull_kv);
+  if (!causal && sp.ns_q == 1) sp.ns_q = split_tail(n_q, occ_q, cus, t_q, &sp.nfull_q);
   return sp;
 }
 
