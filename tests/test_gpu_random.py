@@ -5,8 +5,10 @@ they differ), query and key lengths (decode-like, short-key, ragged, long),
 head dim 1..256, causal, scale (default, positive, zero or negative), the
 tensor layout (contiguous [B,H,S,D], a [B,S,H,D] view, or rows one element
 off 16-byte alignment inside wider rows) and, where the ABI takes one, an
-attention mask (bool or additive, broadcast or full).  The cases are fixed
-by the seed below, so a failure names a case that reruns identically.
+attention mask (bool or additive, broadcast or full); a further set of
+causal cases of one sequence with 1024-2600 queries and keys drives the
+causal key-split plans.  The cases are fixed by the seed below, so a
+failure names a case that reruns identically.
 
 Forward cases run through the C ABI (cmpext3_attn_fwd / _gqa / _masked) into
 an output that is a view inside a larger buffer filled with a sentinel: the
@@ -52,6 +54,7 @@ TDT = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}
 SEED = 20261202
 NCASES = 192
 NTRAIN = 96
+NLONG = 24   # extra causal cases of few blocks and long sweeps (key-split causal plans)
 SENTINEL = -4096.0  # exact in fp16, bf16 and fp32; never an attention output here
 # oracle work bound (B * H * Sq * Sk * D) so that every case checks in about a second
 MAX_WORK = 1.2e9
@@ -113,8 +116,22 @@ def _draw_train(rng):
                 layout=layout, mask=mask, seed=int(rng.integers(1, 2**31 - 1)))
 
 
+def _draw_long_causal(rng):
+    """Causal grids of few blocks with long sweeps: the launches that cut
+    every block's keys into parts (whose rows may see none of a part's keys)."""
+    c = _draw(rng)
+    c.update(causal=True, B=1, Sq=int(rng.integers(1024, 2600)), Sk=int(rng.integers(1024, 2600)))
+    c["H"] = c["Hkv"] * int(rng.choice([1, 2]))
+    while c["H"] * c["Sq"] * c["Sk"] * c["D"] > MAX_WORK:
+        c["Sq"] = max(1024, c["Sq"] // 2)
+        c["D"] = max(8, c["D"] // 2)
+    return c
+
+
 _rng = np.random.default_rng(SEED)
 CASES = [_draw(_rng) for _ in range(NCASES)]
+_rng_long = np.random.default_rng(SEED + 2)
+CASES += [_draw_long_causal(_rng_long) for _ in range(NLONG)]
 _rng_train = np.random.default_rng(SEED + 1)
 TRAIN_CASES = [_draw_train(_rng_train) for _ in range(NTRAIN)]
 
